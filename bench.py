@@ -1,0 +1,421 @@
+"""Benchmark of the MI355X paged KV-cache path (one GPU).
+
+    python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline]
+
+A step is one launch of the hot-path kernel over one batch of synthetic input
+(one decode step's K/V append for one layer, by default).  Launches are
+replayed from a HIP graph of G back-to-back launches, each over a different
+rotation set of inputs and slot mappings, as the reference replays its decode
+step from a CUDA graph (llm.py:634-681); the rotation keeps the working set far
+above the 256 MB Infinity Cache.  Inputs are resident in HBM before timing.
+HIP events on the launch stream bracket exactly K steps after W warmup steps.
+
+The JSON line carries:
+  value            algorithmic HBM GB/s (bytes the kernel must move / time)
+  roofline         the same per launch against MI355X's 8 TB/s peak, plus the
+                   HBM traffic measured with rocprofv3 PMC counters (committed
+                   under profiles/), when present
+  cpu_baseline     the numpy oracle timed on this host on a bounded sample
+
+Workloads (default fp8_decode_append, config 2 of the benchmark plan):
+  fp8_decode_append  128 seqs x 1 token, 8x128 bf16 -> E4M3FN, 65536 blocks
+  bf16_append        512 tokens of Llama-3-8B K/V (8x128), 4096 blocks
+  chunked_append     4096 tokens of Qwen3 K/V (4x128), 32768 blocks
+  gather             the chunked case's 6 sequences (prefix + chunk) to rows
+  mla_prefill / mla_decode   kv_c 512 + k_pe 64, block 64, 20000 blocks
+  copy_blocks        2048 pairs over 61 layers of [8192, 2, 16, 8, 128] bf16
+  swap               8192 scattered blocks x 8 layers (4 GiB) D2H + H2D
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+# --------------------------------------------------------------------------- #
+# workloads: each returns (launch(i), info dict)
+# --------------------------------------------------------------------------- #
+
+
+def _affine_block_maps(R, num_blocks, gen, device):
+    """R bijections b -> (a*b + c) mod num_blocks (num_blocks a power of two, a odd)."""
+    import torch
+
+    a = torch.randint(0, num_blocks // 2, (R,), generator=gen) * 2 + 1
+    c = torch.randint(0, num_blocks, (R,), generator=gen)
+    return a.to(device), c.to(device)
+
+
+def setup_append(args, device, fp8):
+    import torch
+
+    from pipeswift_amd import cache_ops, workloads
+    from pipeswift_amd.reshape_and_cache import reshape_and_cache_flash
+
+    case = workloads.config2_fp8_decode() if fp8 else workloads.config1_append()
+    ps, P = case.cache.shape[2], case.cache.shape[0]
+    N = case.slot_mapping.shape[0]
+    R = args.rotate
+    gen = torch.Generator().manual_seed(99)
+    dgen = torch.Generator(device=device).manual_seed(99)
+    qkv = torch.empty((R,) + tuple(case.qkv.shape), dtype=torch.bfloat16, device=device)
+    qkv.normal_(0.0, 2.0 if fp8 else 1.0, generator=dgen)
+    qkv[0].copy_(case.qkv.to(device))
+    a, c = _affine_block_maps(R, P, gen, device)
+    base = case.slot_mapping.to(device)
+    valid = base >= 0
+    blk = torch.where(valid, base // ps, torch.zeros_like(base))
+    slots = ((a.view(R, 1) * blk.view(1, N) + c.view(R, 1)) % P) * ps + (base % ps).view(1, N)
+    slots = torch.where(valid.view(1, N), slots, torch.full_like(slots, -1)).contiguous()
+    slots[0].copy_(base)
+    cache = case.cache.to(device)
+    k_scale = v_scale = None
+    if fp8:
+        scales = cache_ops.compute_kv_scales(case.key(qkv[0]), case.value(qkv[0]))
+        k_scale, v_scale = scales[0:1], scales[1:2]
+    kc, vc = cache[:, 0], cache[:, 1]
+
+    def launch(i):
+        q = qkv[i]
+        reshape_and_cache_flash(case.key(q), case.value(q), kc, vc, slots[i], k_scale, v_scale)
+
+    nbytes = workloads.append_bytes(case.num_valid, N, case.num_heads, case.head_size, 2, 1 if fp8 else 2)
+    info = {
+        "name": "fp8_decode_append" if fp8 else "bf16_append",
+        "kernel": "paged_scatter_kernel",
+        "bytes": nbytes,
+        "tokens": case.num_valid,
+        "dtype": "fp8_e4m3fn" if fp8 else "bf16",
+        "config": {
+            "workload": "fp8_decode_append (config 2)" if fp8 else "bf16_append (config 1)",
+            "tokens": N, "valid_tokens": case.num_valid, "kv_heads": case.num_heads, "head_dim": case.head_size,
+            "block_size": ps, "num_blocks": P, "in_dtype": "bf16",
+            "cache_dtype": "fp8_e4m3fn" if fp8 else "bf16", "qkv_row_stride": case.qkv.shape[1],
+            "scale": "per-tensor from amax" if fp8 else None,
+        },
+        "cpu": lambda: cpu_append(case, fp8),
+    }
+    return launch, info
+
+
+def setup_chunked(args, device, gather):
+    import torch
+
+    from pipeswift_amd import cache_ops, workloads
+    from pipeswift_amd.reshape_and_cache import reshape_and_cache_flash
+
+    cc = workloads.config3_chunked()
+    a = cc.append
+    P, ps = a.cache.shape[0], a.cache.shape[2]
+    cache = a.cache.to(device)
+    R = args.rotate if not gather else max(1, min(args.rotate, 8))
+    gen = torch.Generator().manual_seed(98)
+    am, cm = _affine_block_maps(R, P, gen, device)
+    if not gather:
+        N = a.slot_mapping.shape[0]
+        dgen = torch.Generator(device=device).manual_seed(98)
+        qkv = torch.empty((R,) + tuple(a.qkv.shape), dtype=torch.bfloat16, device=device)
+        qkv.normal_(generator=dgen)
+        base = a.slot_mapping.to(device)
+        slots = ((am.view(R, 1) * (base // ps).view(1, N) + cm.view(R, 1)) % P) * ps + (base % ps).view(1, N)
+        kc, vc = cache[:, 0], cache[:, 1]
+
+        def launch(i):
+            q = qkv[i]
+            reshape_and_cache_flash(a.key(q), a.value(q), kc, vc, slots[i])
+
+        nbytes = workloads.append_bytes(N, N, a.num_heads, a.head_size, 2, 2)
+        return launch, {
+            "name": "chunked_append", "kernel": "paged_scatter_kernel", "bytes": nbytes, "tokens": N,
+            "dtype": "bf16",
+            "config": {"workload": "chunked_append (config 3)", "tokens": N, "kv_heads": a.num_heads,
+                       "head_dim": a.head_size, "block_size": ps, "num_blocks": P, "sequences": len(cc.chunk)},
+            "cpu": lambda: cpu_append(a, False),
+        }
+    T = int(cc.cu_seq_lens[-1])
+    bt = cc.block_table.to(device)
+    bts = ((am.view(R, 1, 1) * bt.long().view(1, *bt.shape) + cm.view(R, 1, 1)) % P).to(torch.int32).contiguous()
+    cu = cc.cu_seq_lens.to(device)
+    out_k = torch.empty(T, a.num_heads, a.head_size, dtype=torch.bfloat16, device=device)
+    out_v = torch.empty_like(out_k)
+    kc, vc = cache[:, 0], cache[:, 1]
+
+    def launch(i):
+        cache_ops.gather_cache(kc, out_k, bts[i], cu, src_cache_v=vc, dst_v=out_v)
+
+    pages = int(((cc.prefix + cc.chunk + ps - 1) // ps).sum())
+    nbytes = workloads.gather_bytes(T, a.num_heads * a.head_size, 2, 2, pages)
+    return launch, {
+        "name": "gather", "kernel": "paged_gather_kernel", "bytes": nbytes, "tokens": T, "dtype": "bf16",
+        "config": {"workload": "block gather (config 3)", "tokens": T, "sequences": len(cc.chunk),
+                   "kv_heads": a.num_heads, "head_dim": a.head_size, "block_size": ps, "num_blocks": P,
+                   "pages": pages},
+        "cpu": lambda: cpu_gather(cc),
+    }
+
+
+def setup_mla(args, device, decode):
+    import torch
+
+    from pipeswift_amd import workloads
+    from pipeswift_amd.reshape_and_cache import reshape_and_cache_flash_diffkv
+
+    n = 128 if decode else 4096
+    case = workloads.config4_mla(num_tokens=n, decode=decode)
+    P, ps = case.cache.shape[0], case.cache.shape[1]
+    R = args.rotate
+    dgen = torch.Generator(device=device).manual_seed(97)
+    latent = torch.empty((R,) + tuple(case.latent.shape), dtype=torch.bfloat16, device=device)
+    latent.normal_(generator=dgen)
+    kv_c = torch.empty((R,) + tuple(case.kv_c.shape), dtype=torch.bfloat16, device=device)
+    kv_c.normal_(generator=dgen)
+    slots = torch.stack([torch.randperm(P * ps, generator=torch.Generator().manual_seed(97 + r))[:n]
+                         for r in range(min(R, 64))]).to(torch.int64).to(device)
+    slots[0].copy_(case.slot_mapping.to(device))
+    cache = case.cache.to(device).unsqueeze(2)
+
+    def launch(i):
+        reshape_and_cache_flash_diffkv(kv_c[i].unsqueeze(1), case.k_pe(latent[i]).unsqueeze(1), cache,
+                                       slots[i % slots.shape[0]])
+
+    nbytes = workloads.mla_bytes(n, 576, 2, 2)
+    return launch, {
+        "name": "mla_decode" if decode else "mla_prefill", "kernel": "paged_scatter_kernel", "bytes": nbytes,
+        "tokens": n, "dtype": "bf16",
+        "config": {"workload": f"MLA latent append, {'decode' if decode else 'prefill'} (config 4)", "tokens": n,
+                   "row": 576, "block_size": ps, "num_blocks": P},
+        "cpu": None,
+    }
+
+
+def setup_copy_blocks(args, device):
+    import torch
+
+    from pipeswift_amd import cache_ops, workloads
+
+    L, P = 61, 8192
+    stack = torch.empty((L, P, 2, 16, 8, 128), dtype=torch.bfloat16, device=device)
+    stack.view(torch.int16).random_(generator=torch.Generator(device=device).manual_seed(96))
+    pairs = [workloads.config5a_pairs(seed=1005 + r).to(device) for r in range(4)]
+
+    def launch(i):
+        cache_ops.copy_blocks(stack, pairs[i % len(pairs)], validate=False)
+
+    nbytes = workloads.copy_blocks_bytes(2048, L, 2 * 16 * 8 * 128 * 2)
+    return launch, {
+        "name": "copy_blocks", "kernel": "copy_blocks_kernel", "bytes": nbytes, "tokens": 2048 * 16,
+        "dtype": "bf16",
+        "config": {"workload": "copy_blocks (config 5a)", "pairs": 2048, "layers": L, "num_blocks": P,
+                   "block_bytes": 65536},
+        "cpu": None,
+    }
+
+
+# --------------------------------------------------------------------------- #
+# CPU baseline: the numpy oracle on a bounded sample of the same workload
+# --------------------------------------------------------------------------- #
+
+
+def _raw(t):
+    import numpy as np
+    import torch
+
+    t = t.contiguous()
+    if t.dtype in (torch.bfloat16, torch.float16):
+        return t.view(torch.int16).numpy().view(np.uint16)
+    if t.dtype == torch.float8_e4m3fn:
+        return t.view(torch.uint8).numpy()
+    return t.numpy()
+
+
+def cpu_append(case, fp8, budget_s=10.0):
+    import numpy as np
+
+    from oracle import kv_oracle as O
+
+    key, value = _raw(case.key()), _raw(case.value())
+    cache = np.zeros(tuple(case.cache.shape), np.uint8 if fp8 else np.uint16)
+    slots = case.slot_mapping.numpy()
+    ks = vs = None
+    if fp8:
+        ks, _ = O.amax_scale(key, "bf16")
+        vs, _ = O.amax_scale(value, "bf16")
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        O.reshape_and_cache(key, value, cache[:, 0], cache[:, 1], slots, "bf16", "fp8" if fp8 else "bf16", ks, vs)
+        n += 1
+        el = time.perf_counter() - t0
+        if el > budget_s or n >= 20000:
+            break
+    return n, el, f"{n} steps of the numpy oracle append (same inputs and cache geometry)"
+
+
+def cpu_gather(cc, budget_s=10.0):
+    from oracle import kv_oracle as O
+
+    kc = _raw(cc.append.cache[:, 0])
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        O.gather_cache(kc, cc.block_table.numpy(), cc.cu_seq_lens.numpy())
+        n += 1
+        el = time.perf_counter() - t0
+        if el > budget_s:
+            break
+    # the oracle gathered K only; the GPU step moves K and V
+    return n / 2.0, el, f"{n} K-only numpy oracle gathers (counted as {n / 2:.1f} K+V steps)"
+
+
+# --------------------------------------------------------------------------- #
+# main
+# --------------------------------------------------------------------------- #
+
+
+def main():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=2048)
+    p.add_argument("--warmup", type=int, default=256)
+    p.add_argument("--workload", default="fp8_decode_append")
+    p.add_argument("--rotate", type=int, default=512, help="rotation sets of inputs/slots")
+    p.add_argument("--graph", type=int, default=64, help="launches captured per HIP graph (0: eager)")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    args = p.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the KV kernels are rank-local; see the sharding notes). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    name = args.workload
+    if name in ("fp8_decode_append", "bf16_append"):
+        launch, info = setup_append(args, device, fp8=name.startswith("fp8"))
+    elif name in ("chunked_append", "gather"):
+        launch, info = setup_chunked(args, device, gather=name == "gather")
+    elif name in ("mla_prefill", "mla_decode"):
+        launch, info = setup_mla(args, device, decode=name == "mla_decode")
+    elif name == "copy_blocks":
+        launch, info = setup_copy_blocks(args, device)
+        args.graph = min(args.graph, 4)
+        args.rotate = 4
+    else:
+        raise SystemExit(f"unknown workload {name}")
+    R = args.rotate
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.Stream(device)
+    G = args.graph
+    graphs = []
+    with torch.cuda.stream(stream):
+        for i in range(min(R, 8)):
+            launch(i)  # eager warmup of every code path before capture
+        stream.synchronize()
+        if G > 0:
+            n_graphs = max(1, min(R // G, 8))
+            for gi in range(n_graphs):
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, stream=stream):
+                    for j in range(G):
+                        launch((gi * G + j) % R)
+                graphs.append(g)
+    torch.cuda.synchronize()
+
+    def run(steps):
+        with torch.cuda.stream(stream):
+            if G > 0:
+                reps = steps // G
+                for r in range(reps):
+                    graphs[r % len(graphs)].replay()
+                return reps * G
+            for i in range(steps):
+                launch(i % R)
+            return steps
+
+    run(args.warmup)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    done = run(args.steps)
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end)
+    per_launch_s = ms / 1e3 / done
+    achieved = info["bytes"] / per_launch_s / 1e9
+
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get(name, {}).get("bytes_per_launch")
+
+    cpu = None
+    if not args.no_cpu_baseline and info.get("cpu") is not None:
+        torch.set_num_threads(1)
+        n, el, sample = info["cpu"]()
+        cpu = {"value": info["bytes"] * n / el / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+               "sample": f"{sample}; {el:.1f} s on 1 thread of {_cpu_model()} ({os.cpu_count()} cpus visible)",
+               "tokens_per_s": info["tokens"] * n / el}
+
+    line = {
+        "metric": "achieved HBM GB/s (% of MI355X peak) + tokens/s for paged KV append/FP8 quant",
+        "value": round(achieved, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": done,
+        "warmup": args.warmup,
+        "ms_per_step": ms / done,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": info["dtype"],
+        "data": "synthetic (seeded)",
+        "tokens_per_s": round(info["tokens"] / per_launch_s, 1),
+        "pct_of_peak": round(100.0 * achieved / PEAK_HBM_GBS, 3),
+        "config": dict(info["config"], launches_per_graph=G, rotation_sets=R),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": info["kernel"],
+            "achieved": round(achieved, 2),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 5),
+            "bytes_per_launch": info["bytes"],
+            "us_per_launch": round(per_launch_s * 1e6, 3),
+            "traffic": traffic,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

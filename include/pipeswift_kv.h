@@ -1,0 +1,195 @@
+/*
+ * pipeswift_kv.h -- C ABI of the MI355X (gfx950) paged KV-cache data path.
+ *
+ * One shared library, libpipeswift_kv.so, built with hipcc for gfx950 from
+ * pipeswift_amd/csrc/pipeswift_kv.hip.  Every entry point takes plain device
+ * pointers, element or byte strides and sizes, a dtype code and a HIP stream
+ * handle (hipStream_t passed as void*; NULL is the legacy default stream).
+ *
+ * Conventions shared by every entry point:
+ *   - Nothing here allocates device memory or synchronizes the stream, so every
+ *     kernel entry point is safe to capture into a HIP graph.
+ *   - Return value: PSK_OK (0) on success; a negative PSK_E* code when an
+ *     argument violates a precondition (the Python layer raises AssertionError);
+ *     a positive hipError_t when the runtime rejects a launch or copy (the
+ *     Python layer raises RuntimeError).  psk_last_error() returns a message
+ *     for the calling thread's most recent failure.
+ *   - Device-side indices (slot_mapping, block tables, block mappings) that fall
+ *     outside the cache are skipped by the kernels instead of dereferenced; the
+ *     host layer validates them where they live on the host.
+ *
+ * Reference interfaces each entry replaces (wsjdsg/PipeSwift, Python/Triton):
+ *   psk_reshape_and_cache     pipeswift/utils/triton_kernels/reshape_and_cache.py:11-135
+ *   psk_concat_and_cache_mla  pipeswift/utils/triton_kernels/reshape_and_cache.py:138-229
+ *   psk_swap_blocks           pipeswift/utils/copy_engine.py:429-457 (cuMemcpyBatchAsync)
+ * and build-defined operations that have no reference implementation:
+ *   psk_gather_cache          page-table reads done inside attention kernels in the
+ *                             reference (pipeswift/llms/layers/attention.py:189-211)
+ *   psk_copy_blocks           prefix-cache page copy; the reference remaps instead
+ *                             (pipeswift/engine/block_manager.py:841-877)
+ *   psk_kv_amax_scale         per-tensor FP8 scale; the reference fixes it at 1.0
+ *                             (pipeswift/utils/fp8_kv.py:1-3, 75-77)
+ */
+#ifndef PIPESWIFT_KV_H
+#define PIPESWIFT_KV_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes */
+#define PSK_DTYPE_F32 0
+#define PSK_DTYPE_F16 1
+#define PSK_DTYPE_BF16 2
+#define PSK_DTYPE_FP8_E4M3FN 3 /* OCP E4M3FN: bias 7, max 448, 0x7F/0xFF NaN */
+
+/* status codes (positive values are hipError_t) */
+#define PSK_OK 0
+#define PSK_E_ARG (-1)       /* shape, stride, size or pointer precondition */
+#define PSK_E_DTYPE (-2)     /* unsupported dtype combination */
+#define PSK_E_RANGE (-3)     /* host-visible page index out of range */
+#define PSK_E_WORKSPACE (-4) /* workspace too small */
+
+/* swap transports */
+#define PSK_SWAP_MEMCPY 0 /* one hipMemcpyAsync per (view, run) on the stream */
+#define PSK_SWAP_BATCH 1  /* one hipMemcpyBatchAsync over every (view, run) */
+#define PSK_SWAP_BLIT 2   /* one copy kernel reading/writing mapped pinned memory */
+
+/* Message for the calling thread's most recent non-zero status. */
+const char* psk_last_error(void);
+
+/* ABI version of this library. */
+int psk_abi_version(void);
+
+/*
+ * Paged KV append for MHA/GQA.  Replaces triton_reshape_and_cache_flash
+ * (reshape_and_cache.py:83-135) and its kernel (:11-80).
+ *
+ * For each token t < num_tokens with s = slot_mapping[t]:
+ *   s < 0 (padding, foreign DCP token) or s >= num_blocks*block_size: skipped.
+ *   blk = s / block_size, off = s % block_size, for h < num_heads, d < head_size:
+ *     key_cache  [blk*kc[0] + off*kc[1] + h*kc[2] + d*kc[3]] = q(key  [t*key_stride   + h*head_size + d], k_scale)
+ *     value_cache[blk*vc[0] + off*vc[1] + h*vc[2] + d*vc[3]] = q(value[t*value_stride + h*head_size + d], v_scale)
+ * Strides are in elements.  The token's [num_heads, head_size] row is read
+ * contiguously from its row start, as the reference does (:43-47, :63-64).
+ * in_dtype == cache_dtype: q is the identity (bit copy, any dtype).
+ * cache_dtype == FP8_E4M3FN, in_dtype in {BF16, F16, F32}:
+ *   q(x, s) = e4m3fn_rne(clamp(float(x) / s, -448, 448)), NaN -> 0x7F|sign,
+ *   s = *scale (device fp32) or 1.0 when the pointer is NULL.  At s == 1.0 this
+ *   is the reference's IS_FP8 branch (:66-77) and fp8_kv.quantize (fp8_kv.py:75-77).
+ */
+int psk_reshape_and_cache(const void* key, const void* value, void* key_cache, void* value_cache,
+                          const int64_t* slot_mapping, int64_t num_tokens, int64_t num_heads,
+                          int64_t head_size, int64_t block_size, int64_t num_blocks,
+                          int64_t key_stride, int64_t value_stride, const int64_t* key_cache_strides,
+                          const int64_t* value_cache_strides, int in_dtype, int cache_dtype,
+                          const float* k_scale, const float* v_scale, void* stream);
+
+/*
+ * MLA latent-cache append: replaces triton_reshape_and_cache_flash_diffkv
+ * (reshape_and_cache.py:191-229) and its kernel (:138-188).
+ *
+ * For each token t with a valid slot s (as above) the cache row at
+ * kv_cache + blk*cache_block_stride + off*cache_page_stride (elements) receives
+ * key_len elements read flat from kv_c + t*kv_c_stride followed by value_len
+ * elements read flat from k_pe + t*k_pe_stride (the reference's flat tile_pos
+ * addressing, :161-188).  FP8: as psk_reshape_and_cache with one scale.
+ */
+int psk_concat_and_cache_mla(const void* kv_c, const void* k_pe, void* kv_cache,
+                             const int64_t* slot_mapping, int64_t num_tokens, int64_t key_len,
+                             int64_t value_len, int64_t kv_c_stride, int64_t k_pe_stride,
+                             int64_t block_size, int64_t num_blocks, int64_t cache_block_stride,
+                             int64_t cache_page_stride, int in_dtype, int cache_dtype,
+                             const float* scale, void* stream);
+
+/*
+ * Block gather from a paged cache into contiguous rows (build-defined; vLLM's
+ * gather_cache convention).  For sequence b < batch_size and output token
+ * t in [cu_seq_lens[b], cu_seq_lens[b+1]) with p = (seq_starts ? seq_starts[b] : 0)
+ * + t - cu_seq_lens[b]:
+ *   blk = block_table[b*block_table_stride + p / block_size], off = p % block_size
+ *   dst[t*dst_row_stride + i] = dq(src[blk*cache_block_stride + off*cache_page_stride + i]),
+ *   i < row_len.
+ * Rows whose blk is outside [0, num_blocks) are written as zeros; output
+ * tokens at or beyond cu_seq_lens[batch_size] are left untouched.
+ * src1/dst1 (both NULL or both set) gather a second cache (V) with the same
+ * geometry in the same launch.  dq: identity when cache_dtype == out_dtype;
+ * FP8_E4M3FN cache to BF16/F16/F32 out: round(float(q) * scale).
+ */
+int psk_gather_cache(const void* src0, const void* src1, void* dst0, void* dst1,
+                     const int32_t* block_table, const int32_t* cu_seq_lens,
+                     const int32_t* seq_starts, int64_t batch_size, int64_t block_table_stride,
+                     int64_t num_tokens, int64_t row_len, int64_t block_size, int64_t num_blocks,
+                     int64_t cache_block_stride, int64_t cache_page_stride, int64_t dst_row_stride,
+                     int cache_dtype, int out_dtype, const float* scale, void* stream);
+
+/*
+ * Block copy inside a layered cache (build-defined, vLLM's copy_blocks
+ * convention).  For every layer l < num_layers and pair i < num_pairs with
+ * (s, d) = (block_mapping[2i], block_mapping[2i+1]):
+ *   bytes [0, block_bytes) at cache + l*layer_stride + d*block_stride
+ *     = bytes at cache + l*layer_stride + s*block_stride        (strides in bytes)
+ * Pairs with s or d outside [0, num_blocks) are skipped.  Snapshot semantics
+ * hold when destinations are unique and disjoint from sources (the host layer
+ * checks this); otherwise overlapping pairs race.
+ */
+int psk_copy_blocks(void* cache, int64_t num_layers, int64_t layer_stride, int64_t block_stride,
+                    int64_t block_bytes, int64_t num_blocks, const int64_t* block_mapping,
+                    int64_t num_pairs, void* stream);
+
+/*
+ * Page transfer between two tiers (device <-> pinned host), the transport under
+ * CopyEngine.store/load.  Replaces CopyEngine._copy_blocks (copy_engine.py:429-457).
+ *
+ * View v has src_bases[v], dst_bases[v] and bytes_per_page[v]; run r moves
+ * pages [src_start[r], src_start[r]+run_len[r]) to
+ * [dst_start[r], dst_start[r]+run_len[r]) in every view:
+ *   dst_bases[v] + dst_start[r]*bpb[v]  <-  src_bases[v] + src_start[r]*bpb[v],
+ *   run_len[r]*bpb[v] bytes.
+ * All arrays are host memory.  Runs outside [0, src_num_pages) or
+ * [0, dst_num_pages) return PSK_E_RANGE before anything is enqueued.
+ * PSK_SWAP_BLIT needs `staging`: host memory from psk_host_alloc of at least
+ * psk_swap_staging_bytes(num_views, pages) bytes that stays untouched until
+ * the enqueued work completes; the other transports ignore it.
+ * host pointers must come from psk_host_alloc (mapped pinned memory).
+ */
+int psk_swap_blocks(int transport, const uint64_t* src_bases, const uint64_t* dst_bases,
+                    const uint64_t* bytes_per_page, int64_t num_views, const int64_t* src_start,
+                    const int64_t* dst_start, const int64_t* run_len, int64_t num_runs,
+                    int64_t src_num_pages, int64_t dst_num_pages, void* staging,
+                    int64_t staging_bytes, void* stream);
+
+/* Staging bytes PSK_SWAP_BLIT needs for num_views views and num_pages pages. */
+int64_t psk_swap_staging_bytes(int64_t num_views, int64_t num_pages);
+
+/*
+ * Per-tensor FP8 scale from amax (build-defined; the reference uses 1.0).
+ * For tensor j in {0, 1} (x1 may be NULL): amax_j = max |x_j| over `rows` rows
+ * of `row_len` elements at element stride row_stride_j, NaN ignored;
+ * scale_out[j] = amax_j > 0 ? amax_j / qmax : 1.0f (IEEE fp32 divide);
+ * amax_out[j] = amax_j when amax_out is not NULL.  `workspace` is device
+ * memory of psk_kv_amax_workspace_len() uint32 words that is zero before the
+ * first call; each call leaves it zero again.  Calls sharing a workspace must
+ * not overlap.
+ */
+int psk_kv_amax_scale(const void* x0, const void* x1, int64_t rows, int64_t row_len,
+                      int64_t row_stride0, int64_t row_stride1, int dtype, float qmax,
+                      float* scale_out, float* amax_out, uint32_t* workspace,
+                      int64_t workspace_len, void* stream);
+
+int64_t psk_kv_amax_workspace_len(void);
+
+/*
+ * Pinned, device-mapped host memory for the L2 mirror and swap staging
+ * (hipHostMalloc).  Allocation happens at set-up, never on the hot path.
+ */
+int psk_host_alloc(int64_t bytes, void** ptr);
+int psk_host_free(void* ptr);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PIPESWIFT_KV_H */

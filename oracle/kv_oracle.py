@@ -1,0 +1,370 @@
+"""numpy restatement of the reference's paged KV-cache semantics (test-only).
+
+Tensors are numpy arrays holding raw element bits: bf16 and fp16 as uint16,
+fp32 as float32, fp8 E4M3FN as uint8.  ``dtype`` arguments are the strings
+"bf16", "f16", "f32", "fp8".  Byte-copy semantics never look at the values;
+only the FP8 paths convert to float32.
+
+Reference files restated here (wsjdsg/PipeSwift):
+  pipeswift/utils/triton_kernels/reshape_and_cache.py  (append, MLA concat, FP8)
+  pipeswift/utils/fp8_kv.py:24-25,75-77                 (FP8 constants, quantize)
+  pipeswift/utils/metadata.py:264-295, 351-392          (slot_mapping, page_table)
+  pipeswift/utils/copy_engine.py:121-142, 373-427       (page bytes, views, range
+                                                         check, run coalescing)
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+FP8_E4M3_MAX = 448.0  # fp8_kv.py:25, reshape_and_cache.py:8
+
+RAW = {"bf16": np.uint16, "f16": np.uint16, "f32": np.float32, "fp8": np.uint8}
+
+
+# --------------------------------------------------------------------------- #
+# element conversions
+# --------------------------------------------------------------------------- #
+
+
+def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    """bf16 bits -> float32 (exact: bf16 is the top half of an fp32)."""
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def bf16_from_f32(x: np.ndarray) -> np.ndarray:
+    """float32 -> bf16 bits, round to nearest even; NaN -> 0x7FC0.
+
+    Pinned against torch's ``Tensor.to(torch.bfloat16)`` on CPU.
+    """
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return np.where(np.isnan(x), np.uint16(0x7FC0), r).astype(np.uint16)
+
+
+def to_f32(raw: np.ndarray, dtype: str) -> np.ndarray:
+    if dtype == "bf16":
+        return bf16_to_f32(raw)
+    if dtype == "f16":
+        return np.asarray(raw, dtype=np.uint16).view(np.float16).astype(np.float32)
+    if dtype == "f32":
+        return np.asarray(raw, dtype=np.float32)
+    if dtype == "fp8":
+        return e4m3fn_to_f32(raw)
+    raise ValueError(dtype)
+
+
+def from_f32(x: np.ndarray, dtype: str) -> np.ndarray:
+    if dtype == "bf16":
+        return bf16_from_f32(x)
+    if dtype == "f16":
+        return np.asarray(x, dtype=np.float32).astype(np.float16).view(np.uint16)
+    if dtype == "f32":
+        return np.asarray(x, dtype=np.float32)
+    raise ValueError(dtype)
+
+
+def e4m3fn_from_f32(x: np.ndarray) -> np.ndarray:
+    """float32 -> OCP E4M3FN byte, round to nearest even, NOT saturating.
+
+    This is the plain dtype conversion ``Tensor.to(torch.float8_e4m3fn)``: a
+    magnitude that rounds above 448 (anything above 464), inf and NaN all
+    become the NaN code 0x7F with the input's sign.  The reference always
+    clamps to +-448 first (reshape_and_cache.py:70-77, fp8_kv.py:75-77), so
+    after the clamp only NaN reaches the NaN code.
+
+    Method: for |x| >= 2^-6 (E4M3FN normals) drop 20 of fp32's 23 mantissa bits
+    with round-half-even and rebias the exponent from 127 to 7; a mantissa
+    carry rolls into the exponent by itself.  Below 2^-6 the code is
+    round_half_even(|x| * 2^9), the count of 2^-9 subnormal steps (8 steps is
+    the smallest normal, code 0x08).
+    """
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    bits = x.view(np.uint32)
+    sign = ((bits >> 24) & 0x80).astype(np.uint8)
+    mag = bits & np.uint32(0x7FFFFFFF)
+    lsb = (mag >> 20) & 1
+    rounded = (mag.astype(np.uint64) + 0x7FFFF + lsb) >> 20
+    normal = rounded.astype(np.int64) - (120 << 3)  # (127 - 7) << 3
+    with np.errstate(invalid="ignore", over="ignore"):
+        sub = np.rint(np.abs(x) * np.float32(512.0))
+    sub = np.where(mag < 0x3C800000, sub, 0).astype(np.int64)
+    code = np.where(mag < 0x3C800000, sub, normal)
+    code = np.where((mag >= 0x7F800000) | (code > 0x7E), 0x7F, code)
+    return (code.astype(np.uint8) | sign).astype(np.uint8)
+
+
+_E4M3_TABLE = None
+
+
+def _e4m3_table() -> np.ndarray:
+    global _E4M3_TABLE
+    if _E4M3_TABLE is None:
+        b = np.arange(256, dtype=np.int64)
+        s = np.where(b & 0x80, -1.0, 1.0)
+        e = (b >> 3) & 0xF
+        m = b & 7
+        val = np.where(e == 0, np.ldexp(m.astype(np.float64), -9), np.ldexp(1.0 + m / 8.0, (e - 7).astype(np.int64)))
+        val = s * val
+        val[(e == 15) & (m == 7)] = np.nan
+        _E4M3_TABLE = val.astype(np.float32)
+    return _E4M3_TABLE
+
+
+def e4m3fn_to_f32(q: np.ndarray) -> np.ndarray:
+    """E4M3FN byte -> float32, exact; 0x7F/0xFF -> NaN.
+
+    Pinned against torch's ``Tensor.view(torch.float8_e4m3fn).float()``.
+    """
+    return _e4m3_table()[np.asarray(q, dtype=np.uint8)]
+
+
+def quantize_e4m3(x: np.ndarray, scale: float = 1.0) -> np.ndarray:
+    """q = e4m3fn(clamp(float32(x) / scale, -448, 448)), NaN kept as NaN.
+
+    At scale 1.0 this is the reference's FP8 append (reshape_and_cache.py:66-77)
+    and ``fp8_kv.quantize`` (fp8_kv.py:75-77); the division by a per-tensor
+    fp32 scale is the build's extension.  torch.clamp propagates NaN, so a NaN
+    input becomes 0x7F|sign.
+    """
+    x = np.asarray(x, dtype=np.float32)
+    with np.errstate(invalid="ignore", divide="ignore", over="ignore"):
+        y = (x / np.float32(scale)).astype(np.float32)
+    y = np.where(np.isnan(y), y, np.clip(y, -FP8_E4M3_MAX, FP8_E4M3_MAX)).astype(np.float32)
+    return e4m3fn_from_f32(y)
+
+
+def dequantize_e4m3(q: np.ndarray, scale: float, out_dtype: str) -> np.ndarray:
+    """y = round_out_dtype(float32(q) * scale) (build-defined gather dequant)."""
+    with np.errstate(invalid="ignore", over="ignore"):
+        y = (e4m3fn_to_f32(q) * np.float32(scale)).astype(np.float32)
+    return from_f32(y, out_dtype)
+
+
+# --------------------------------------------------------------------------- #
+# append (MHA/GQA), reshape_and_cache.py:11-80
+# --------------------------------------------------------------------------- #
+
+
+def _slot_parts(slot_mapping, block_size, num_blocks):
+    slots = np.asarray(slot_mapping, dtype=np.int64)
+    tok = np.flatnonzero((slots >= 0) & (slots < num_blocks * block_size))  # :33-34
+    s = slots[tok]
+    return tok, s // block_size, s % block_size  # :36-37
+
+
+def _write_rows(cache, tok, blk, off, rows, in_dtype, cache_dtype, scale):
+    if cache_dtype == in_dtype:
+        vals = rows[tok]
+    elif cache_dtype == "fp8":
+        vals = quantize_e4m3(to_f32(rows[tok], in_dtype), 1.0 if scale is None else scale)
+    else:
+        raise ValueError(f"cache dtype {cache_dtype} vs input {in_dtype}")
+    cache[blk, off] = vals.reshape((len(tok),) + cache.shape[2:])
+
+
+def reshape_and_cache(key, value, key_cache, value_cache, slot_mapping, in_dtype="bf16", cache_dtype="bf16",
+                      k_scale=None, v_scale=None):
+    """In-place paged append; reshape_and_cache.py:11-80 (kernel), :83-135 (wrapper).
+
+    key/value: [N, H, D] raw arrays.  key_cache/value_cache: [P, ps, H, D]
+    arrays (views of a fused [P, 2, ps, H, D] tensor are fine).  For every
+    token t with 0 <= slot < P*ps: cache[slot // ps, slot % ps] = q(x[t]).
+    Other slots are untouched.
+    """
+    ps = key_cache.shape[1]
+    tok, blk, off = _slot_parts(slot_mapping, ps, key_cache.shape[0])
+    _write_rows(key_cache, tok, blk, off, np.asarray(key), in_dtype, cache_dtype, k_scale)
+    _write_rows(value_cache, tok, blk, off, np.asarray(value), in_dtype, cache_dtype, v_scale)
+
+
+def concat_and_cache_mla(kv_c, k_pe, kv_cache, slot_mapping, in_dtype="bf16", cache_dtype="bf16", scale=None):
+    """MLA latent append; reshape_and_cache.py:138-188 (kernel), :191-229 (wrapper).
+
+    kv_c: [N, Lk], k_pe: [N, Lv] (flat per token, reference :176-185);
+    kv_cache: [P, ps, Lk + Lv].  cache[slot // ps, slot % ps] = [kv_c[t] | k_pe[t]].
+    """
+    ps = kv_cache.shape[1]
+    kv_c = np.asarray(kv_c).reshape(kv_c.shape[0], -1)
+    k_pe = np.asarray(k_pe).reshape(k_pe.shape[0], -1)
+    tok, blk, off = _slot_parts(slot_mapping, ps, kv_cache.shape[0])
+    row = np.concatenate([kv_c[tok], k_pe[tok]], axis=1)
+    if cache_dtype == in_dtype:
+        kv_cache[blk, off] = row.reshape((len(tok),) + kv_cache.shape[2:])
+    elif cache_dtype == "fp8":
+        q = quantize_e4m3(to_f32(row, in_dtype), 1.0 if scale is None else scale)
+        kv_cache[blk, off] = q.reshape((len(tok),) + kv_cache.shape[2:])
+    else:
+        raise ValueError(f"cache dtype {cache_dtype} vs input {in_dtype}")
+
+
+# --------------------------------------------------------------------------- #
+# gather (build-defined; vLLM gather_cache convention)
+# --------------------------------------------------------------------------- #
+
+
+def gather_cache(cache, block_table, cu_seq_lens, seq_starts=None, out=None, cache_dtype="bf16", out_dtype=None,
+                 scale=None):
+    """Contiguous rows from a paged cache.
+
+    For sequence b and output token t in [cu[b], cu[b+1]):
+    p = seq_starts[b] + t - cu[b] (seq_starts defaults to 0),
+    out[t] = dq(cache[block_table[b, p // ps], p % ps]).
+    A block id outside [0, P) or a page index beyond the table row gives a
+    zero row.  The reference has no such op: its attention kernels read the
+    cache through the same page_table (attention.py:189-211).
+    """
+    out_dtype = out_dtype or cache_dtype
+    ps = cache.shape[1]
+    P = cache.shape[0]
+    cu = np.asarray(cu_seq_lens, dtype=np.int64)
+    bt = np.asarray(block_table, dtype=np.int64)
+    B = len(cu) - 1
+    T = int(cu[-1]) if out is None else out.shape[0]
+    row_shape = cache.shape[2:]
+    if out is None:
+        out = np.zeros((T,) + row_shape, dtype=RAW[out_dtype])
+    for b in range(B):
+        n = int(cu[b + 1] - cu[b])
+        if n <= 0:
+            continue
+        start = 0 if seq_starts is None else int(seq_starts[b])
+        t = np.arange(n, dtype=np.int64)
+        p = start + t
+        page = p // ps
+        inb = page < bt.shape[1]
+        blk = np.full(n, -1, dtype=np.int64)
+        blk[inb] = bt[b, page[inb]]
+        good = (blk >= 0) & (blk < P)
+        rows = np.zeros((n,) + row_shape, dtype=RAW[cache_dtype])
+        rows[good] = cache[blk[good], (p % ps)[good]]
+        if out_dtype == cache_dtype:
+            vals = rows
+        else:
+            vals = dequantize_e4m3(rows, 1.0 if scale is None else scale, out_dtype)
+            vals[~good] = 0
+        dst = np.arange(cu[b], cu[b + 1])
+        keep = dst < T
+        out[dst[keep]] = vals[keep]
+    return out
+
+
+# --------------------------------------------------------------------------- #
+# copy_blocks (build-defined; vLLM copy_blocks convention, snapshot semantics)
+# --------------------------------------------------------------------------- #
+
+
+def validate_block_mapping(block_mapping, num_blocks):
+    """Preconditions for snapshot semantics: ids in range, unique destinations,
+    destinations disjoint from sources.  Raises AssertionError like the
+    reference's host-side checks (copy_engine.py:373-385)."""
+    m = np.asarray(block_mapping, dtype=np.int64).reshape(-1, 2)
+    assert ((m >= 0) & (m < num_blocks)).all(), "block id out of range"
+    assert len(np.unique(m[:, 1])) == len(m), "duplicate destination block"
+    assert not np.isin(m[:, 1], m[:, 0]).any(), "a destination block is also a source"
+
+
+def copy_blocks(stack, block_mapping):
+    """stack: [L, P, ...]; for every layer and pair (s, d): stack[l, d] = stack[l, s].
+
+    All reads happen before any write (snapshot), which is what an overlap-free
+    mapping gives any execution order.
+    """
+    m = np.asarray(block_mapping, dtype=np.int64).reshape(-1, 2)
+    if len(m) == 0:
+        return
+    stack[:, m[:, 1]] = stack[:, m[:, 0]].copy()
+
+
+# --------------------------------------------------------------------------- #
+# FP8 amax -> scale (build-defined; the reference fixes scale = 1.0)
+# --------------------------------------------------------------------------- #
+
+
+def amax_scale(x, dtype="bf16", qmax=FP8_E4M3_MAX):
+    """(scale, amax): amax = max |x| ignoring NaN; scale = amax / qmax in fp32,
+    or 1.0 when amax == 0."""
+    f = np.abs(to_f32(np.asarray(x), dtype)).ravel()
+    f = f[~np.isnan(f)]
+    amax = np.float32(f.max()) if f.size else np.float32(0.0)
+    scale = np.float32(amax / np.float32(qmax)) if amax > 0 else np.float32(1.0)
+    return scale, amax
+
+
+# --------------------------------------------------------------------------- #
+# L2 offload transport helpers, copy_engine.py
+# --------------------------------------------------------------------------- #
+
+
+def page_bytes(shapes_itemsizes):
+    """Bytes of one page across every layer of every cache tensor
+    (copy_engine.py:121-125): sum over caches of L * prod(shape[2:]) * itemsize."""
+    total = 0
+    for shape, itemsize in shapes_itemsizes:
+        total += int(np.prod(shape[2:], dtype=np.int64)) * itemsize * shape[0]
+    return total
+
+
+def coalesce(src_ids, dst_ids):
+    """Runs of pages that advance together on both tiers (copy_engine.py:407-427).
+
+    Sort by source (stable), split wherever src or dst does not step by one.
+    Returns (src_start, dst_start, run_len) as uint64 arrays.
+    """
+    src_ids = np.asarray(src_ids, dtype=np.uint64)
+    dst_ids = np.asarray(dst_ids, dtype=np.uint64)
+    order = np.argsort(src_ids, kind="stable")
+    src = src_ids[order]
+    dst = dst_ids[order]
+    breaks = (src[1:] != src[:-1] + 1) | (dst[1:] != dst[:-1] + 1)
+    starts = np.flatnonzero(np.concatenate(([True], breaks)))
+    lens = np.diff(np.append(starts, len(src))).astype(np.uint64)
+    return src[starts], dst[starts], lens
+
+
+def swap_pages(src_views, dst_views, src_ids, dst_ids):
+    """Byte copy of page rows between [P, bpb] views: dst[v][d] = src[v][s]."""
+    for sv, dv in zip(src_views, dst_views):
+        dv[np.asarray(dst_ids, dtype=np.int64)] = sv[np.asarray(src_ids, dtype=np.int64)]
+
+
+# --------------------------------------------------------------------------- #
+# slot mapping and page table, metadata.py
+# --------------------------------------------------------------------------- #
+
+
+def slot_mapping(page_table_row, offset, num_tokens, page_size, dcp_deg=1, dcp_rank=0, dcp_interleave_size=1):
+    """Slots of positions [offset, num_tokens) of one sequence (metadata.py:272-295).
+
+    dcp_deg == 1: slot = page_table[pos // ps] * ps + pos % ps.
+    DCP: tokens interleave over ranks in runs of dcp_interleave_size; a rank
+    owns pos when (pos // interleave) % dcp == rank and writes it at
+    local_pos = pos % interleave + pos // (interleave * dcp) * interleave into
+    physical pages of ps // dcp slots; foreign tokens get -1.
+    """
+    out = []
+    if dcp_deg == 1:
+        for pos in range(offset, num_tokens):
+            out.append(page_table_row[pos // page_size] * page_size + pos % page_size)
+        return out
+    phys = page_size // dcp_deg
+    stride = dcp_interleave_size * dcp_deg
+    for pos in range(offset, num_tokens):
+        if (pos // dcp_interleave_size) % dcp_deg == dcp_rank:
+            local = pos % dcp_interleave_size + pos // stride * dcp_interleave_size
+            out.append(page_table_row[pos // page_size] * phys + local % phys)
+        else:
+            out.append(-1)
+    return out
+
+
+def dcp_kv_len(prefix_len, dcp_deg, dcp_rank, dcp_interleave_size):
+    """Tokens of a prefix a DCP rank holds (metadata.py:246-255)."""
+    n = prefix_len // (dcp_interleave_size * dcp_deg) * dcp_interleave_size
+    rem = prefix_len % (dcp_interleave_size * dcp_deg)
+    if rem >= (dcp_rank + 1) * dcp_interleave_size:
+        n += dcp_interleave_size
+    elif rem >= dcp_rank * dcp_interleave_size:
+        n += rem % dcp_interleave_size
+    return n

@@ -1,0 +1,1169 @@
+// Paged KV-cache data path for MI355X (gfx950, CDNA4): append (MHA/GQA and MLA),
+// FP8 E4M3FN quantization fused into the append, block gather, copy_blocks,
+// per-tensor amax/scale and the device<->pinned-host page transport.
+//
+// Every kernel here is a memory-bound byte mover; none is a contraction, so no
+// MFMA.  Design points shared by all of them:
+//   * wavefront-granular work: one 64-lane wave owns one (token-chunk, part) or
+//     one page-unit, so the slot / block-table lookups are wave-uniform scalar
+//     loads and the row pointers live in SGPRs;
+//   * 16-byte lanes (global_load/store_dwordx4) whenever every base pointer,
+//     stride and row length allows it, falling back to 8/4/2/1 bytes;
+//   * all loads of a wave are issued before its stores so each lane keeps
+//     several 16 B requests in flight against HBM latency;
+//   * 64-bit address arithmetic throughout (a 65536-block fp8 cache is 2^31 B).
+//
+// C ABI: include/pipeswift_kv.h.  Nothing here allocates device memory or
+// synchronizes a stream.
+
+#include <hip/hip_runtime.h>
+
+#include <dlfcn.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <vector>
+
+#include "pipeswift_kv.h"
+
+namespace {
+
+constexpr int kWave = 64;
+
+// ----------------------------------------------------------------------------
+// error reporting
+// ----------------------------------------------------------------------------
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  snprintf(g_err, sizeof(g_err), "%s: %s (hipError_t %d)", what, hipGetErrorString(e), (int)e);
+  return (int)e;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? PSK_OK : hip_fail(e, what);
+}
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+int dtype_size(int dt) {
+  switch (dt) {
+    case PSK_DTYPE_F32: return 4;
+    case PSK_DTYPE_F16: return 2;
+    case PSK_DTYPE_BF16: return 2;
+    case PSK_DTYPE_FP8_E4M3FN: return 1;
+    default: return 0;
+  }
+}
+
+int log2_exact(int64_t v) {
+  if (v <= 0 || (v & (v - 1))) return -1;
+  int s = 0;
+  while ((int64_t(1) << s) < v) ++s;
+  return s;
+}
+
+// Largest power-of-two byte width <= max_bytes dividing every value in vals.
+int common_align(const uint64_t* vals, int n, int max_bytes) {
+  uint64_t acc = 0;
+  for (int i = 0; i < n; ++i) acc |= vals[i];
+  int b = max_bytes;
+  while (b > 1 && (acc & uint64_t(b - 1))) b >>= 1;
+  return b;
+}
+
+// ----------------------------------------------------------------------------
+// vectors and element conversions
+// ----------------------------------------------------------------------------
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+template <int B> struct VecT;
+template <> struct VecT<16> { using T = u32x4; };
+template <> struct VecT<8> { using T = u32x2; };
+template <> struct VecT<4> { using T = uint32_t; };
+template <> struct VecT<2> { using T = uint16_t; };
+template <> struct VecT<1> { using T = uint8_t; };
+
+template <int B>
+__device__ __forceinline__ typename VecT<B>::T vload(const char* p) {
+  return *reinterpret_cast<const typename VecT<B>::T*>(p);
+}
+template <int B>
+__device__ __forceinline__ void vstore(char* p, typename VecT<B>::T v) {
+  *reinterpret_cast<typename VecT<B>::T*>(p) = v;
+}
+
+template <int DT> struct Elt;
+template <> struct Elt<PSK_DTYPE_F32> {
+  using Bits = uint32_t;
+  static constexpr int kSize = 4;
+  __device__ static float to_f32(Bits b) { return __uint_as_float(b); }
+  __device__ static Bits from_f32(float f) { return __float_as_uint(f); }
+};
+template <> struct Elt<PSK_DTYPE_BF16> {
+  using Bits = uint16_t;
+  static constexpr int kSize = 2;
+  __device__ static float to_f32(Bits b) { return __uint_as_float(uint32_t(b) << 16); }
+  // Round to nearest even; NaN becomes the canonical quiet NaN 0x7FC0.
+  __device__ static Bits from_f32(float f) {
+    uint32_t u = __float_as_uint(f);
+    if (__builtin_isnan(f)) return 0x7FC0;
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return Bits(u >> 16);
+  }
+};
+template <> struct Elt<PSK_DTYPE_F16> {
+  using Bits = uint16_t;
+  static constexpr int kSize = 2;
+  __device__ static float to_f32(Bits b) { return float(__builtin_bit_cast(_Float16, b)); }
+  __device__ static Bits from_f32(float f) { return __builtin_bit_cast(Bits, _Float16(f)); }
+};
+
+// OCP E4M3FN byte for a NaN: 0x7F with the sign bit of the input, which is what
+// torch's float -> float8_e4m3fn conversion produces.
+__device__ __forceinline__ uint32_t e4m3_nan_byte(float x) {
+  return ((__float_as_uint(x) >> 24) & 0x80u) | 0x7Fu;
+}
+
+// Saturate to the finite E4M3FN range.  NaN passes through, as torch.clamp does.
+__device__ __forceinline__ float clamp_e4m3(float x) {
+  return __builtin_isnan(x) ? x : __builtin_fminf(__builtin_fmaxf(x, -448.0f), 448.0f);
+}
+
+// Two floats -> two E4M3FN bytes (low byte = a) with the native gfx950 OCP
+// conversion (v_cvt_pk_fp8_f32, round to nearest even).  Inputs are clamped
+// first, so the conversion never overflows; NaN lanes are rewritten to the
+// torch NaN byte.
+__device__ __forceinline__ uint32_t e4m3_pack2(float a, float b) {
+  uint32_t w = uint32_t(__builtin_amdgcn_cvt_pk_fp8_f32(clamp_e4m3(a), clamp_e4m3(b), 0, false)) & 0xFFFFu;
+  if (__builtin_expect(__builtin_isnan(a) || __builtin_isnan(b), 0)) {
+    if (__builtin_isnan(a)) w = (w & 0xFF00u) | e4m3_nan_byte(a);
+    if (__builtin_isnan(b)) w = (w & 0x00FFu) | (e4m3_nan_byte(b) << 8);
+  }
+  return w;
+}
+
+// E4M3FN bytes 0 and 1 (or 2 and 3 with hi) of w -> floats, native conversion.
+__device__ __forceinline__ f32x2 e4m3_unpack2(uint32_t w, bool hi) {
+  return hi ? __builtin_amdgcn_cvt_pk_f32_fp8(int(w), true) : __builtin_amdgcn_cvt_pk_f32_fp8(int(w), false);
+}
+
+// ---- conversion policies: In vector (IN_B bytes) -> Out vector (OUT_B bytes)
+
+template <int B>
+struct CopyConv {
+  static constexpr int IN_B = B;
+  static constexpr int OUT_B = B;
+  using In = typename VecT<B>::T;
+  using Out = typename VecT<B>::T;
+  __device__ static Out apply(In v, float) { return v; }
+  __device__ static Out zero() { return Out(0); }
+};
+
+// E input elements of type IN_DT -> E E4M3FN bytes, q = e4m3(clamp(x / scale)).
+template <int IN_DT, int E>
+struct QuantConv {
+  using EltT = Elt<IN_DT>;
+  static constexpr int IN_B = E * EltT::kSize;
+  static constexpr int OUT_B = E;
+  using In = typename VecT<IN_B>::T;
+  using Out = typename VecT<OUT_B>::T;
+  __device__ static Out apply(In v, float scale) {
+    typename EltT::Bits e[E];
+    __builtin_memcpy(e, &v, sizeof(v));
+    float f[E];
+#pragma unroll
+    for (int i = 0; i < E; ++i) f[i] = EltT::to_f32(e[i]) / scale;
+    if constexpr (E == 1) {
+      return Out(e4m3_pack2(f[0], 0.0f) & 0xFFu);
+    } else {
+      uint8_t o[E];
+#pragma unroll
+      for (int i = 0; i < E; i += 2) {
+        uint32_t w = e4m3_pack2(f[i], f[i + 1]);
+        o[i] = uint8_t(w);
+        o[i + 1] = uint8_t(w >> 8);
+      }
+      Out r;
+      __builtin_memcpy(&r, o, sizeof(r));
+      return r;
+    }
+  }
+  __device__ static Out zero() { return Out(0); }
+};
+
+// E E4M3FN bytes -> E elements of OUT_DT, y = round(float(q) * scale).
+template <int OUT_DT, int E>
+struct DequantConv {
+  using EltT = Elt<OUT_DT>;
+  static constexpr int IN_B = E;
+  static constexpr int OUT_B = E * EltT::kSize;
+  using In = typename VecT<IN_B>::T;
+  using Out = typename VecT<OUT_B>::T;
+  __device__ static Out apply(In v, float scale) {
+    uint8_t q[E];
+    __builtin_memcpy(q, &v, sizeof(v));
+    typename EltT::Bits o[E];
+    if constexpr (E == 1) {
+      o[0] = EltT::from_f32(e4m3_unpack2(uint32_t(q[0]), false).x * scale);
+    } else {
+#pragma unroll
+      for (int i = 0; i < E; i += 2) {
+        const f32x2 f = e4m3_unpack2(uint32_t(q[i]) | (uint32_t(q[i + 1]) << 8), false);
+        o[i] = EltT::from_f32(f.x * scale);
+        o[i + 1] = EltT::from_f32(f.y * scale);
+      }
+    }
+    Out r;
+    __builtin_memcpy(&r, o, sizeof(r));
+    return r;
+  }
+  __device__ static Out zero() { return Out(0); }
+};
+
+// ----------------------------------------------------------------------------
+// paged scatter: append (MHA/GQA, two parts K and V) and MLA concat (two parts
+// kv_c and k_pe into one row)
+// ----------------------------------------------------------------------------
+
+struct ScatterPart {
+  const char* src;      // row 0 of this part's input
+  char* dst;            // cache base this part writes into
+  const float* scale;   // FP8 scale (device) or nullptr for 1.0
+  int64_t src_stride;   // bytes between consecutive input token rows
+  int64_t blk_stride;   // bytes between cache blocks
+  int64_t page_stride;  // bytes between consecutive slots of a block
+  int64_t dst_off;      // bytes from the slot's row start to this part
+  int64_t seg_stride;   // cache bytes between segments (heads)
+  int64_t inner_stride; // cache bytes between consecutive output vectors of a segment
+  int32_t nseg;         // segments per row
+  int32_t seg_vecs;     // vectors per segment
+};
+
+struct ScatterGeom {
+  const int64_t* slots;
+  int64_t num_tokens;
+  int64_t block_size;
+  int64_t num_slots;  // num_blocks * block_size
+  int32_t bs_shift;   // log2(block_size), or -1 when not a power of two
+  int32_t nparts;     // 1 or 2
+};
+
+template <class C, int CH, int U>
+__global__ void __launch_bounds__(256) paged_scatter_kernel(ScatterGeom g, ScatterPart p0, ScatterPart p1) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t wave = int64_t(blockIdx.x) * (blockDim.x / kWave) +
+                       __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
+  const int part = g.nparts == 2 ? int(wave & 1) : 0;
+  const int64_t t0 = (g.nparts == 2 ? (wave >> 1) : wave) * CH;
+  if (t0 >= g.num_tokens) return;
+
+  const char* src = part ? p1.src : p0.src;
+  char* dst = part ? p1.dst : p0.dst;
+  const float* scale_p = part ? p1.scale : p0.scale;
+  const int64_t src_stride = part ? p1.src_stride : p0.src_stride;
+  const int64_t blk_stride = part ? p1.blk_stride : p0.blk_stride;
+  const int64_t page_stride = part ? p1.page_stride : p0.page_stride;
+  const int64_t dst_off = part ? p1.dst_off : p0.dst_off;
+  const int64_t seg_stride = part ? p1.seg_stride : p0.seg_stride;
+  const int64_t inner_stride = part ? p1.inner_stride : p0.inner_stride;
+  const int nseg = part ? p1.nseg : p0.nseg;
+  const int seg_vecs = part ? p1.seg_vecs : p0.seg_vecs;
+  const float scale = scale_p ? *scale_p : 1.0f;
+  const bool flat = nseg == 1 && inner_stride == C::OUT_B;
+
+  const char* srow[CH];
+  char* drow[CH];
+  bool ok[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int64_t t = t0 + c;
+    int64_t slot = -1;
+    if (t < g.num_tokens) slot = g.slots[t];
+    ok[c] = slot >= 0 && slot < g.num_slots;
+    int64_t blk, off;
+    if (g.bs_shift >= 0) {
+      blk = slot >> g.bs_shift;
+      off = slot & (g.block_size - 1);
+    } else {
+      blk = slot / g.block_size;
+      off = slot - blk * g.block_size;
+    }
+    srow[c] = src + t * src_stride;
+    drow[c] = dst + blk * blk_stride + off * page_stride + dst_off;
+  }
+
+  const int total = nseg * seg_vecs;
+  for (int base = 0; base < total; base += kWave * U) {
+    typename C::In v[CH][U];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = base + u * kWave + lane;
+        if (ok[c] && i < total) v[c][u] = vload<C::IN_B>(srow[c] + int64_t(i) * C::IN_B);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = base + u * kWave + lane;
+        if (ok[c] && i < total) {
+          int64_t o;
+          if (flat) {
+            o = int64_t(i) * C::OUT_B;
+          } else {
+            const int s = i / seg_vecs;
+            o = int64_t(s) * seg_stride + int64_t(i - s * seg_vecs) * inner_stride;
+          }
+          vstore<C::OUT_B>(drow[c] + o, C::apply(v[c][u], scale));
+        }
+      }
+    }
+  }
+}
+
+template <class C>
+int launch_scatter(const ScatterGeom& g, const ScatterPart& p0, const ScatterPart& p1, hipStream_t st) {
+  // Decode-sized batches: one token per wave and 64-thread workgroups, to spread
+  // the few waves over as many CUs as possible.  Prefill-sized batches: four
+  // tokens per wave so each lane keeps 4-8 loads in flight.
+  if (g.num_tokens < 4096) {
+    const int64_t waves = g.num_tokens * g.nparts;
+    const int threads = g.num_tokens <= 1024 ? 64 : 256;
+    const int64_t grid = ceil_div(waves, threads / kWave);
+    hipLaunchKernelGGL((paged_scatter_kernel<C, 1, 2>), dim3(grid), dim3(threads), 0, st, g, p0, p1);
+  } else {
+    const int64_t waves = ceil_div(g.num_tokens, 4) * g.nparts;
+    const int64_t grid = ceil_div(waves, 4);
+    hipLaunchKernelGGL((paged_scatter_kernel<C, 4, 2>), dim3(grid), dim3(256), 0, st, g, p0, p1);
+  }
+  return check_launch("paged_scatter_kernel launch");
+}
+
+// Dispatch on (in_dtype, cache_dtype, vector elements).
+int dispatch_scatter(int in_dt, int cache_dt, int elems, const ScatterGeom& g, const ScatterPart& p0,
+                     const ScatterPart& p1, hipStream_t st) {
+  if (in_dt == cache_dt) {
+    switch (elems * dtype_size(in_dt)) {
+      case 16: return launch_scatter<CopyConv<16>>(g, p0, p1, st);
+      case 8: return launch_scatter<CopyConv<8>>(g, p0, p1, st);
+      case 4: return launch_scatter<CopyConv<4>>(g, p0, p1, st);
+      case 2: return launch_scatter<CopyConv<2>>(g, p0, p1, st);
+      case 1: return launch_scatter<CopyConv<1>>(g, p0, p1, st);
+    }
+    return fail(PSK_E_ARG, "internal: bad copy vector width");
+  }
+  if (cache_dt != PSK_DTYPE_FP8_E4M3FN) return fail(PSK_E_DTYPE, "cache dtype must equal the input dtype or be fp8_e4m3fn");
+#define PSK_QUANT_CASES(DT)                                                   \
+  switch (elems) {                                                            \
+    case 8: return launch_scatter<QuantConv<DT, 8>>(g, p0, p1, st);           \
+    case 4: return launch_scatter<QuantConv<DT, 4>>(g, p0, p1, st);           \
+    case 2: return launch_scatter<QuantConv<DT, 2>>(g, p0, p1, st);           \
+    case 1: return launch_scatter<QuantConv<DT, 1>>(g, p0, p1, st);           \
+  }                                                                           \
+  return fail(PSK_E_ARG, "internal: bad quant vector width");
+  switch (in_dt) {
+    case PSK_DTYPE_BF16: { PSK_QUANT_CASES(PSK_DTYPE_BF16) }
+    case PSK_DTYPE_F16: { PSK_QUANT_CASES(PSK_DTYPE_F16) }
+    case PSK_DTYPE_F32: {
+      switch (elems) {
+        case 4: return launch_scatter<QuantConv<PSK_DTYPE_F32, 4>>(g, p0, p1, st);
+        case 2: return launch_scatter<QuantConv<PSK_DTYPE_F32, 2>>(g, p0, p1, st);
+        case 1: return launch_scatter<QuantConv<PSK_DTYPE_F32, 1>>(g, p0, p1, st);
+      }
+      return fail(PSK_E_ARG, "internal: bad quant vector width");
+    }
+  }
+#undef PSK_QUANT_CASES
+  return fail(PSK_E_DTYPE, "fp8 append needs a bf16, fp16 or fp32 input");
+}
+
+// Largest vector (in elements) such that every input address/stride is a
+// multiple of elems*in_size bytes and every output one of elems*out_size bytes.
+int pick_elems(int in_size, int out_size, const std::vector<uint64_t>& in_bytes,
+               const std::vector<uint64_t>& out_bytes, int64_t seg_elems) {
+  int e = 16 / in_size;
+  if (16 / out_size < e) e = 16 / out_size;
+  while (e > 1) {
+    bool ok = (seg_elems % e) == 0;
+    for (uint64_t v : in_bytes) ok = ok && (v % uint64_t(e * in_size)) == 0;
+    for (uint64_t v : out_bytes) ok = ok && (v % uint64_t(e * out_size)) == 0;
+    if (ok) break;
+    e >>= 1;
+  }
+  return e;
+}
+
+// ----------------------------------------------------------------------------
+// paged gather: block table -> contiguous rows
+// ----------------------------------------------------------------------------
+
+struct GatherGeom {
+  const char* src0;
+  const char* src1;
+  char* dst0;
+  char* dst1;
+  const int32_t* block_table;
+  const int32_t* cu;
+  const int32_t* starts;
+  const float* scale;
+  int64_t batch;
+  int64_t bt_stride;
+  int64_t num_tokens;
+  int64_t block_size;
+  int64_t num_blocks;
+  int64_t blk_stride;   // bytes
+  int64_t page_stride;  // bytes
+  int64_t dst_stride;   // bytes
+  int32_t row_vecs;
+  int32_t bs_shift;
+  int32_t nparts;
+};
+
+template <class C, int CH, int U>
+__global__ void __launch_bounds__(256) paged_gather_kernel(GatherGeom g) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t wave = int64_t(blockIdx.x) * (blockDim.x / kWave) +
+                       __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
+  const int part = g.nparts == 2 ? int(wave & 1) : 0;
+  const int64_t t0 = (g.nparts == 2 ? (wave >> 1) : wave) * CH;
+  if (t0 >= g.num_tokens) return;
+  const char* src = part ? g.src1 : g.src0;
+  char* dst = part ? g.dst1 : g.dst0;
+  const float scale = g.scale ? *g.scale : 1.0f;
+
+  // Sequence of the first token: largest b in [0, batch] with cu[b] <= t0.
+  int lo = 0, hi = int(g.batch);
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (int64_t(g.cu[mid]) <= t0) lo = mid; else hi = mid - 1;
+  }
+  int b = lo;
+
+  const char* srow[CH];
+  char* drow[CH];
+  bool rd[CH], wr[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int64_t t = t0 + c;
+    while (b < g.batch && t >= int64_t(g.cu[b + 1])) ++b;
+    wr[c] = t < g.num_tokens && b < g.batch && t >= int64_t(g.cu[0]);
+    int64_t blk = -1, off = 0;
+    if (wr[c]) {
+      const int64_t p = (g.starts ? int64_t(g.starts[b]) : 0) + t - int64_t(g.cu[b]);
+      int64_t page;
+      if (g.bs_shift >= 0) {
+        page = p >> g.bs_shift;
+        off = p & (g.block_size - 1);
+      } else {
+        page = p / g.block_size;
+        off = p - page * g.block_size;
+      }
+      if (p >= 0 && page < g.bt_stride) blk = g.block_table[int64_t(b) * g.bt_stride + page];
+    }
+    rd[c] = wr[c] && blk >= 0 && blk < g.num_blocks;
+    srow[c] = src + blk * g.blk_stride + off * g.page_stride;
+    drow[c] = dst + t * g.dst_stride;
+  }
+
+  const int total = g.row_vecs;
+  for (int base = 0; base < total; base += kWave * U) {
+    typename C::In v[CH][U];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = base + u * kWave + lane;
+        if (rd[c] && i < total) v[c][u] = vload<C::IN_B>(srow[c] + int64_t(i) * C::IN_B);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = base + u * kWave + lane;
+        if (wr[c] && i < total)
+          vstore<C::OUT_B>(drow[c] + int64_t(i) * C::OUT_B, rd[c] ? C::apply(v[c][u], scale) : C::zero());
+      }
+    }
+  }
+}
+
+template <class C>
+int launch_gather(const GatherGeom& g, hipStream_t st) {
+  if (g.num_tokens < 4096) {
+    const int64_t waves = g.num_tokens * g.nparts;
+    const int threads = g.num_tokens <= 1024 ? 64 : 256;
+    hipLaunchKernelGGL((paged_gather_kernel<C, 1, 2>), dim3(ceil_div(waves, threads / kWave)), dim3(threads), 0,
+                       st, g);
+  } else {
+    const int64_t waves = ceil_div(g.num_tokens, 4) * g.nparts;
+    hipLaunchKernelGGL((paged_gather_kernel<C, 4, 2>), dim3(ceil_div(waves, 4)), dim3(256), 0, st, g);
+  }
+  return check_launch("paged_gather_kernel launch");
+}
+
+int dispatch_gather(int cache_dt, int out_dt, int elems, const GatherGeom& g, hipStream_t st) {
+  if (cache_dt == out_dt) {
+    switch (elems * dtype_size(cache_dt)) {
+      case 16: return launch_gather<CopyConv<16>>(g, st);
+      case 8: return launch_gather<CopyConv<8>>(g, st);
+      case 4: return launch_gather<CopyConv<4>>(g, st);
+      case 2: return launch_gather<CopyConv<2>>(g, st);
+      case 1: return launch_gather<CopyConv<1>>(g, st);
+    }
+    return fail(PSK_E_ARG, "internal: bad copy vector width");
+  }
+  if (cache_dt != PSK_DTYPE_FP8_E4M3FN) return fail(PSK_E_DTYPE, "output dtype must equal the cache dtype unless the cache is fp8");
+#define PSK_DEQ_CASES(DT)                                         \
+  switch (elems) {                                                \
+    case 8: return launch_gather<DequantConv<DT, 8>>(g, st);      \
+    case 4: return launch_gather<DequantConv<DT, 4>>(g, st);      \
+    case 2: return launch_gather<DequantConv<DT, 2>>(g, st);      \
+    case 1: return launch_gather<DequantConv<DT, 1>>(g, st);      \
+  }                                                               \
+  return fail(PSK_E_ARG, "internal: bad dequant vector width");
+  switch (out_dt) {
+    case PSK_DTYPE_BF16: { PSK_DEQ_CASES(PSK_DTYPE_BF16) }
+    case PSK_DTYPE_F16: { PSK_DEQ_CASES(PSK_DTYPE_F16) }
+    case PSK_DTYPE_F32: {
+      switch (elems) {
+        case 4: return launch_gather<DequantConv<PSK_DTYPE_F32, 4>>(g, st);
+        case 2: return launch_gather<DequantConv<PSK_DTYPE_F32, 2>>(g, st);
+        case 1: return launch_gather<DequantConv<PSK_DTYPE_F32, 1>>(g, st);
+      }
+      return fail(PSK_E_ARG, "internal: bad dequant vector width");
+    }
+  }
+#undef PSK_DEQ_CASES
+  return fail(PSK_E_DTYPE, "fp8 gather output must be bf16, fp16 or fp32");
+}
+
+// ----------------------------------------------------------------------------
+// copy_blocks: (pair, layer) units of block_bytes, one workgroup per unit
+// ----------------------------------------------------------------------------
+
+template <int B, int U>
+__global__ void __launch_bounds__(256) copy_blocks_kernel(char* cache, int64_t num_layers, int64_t layer_stride,
+                                                          int64_t block_stride, int64_t block_bytes,
+                                                          int64_t num_blocks, const int64_t* mapping,
+                                                          int64_t num_units) {
+  using V = typename VecT<B>::T;
+  const int64_t nvec = block_bytes / B;
+  for (int64_t unit = blockIdx.x; unit < num_units; unit += gridDim.x) {
+    const int64_t pair = unit / num_layers;
+    const int64_t layer = unit - pair * num_layers;
+    const int64_t s = mapping[2 * pair];
+    const int64_t d = mapping[2 * pair + 1];
+    if (s < 0 || s >= num_blocks || d < 0 || d >= num_blocks) continue;
+    const char* src = cache + layer * layer_stride + s * block_stride;
+    char* dst = cache + layer * layer_stride + d * block_stride;
+    for (int64_t base = 0; base < nvec; base += int64_t(blockDim.x) * U) {
+      V v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t i = base + int64_t(u) * blockDim.x + threadIdx.x;
+        if (i < nvec) v[u] = __builtin_nontemporal_load(reinterpret_cast<const V*>(src) + i);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t i = base + int64_t(u) * blockDim.x + threadIdx.x;
+        if (i < nvec) __builtin_nontemporal_store(v[u], reinterpret_cast<V*>(dst) + i);
+      }
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------
+// amax -> scale (two-phase, last workgroup finishes; graph-safe, no memset)
+// ----------------------------------------------------------------------------
+
+constexpr int kAmaxMaxBlocks = 1024;
+constexpr int64_t kAmaxWsLen = 2 + 2 * int64_t(kAmaxMaxBlocks);
+
+struct AmaxArgs {
+  const char* x0;
+  const char* x1;
+  int64_t rows;
+  int64_t row_vecs;
+  int64_t stride0;  // bytes
+  int64_t stride1;  // bytes
+  float qmax;
+  float* scale_out;
+  float* amax_out;
+  uint32_t* ws;
+};
+
+// |x| as the bit pattern of a non-negative float; NaN -> 0 so it never wins.
+template <int DT> __device__ __forceinline__ uint32_t abs_bits(typename Elt<DT>::Bits b);
+template <> __device__ __forceinline__ uint32_t abs_bits<PSK_DTYPE_BF16>(uint16_t b) {
+  const uint32_t a = b & 0x7FFFu;
+  return a > 0x7F80u ? 0u : a << 16;
+}
+template <> __device__ __forceinline__ uint32_t abs_bits<PSK_DTYPE_F16>(uint16_t b) {
+  const float f = __builtin_fabsf(float(__builtin_bit_cast(_Float16, b)));
+  return __builtin_isnan(f) ? 0u : __float_as_uint(f);
+}
+template <> __device__ __forceinline__ uint32_t abs_bits<PSK_DTYPE_F32>(uint32_t b) {
+  const uint32_t a = b & 0x7FFFFFFFu;
+  return a > 0x7F800000u ? 0u : a;
+}
+
+__device__ __forceinline__ uint32_t block_max_u32(uint32_t m, uint32_t* red) {
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    const uint32_t o = uint32_t(__shfl_xor(int(m), off, kWave));
+    m = o > m ? o : m;
+  }
+  const int w = threadIdx.x / kWave;
+  if ((threadIdx.x & (kWave - 1)) == 0) red[w] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int i = 1; i < int(blockDim.x / kWave); ++i) m = red[i] > m ? red[i] : m;
+  }
+  return m;  // valid in thread 0
+}
+
+template <int DT, int B>
+__global__ void __launch_bounds__(256) amax_scale_kernel(AmaxArgs a) {
+  using Bits = typename Elt<DT>::Bits;
+  constexpr int E = B / int(sizeof(Bits));
+  using V = typename VecT<B>::T;
+  __shared__ uint32_t red[4];
+  __shared__ int last;
+  const int j = blockIdx.y;
+  const char* x = j ? a.x1 : a.x0;
+  const int64_t stride = j ? a.stride1 : a.stride0;
+  uint32_t m = 0;
+  const int64_t total = a.rows * a.row_vecs;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t r = a.rows == 1 ? 0 : i / a.row_vecs;
+    const int64_t c = i - r * a.row_vecs;
+    const V v = vload<B>(x + r * stride + c * B);
+    Bits e[E];
+    __builtin_memcpy(e, &v, sizeof(v));
+#pragma unroll
+    for (int k = 0; k < E; ++k) {
+      const uint32_t q = abs_bits<DT>(e[k]);
+      m = q > m ? q : m;
+    }
+  }
+  m = block_max_u32(m, red);
+  uint32_t* counter = a.ws + j;
+  uint32_t* partial = a.ws + 2 + int64_t(j) * kAmaxMaxBlocks;
+  if (threadIdx.x == 0) {
+    __hip_atomic_store(partial + blockIdx.x, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __threadfence();
+    const uint32_t ticket = atomicAdd(counter, 1u);
+    last = ticket == gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  uint32_t m2 = 0;
+  for (int i = threadIdx.x; i < int(gridDim.x); i += blockDim.x) {
+    const uint32_t q = __hip_atomic_load(partial + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    m2 = q > m2 ? q : m2;
+  }
+  __syncthreads();
+  m2 = block_max_u32(m2, red);
+  if (threadIdx.x == 0) {
+    const float amax = __uint_as_float(m2);
+    a.scale_out[j] = amax > 0.0f ? amax / a.qmax : 1.0f;
+    if (a.amax_out) a.amax_out[j] = amax;
+    __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// ----------------------------------------------------------------------------
+// swap: blit kernel over (view, page) units reading/writing mapped host memory
+// ----------------------------------------------------------------------------
+
+struct SwapView {
+  uint64_t src;
+  uint64_t dst;
+  uint64_t bpb;
+};
+
+template <int B, int U>
+__global__ void __launch_bounds__(256) blit_pages_kernel(const SwapView* views, const int64_t* src_pages,
+                                                         const int64_t* dst_pages, int64_t num_views,
+                                                         int64_t num_pages) {
+  using V = typename VecT<B>::T;
+  const int64_t units = num_views * num_pages;
+  for (int64_t unit = blockIdx.x; unit < units; unit += gridDim.x) {
+    const int64_t k = unit / num_views;
+    const int64_t vi = unit - k * num_views;
+    const SwapView view = views[vi];
+    const char* src = reinterpret_cast<const char*>(view.src + uint64_t(src_pages[k]) * view.bpb);
+    char* dst = reinterpret_cast<char*>(view.dst + uint64_t(dst_pages[k]) * view.bpb);
+    const int64_t nvec = int64_t(view.bpb) / B;
+    for (int64_t base = 0; base < nvec; base += int64_t(blockDim.x) * U) {
+      V v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t i = base + int64_t(u) * blockDim.x + threadIdx.x;
+        if (i < nvec) v[u] = __builtin_nontemporal_load(reinterpret_cast<const V*>(src) + i);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t i = base + int64_t(u) * blockDim.x + threadIdx.x;
+        if (i < nvec) __builtin_nontemporal_store(v[u], reinterpret_cast<V*>(dst) + i);
+      }
+    }
+  }
+}
+
+// hipMemcpyBatchAsync is resolved at run time: the process uses whichever HIP
+// runtime PyTorch loaded, and older runtimes do not export it.
+using BatchMemcpyFn = hipError_t (*)(void**, void**, size_t*, size_t, hipMemcpyAttributes*, size_t*, size_t,
+                                     size_t*, hipStream_t);
+
+BatchMemcpyFn batch_memcpy_fn() {
+  static BatchMemcpyFn fn = [] {
+    void* p = dlvsym(RTLD_DEFAULT, "hipMemcpyBatchAsync", "hip_7.1");
+    return reinterpret_cast<BatchMemcpyFn>(p);
+  }();
+  return fn;
+}
+
+int64_t staging_bytes(int64_t num_views, int64_t num_pages) {
+  return num_views * int64_t(sizeof(SwapView)) + 2 * num_pages * int64_t(sizeof(int64_t)) + 64;
+}
+
+}  // namespace
+
+// ============================================================================
+// C ABI
+// ============================================================================
+
+extern "C" {
+
+const char* psk_last_error(void) { return g_err; }
+
+int psk_abi_version(void) { return 1; }
+
+int psk_reshape_and_cache(const void* key, const void* value, void* key_cache, void* value_cache,
+                          const int64_t* slot_mapping, int64_t num_tokens, int64_t num_heads,
+                          int64_t head_size, int64_t block_size, int64_t num_blocks, int64_t key_stride,
+                          int64_t value_stride, const int64_t* kc, const int64_t* vc, int in_dtype,
+                          int cache_dtype, const float* k_scale, const float* v_scale, void* stream) {
+  g_err[0] = 0;
+  if (num_tokens < 0 || num_heads <= 0 || head_size <= 0 || block_size <= 0 || num_blocks < 0)
+    return fail(PSK_E_ARG, "bad sizes: num_tokens=%lld num_heads=%lld head_size=%lld block_size=%lld num_blocks=%lld",
+                (long long)num_tokens, (long long)num_heads, (long long)head_size, (long long)block_size,
+                (long long)num_blocks);
+  if (!kc || !vc) return fail(PSK_E_ARG, "cache stride arrays must not be NULL");
+  const int in_sz = dtype_size(in_dtype), c_sz = dtype_size(cache_dtype);
+  if (!in_sz || !c_sz) return fail(PSK_E_DTYPE, "unknown dtype code (in=%d cache=%d)", in_dtype, cache_dtype);
+  if (in_dtype != cache_dtype && (cache_dtype != PSK_DTYPE_FP8_E4M3FN || in_dtype == PSK_DTYPE_FP8_E4M3FN))
+    return fail(PSK_E_DTYPE, "cache dtype must equal the input dtype or be fp8_e4m3fn (in=%d cache=%d)", in_dtype,
+                cache_dtype);
+  if (in_dtype == cache_dtype && (k_scale || v_scale))
+    return fail(PSK_E_ARG, "k_scale/v_scale only apply to an fp8 cache");
+  if (num_tokens == 0) return PSK_OK;
+  if (!key || !value || !key_cache || !value_cache || !slot_mapping)
+    return fail(PSK_E_ARG, "NULL tensor pointer");
+
+  const int64_t row = num_heads * head_size;
+  ScatterGeom g;
+  g.slots = slot_mapping;
+  g.num_tokens = num_tokens;
+  g.block_size = block_size;
+  g.num_slots = num_blocks * block_size;
+  g.bs_shift = log2_exact(block_size);
+  g.nparts = 2;
+
+  // Heads are one contiguous run in the cache when dim stride is 1 and the head
+  // stride is head_size; then a token's part is one flat row of row elements.
+  const bool k_flat = kc[3] == 1 && (kc[2] == head_size || num_heads == 1);
+  const bool v_flat = vc[3] == 1 && (vc[2] == head_size || num_heads == 1);
+  const bool dim_contig = kc[3] == 1 && vc[3] == 1;
+  int elems = 1;
+  if (dim_contig) {
+    std::vector<uint64_t> in_b = {uint64_t(uintptr_t(key)), uint64_t(uintptr_t(value)), uint64_t(key_stride * in_sz),
+                                  uint64_t(value_stride * in_sz)};
+    std::vector<uint64_t> out_b = {uint64_t(uintptr_t(key_cache)), uint64_t(uintptr_t(value_cache)),
+                                   uint64_t(kc[0] * c_sz), uint64_t(kc[1] * c_sz), uint64_t(vc[0] * c_sz),
+                                   uint64_t(vc[1] * c_sz)};
+    if (!(k_flat && v_flat)) {
+      out_b.push_back(uint64_t(kc[2] * c_sz));
+      out_b.push_back(uint64_t(vc[2] * c_sz));
+    }
+    elems = pick_elems(in_sz, c_sz, in_b, out_b, (k_flat && v_flat) ? row : head_size);
+  }
+
+  auto make_part = [&](const void* src, void* dst, int64_t src_stride, const int64_t* cs, const float* scale,
+                       bool flat) {
+    ScatterPart p;
+    p.src = static_cast<const char*>(src);
+    p.dst = static_cast<char*>(dst);
+    p.scale = scale;
+    p.src_stride = src_stride * in_sz;
+    p.blk_stride = cs[0] * c_sz;
+    p.page_stride = cs[1] * c_sz;
+    p.dst_off = 0;
+    if (dim_contig && flat && elems > 1) {
+      p.nseg = 1;
+      p.seg_vecs = int32_t(row / elems);
+      p.seg_stride = 0;
+      p.inner_stride = int64_t(elems) * c_sz;
+    } else if (dim_contig) {
+      p.nseg = int32_t(num_heads);
+      p.seg_vecs = int32_t(head_size / elems);
+      p.seg_stride = cs[2] * c_sz;
+      p.inner_stride = int64_t(elems) * c_sz;
+    } else {
+      p.nseg = int32_t(num_heads);
+      p.seg_vecs = int32_t(head_size);
+      p.seg_stride = cs[2] * c_sz;
+      p.inner_stride = cs[3] * c_sz;
+    }
+    return p;
+  };
+  const ScatterPart pk = make_part(key, key_cache, key_stride, kc, k_scale, k_flat);
+  const ScatterPart pv = make_part(value, value_cache, value_stride, vc, v_scale, v_flat);
+  return dispatch_scatter(in_dtype, cache_dtype, elems, g, pk, pv, static_cast<hipStream_t>(stream));
+}
+
+int psk_concat_and_cache_mla(const void* kv_c, const void* k_pe, void* kv_cache, const int64_t* slot_mapping,
+                             int64_t num_tokens, int64_t key_len, int64_t value_len, int64_t kv_c_stride,
+                             int64_t k_pe_stride, int64_t block_size, int64_t num_blocks,
+                             int64_t cache_block_stride, int64_t cache_page_stride, int in_dtype, int cache_dtype,
+                             const float* scale, void* stream) {
+  g_err[0] = 0;
+  if (num_tokens < 0 || key_len <= 0 || value_len < 0 || block_size <= 0 || num_blocks < 0)
+    return fail(PSK_E_ARG, "bad sizes: num_tokens=%lld key_len=%lld value_len=%lld block_size=%lld",
+                (long long)num_tokens, (long long)key_len, (long long)value_len, (long long)block_size);
+  const int in_sz = dtype_size(in_dtype), c_sz = dtype_size(cache_dtype);
+  if (!in_sz || !c_sz) return fail(PSK_E_DTYPE, "unknown dtype code (in=%d cache=%d)", in_dtype, cache_dtype);
+  if (in_dtype != cache_dtype && (cache_dtype != PSK_DTYPE_FP8_E4M3FN || in_dtype == PSK_DTYPE_FP8_E4M3FN))
+    return fail(PSK_E_DTYPE, "cache dtype must equal the input dtype or be fp8_e4m3fn (in=%d cache=%d)", in_dtype,
+                cache_dtype);
+  if (in_dtype == cache_dtype && scale) return fail(PSK_E_ARG, "scale only applies to an fp8 cache");
+  if (num_tokens == 0) return PSK_OK;
+  if (!kv_c || !kv_cache || !slot_mapping || (value_len > 0 && !k_pe)) return fail(PSK_E_ARG, "NULL tensor pointer");
+
+  std::vector<uint64_t> in_b = {uint64_t(uintptr_t(kv_c)), uint64_t(kv_c_stride * in_sz)};
+  if (value_len > 0) {
+    in_b.push_back(uint64_t(uintptr_t(k_pe)));
+    in_b.push_back(uint64_t(k_pe_stride * in_sz));
+  }
+  std::vector<uint64_t> out_b = {uint64_t(uintptr_t(kv_cache)), uint64_t(cache_block_stride * c_sz),
+                                 uint64_t(cache_page_stride * c_sz), uint64_t(key_len * c_sz)};
+  int64_t seg = key_len;
+  // the vector must also divide value_len; fold it in through the gcd
+  int64_t a = key_len, b = value_len;
+  while (b) { const int64_t t = a % b; a = b; b = t; }
+  seg = a;
+  const int elems = pick_elems(in_sz, c_sz, in_b, out_b, seg);
+
+  ScatterGeom g;
+  g.slots = slot_mapping;
+  g.num_tokens = num_tokens;
+  g.block_size = block_size;
+  g.num_slots = num_blocks * block_size;
+  g.bs_shift = log2_exact(block_size);
+  g.nparts = value_len > 0 ? 2 : 1;
+  auto make_part = [&](const void* src, int64_t src_stride, int64_t len, int64_t dst_off) {
+    ScatterPart p;
+    p.src = static_cast<const char*>(src);
+    p.dst = static_cast<char*>(kv_cache);
+    p.scale = scale;
+    p.src_stride = src_stride * in_sz;
+    p.blk_stride = cache_block_stride * c_sz;
+    p.page_stride = cache_page_stride * c_sz;
+    p.dst_off = dst_off * c_sz;
+    p.nseg = 1;
+    p.seg_vecs = int32_t(len / elems);
+    p.seg_stride = 0;
+    p.inner_stride = int64_t(elems) * c_sz;
+    return p;
+  };
+  const ScatterPart p0 = make_part(kv_c, kv_c_stride, key_len, 0);
+  const ScatterPart p1 = value_len > 0 ? make_part(k_pe, k_pe_stride, value_len, key_len) : p0;
+  return dispatch_scatter(in_dtype, cache_dtype, elems, g, p0, p1, static_cast<hipStream_t>(stream));
+}
+
+int psk_gather_cache(const void* src0, const void* src1, void* dst0, void* dst1, const int32_t* block_table,
+                     const int32_t* cu_seq_lens, const int32_t* seq_starts, int64_t batch_size,
+                     int64_t block_table_stride, int64_t num_tokens, int64_t row_len, int64_t block_size,
+                     int64_t num_blocks, int64_t cache_block_stride, int64_t cache_page_stride,
+                     int64_t dst_row_stride, int cache_dtype, int out_dtype, const float* scale, void* stream) {
+  g_err[0] = 0;
+  if (batch_size < 0 || num_tokens < 0 || row_len <= 0 || block_size <= 0 || num_blocks < 0 ||
+      block_table_stride < 0)
+    return fail(PSK_E_ARG, "bad sizes: batch=%lld num_tokens=%lld row_len=%lld block_size=%lld",
+                (long long)batch_size, (long long)num_tokens, (long long)row_len, (long long)block_size);
+  if ((src1 == nullptr) != (dst1 == nullptr)) return fail(PSK_E_ARG, "src1 and dst1 must both be set or both NULL");
+  const int c_sz = dtype_size(cache_dtype), o_sz = dtype_size(out_dtype);
+  if (!c_sz || !o_sz) return fail(PSK_E_DTYPE, "unknown dtype code (cache=%d out=%d)", cache_dtype, out_dtype);
+  if (cache_dtype != out_dtype && (cache_dtype != PSK_DTYPE_FP8_E4M3FN || out_dtype == PSK_DTYPE_FP8_E4M3FN))
+    return fail(PSK_E_DTYPE, "out dtype must equal the cache dtype unless the cache is fp8 (cache=%d out=%d)",
+                cache_dtype, out_dtype);
+  if (cache_dtype == out_dtype && scale) return fail(PSK_E_ARG, "scale only applies to an fp8 -> float gather");
+  if (num_tokens == 0 || batch_size == 0) return PSK_OK;
+  if (!src0 || !dst0 || !block_table || !cu_seq_lens) return fail(PSK_E_ARG, "NULL tensor pointer");
+
+  std::vector<uint64_t> in_b = {uint64_t(uintptr_t(src0)), uint64_t(cache_block_stride * c_sz),
+                                uint64_t(cache_page_stride * c_sz)};
+  std::vector<uint64_t> out_b = {uint64_t(uintptr_t(dst0)), uint64_t(dst_row_stride * o_sz)};
+  if (src1) {
+    in_b.push_back(uint64_t(uintptr_t(src1)));
+    out_b.push_back(uint64_t(uintptr_t(dst1)));
+  }
+  const int elems = pick_elems(c_sz, o_sz, in_b, out_b, row_len);
+
+  GatherGeom g;
+  g.src0 = static_cast<const char*>(src0);
+  g.src1 = static_cast<const char*>(src1);
+  g.dst0 = static_cast<char*>(dst0);
+  g.dst1 = static_cast<char*>(dst1);
+  g.block_table = block_table;
+  g.cu = cu_seq_lens;
+  g.starts = seq_starts;
+  g.scale = scale;
+  g.batch = batch_size;
+  g.bt_stride = block_table_stride;
+  g.num_tokens = num_tokens;
+  g.block_size = block_size;
+  g.num_blocks = num_blocks;
+  g.blk_stride = cache_block_stride * c_sz;
+  g.page_stride = cache_page_stride * c_sz;
+  g.dst_stride = dst_row_stride * o_sz;
+  g.row_vecs = int32_t(row_len / elems);
+  g.bs_shift = log2_exact(block_size);
+  g.nparts = src1 ? 2 : 1;
+  return dispatch_gather(cache_dtype, out_dtype, elems, g, static_cast<hipStream_t>(stream));
+}
+
+int psk_copy_blocks(void* cache, int64_t num_layers, int64_t layer_stride, int64_t block_stride,
+                    int64_t block_bytes, int64_t num_blocks, const int64_t* block_mapping, int64_t num_pairs,
+                    void* stream) {
+  g_err[0] = 0;
+  if (num_layers < 0 || num_pairs < 0 || block_bytes < 0 || num_blocks < 0 || layer_stride < 0 ||
+      block_stride < 0)
+    return fail(PSK_E_ARG, "bad sizes: layers=%lld pairs=%lld block_bytes=%lld", (long long)num_layers,
+                (long long)num_pairs, (long long)block_bytes);
+  if (block_bytes > block_stride && num_blocks > 1)
+    return fail(PSK_E_ARG, "block_bytes %lld exceeds block_stride %lld", (long long)block_bytes,
+                (long long)block_stride);
+  if (num_layers == 0 || num_pairs == 0 || block_bytes == 0) return PSK_OK;
+  if (!cache || !block_mapping) return fail(PSK_E_ARG, "NULL pointer");
+  const uint64_t vals[4] = {uint64_t(uintptr_t(cache)), uint64_t(layer_stride), uint64_t(block_stride),
+                            uint64_t(block_bytes)};
+  const int vb = common_align(vals, 4, 16);
+  const int64_t units = num_pairs * num_layers;
+  const int64_t grid = units < 8192 ? units : 8192;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  char* c = static_cast<char*>(cache);
+  switch (vb) {
+    case 16: hipLaunchKernelGGL((copy_blocks_kernel<16, 4>), dim3(grid), dim3(256), 0, st, c, num_layers, layer_stride, block_stride, block_bytes, num_blocks, block_mapping, units); break;
+    case 8: hipLaunchKernelGGL((copy_blocks_kernel<8, 4>), dim3(grid), dim3(256), 0, st, c, num_layers, layer_stride, block_stride, block_bytes, num_blocks, block_mapping, units); break;
+    case 4: hipLaunchKernelGGL((copy_blocks_kernel<4, 4>), dim3(grid), dim3(256), 0, st, c, num_layers, layer_stride, block_stride, block_bytes, num_blocks, block_mapping, units); break;
+    case 2: hipLaunchKernelGGL((copy_blocks_kernel<2, 4>), dim3(grid), dim3(256), 0, st, c, num_layers, layer_stride, block_stride, block_bytes, num_blocks, block_mapping, units); break;
+    default: hipLaunchKernelGGL((copy_blocks_kernel<1, 4>), dim3(grid), dim3(256), 0, st, c, num_layers, layer_stride, block_stride, block_bytes, num_blocks, block_mapping, units); break;
+  }
+  return check_launch("copy_blocks_kernel launch");
+}
+
+int64_t psk_swap_staging_bytes(int64_t num_views, int64_t num_pages) { return staging_bytes(num_views, num_pages); }
+
+int psk_swap_blocks(int transport, const uint64_t* src_bases, const uint64_t* dst_bases,
+                    const uint64_t* bytes_per_page, int64_t num_views, const int64_t* src_start,
+                    const int64_t* dst_start, const int64_t* run_len, int64_t num_runs, int64_t src_num_pages,
+                    int64_t dst_num_pages, void* staging, int64_t staging_bytes_avail, void* stream) {
+  g_err[0] = 0;
+  if (num_views < 0 || num_runs < 0) return fail(PSK_E_ARG, "negative view or run count");
+  if (num_views == 0 || num_runs == 0) return PSK_OK;
+  if (!src_bases || !dst_bases || !bytes_per_page || !src_start || !dst_start || !run_len)
+    return fail(PSK_E_ARG, "NULL descriptor array");
+  int64_t pages = 0;
+  for (int64_t r = 0; r < num_runs; ++r) {
+    const int64_t s = src_start[r], d = dst_start[r], n = run_len[r];
+    if (n <= 0) return fail(PSK_E_ARG, "run %lld has length %lld", (long long)r, (long long)n);
+    if (s < 0 || s + n > src_num_pages)
+      return fail(PSK_E_RANGE, "run %lld src pages [%lld, %lld) outside [0, %lld)", (long long)r, (long long)s,
+                  (long long)(s + n), (long long)src_num_pages);
+    if (d < 0 || d + n > dst_num_pages)
+      return fail(PSK_E_RANGE, "run %lld dst pages [%lld, %lld) outside [0, %lld)", (long long)r, (long long)d,
+                  (long long)(d + n), (long long)dst_num_pages);
+    pages += n;
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (transport == PSK_SWAP_MEMCPY) {
+    for (int64_t v = 0; v < num_views; ++v) {
+      for (int64_t r = 0; r < num_runs; ++r) {
+        const uint64_t bpb = bytes_per_page[v];
+        hipError_t e = hipMemcpyAsync(reinterpret_cast<void*>(dst_bases[v] + uint64_t(dst_start[r]) * bpb),
+                                      reinterpret_cast<const void*>(src_bases[v] + uint64_t(src_start[r]) * bpb),
+                                      size_t(bpb * uint64_t(run_len[r])), hipMemcpyDefault, st);
+        if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync");
+      }
+    }
+    return PSK_OK;
+  }
+  if (transport == PSK_SWAP_BATCH) {
+    const size_t n = size_t(num_views * num_runs);
+    std::vector<void*> dsts(n), srcs(n);
+    std::vector<size_t> sizes(n);
+    size_t k = 0;
+    for (int64_t v = 0; v < num_views; ++v) {
+      const uint64_t bpb = bytes_per_page[v];
+      for (int64_t r = 0; r < num_runs; ++r, ++k) {
+        dsts[k] = reinterpret_cast<void*>(dst_bases[v] + uint64_t(dst_start[r]) * bpb);
+        srcs[k] = reinterpret_cast<void*>(src_bases[v] + uint64_t(src_start[r]) * bpb);
+        sizes[k] = size_t(bpb * uint64_t(run_len[r]));
+      }
+    }
+    hipMemcpyAttributes attr;
+    memset(&attr, 0, sizeof(attr));
+    attr.srcAccessOrder = hipMemcpySrcAccessOrderStream;
+    size_t attr_idx = 0, fail_idx = 0;
+    BatchMemcpyFn batch = batch_memcpy_fn();
+    if (!batch) return fail(PSK_E_ARG, "hipMemcpyBatchAsync is not exported by the loaded HIP runtime");
+    hipError_t e = batch(dsts.data(), srcs.data(), sizes.data(), n, &attr, &attr_idx, 1, &fail_idx, st);
+    if (e != hipSuccess) {
+      snprintf(g_err, sizeof(g_err), "hipMemcpyBatchAsync: %s (failIdx %zu)", hipGetErrorString(e), fail_idx);
+      return int(e);
+    }
+    return PSK_OK;
+  }
+  if (transport != PSK_SWAP_BLIT) return fail(PSK_E_ARG, "unknown swap transport %d", transport);
+  const int64_t need = staging_bytes(num_views, pages);
+  if (!staging || staging_bytes_avail < need)
+    return fail(PSK_E_WORKSPACE, "swap staging needs %lld bytes, got %lld", (long long)need,
+                (long long)staging_bytes_avail);
+  // Staging layout: SwapView[num_views] | int64 src_pages[pages] | int64 dst_pages[pages]
+  char* base = reinterpret_cast<char*>((uintptr_t(staging) + 15) & ~uintptr_t(15));
+  SwapView* views = reinterpret_cast<SwapView*>(base);
+  int64_t* sp = reinterpret_cast<int64_t*>(base + num_views * int64_t(sizeof(SwapView)));
+  int64_t* dp = sp + pages;
+  uint64_t acc = 0;
+  for (int64_t v = 0; v < num_views; ++v) {
+    views[v].src = src_bases[v];
+    views[v].dst = dst_bases[v];
+    views[v].bpb = bytes_per_page[v];
+    acc |= src_bases[v] | dst_bases[v] | bytes_per_page[v];
+  }
+  int64_t k = 0;
+  for (int64_t r = 0; r < num_runs; ++r)
+    for (int64_t i = 0; i < run_len[r]; ++i, ++k) {
+      sp[k] = src_start[r] + i;
+      dp[k] = dst_start[r] + i;
+    }
+  const int64_t units = num_views * pages;
+  const int64_t grid = units < 4096 ? units : 4096;
+  if ((acc & 15) == 0)
+    hipLaunchKernelGGL((blit_pages_kernel<16, 4>), dim3(grid), dim3(256), 0, st, views, sp, dp, num_views, pages);
+  else if ((acc & 3) == 0)
+    hipLaunchKernelGGL((blit_pages_kernel<4, 4>), dim3(grid), dim3(256), 0, st, views, sp, dp, num_views, pages);
+  else
+    hipLaunchKernelGGL((blit_pages_kernel<1, 4>), dim3(grid), dim3(256), 0, st, views, sp, dp, num_views, pages);
+  return check_launch("blit_pages_kernel launch");
+}
+
+int64_t psk_kv_amax_workspace_len(void) { return kAmaxWsLen; }
+
+int psk_kv_amax_scale(const void* x0, const void* x1, int64_t rows, int64_t row_len, int64_t row_stride0,
+                      int64_t row_stride1, int dtype, float qmax, float* scale_out, float* amax_out,
+                      uint32_t* workspace, int64_t workspace_len, void* stream) {
+  g_err[0] = 0;
+  if (rows < 0 || row_len < 0) return fail(PSK_E_ARG, "negative size");
+  const int sz = dtype_size(dtype);
+  if (!sz || dtype == PSK_DTYPE_FP8_E4M3FN) return fail(PSK_E_DTYPE, "amax input must be bf16, fp16 or fp32");
+  if (!(qmax > 0.0f)) return fail(PSK_E_ARG, "qmax must be positive");
+  if (!x0 || !scale_out || !workspace) return fail(PSK_E_ARG, "NULL pointer");
+  if (workspace_len < kAmaxWsLen)
+    return fail(PSK_E_WORKSPACE, "amax workspace needs %lld uint32 words, got %lld", (long long)kAmaxWsLen,
+                (long long)workspace_len);
+  int64_t rws = rows, rl = row_len;
+  // A contiguous tensor is one long row.
+  const bool contig0 = row_stride0 == row_len, contig1 = !x1 || row_stride1 == row_len;
+  if (contig0 && contig1) {
+    rl = rows * row_len;
+    rws = rl > 0 ? 1 : 0;
+  }
+  const uint64_t vals[4] = {uint64_t(uintptr_t(x0)), uint64_t(uintptr_t(x1)), uint64_t(row_stride0 * sz),
+                            uint64_t(rl * sz)};
+  uint64_t vals2[5] = {vals[0], vals[1], vals[2], vals[3], uint64_t(row_stride1 * sz)};
+  const int vb = common_align(vals2, 5, 16);
+  const int64_t row_vecs = rl * sz / vb;
+  const int64_t total = rws * row_vecs;
+  int64_t blocks = ceil_div(total > 0 ? total : 1, 256);
+  if (blocks > kAmaxMaxBlocks) blocks = kAmaxMaxBlocks;
+  AmaxArgs a;
+  a.x0 = static_cast<const char*>(x0);
+  a.x1 = static_cast<const char*>(x1 ? x1 : x0);
+  a.rows = rws;
+  a.row_vecs = row_vecs;
+  a.stride0 = row_stride0 * sz;
+  a.stride1 = (x1 ? row_stride1 : row_stride0) * sz;
+  a.qmax = qmax;
+  a.scale_out = scale_out;
+  a.amax_out = amax_out;
+  a.ws = workspace;
+  const dim3 grid(unsigned(blocks), x1 ? 2u : 1u);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+#define PSK_AMAX_LAUNCH(DT)                                                                                     \
+  switch (vb) {                                                                                                 \
+    case 16: hipLaunchKernelGGL((amax_scale_kernel<DT, 16>), grid, dim3(256), 0, st, a); break;                 \
+    case 8: hipLaunchKernelGGL((amax_scale_kernel<DT, 8>), grid, dim3(256), 0, st, a); break;                   \
+    case 4: hipLaunchKernelGGL((amax_scale_kernel<DT, 4>), grid, dim3(256), 0, st, a); break;                   \
+    default: hipLaunchKernelGGL((amax_scale_kernel<DT, (DT == PSK_DTYPE_F32 ? 4 : 2)>), grid, dim3(256), 0, st, a); break; \
+  }
+  switch (dtype) {
+    case PSK_DTYPE_BF16: PSK_AMAX_LAUNCH(PSK_DTYPE_BF16) break;
+    case PSK_DTYPE_F16: PSK_AMAX_LAUNCH(PSK_DTYPE_F16) break;
+    case PSK_DTYPE_F32: PSK_AMAX_LAUNCH(PSK_DTYPE_F32) break;
+  }
+#undef PSK_AMAX_LAUNCH
+  return check_launch("amax_scale_kernel launch");
+}
+
+int psk_host_alloc(int64_t bytes, void** ptr) {
+  g_err[0] = 0;
+  if (!ptr || bytes <= 0) return fail(PSK_E_ARG, "bad host allocation request (%lld bytes)", (long long)bytes);
+  *ptr = nullptr;
+  void* p = nullptr;
+  hipError_t e = hipHostMalloc(&p, size_t(bytes), hipHostMallocMapped | hipHostMallocPortable);
+  if (e != hipSuccess) return hip_fail(e, "hipHostMalloc");
+  void* dp = nullptr;
+  e = hipHostGetDevicePointer(&dp, p, 0);
+  if (e != hipSuccess) {
+    (void)hipHostFree(p);
+    return hip_fail(e, "hipHostGetDevicePointer");
+  }
+  if (dp != p) {
+    (void)hipHostFree(p);
+    return fail(PSK_E_ARG, "pinned host memory is not mapped at its host address (%p vs %p)", p, dp);
+  }
+  *ptr = p;
+  return PSK_OK;
+}
+
+int psk_host_free(void* ptr) {
+  g_err[0] = 0;
+  if (!ptr) return PSK_OK;
+  hipError_t e = hipHostFree(ptr);
+  return e == hipSuccess ? PSK_OK : hip_fail(e, "hipHostFree");
+}
+
+}  // extern "C"

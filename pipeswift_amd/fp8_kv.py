@@ -1,0 +1,58 @@
+"""FP8 (OCP E4M3FN) KV-cache settings.
+
+Mirrors the cache-side part of pipeswift/utils/fp8_kv.py: the dtype and
+saturation constants (:24-25), the global flag (:35-41), ``quantize``
+(:75-77) and the graph-safe warmup (:80-91).  The attention-reader loader and
+descale helpers of that file belong to the attention kernels and are not part
+of this package.
+
+gfx950 converts to the OCP E4M3FN format natively (max 448, 0x7F/0xFF NaN);
+this is not MI300's FNUZ variant (max 240).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import cache_ops
+
+FP8_KV_DTYPE = torch.float8_e4m3fn
+FP8_E4M3_MAX = 448.0
+
+_ENABLED = False
+_scale_one: dict = {}
+
+
+def set_enabled(enabled: bool) -> None:
+    global _ENABLED
+    _ENABLED = bool(enabled)
+
+
+def is_enabled() -> bool:
+    return _ENABLED
+
+
+def quantize(x: torch.Tensor) -> torch.Tensor:
+    """Per-tensor e4m3 cast at scale 1.0, saturating (fp8_kv.py:75-77).
+
+    Elementwise torch on the tensor's device; the cache write itself fuses
+    the same conversion into the append kernel.
+    """
+    return x.clamp(-FP8_E4M3_MAX, FP8_E4M3_MAX).to(FP8_KV_DTYPE)
+
+
+def warmup(device) -> None:
+    """Allocate the unit scale and the amax workspace outside graph capture."""
+    assert not torch.cuda.is_current_stream_capturing(), "fp8_kv.warmup must run outside graph capture"
+    device = torch.device(device)
+    if device not in _scale_one:
+        _scale_one[device] = torch.ones((1,), dtype=torch.float32, device=device)
+    cache_ops.warmup(device)
+
+
+def unit_scale(device) -> torch.Tensor:
+    """A one-element fp32 1.0 on ``device`` (the reference's fixed scale)."""
+    device = torch.device(device)
+    if device not in _scale_one:
+        warmup(device)
+    return _scale_one[device]

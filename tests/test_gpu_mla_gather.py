@@ -1,0 +1,162 @@
+"""GPU parity of the MLA latent append and the block gather vs the CPU oracle."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kv_oracle as O
+from pipeswift_amd import cache_ops, impl_utils, metadata, workloads
+from pipeswift_amd.reshape_and_cache import reshape_and_cache_flash, reshape_and_cache_flash_diffkv
+from tests.conftest import raw
+
+pytestmark = pytest.mark.gpu
+
+
+def _mla(case, dev, fp8_scale=None):
+    n = case.slot_mapping.shape[0]
+    print(f"mla case: N={n} cache={tuple(case.cache.shape)} fp8={fp8_scale is not None}", flush=True)
+    latent_d = case.latent.to(dev)
+    kv_c_d = case.kv_c.to(dev)
+    if fp8_scale is None:
+        cache_d = case.cache.to(dev)
+        sc = None
+    else:
+        cache_d = torch.zeros(case.cache.shape, dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
+        sc = torch.tensor([fp8_scale], dtype=torch.float32, device=dev)
+    k_pe_d = case.k_pe(latent_d)
+    assert k_pe_d.stride(0) == 2112
+    reshape_and_cache_flash_diffkv(kv_c_d.unsqueeze(1), k_pe_d.unsqueeze(1), cache_d.unsqueeze(2),
+                                   case.slot_mapping.to(dev), sc)
+    if fp8_scale is None:
+        exp = raw(case.cache).copy()
+        O.concat_and_cache_mla(raw(case.kv_c), raw(case.k_pe()), exp, case.slot_mapping.numpy())
+    else:
+        exp = np.zeros(case.cache.shape, np.uint8)
+        O.concat_and_cache_mla(raw(case.kv_c), raw(case.k_pe()), exp, case.slot_mapping.numpy(), "bf16", "fp8",
+                               fp8_scale)
+    return raw(cache_d), exp
+
+
+@pytest.mark.parametrize("decode", [False, True])
+def test_config4_mla_bf16(dev, decode):
+    case = workloads.config4_mla(num_tokens=128 if decode else 4096, decode=decode)
+    got, exp = _mla(case, dev)
+    assert np.array_equal(got, exp)
+
+
+@pytest.mark.parametrize("decode", [False, True])
+def test_config4_mla_fp8(dev, decode):
+    case = workloads.config4_mla(num_tokens=128 if decode else 4096, decode=decode)
+    got, exp = _mla(case, dev, fp8_scale=0.0371)
+    assert np.array_equal(got, exp)
+
+
+def test_mla_through_append_mla_kv_cache(dev):
+    L, P, ps = 2, 300, 64
+    mla = workloads.sentinel((L, P, ps, 576), torch.bfloat16, 31)
+    md = mla.to(dev)
+    g = torch.Generator().manual_seed(32)
+    n = 200
+    latent = torch.randn(n, 1536 + 576, generator=g).to(torch.bfloat16)
+    ckv = torch.randn(n, 512, generator=g).to(torch.bfloat16)
+    slots = torch.randperm(P * ps, generator=g)[:n].to(torch.int64)
+    slots[::13] = -1
+    info = metadata.KVCacheInfo(mla_cache_tensor=md, slot_mapping=slots.to(dev))
+    ld = latent.to(dev)
+    impl_utils.append_mla_kv_cache(ckv.to(dev), ld[:, 1536 + 512:], info, layer_idx=1)
+    exp = raw(mla).copy()
+    O.concat_and_cache_mla(raw(ckv), raw(latent[:, 2048:]), exp[1], slots.numpy())
+    assert np.array_equal(raw(md), exp)
+
+
+def test_mla_multi_head_flat_layout(dev):
+    """H > 1: the reference writes all key elements then all value elements
+    flat from the row start (reshape_and_cache.py:161-188)."""
+    g = torch.Generator().manual_seed(33)
+    n, H, Dk, Dv, P, ps = 50, 3, 16, 8, 20, 4
+    key = torch.randn(n, H, Dk, generator=g).to(torch.bfloat16)
+    value = torch.randn(n, H, Dv, generator=g).to(torch.bfloat16)
+    cache = workloads.sentinel((P, ps, H, Dk + Dv), torch.bfloat16, 34)
+    slots = torch.randperm(P * ps, generator=g)[:n].to(torch.int64)
+    cd = cache.to(dev)
+    reshape_and_cache_flash_diffkv(key.to(dev), value.to(dev), cd, slots.to(dev))
+    exp = raw(cache).copy().reshape(P, ps, H * (Dk + Dv))
+    O.concat_and_cache_mla(raw(key).reshape(n, -1), raw(value).reshape(n, -1), exp, slots.numpy())
+    assert np.array_equal(raw(cd).reshape(P, ps, -1), exp)
+
+
+# --------------------------------------------------------------------------- #
+# chunked prefill append + gather (config 3)
+# --------------------------------------------------------------------------- #
+
+
+def test_config3_chunked_append_then_gather(dev):
+    cc = workloads.config3_chunked()
+    a = cc.append
+    print(f"config3: chunks={cc.chunk.tolist()} prefix={cc.prefix.tolist()} T={int(cc.cu_seq_lens[-1])}",
+          flush=True)
+    qd = a.qkv.to(dev)
+    cache_d = a.cache.to(dev)
+    reshape_and_cache_flash(a.key(qd), a.value(qd), cache_d[:, 0], cache_d[:, 1], a.slot_mapping.to(dev))
+    exp = raw(a.cache).copy()
+    O.reshape_and_cache(raw(a.key()), raw(a.value()), exp[:, 0], exp[:, 1], a.slot_mapping.numpy())
+    assert np.array_equal(raw(cache_d), exp)
+
+    T = int(cc.cu_seq_lens[-1])
+    out_k = torch.empty(T, a.num_heads, a.head_size, dtype=torch.bfloat16, device=dev)
+    out_v = torch.empty_like(out_k)
+    cache_ops.gather_cache(cache_d[:, 0], out_k, cc.block_table.to(dev), cc.cu_seq_lens.to(dev),
+                           src_cache_v=cache_d[:, 1], dst_v=out_v)
+    ek = O.gather_cache(exp[:, 0], cc.block_table.numpy(), cc.cu_seq_lens.numpy())
+    ev = O.gather_cache(exp[:, 1], cc.block_table.numpy(), cc.cu_seq_lens.numpy())
+    assert np.array_equal(raw(out_k), ek) and np.array_equal(raw(out_v), ev)
+    # round trip: the newly appended chunk of every sequence reads back as its input rows
+    cu = cc.cu_seq_lens.numpy()
+    rows = []
+    for b in range(len(cc.chunk)):
+        rows.append(raw(out_k)[cu[b] + int(cc.prefix[b]): cu[b + 1]])
+    assert np.array_equal(np.concatenate(rows), raw(a.key()))
+
+
+def test_gather_fp8_dequant_seq_starts_and_bad_ids(dev):
+    g = torch.Generator().manual_seed(35)
+    P, ps, H, D = 64, 16, 4, 128
+    cache = torch.randint(0, 256, (P, ps, H, D), generator=g, dtype=torch.uint8)
+    cache[(cache & 0x7F) == 0x7F] = 0x11  # no NaN codes: NaN payloads are not pinned
+    bt = torch.randperm(P, generator=g)[:24].to(torch.int32).view(3, 8)
+    bt[0, 2] = 9999  # out of range -> zero rows
+    bt[2, 0] = -5
+    cu = torch.tensor([0, 40, 40, 100], dtype=torch.int32)
+    starts = torch.tensor([16, 0, 3], dtype=torch.int32)
+    cd = cache.to(dev).view(torch.float8_e4m3fn)
+    scale = 0.0625 * 3
+    for out_dtype, name in [(torch.bfloat16, "bf16"), (torch.float16, "f16"), (torch.float32, "f32")]:
+        out = torch.full((100, H, D), 7, dtype=out_dtype, device=dev)
+        cache_ops.gather_cache(cd, out, bt.to(dev), cu.to(dev), seq_starts=starts.to(dev),
+                               scale=torch.tensor([scale], dtype=torch.float32, device=dev))
+        exp = O.gather_cache(cache.numpy(), bt.numpy(), cu.numpy(), seq_starts=starts.numpy(), cache_dtype="fp8",
+                             out_dtype=name, scale=scale)
+        assert np.array_equal(raw(out), exp), name
+    raw_out = torch.zeros(100, H, D, dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
+    cache_ops.gather_cache(cd, raw_out, bt.to(dev), cu.to(dev), seq_starts=starts.to(dev))
+    exp = O.gather_cache(cache.numpy(), bt.numpy(), cu.numpy(), seq_starts=starts.numpy(), cache_dtype="fp8")
+    assert np.array_equal(raw(raw_out), exp)
+
+
+def test_gather_many_sequences_and_tail_untouched(dev):
+    """300 sequences (binary search over cu_seq_lens), output longer than cu[-1]."""
+    g = torch.Generator().manual_seed(36)
+    P, ps, H, D = 2048, 16, 2, 64
+    cache = workloads.sentinel((P, ps, H, D), torch.bfloat16, 37)
+    lens = torch.randint(0, 90, (300,), generator=g)
+    cu = torch.zeros(301, dtype=torch.int32)
+    cu[1:] = torch.cumsum(lens, 0)
+    W = 6
+    bt = torch.randint(0, P, (300, W), generator=g, dtype=torch.int32)
+    T = int(cu[-1]) + 77
+    cd = cache.to(dev)
+    out = torch.full((T, H, D), 3, dtype=torch.bfloat16, device=dev)
+    cache_ops.gather_cache(cd, out, bt.to(dev), cu.to(dev))
+    exp = np.full((T, H, D), raw(torch.full((1,), 3, dtype=torch.bfloat16))[0], np.uint16)
+    O.gather_cache(raw(cache), bt.numpy(), cu.numpy(), out=exp)
+    assert np.array_equal(raw(out), exp)

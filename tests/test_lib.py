@@ -1,0 +1,71 @@
+"""The C ABI library loads and exports what include/pipeswift_kv.h declares.
+
+CPU-only: argument checks that return before any HIP call are exercised, no
+kernel is launched.
+"""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from pipeswift_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    text = open(os.path.join(ROOT, "include", "pipeswift_kv.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(psk_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    names = declared_symbols()
+    assert len(names) >= 10
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(_lib.EXPORTED_SYMBOLS), "ctypes signatures and header disagree"
+    assert lib.psk_abi_version() == 1
+
+
+def test_argument_errors_return_before_any_device_call():
+    lib = _lib.lib()
+    z = _lib.i64_array([0, 0, 0, 1])
+    st = lib.psk_reshape_and_cache(None, None, None, None, None, 4, 0, 128, 16, 8, 0, 0, z, z, 2, 2,
+                                   None, None, None)
+    assert st == -1 and b"bad sizes" in lib.psk_last_error()
+    st = lib.psk_reshape_and_cache(None, None, None, None, None, 4, 8, 128, 16, 8, 0, 0, z, z, 2, 0,
+                                   None, None, None)
+    assert st == -2
+    # zero tokens is a no-op, even with NULL pointers (impl_utils returns early too)
+    assert lib.psk_reshape_and_cache(None, None, None, None, None, 0, 8, 128, 16, 8, 0, 0, z, z, 2, 3,
+                                     None, None, None) == 0
+    with pytest.raises(AssertionError, match="bad sizes"):
+        _lib.check(lib.psk_gather_cache(None, None, None, None, None, None, None, 1, 1, 1, 0, 16, 8, 1, 1, 1,
+                                        2, 2, None, None), "gather")
+    assert lib.psk_kv_amax_workspace_len() >= 2
+
+
+def test_swap_range_is_checked_on_the_host():
+    lib = _lib.lib()
+    u = (ctypes.c_uint64 * 1)(0)
+    b = (ctypes.c_uint64 * 1)(4096)
+    s = _lib.i64_array([5])
+    d = _lib.i64_array([0])
+    n = _lib.i64_array([2])
+    st = lib.psk_swap_blocks(_lib.SWAP_MEMCPY, u, u, b, 1, s, d, n, 1, 6, 10, None, 0, None)
+    assert st == -3 and b"src pages [5, 7)" in lib.psk_last_error()
+    st = lib.psk_swap_blocks(_lib.SWAP_BLIT, u, u, b, 1, d, d, n, 1, 6, 10, None, 0, None)
+    assert st == -4
+    assert lib.psk_swap_staging_bytes(2, 10) >= 2 * 24 + 2 * 10 * 8
+
+
+def test_build_flags_disable_packed_fp32():
+    import __graft_entry__ as g
+
+    flags = " ".join(g.FLAGS)
+    assert "-packed-fp32-ops" in flags and "gfx950" in flags
