@@ -25,6 +25,8 @@ Workloads (default fp8_decode_append, config 2 of the benchmark plan):
   mla_prefill / mla_decode   kv_c 512 + k_pe 64, block 64, 20000 blocks
   copy_blocks        2048 pairs over 61 layers of [8192, 2, 16, 8, 128] bf16
   swap               8192 scattered blocks x 8 layers (4 GiB) D2H + H2D
+  hbm_copy           1 GiB device copy (achievable-bandwidth reference and the
+                     PMC calibration run)
 """
 
 from __future__ import annotations
@@ -171,6 +173,7 @@ def setup_chunked(args, device, gather):
     nbytes = workloads.gather_bytes(T, a.num_heads * a.head_size, 2, 2, pages)
     return launch, {
         "name": "gather", "kernel": "paged_gather_kernel", "bytes": nbytes, "tokens": T, "dtype": "bf16",
+        "rotate": R,
         "config": {"workload": "block gather (config 3)", "tokens": T, "sequences": len(cc.chunk),
                    "kv_heads": a.num_heads, "head_dim": a.head_size, "block_size": ps, "num_blocks": P,
                    "pages": pages},
@@ -204,6 +207,7 @@ def setup_mla(args, device, decode):
 
     nbytes = workloads.mla_bytes(n, 576, 2, 2)
     return launch, {
+        "rotate": R,
         "name": "mla_decode" if decode else "mla_prefill", "kernel": "paged_scatter_kernel", "bytes": nbytes,
         "tokens": n, "dtype": "bf16",
         "config": {"workload": f"MLA latent append, {'decode' if decode else 'prefill'} (config 4)", "tokens": n,
@@ -227,12 +231,103 @@ def setup_copy_blocks(args, device):
 
     nbytes = workloads.copy_blocks_bytes(2048, L, 2 * 16 * 8 * 128 * 2)
     return launch, {
+        "rotate": len(pairs),
         "name": "copy_blocks", "kernel": "copy_blocks_kernel", "bytes": nbytes, "tokens": 2048 * 16,
         "dtype": "bf16",
         "config": {"workload": "copy_blocks (config 5a)", "pairs": 2048, "layers": L, "num_blocks": P,
                    "block_bytes": 65536},
         "cpu": None,
     }
+
+
+def run_hbm_copy(args, device):
+    """Achievable-bandwidth reference: a 1 GiB device-to-device copy, once with
+    torch (the runtime's copy kernel) and once with copy_blocks_kernel over
+    16384 contiguous 64 KiB blocks; also the PMC calibration workload (each
+    dispatch must read and write exactly 1 GiB)."""
+    import torch
+
+    from pipeswift_amd import cache_ops
+
+    n = 1 << 30
+    a = torch.empty(n, dtype=torch.uint8, device=device)
+    a.random_(generator=torch.Generator(device=device).manual_seed(94))
+    b = torch.empty_like(a)
+    out = {}
+    stack = torch.empty((1, 2 * 16384, 65536), dtype=torch.uint8, device=device)
+    pairs = torch.stack([torch.arange(16384), torch.arange(16384) + 16384], 1).to(torch.int64).to(device)
+    for name, fn in (("torch_copy", lambda: b.copy_(a)),
+                     ("copy_blocks_kernel", lambda: cache_ops.copy_blocks(stack, pairs, validate=False))):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 20
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = 2 * n / (e0.elapsed_time(e1) / 1e3 / reps) / 1e9
+    line = {"metric": "device copy GB/s (read + write), 1 GiB", "value": round(max(out.values()), 2), "unit": "GB/s",
+            "n_gpus": 1, "steps": 20, "warmup": 3, "higher_is_better": True, "vs_baseline": None, "dtype": "bytes",
+            "data": "synthetic", "config": {"workload": "hbm_copy (roofline reference)", "results": out},
+            "roofline": {"bound": "hbm", "achieved": round(max(out.values()), 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": round(max(out.values()) / PEAK_HBM_GBS, 4), "traffic": None}}
+    print(json.dumps(line), flush=True)
+
+
+def run_swap(args, device):
+    """D2H store then H2D load of 8192 scattered blocks x 8 layers (4 GiB each
+    way) through CopyEngine; wall time from submit to CopyHandle.wait()."""
+    import numpy as np
+    import torch
+
+    from pipeswift_amd import copy_engine, workloads
+
+    L, Pg, P2 = 8, 16384, 8192
+    gpu_ids, l2_ids = workloads.config5b_pages(gpu_pages=Pg, l2_pages=P2)
+    cache = torch.empty((L, Pg, 2, 16, 8, 128), dtype=torch.bfloat16, device=device)
+    cache.view(torch.int16).random_(generator=torch.Generator(device=device).manual_seed(95))
+    nbytes = len(gpu_ids) * L * 65536
+    results = {}
+    for transport in args.transports.split(","):
+        eng = copy_engine.CopyEngine([cache], Pg, P2, transport=transport)
+        try:
+            res = {}
+            for direction in ("store", "load"):
+                times = []
+                for rep in range(args.swap_reps + 1):
+                    torch.cuda.synchronize()
+                    t0 = time.perf_counter()
+                    if direction == "store":
+                        h = eng.store(gpu_ids.tolist(), l2_ids.tolist())
+                    else:
+                        h = eng.load(l2_ids.tolist(), gpu_ids.tolist())
+                    h.wait()
+                    if rep:
+                        times.append(time.perf_counter() - t0)
+                res[direction] = {"GB/s": nbytes / float(np.median(times)) / 1e9, "ms": 1e3 * float(np.median(times)),
+                                  "runs": h.num_runs * L}
+            results[transport] = res
+        finally:
+            eng.close()
+    best = max(results, key=lambda t: min(results[t]["store"]["GB/s"], results[t]["load"]["GB/s"]))
+    st, ld = results[best]["store"]["GB/s"], results[best]["load"]["GB/s"]
+    value = 2.0 / (1.0 / st + 1.0 / ld)  # both directions, harmonic mean
+    line = {
+        "metric": "swap_blocks host-link GB/s (D2H store + H2D load, 4 GiB each way)",
+        "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.swap_reps, "warmup": 1,
+        "ms_per_step": results[best]["store"]["ms"] + results[best]["load"]["ms"],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bytes",
+        "data": "synthetic (seeded)",
+        "config": {"workload": "swap_blocks (config 5b)", "blocks": len(gpu_ids), "layers": L,
+                   "bytes_per_block_layer": 65536, "transport": best, "all_transports": results},
+        "roofline": {"bound": "pcie", "achieved": round(value, 2), "peak": 64.0, "unit": "GB/s",
+                     "frac": round(value / 64.0, 4), "traffic": None},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
 
 
 # --------------------------------------------------------------------------- #
@@ -305,6 +400,8 @@ def main():
     p.add_argument("--rotate", type=int, default=512, help="rotation sets of inputs/slots")
     p.add_argument("--graph", type=int, default=64, help="launches captured per HIP graph (0: eager)")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--transports", default="blit,memcpy", help="swap workload: transports to compare")
+    p.add_argument("--swap-reps", type=int, default=3)
     args = p.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -323,13 +420,18 @@ def main():
         launch, info = setup_chunked(args, device, gather=name == "gather")
     elif name in ("mla_prefill", "mla_decode"):
         launch, info = setup_mla(args, device, decode=name == "mla_decode")
+    elif name == "swap":
+        return run_swap(args, device)
+    elif name == "hbm_copy":
+        return run_hbm_copy(args, device)
     elif name == "copy_blocks":
         launch, info = setup_copy_blocks(args, device)
         args.graph = min(args.graph, 4)
-        args.rotate = 4
     else:
         raise SystemExit(f"unknown workload {name}")
-    R = args.rotate
+    R = info.get("rotate", args.rotate)
+    if args.graph > R:
+        args.graph = R
     torch.cuda.synchronize()
 
     stream = torch.cuda.Stream(device)

@@ -1,7 +1,7 @@
 """numpy restatement of the reference's paged KV-cache semantics (test-only).
 
 Tensors are numpy arrays holding raw element bits: bf16 and fp16 as uint16,
-fp32 as float32, fp8 E4M3FN as uint8.  ``dtype`` arguments are the strings
+fp32 as uint32, fp8 E4M3FN as uint8.  ``dtype`` arguments are the strings
 "bf16", "f16", "f32", "fp8".  Byte-copy semantics never look at the values;
 only the FP8 paths convert to float32.
 
@@ -19,7 +19,7 @@ import numpy as np
 
 FP8_E4M3_MAX = 448.0  # fp8_kv.py:25, reshape_and_cache.py:8
 
-RAW = {"bf16": np.uint16, "f16": np.uint16, "f32": np.float32, "fp8": np.uint8}
+RAW = {"bf16": np.uint16, "f16": np.uint16, "f32": np.uint32, "fp8": np.uint8}
 
 
 # --------------------------------------------------------------------------- #
@@ -49,7 +49,8 @@ def to_f32(raw: np.ndarray, dtype: str) -> np.ndarray:
     if dtype == "f16":
         return np.asarray(raw, dtype=np.uint16).view(np.float16).astype(np.float32)
     if dtype == "f32":
-        return np.asarray(raw, dtype=np.float32)
+        raw = np.asarray(raw)
+        return raw.view(np.float32) if raw.dtype == np.uint32 else raw.astype(np.float32)
     if dtype == "fp8":
         return e4m3fn_to_f32(raw)
     raise ValueError(dtype)
@@ -61,7 +62,7 @@ def from_f32(x: np.ndarray, dtype: str) -> np.ndarray:
     if dtype == "f16":
         return np.asarray(x, dtype=np.float32).astype(np.float16).view(np.uint16)
     if dtype == "f32":
-        return np.asarray(x, dtype=np.float32)
+        return np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
     raise ValueError(dtype)
 
 

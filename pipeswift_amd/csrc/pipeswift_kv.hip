@@ -163,6 +163,41 @@ __device__ __forceinline__ f32x2 e4m3_unpack2(uint32_t w, bool hi) {
   return hi ? __builtin_amdgcn_cvt_pk_f32_fp8(int(w), true) : __builtin_amdgcn_cvt_pk_f32_fp8(int(w), false);
 }
 
+// ---- per-tensor scale, prepared once per wave
+
+// x / s must be the correctly rounded IEEE quotient (the oracle divides in
+// fp32).  With r = RN(1/s) computed once, y = RN(x*r) is within an ulp of x/s,
+// the residual e = x - y*s is exact in one FMA, and RN(y + e*r) is the
+// correctly rounded quotient (Markstein's theorem) whenever nothing under- or
+// overflows: |s|, |x| and |y| inside [2^-100, 2^100).  Outside that range,
+// and for zeros, infinities and NaN, the plain IEEE division runs instead.
+struct QScale {
+  float s;
+  float r;
+  bool fast;
+};
+
+__device__ __forceinline__ QScale make_qscale(float s) {
+  QScale q;
+  q.s = s;
+  q.r = 1.0f / s;
+  const float a = __builtin_fabsf(s);
+  q.fast = a >= 0x1p-100f && a < 0x1p100f;
+  return q;
+}
+
+__device__ __forceinline__ float div_by_scale(float x, const QScale& q) {
+  if (q.fast) {
+    const float y = x * q.r;
+    const float a = __builtin_fabsf(x);
+    if (a >= 0x1p-100f && a < 0x1p100f && __builtin_fabsf(y) < 0x1p100f) {
+      const float e = __builtin_fmaf(-y, q.s, x);
+      return __builtin_fmaf(e, q.r, y);
+    }
+  }
+  return x / q.s;
+}
+
 // ---- conversion policies: In vector (IN_B bytes) -> Out vector (OUT_B bytes)
 
 template <int B>
@@ -171,7 +206,7 @@ struct CopyConv {
   static constexpr int OUT_B = B;
   using In = typename VecT<B>::T;
   using Out = typename VecT<B>::T;
-  __device__ static Out apply(In v, float) { return v; }
+  __device__ static Out apply(In v, const QScale&) { return v; }
   __device__ static Out zero() { return Out(0); }
 };
 
@@ -183,12 +218,12 @@ struct QuantConv {
   static constexpr int OUT_B = E;
   using In = typename VecT<IN_B>::T;
   using Out = typename VecT<OUT_B>::T;
-  __device__ static Out apply(In v, float scale) {
+  __device__ static Out apply(In v, const QScale& qs) {
     typename EltT::Bits e[E];
     __builtin_memcpy(e, &v, sizeof(v));
     float f[E];
 #pragma unroll
-    for (int i = 0; i < E; ++i) f[i] = EltT::to_f32(e[i]) / scale;
+    for (int i = 0; i < E; ++i) f[i] = div_by_scale(EltT::to_f32(e[i]), qs);
     if constexpr (E == 1) {
       return Out(e4m3_pack2(f[0], 0.0f) & 0xFFu);
     } else {
@@ -215,18 +250,18 @@ struct DequantConv {
   static constexpr int OUT_B = E * EltT::kSize;
   using In = typename VecT<IN_B>::T;
   using Out = typename VecT<OUT_B>::T;
-  __device__ static Out apply(In v, float scale) {
+  __device__ static Out apply(In v, const QScale& qs) {
     uint8_t q[E];
     __builtin_memcpy(q, &v, sizeof(v));
     typename EltT::Bits o[E];
     if constexpr (E == 1) {
-      o[0] = EltT::from_f32(e4m3_unpack2(uint32_t(q[0]), false).x * scale);
+      o[0] = EltT::from_f32(e4m3_unpack2(uint32_t(q[0]), false).x * qs.s);
     } else {
 #pragma unroll
       for (int i = 0; i < E; i += 2) {
         const f32x2 f = e4m3_unpack2(uint32_t(q[i]) | (uint32_t(q[i + 1]) << 8), false);
-        o[i] = EltT::from_f32(f.x * scale);
-        o[i + 1] = EltT::from_f32(f.y * scale);
+        o[i] = EltT::from_f32(f.x * qs.s);
+        o[i + 1] = EltT::from_f32(f.y * qs.s);
       }
     }
     Out r;
@@ -284,17 +319,33 @@ __global__ void __launch_bounds__(256) paged_scatter_kernel(ScatterGeom g, Scatt
   const int64_t inner_stride = part ? p1.inner_stride : p0.inner_stride;
   const int nseg = part ? p1.nseg : p0.nseg;
   const int seg_vecs = part ? p1.seg_vecs : p0.seg_vecs;
-  const float scale = scale_p ? *scale_p : 1.0f;
   const bool flat = nseg == 1 && inner_stride == C::OUT_B;
+  const int total = nseg * seg_vecs;
 
+  // The input rows do not depend on the slots: their loads are issued first
+  // so the slot lookups (scalar loads) overlap the HBM latency of the data.
+  bool tv[CH];
   const char* srow[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    tv[c] = t0 + c < g.num_tokens;
+    srow[c] = src + (t0 + c) * src_stride;
+  }
+  typename C::In v[CH][U];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = u * kWave + lane;
+      if (tv[c] && i < total) v[c][u] = vload<C::IN_B>(srow[c] + int64_t(i) * C::IN_B);
+    }
+  }
+
   char* drow[CH];
   bool ok[CH];
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    const int64_t t = t0 + c;
-    int64_t slot = -1;
-    if (t < g.num_tokens) slot = g.slots[t];
+    const int64_t slot = tv[c] ? g.slots[t0 + c] : int64_t(-1);
     ok[c] = slot >= 0 && slot < g.num_slots;
     int64_t blk, off;
     if (g.bs_shift >= 0) {
@@ -304,21 +355,11 @@ __global__ void __launch_bounds__(256) paged_scatter_kernel(ScatterGeom g, Scatt
       blk = slot / g.block_size;
       off = slot - blk * g.block_size;
     }
-    srow[c] = src + t * src_stride;
     drow[c] = dst + blk * blk_stride + off * page_stride + dst_off;
   }
+  const QScale qs = make_qscale(scale_p ? *scale_p : 1.0f);
 
-  const int total = nseg * seg_vecs;
-  for (int base = 0; base < total; base += kWave * U) {
-    typename C::In v[CH][U];
-#pragma unroll
-    for (int c = 0; c < CH; ++c) {
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int i = base + u * kWave + lane;
-        if (ok[c] && i < total) v[c][u] = vload<C::IN_B>(srow[c] + int64_t(i) * C::IN_B);
-      }
-    }
+  for (int base = 0;;) {
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
 #pragma unroll
@@ -332,8 +373,19 @@ __global__ void __launch_bounds__(256) paged_scatter_kernel(ScatterGeom g, Scatt
             const int s = i / seg_vecs;
             o = int64_t(s) * seg_stride + int64_t(i - s * seg_vecs) * inner_stride;
           }
-          vstore<C::OUT_B>(drow[c] + o, C::apply(v[c][u], scale));
+          vstore<C::OUT_B>(drow[c] + o, C::apply(v[c][u], qs));
         }
+      }
+    }
+    base += kWave * U;
+    if (base >= total) break;
+    // rows longer than one pass (e.g. 32 heads x 128): next slice
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = base + u * kWave + lane;
+        if (ok[c] && i < total) v[c][u] = vload<C::IN_B>(srow[c] + int64_t(i) * C::IN_B);
       }
     }
   }
@@ -447,7 +499,10 @@ __global__ void __launch_bounds__(256) paged_gather_kernel(GatherGeom g) {
   if (t0 >= g.num_tokens) return;
   const char* src = part ? g.src1 : g.src0;
   char* dst = part ? g.dst1 : g.dst0;
-  const float scale = g.scale ? *g.scale : 1.0f;
+  QScale qs;
+  qs.s = g.scale ? *g.scale : 1.0f;
+  qs.r = 0.0f;
+  qs.fast = false;
 
   // Sequence of the first token: largest b in [0, batch] with cu[b] <= t0.
   int lo = 0, hi = int(g.batch);
@@ -500,7 +555,7 @@ __global__ void __launch_bounds__(256) paged_gather_kernel(GatherGeom g) {
       for (int u = 0; u < U; ++u) {
         const int i = base + u * kWave + lane;
         if (wr[c] && i < total)
-          vstore<C::OUT_B>(drow[c] + int64_t(i) * C::OUT_B, rd[c] ? C::apply(v[c][u], scale) : C::zero());
+          vstore<C::OUT_B>(drow[c] + int64_t(i) * C::OUT_B, rd[c] ? C::apply(v[c][u], qs) : C::zero());
       }
     }
   }

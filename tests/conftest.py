@@ -25,14 +25,14 @@ def pytest_collection_modifyitems(config, items):
 
 def raw(t: torch.Tensor) -> np.ndarray:
     """Raw element bits of a tensor as a host numpy array (uint16 for 16-bit
-    floats, uint8 for fp8, float32 for fp32)."""
+    floats, uint8 for fp8, uint32 for fp32)."""
     t = t.detach().contiguous().cpu()
     if t.dtype in (torch.bfloat16, torch.float16):
         return t.view(torch.int16).numpy().view(np.uint16)
     if t.dtype == torch.float8_e4m3fn:
         return t.view(torch.uint8).numpy()
     if t.dtype == torch.float32:
-        return t.numpy()
+        return t.view(torch.int32).numpy().view(np.uint32)
     return t.numpy()
 
 

@@ -181,6 +181,25 @@ def test_fp8_scaled_boundaries_match_golden(dev, in_dtype):
             assert np.array_equal(got, q[a:b])
 
 
+@pytest.mark.parametrize("scale", [3.0, 7.77, 0.0123456789, 1e-3, 448.0 / 447.0, 2.5e-30, 3e29, 1e-39])
+def test_fp8_every_bf16_pattern_at_scale(dev, scale):
+    """All 65536 bf16 patterns at non-trivial scales: the reciprocal + FMA
+    quotient must equal the IEEE fp32 quotient the oracle takes (1e-39 is a
+    subnormal scale, which takes the plain division)."""
+    H, D = 4, 128
+    N = 65536 // (H * D)
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16).view(N, H, D)
+    cache = torch.zeros(N, 2, 1, H, D, dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
+    x = bits.to(dev)
+    sc = torch.tensor([scale], dtype=torch.float32, device=dev)
+    reshape_and_cache_flash(x, x, cache[:, 0], cache[:, 1], torch.arange(N, dtype=torch.int64, device=dev), sc, sc)
+    s32 = float(np.float32(scale))
+    exp = O.quantize_e4m3(O.bf16_to_f32(raw(bits).reshape(-1)), s32)
+    assert np.array_equal(raw(cache)[:, 0].reshape(-1), exp)
+    ref = (bits.float().reshape(-1) / torch.tensor(s32)).clamp(-448, 448).to(torch.float8_e4m3fn)
+    assert np.array_equal(raw(cache)[:, 1].reshape(-1), raw(ref))
+
+
 def test_fp8_nan_policy(dev):
     x = torch.tensor([float("nan"), -float("nan"), 1.0, float("inf"), -float("inf"), -0.0], dtype=torch.float32)
     n = x.shape[0]

@@ -1,0 +1,115 @@
+"""Host-side logic of the path, on the CPU: slot mapping / page table builder,
+graph metadata refresh, the CopyEngine's coalescing and range check, and the
+shims' argument checks that fire before any device call."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kv_oracle as O
+from pipeswift_amd import cudagraph, metadata
+from pipeswift_amd.copy_engine import CopyEngine, page_bytes
+
+
+class Seq:
+    def __init__(self, seq_id, n_tokens, offset):
+        self.seq_id = seq_id
+        self.token_ids = list(range(n_tokens))
+        self.offset = offset
+
+
+@pytest.mark.parametrize("dcp,il", [(1, 1), (2, 1), (2, 8), (4, 4)])
+def test_prepare_kv_info_matches_oracle(dcp, il):
+    rng = np.random.default_rng(dcp * 7 + il)
+    ps = 16
+    seqs = [Seq(3, 100, 0), Seq(7, 45, 33), Seq(9, 17, 16), Seq(11, 64, 63)]
+    table = {s.seq_id: rng.permutation(500)[: (len(s.token_ids) + ps - 1) // ps + 1].tolist() for s in seqs}
+    for rank in range(dcp):
+        info = metadata.prepare_kv_info(seqs, table, ps, None, None, dcp_interleave_size=il, dcp_deg=dcp,
+                                        dcp_rank=rank, device="cpu")
+        exp = np.concatenate([O.slot_mapping(table[s.seq_id], s.offset, len(s.token_ids), ps, dcp, rank, il)
+                              for s in seqs])
+        assert info.slot_mapping.dtype == torch.int64
+        assert np.array_equal(info.slot_mapping.numpy(), exp)
+        W = max(len(v) for v in table.values())
+        assert info.page_table.shape == (4, W) and info.page_table.dtype == torch.int32
+        for i, s in enumerate(seqs):
+            row = info.page_table[i].numpy()
+            assert list(row[: len(table[s.seq_id])]) == table[s.seq_id] and not row[len(table[s.seq_id]):].any()
+        q = [len(s.token_ids) - s.offset for s in seqs]
+        assert info.actual_lens_q.tolist() == q
+        assert info.cu_seqlens_q.tolist() == [0] + list(np.cumsum(q))
+        kv = [len(s.token_ids) if dcp == 1 else O.dcp_kv_len(s.offset, dcp, rank, il) for s in seqs]
+        assert info.actual_lens_kv.tolist() == kv
+
+
+def test_next_decode_step_metadata():
+    ps = 16
+    seqs = [Seq(0, 40, 39), Seq(1, 16, 15)]
+    table = {0: [5, 9, 2, 7], 1: [4, 8]}
+    info = metadata.prepare_kv_info(seqs, table, ps, None, None, is_decode=True, device="cpu")
+    for s in seqs:
+        s.offset += 1
+        s.token_ids.append(0)
+    nxt = metadata.derive_kvcache_info_next_decode_step(info, seqs, table, ps, device="cpu")
+    assert nxt.slot_mapping.tolist() == [2 * 16 + 8, 8 * 16 + 0]
+    assert nxt.actual_lens_kv.tolist() == [41, 17]
+
+
+def test_graph_metadata_refresh_pads_with_minus_one():
+    static = cudagraph.initialize_graph_kvcacheinfo(8, 4, device="cpu")
+    assert (static.slot_mapping == -1).all()
+    info = metadata.KVCacheInfo(page_table=torch.ones(3, 2, dtype=torch.int32),
+                                slot_mapping=torch.tensor([5, 6, 7]), actual_lens_q=torch.ones(3, dtype=torch.int32),
+                                actual_lens_kv=torch.full((3,), 9, dtype=torch.int32),
+                                cu_seqlens_q=torch.arange(4, dtype=torch.int32))
+    static.slot_mapping.fill_(123)
+    cudagraph.set_graph_kvcacheinfo(static, info, 8)
+    assert static.slot_mapping.tolist() == [5, 6, 7, -1, -1, -1, -1, -1]
+    assert static.page_table[3:].abs().sum() == 0
+    assert static.cu_seqlens_q.tolist() == list(range(9))
+    sl = cudagraph.slice_kvcache_info(static, 3)
+    assert sl.slot_mapping.tolist() == [5, 6, 7] and sl.cg_bsz == 3
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_copy_engine_coalesce_matches_oracle(seed):
+    rng = np.random.default_rng(seed)
+    n = int(rng.integers(1, 300))
+    src = rng.permutation(1000)[:n].astype(np.uint64)
+    dst = (src + 3) if seed % 2 else rng.permutation(1000)[:n].astype(np.uint64)
+    got = CopyEngine._coalesce(src, dst)
+    exp = O.coalesce(src, dst)
+    for a, b in zip(got, exp):
+        assert np.array_equal(a, b)
+    # runs cover every page once and preserve the pairing
+    s, d, ln = got
+    pairs = {(int(a) + i, int(b) + i) for a, b, k in zip(s, d, ln) for i in range(int(k))}
+    assert pairs == {(int(a), int(b)) for a, b in zip(src, dst)}
+
+
+def test_copy_engine_range_check_message():
+    with pytest.raises(AssertionError, match=r"L2 store src page index out of range for the gpu tier: \[10\] >= 10"):
+        CopyEngine._check_range(np.array([1, 10], np.uint64), np.array([0, 1], np.uint64), 10, 20, True)
+    with pytest.raises(AssertionError, match="L2 load dst page index out of range for the gpu tier"):
+        CopyEngine._check_range(np.array([0], np.uint64), np.array([50], np.uint64), 20, 10, False)
+    CopyEngine._check_range(np.array([9], np.uint64), np.array([19], np.uint64), 10, 20, True)
+
+
+def test_page_bytes_matches_oracle():
+    a = torch.empty(3, 10, 2, 16, 8, 128, dtype=torch.bfloat16)
+    b = torch.empty(2, 10, 64, 576, dtype=torch.float8_e4m3fn)
+    assert page_bytes([a, b]) == O.page_bytes([(a.shape, 2), (b.shape, 1)]) == 3 * 65536 + 2 * 64 * 576
+
+
+def test_shim_asserts_fire_before_device_calls():
+    from pipeswift_amd.reshape_and_cache import reshape_and_cache_flash, reshape_and_cache_flash_diffkv
+
+    k = torch.zeros(4, 8, 128, dtype=torch.bfloat16)
+    c = torch.zeros(2, 16, 8, 128, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError):  # CPU tensors: the reference asserts is_cuda too
+        reshape_and_cache_flash(k, k, c, c, torch.zeros(4, dtype=torch.int64))
+    with pytest.raises(AssertionError):
+        reshape_and_cache_flash(k.view(4, 1024)[None], k, c, c, torch.zeros(4, dtype=torch.int64))
+    with pytest.raises(AssertionError):
+        reshape_and_cache_flash_diffkv(k, k, torch.zeros(2, 16, 8, 100), torch.zeros(4, dtype=torch.int64))
