@@ -140,24 +140,6 @@ __device__ __forceinline__ uint32_t e4m3_nan_byte(float x) {
   return ((__float_as_uint(x) >> 24) & 0x80u) | 0x7Fu;
 }
 
-// Saturate to the finite E4M3FN range.  NaN passes through, as torch.clamp does.
-__device__ __forceinline__ float clamp_e4m3(float x) {
-  return __builtin_isnan(x) ? x : __builtin_fminf(__builtin_fmaxf(x, -448.0f), 448.0f);
-}
-
-// Two floats -> two E4M3FN bytes (low byte = a) with the native gfx950 OCP
-// conversion (v_cvt_pk_fp8_f32, round to nearest even).  Inputs are clamped
-// first, so the conversion never overflows; NaN lanes are rewritten to the
-// torch NaN byte.
-__device__ __forceinline__ uint32_t e4m3_pack2(float a, float b) {
-  uint32_t w = uint32_t(__builtin_amdgcn_cvt_pk_fp8_f32(clamp_e4m3(a), clamp_e4m3(b), 0, false)) & 0xFFFFu;
-  if (__builtin_expect(__builtin_isnan(a) || __builtin_isnan(b), 0)) {
-    if (__builtin_isnan(a)) w = (w & 0xFF00u) | e4m3_nan_byte(a);
-    if (__builtin_isnan(b)) w = (w & 0x00FFu) | (e4m3_nan_byte(b) << 8);
-  }
-  return w;
-}
-
 // E4M3FN bytes 0 and 1 (or 2 and 3 with hi) of w -> floats, native conversion.
 __device__ __forceinline__ f32x2 e4m3_unpack2(uint32_t w, bool hi) {
   return hi ? __builtin_amdgcn_cvt_pk_f32_fp8(int(w), true) : __builtin_amdgcn_cvt_pk_f32_fp8(int(w), false);
@@ -166,11 +148,16 @@ __device__ __forceinline__ f32x2 e4m3_unpack2(uint32_t w, bool hi) {
 // ---- per-tensor scale, prepared once per wave
 
 // x / s must be the correctly rounded IEEE quotient (the oracle divides in
-// fp32).  With r = RN(1/s) computed once, y = RN(x*r) is within an ulp of x/s,
-// the residual e = x - y*s is exact in one FMA, and RN(y + e*r) is the
-// correctly rounded quotient (Markstein's theorem) whenever nothing under- or
-// overflows: |s|, |x| and |y| inside [2^-100, 2^100).  Outside that range,
-// and for zeros, infinities and NaN, the plain IEEE division runs instead.
+// fp32).  With r = RN(1/s) computed once per wave, y = RN(x*r) is within an ulp
+// of x/s, the residual e = x - y*s is exact in one FMA and RN(y + e*r) is the
+// correctly rounded quotient (Markstein's theorem) as long as nothing under- or
+// overflows.  For |s| in [2^-80, 2^100) the only cases outside that are:
+//   * |x| < 2^-100: the quotient is below 2^-20 and converts to a signed zero,
+//     so only its sign matters, which copysign(., y) keeps (also for x = +-0);
+//   * y = +-inf or NaN (x infinite, NaN, or the quotient overflows): y itself
+//     is the right input to the clamp.
+// Any other scale (0, inf, NaN, tiny) takes the plain IEEE division.  A scale
+// of exactly 1.0 (the reference's fixed scale) skips the division.
 struct QScale {
   float s;
   float r;
@@ -182,20 +169,16 @@ __device__ __forceinline__ QScale make_qscale(float s) {
   q.s = s;
   q.r = 1.0f / s;
   const float a = __builtin_fabsf(s);
-  q.fast = a >= 0x1p-100f && a < 0x1p100f;
+  q.fast = a >= 0x1p-80f && a < 0x1p100f;
   return q;
 }
 
-__device__ __forceinline__ float div_by_scale(float x, const QScale& q) {
-  if (q.fast) {
-    const float y = x * q.r;
-    const float a = __builtin_fabsf(x);
-    if (a >= 0x1p-100f && a < 0x1p100f && __builtin_fabsf(y) < 0x1p100f) {
-      const float e = __builtin_fmaf(-y, q.s, x);
-      return __builtin_fmaf(e, q.r, y);
-    }
-  }
-  return x / q.s;
+// Exact for s == 1.0 as well: r = 1, y = x, e = 0.
+__device__ __forceinline__ float div_fast(float x, const QScale& q) {
+  const float y = x * q.r;
+  const float e = __builtin_fmaf(-y, q.s, x);
+  const float z = __builtin_copysignf(__builtin_fmaf(e, q.r, y), y);
+  return __builtin_fabsf(y) < __builtin_inff() ? z : y;
 }
 
 // ---- conversion policies: In vector (IN_B bytes) -> Out vector (OUT_B bytes)
@@ -211,6 +194,9 @@ struct CopyConv {
 };
 
 // E input elements of type IN_DT -> E E4M3FN bytes, q = e4m3(clamp(x / scale)).
+// The clamp is v_med3_f32 (exact for every non-NaN input, +-inf included);
+// the native convert turns NaN into 0xFF, so NaN lanes are patched to torch's
+// 0x7F|sign afterwards (rare path).
 template <int IN_DT, int E>
 struct QuantConv {
   using EltT = Elt<IN_DT>;
@@ -222,22 +208,34 @@ struct QuantConv {
     typename EltT::Bits e[E];
     __builtin_memcpy(e, &v, sizeof(v));
     float f[E];
+    if (__builtin_expect(qs.fast, 1)) {
 #pragma unroll
-    for (int i = 0; i < E; ++i) f[i] = div_by_scale(EltT::to_f32(e[i]), qs);
-    if constexpr (E == 1) {
-      return Out(e4m3_pack2(f[0], 0.0f) & 0xFFu);
+      for (int i = 0; i < E; ++i) f[i] = div_fast(EltT::to_f32(e[i]), qs);
     } else {
-      uint8_t o[E];
+      // scales outside [2^-80, 2^100) (0, inf, NaN, subnormal): IEEE division
 #pragma unroll
-      for (int i = 0; i < E; i += 2) {
-        uint32_t w = e4m3_pack2(f[i], f[i + 1]);
-        o[i] = uint8_t(w);
-        o[i + 1] = uint8_t(w >> 8);
-      }
-      Out r;
-      __builtin_memcpy(&r, o, sizeof(r));
-      return r;
+      for (int i = 0; i < E; ++i) f[i] = EltT::to_f32(e[i]) / qs.s;
     }
+    bool any_nan = false;
+#pragma unroll
+    for (int i = 0; i < E; ++i) any_nan |= __builtin_isnan(f[i]);
+    uint8_t o[E];
+#pragma unroll
+    for (int i = 0; i < E; i += 2) {
+      const float a = __builtin_amdgcn_fmed3f(f[i], -448.0f, 448.0f);
+      const float b = i + 1 < E ? __builtin_amdgcn_fmed3f(f[i + 1], -448.0f, 448.0f) : 0.0f;
+      const uint32_t w = uint32_t(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false));
+      o[i] = uint8_t(w);
+      if (i + 1 < E) o[i + 1] = uint8_t(w >> 8);
+    }
+    if (__builtin_expect(any_nan, 0)) {
+#pragma unroll
+      for (int i = 0; i < E; ++i)
+        if (__builtin_isnan(f[i])) o[i] = uint8_t(e4m3_nan_byte(f[i]));
+    }
+    Out r;
+    __builtin_memcpy(&r, o, sizeof(r));
+    return r;
   }
   __device__ static Out zero() { return Out(0); }
 };
@@ -294,20 +292,29 @@ struct ScatterGeom {
   const int64_t* slots;
   int64_t num_tokens;
   int64_t block_size;
-  int64_t num_slots;  // num_blocks * block_size
-  int32_t bs_shift;   // log2(block_size), or -1 when not a power of two
-  int32_t nparts;     // 1 or 2
+  int64_t num_slots;    // num_blocks * block_size
+  int32_t bs_shift;     // log2(block_size), or -1 when not a power of two
+  int32_t nparts;       // 1 or 2
+  int32_t slice_shift;  // log2(waves per (token chunk, part))
 };
 
-template <class C, int CH, int U>
-__global__ void __launch_bounds__(256) paged_scatter_kernel(ScatterGeom g, ScatterPart p0, ScatterPart p1) {
+// One wave per (chunk of CH tokens, part, slice).  A part's row of `total`
+// vectors is cut into 2^slice_shift slices of 64*U vectors (a slice loops when
+// the row is longer), so decode-sized batches spread one row over several
+// waves and prefill-sized ones give each wave CH rows.
+template <class C, int CH, int U, bool FAST, int WPB>
+__global__ void __launch_bounds__(WPB * 64) paged_scatter_kernel(ScatterGeom g, ScatterPart p0, ScatterPart p1) {
+  // No branch before the row loads: a wave with nothing to do runs with its
+  // lanes predicated off, so the scalar loads of the argument segment can
+  // issue as one batch.  The workgroup size is a compile-time constant (WPB
+  // waves), which keeps blockDim out of the argument segment reads.
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t wave = int64_t(blockIdx.x) * (blockDim.x / kWave) +
-                       __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
-  const int part = g.nparts == 2 ? int(wave & 1) : 0;
-  const int64_t t0 = (g.nparts == 2 ? (wave >> 1) : wave) * CH;
-  if (t0 >= g.num_tokens) return;
-
+  const int64_t wave = int64_t(blockIdx.x) * WPB + __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
+  const int slice = int(wave & ((int64_t(1) << g.slice_shift) - 1));
+  const int64_t rest = wave >> g.slice_shift;
+  const bool two = g.nparts == 2;
+  const int part = two ? int(rest & 1) : 0;
+  const int64_t t0 = (two ? (rest >> 1) : rest) * CH;
   const char* src = part ? p1.src : p0.src;
   char* dst = part ? p1.dst : p0.dst;
   const float* scale_p = part ? p1.scale : p0.scale;
@@ -315,12 +322,14 @@ __global__ void __launch_bounds__(256) paged_scatter_kernel(ScatterGeom g, Scatt
   const int64_t blk_stride = part ? p1.blk_stride : p0.blk_stride;
   const int64_t page_stride = part ? p1.page_stride : p0.page_stride;
   const int64_t dst_off = part ? p1.dst_off : p0.dst_off;
-  const int64_t seg_stride = part ? p1.seg_stride : p0.seg_stride;
-  const int64_t inner_stride = part ? p1.inner_stride : p0.inner_stride;
-  const int nseg = part ? p1.nseg : p0.nseg;
+  const int64_t seg_stride = FAST ? 0 : (part ? p1.seg_stride : p0.seg_stride);
+  const int64_t inner_stride = FAST ? C::OUT_B : (part ? p1.inner_stride : p0.inner_stride);
+  const int nseg = FAST ? 1 : (part ? p1.nseg : p0.nseg);
   const int seg_vecs = part ? p1.seg_vecs : p0.seg_vecs;
-  const bool flat = nseg == 1 && inner_stride == C::OUT_B;
+  const bool flat = FAST || (nseg == 1 && inner_stride == C::OUT_B);
   const int total = nseg * seg_vecs;
+  const int step = (kWave * U) << g.slice_shift;
+  int base = slice * (kWave * U);
 
   // The input rows do not depend on the slots: their loads are issued first
   // so the slot lookups (scalar loads) overlap the HBM latency of the data.
@@ -336,7 +345,7 @@ __global__ void __launch_bounds__(256) paged_scatter_kernel(ScatterGeom g, Scatt
   for (int c = 0; c < CH; ++c) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int i = u * kWave + lane;
+      const int i = base + u * kWave + lane;
       if (tv[c] && i < total) v[c][u] = vload<C::IN_B>(srow[c] + int64_t(i) * C::IN_B);
     }
   }
@@ -348,7 +357,7 @@ __global__ void __launch_bounds__(256) paged_scatter_kernel(ScatterGeom g, Scatt
     const int64_t slot = tv[c] ? g.slots[t0 + c] : int64_t(-1);
     ok[c] = slot >= 0 && slot < g.num_slots;
     int64_t blk, off;
-    if (g.bs_shift >= 0) {
+    if (FAST || g.bs_shift >= 0) {
       blk = slot >> g.bs_shift;
       off = slot & (g.block_size - 1);
     } else {
@@ -359,7 +368,7 @@ __global__ void __launch_bounds__(256) paged_scatter_kernel(ScatterGeom g, Scatt
   }
   const QScale qs = make_qscale(scale_p ? *scale_p : 1.0f);
 
-  for (int base = 0;;) {
+  for (;;) {
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
 #pragma unroll
@@ -370,43 +379,74 @@ __global__ void __launch_bounds__(256) paged_scatter_kernel(ScatterGeom g, Scatt
           if (flat) {
             o = int64_t(i) * C::OUT_B;
           } else {
-            const int s = i / seg_vecs;
-            o = int64_t(s) * seg_stride + int64_t(i - s * seg_vecs) * inner_stride;
+            const int sg = i / seg_vecs;
+            o = int64_t(sg) * seg_stride + int64_t(i - sg * seg_vecs) * inner_stride;
           }
           vstore<C::OUT_B>(drow[c] + o, C::apply(v[c][u], qs));
         }
       }
     }
-    base += kWave * U;
+    base += step;
     if (base >= total) break;
-    // rows longer than one pass (e.g. 32 heads x 128): next slice
+    // rows longer than one pass of the slice: next stretch
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int i = base + u * kWave + lane;
-        if (ok[c] && i < total) v[c][u] = vload<C::IN_B>(srow[c] + int64_t(i) * C::IN_B);
+        if (tv[c] && i < total) v[c][u] = vload<C::IN_B>(srow[c] + int64_t(i) * C::IN_B);
       }
     }
   }
 }
 
+// Launch shape.  Decode-sized batches (< 1024 tokens) are latency bound: one
+// vector per lane (U = 1) and rows split over as many slices as they have
+// 64-vector stretches, so e.g. 128 tokens x (K, V) x 1024 bf16 -> 512 waves.
+// Larger batches give each wave 4 tokens and 2 vectors per lane.
+struct ScatterShape {
+  int ch;
+  int u;
+  int slice_shift;
+};
+
+ScatterShape scatter_shape(int64_t num_tokens, int total_vecs) {
+  ScatterShape sh;
+  if (num_tokens < 1024) {
+    sh.ch = 1;
+    sh.u = 1;
+    int slices = int(ceil_div(total_vecs, kWave));
+    if (slices > 8) slices = 8;
+    sh.slice_shift = 0;
+    while ((1 << sh.slice_shift) < slices) ++sh.slice_shift;
+  } else {
+    sh.ch = 4;
+    sh.u = 2;
+    sh.slice_shift = 0;
+  }
+  return sh;
+}
+
+template <class C, int CH, int U, bool FAST, int WPB>
+int launch_scatter_shape(ScatterGeom g, const ScatterPart& p0, const ScatterPart& p1, int slice_shift,
+                         hipStream_t st) {
+  g.slice_shift = slice_shift;
+  const int64_t waves = (ceil_div(g.num_tokens, CH) * g.nparts) << slice_shift;
+  const int64_t grid = ceil_div(waves, WPB);
+  hipLaunchKernelGGL((paged_scatter_kernel<C, CH, U, FAST, WPB>), dim3(grid), dim3(WPB * kWave), 0, st, g, p0, p1);
+  return check_launch("paged_scatter_kernel launch");
+}
+
+bool part_flat(const ScatterPart& p, int out_b) { return p.nseg == 1 && p.inner_stride == out_b; }
+
 template <class C>
 int launch_scatter(const ScatterGeom& g, const ScatterPart& p0, const ScatterPart& p1, hipStream_t st) {
-  // Decode-sized batches: one token per wave and 64-thread workgroups, to spread
-  // the few waves over as many CUs as possible.  Prefill-sized batches: four
-  // tokens per wave so each lane keeps 4-8 loads in flight.
-  if (g.num_tokens < 4096) {
-    const int64_t waves = g.num_tokens * g.nparts;
-    const int threads = g.num_tokens <= 1024 ? 64 : 256;
-    const int64_t grid = ceil_div(waves, threads / kWave);
-    hipLaunchKernelGGL((paged_scatter_kernel<C, 1, 2>), dim3(grid), dim3(threads), 0, st, g, p0, p1);
-  } else {
-    const int64_t waves = ceil_div(g.num_tokens, 4) * g.nparts;
-    const int64_t grid = ceil_div(waves, 4);
-    hipLaunchKernelGGL((paged_scatter_kernel<C, 4, 2>), dim3(grid), dim3(256), 0, st, g, p0, p1);
-  }
-  return check_launch("paged_scatter_kernel launch");
+  const int total = p0.nseg * p0.seg_vecs > p1.nseg * p1.seg_vecs ? p0.nseg * p0.seg_vecs : p1.nseg * p1.seg_vecs;
+  const ScatterShape sh = scatter_shape(g.num_tokens, total);
+  const bool fast = g.bs_shift >= 0 && part_flat(p0, C::OUT_B) && (g.nparts == 1 || part_flat(p1, C::OUT_B));
+  if (!fast) return launch_scatter_shape<C, 1, 2, false, 4>(g, p0, p1, sh.ch == 1 ? sh.slice_shift : 0, st);
+  if (sh.ch == 1) return launch_scatter_shape<C, 1, 1, true, 1>(g, p0, p1, sh.slice_shift, st);
+  return launch_scatter_shape<C, 4, 2, true, 4>(g, p0, p1, sh.slice_shift, st);
 }
 
 // Dispatch on (in_dtype, cache_dtype, vector elements).
@@ -845,6 +885,7 @@ int psk_reshape_and_cache(const void* key, const void* value, void* key_cache, v
   g.num_slots = num_blocks * block_size;
   g.bs_shift = log2_exact(block_size);
   g.nparts = 2;
+  g.slice_shift = 0;
 
   // Heads are one contiguous run in the cache when dim stride is 1 and the head
   // stride is head_size; then a token's part is one flat row of row elements.
@@ -937,6 +978,7 @@ int psk_concat_and_cache_mla(const void* kv_c, const void* k_pe, void* kv_cache,
   g.num_slots = num_blocks * block_size;
   g.bs_shift = log2_exact(block_size);
   g.nparts = value_len > 0 ? 2 : 1;
+  g.slice_shift = 0;
   auto make_part = [&](const void* src, int64_t src_stride, int64_t len, int64_t dst_off) {
     ScatterPart p;
     p.src = static_cast<const char*>(src);
