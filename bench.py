@@ -25,6 +25,7 @@ Workloads (default fp8_decode_append, config 2 of the benchmark plan):
   mla_prefill / mla_decode   kv_c 512 + k_pe 64, block 64, 20000 blocks
   copy_blocks        2048 pairs over 61 layers of [8192, 2, 16, 8, 128] bf16
   swap               8192 scattered blocks x 8 layers (4 GiB) D2H + H2D
+  kv_scales          config 2's per-tensor K/V scales (amax kernel)
   hbm_copy           1 GiB device copy (achievable-bandwidth reference and the
                      PMC calibration run)
 """
@@ -122,6 +123,33 @@ def setup_append(args, device, fp8):
         "cpu": lambda: cpu_append(case, fp8),
     }
     return launch, info
+
+
+def setup_kv_scales(args, device):
+    """Per-tensor FP8 scales of config 2's K and V (amax / 448), one launch."""
+    import torch
+
+    from pipeswift_amd import cache_ops, workloads
+
+    case = workloads.config2_fp8_decode()
+    R = args.rotate
+    dgen = torch.Generator(device=device).manual_seed(93)
+    qkv = torch.empty((R,) + tuple(case.qkv.shape), dtype=torch.bfloat16, device=device)
+    qkv.normal_(0.0, 2.0, generator=dgen)
+    out = torch.empty(2, dtype=torch.float32, device=device)
+    cache_ops.warmup(device)
+
+    def launch(i):
+        q = qkv[i]
+        cache_ops.compute_kv_scales(case.key(q), case.value(q), out=out)
+
+    nbytes = 2 * case.qkv.shape[0] * case.num_heads * case.head_size * 2
+    return launch, {
+        "name": "kv_scales", "kernel": "amax_scale_kernel", "bytes": nbytes, "tokens": case.qkv.shape[0],
+        "dtype": "bf16",
+        "config": {"workload": "FP8 per-tensor scale from amax, config 2 K and V", "tokens": case.qkv.shape[0]},
+        "cpu": None,
+    }
 
 
 def setup_chunked(args, device, gather):
@@ -416,6 +444,8 @@ def main():
     name = args.workload
     if name in ("fp8_decode_append", "bf16_append"):
         launch, info = setup_append(args, device, fp8=name.startswith("fp8"))
+    elif name == "kv_scales":
+        launch, info = setup_kv_scales(args, device)
     elif name in ("chunked_append", "gather"):
         launch, info = setup_chunked(args, device, gather=name == "gather")
     elif name in ("mla_prefill", "mla_decode"):

@@ -169,10 +169,11 @@ int64_t psk_swap_staging_bytes(int64_t num_views, int64_t num_pages);
  * For tensor j in {0, 1} (x1 may be NULL): amax_j = max |x_j| over `rows` rows
  * of `row_len` elements at element stride row_stride_j, NaN ignored;
  * scale_out[j] = amax_j > 0 ? amax_j / qmax : 1.0f (IEEE fp32 divide);
- * amax_out[j] = amax_j when amax_out is not NULL.  `workspace` is device
- * memory of psk_kv_amax_workspace_len() uint32 words that is zero before the
- * first call; each call leaves it zero again.  Calls sharing a workspace must
- * not overlap.
+ * amax_out[j] = amax_j when amax_out is not NULL.  Two launches on `stream`:
+ * per-workgroup partial maxima into `workspace` (device memory of
+ * psk_kv_amax_workspace_len() uint32 words, no initial contents required),
+ * then one workgroup that reduces them.  Calls sharing a workspace must be
+ * ordered on one stream.
  */
 int psk_kv_amax_scale(const void* x0, const void* x1, int64_t rows, int64_t row_len,
                       int64_t row_stride0, int64_t row_stride1, int dtype, float qmax,

@@ -187,11 +187,11 @@ _ws_lock = threading.Lock()
 
 
 def amax_workspace(device) -> torch.Tensor:
-    """Per-device zeroed uint32 workspace of the amax kernel.
+    """Per-device uint32 workspace of the amax kernels (partial maxima).
 
-    Allocate it (``warmup``) before any HIP graph capture: each call leaves it
-    zeroed again, so it is reusable inside graphs.  Calls that share it must
-    not overlap (they run on one stream in practice).
+    Allocate it (``warmup``) before any HIP graph capture; it needs no initial
+    contents, so it is reusable inside graphs.  Calls that share it must be
+    ordered on one stream (they run on the caller's stream).
     """
     device = torch.device(device)
     if device.index is None:

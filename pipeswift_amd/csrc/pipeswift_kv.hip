@@ -705,13 +705,14 @@ __global__ void __launch_bounds__(256) copy_blocks_kernel(char* cache, int64_t n
 // ----------------------------------------------------------------------------
 
 constexpr int kAmaxMaxBlocks = 1024;
-constexpr int64_t kAmaxWsLen = 2 + 2 * int64_t(kAmaxMaxBlocks);
+constexpr int64_t kAmaxWsLen = 2 * int64_t(kAmaxMaxBlocks);
 
 struct AmaxArgs {
   const char* x0;
   const char* x1;
   int64_t rows;
   int64_t row_vecs;
+  int32_t tpr_shift;  // strided rows: log2(threads per row); rows == 1: unused
   int64_t stride0;  // bytes
   int64_t stride1;  // bytes
   float qmax;
@@ -751,21 +752,17 @@ __device__ __forceinline__ uint32_t block_max_u32(uint32_t m, uint32_t* red) {
 }
 
 template <int DT, int B>
-__global__ void __launch_bounds__(256) amax_scale_kernel(AmaxArgs a) {
+__global__ void __launch_bounds__(256) amax_partial_kernel(AmaxArgs a) {
   using Bits = typename Elt<DT>::Bits;
   constexpr int E = B / int(sizeof(Bits));
   using V = typename VecT<B>::T;
   __shared__ uint32_t red[4];
-  __shared__ int last;
   const int j = blockIdx.y;
   const char* x = j ? a.x1 : a.x0;
   const int64_t stride = j ? a.stride1 : a.stride0;
   uint32_t m = 0;
-  const int64_t total = a.rows * a.row_vecs;
-  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += int64_t(gridDim.x) * blockDim.x) {
-    const int64_t r = a.rows == 1 ? 0 : i / a.row_vecs;
-    const int64_t c = i - r * a.row_vecs;
-    const V v = vload<B>(x + r * stride + c * B);
+  auto take = [&](const char* p) {
+    const V v = vload_nt<B>(p);
     Bits e[E];
     __builtin_memcpy(e, &v, sizeof(v));
 #pragma unroll
@@ -773,31 +770,41 @@ __global__ void __launch_bounds__(256) amax_scale_kernel(AmaxArgs a) {
       const uint32_t q = abs_bits<DT>(e[k]);
       m = q > m ? q : m;
     }
+  };
+  if (a.rows == 1) {
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < a.row_vecs;
+         i += int64_t(gridDim.x) * blockDim.x)
+      take(x + i * B);
+  } else {
+    // 2^tpr_shift threads per row, 256 >> tpr_shift rows per workgroup pass
+    const int rpp = int(blockDim.x) >> a.tpr_shift;
+    const int64_t rsub = threadIdx.x >> a.tpr_shift;
+    const int64_t col0 = threadIdx.x & ((1 << a.tpr_shift) - 1);
+    for (int64_t r = int64_t(blockIdx.x) * rpp + rsub; r < a.rows; r += int64_t(gridDim.x) * rpp)
+      for (int64_t c = col0; c < a.row_vecs; c += (int64_t(1) << a.tpr_shift)) take(x + r * stride + c * B);
   }
   m = block_max_u32(m, red);
-  uint32_t* counter = a.ws + j;
-  uint32_t* partial = a.ws + 2 + int64_t(j) * kAmaxMaxBlocks;
-  if (threadIdx.x == 0) {
-    __hip_atomic_store(partial + blockIdx.x, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __threadfence();
-    const uint32_t ticket = atomicAdd(counter, 1u);
-    last = ticket == gridDim.x - 1;
-  }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  uint32_t m2 = 0;
-  for (int i = threadIdx.x; i < int(gridDim.x); i += blockDim.x) {
-    const uint32_t q = __hip_atomic_load(partial + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    m2 = q > m2 ? q : m2;
-  }
-  __syncthreads();
-  m2 = block_max_u32(m2, red);
-  if (threadIdx.x == 0) {
-    const float amax = __uint_as_float(m2);
-    a.scale_out[j] = amax > 0.0f ? amax / a.qmax : 1.0f;
-    if (a.amax_out) a.amax_out[j] = amax;
-    __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) a.ws[int64_t(j) * kAmaxMaxBlocks + blockIdx.x] = m;
+}
+
+// One workgroup: max over the partials of each tensor, then the scale.  A
+// second launch instead of a last-workgroup finish: device-scope atomics and
+// release fences cost more on MI355X than a kernel boundary.
+__global__ void __launch_bounds__(256) amax_finalize_kernel(AmaxArgs a, int nparts, int ntensors) {
+  __shared__ uint32_t red[4];
+  for (int j = 0; j < ntensors; ++j) {
+    uint32_t m = 0;
+    for (int i = threadIdx.x; i < nparts; i += blockDim.x) {
+      const uint32_t q = a.ws[int64_t(j) * kAmaxMaxBlocks + i];
+      m = q > m ? q : m;
+    }
+    m = block_max_u32(m, red);
+    if (threadIdx.x == 0) {
+      const float amax = __uint_as_float(m);
+      a.scale_out[j] = amax > 0.0f ? amax / a.qmax : 1.0f;
+      if (a.amax_out) a.amax_out[j] = amax;
+    }
+    __syncthreads();
   }
 }
 
@@ -1217,14 +1224,19 @@ int psk_kv_amax_scale(const void* x0, const void* x1, int64_t rows, int64_t row_
   uint64_t vals2[5] = {vals[0], vals[1], vals[2], vals[3], uint64_t(row_stride1 * sz)};
   const int vb = common_align(vals2, 5, 16);
   const int64_t row_vecs = rl * sz / vb;
-  const int64_t total = rws * row_vecs;
-  int64_t blocks = ceil_div(total > 0 ? total : 1, 256);
+  int tpr_shift = 0;
+  while (tpr_shift < 8 && (int64_t(1) << tpr_shift) < row_vecs) ++tpr_shift;
+  int64_t blocks;
+  if (rws == 1) blocks = ceil_div(row_vecs > 0 ? row_vecs : 1, 256);
+  else blocks = ceil_div(rws, int64_t(256) >> tpr_shift);
+  if (blocks < 1) blocks = 1;
   if (blocks > kAmaxMaxBlocks) blocks = kAmaxMaxBlocks;
   AmaxArgs a;
   a.x0 = static_cast<const char*>(x0);
   a.x1 = static_cast<const char*>(x1 ? x1 : x0);
   a.rows = rws;
   a.row_vecs = row_vecs;
+  a.tpr_shift = tpr_shift;
   a.stride0 = row_stride0 * sz;
   a.stride1 = (x1 ? row_stride1 : row_stride0) * sz;
   a.qmax = qmax;
@@ -1235,10 +1247,10 @@ int psk_kv_amax_scale(const void* x0, const void* x1, int64_t rows, int64_t row_
   hipStream_t st = static_cast<hipStream_t>(stream);
 #define PSK_AMAX_LAUNCH(DT)                                                                                     \
   switch (vb) {                                                                                                 \
-    case 16: hipLaunchKernelGGL((amax_scale_kernel<DT, 16>), grid, dim3(256), 0, st, a); break;                 \
-    case 8: hipLaunchKernelGGL((amax_scale_kernel<DT, 8>), grid, dim3(256), 0, st, a); break;                   \
-    case 4: hipLaunchKernelGGL((amax_scale_kernel<DT, 4>), grid, dim3(256), 0, st, a); break;                   \
-    default: hipLaunchKernelGGL((amax_scale_kernel<DT, (DT == PSK_DTYPE_F32 ? 4 : 2)>), grid, dim3(256), 0, st, a); break; \
+    case 16: hipLaunchKernelGGL((amax_partial_kernel<DT, 16>), grid, dim3(256), 0, st, a); break;               \
+    case 8: hipLaunchKernelGGL((amax_partial_kernel<DT, 8>), grid, dim3(256), 0, st, a); break;                 \
+    case 4: hipLaunchKernelGGL((amax_partial_kernel<DT, 4>), grid, dim3(256), 0, st, a); break;                 \
+    default: hipLaunchKernelGGL((amax_partial_kernel<DT, (DT == PSK_DTYPE_F32 ? 4 : 2)>), grid, dim3(256), 0, st, a); break; \
   }
   switch (dtype) {
     case PSK_DTYPE_BF16: PSK_AMAX_LAUNCH(PSK_DTYPE_BF16) break;
@@ -1246,7 +1258,10 @@ int psk_kv_amax_scale(const void* x0, const void* x1, int64_t rows, int64_t row_
     case PSK_DTYPE_F32: PSK_AMAX_LAUNCH(PSK_DTYPE_F32) break;
   }
 #undef PSK_AMAX_LAUNCH
-  return check_launch("amax_scale_kernel launch");
+  const int st1 = check_launch("amax_partial_kernel launch");
+  if (st1 != PSK_OK) return st1;
+  hipLaunchKernelGGL(amax_finalize_kernel, dim3(1), dim3(256), 0, st, a, int(blocks), x1 ? 2 : 1);
+  return check_launch("amax_finalize_kernel launch");
 }
 
 int psk_host_alloc(int64_t bytes, void** ptr) {

@@ -267,6 +267,39 @@ def test_amax_kernel_shapes(dev):
     assert s.cpu().tolist() == [float(ks), float(vs)]
 
 
+def test_kv_scales_replay_in_a_hip_graph(dev):
+    """Both amax launches captured once and replayed over new data; every replay
+    matches the oracle (no memset node, no workspace state carried over)."""
+    from pipeswift_amd import fp8_kv
+
+    fp8_kv.warmup(dev)
+    g = torch.Generator().manual_seed(22)
+    k_buf = torch.zeros(64, 8, 128, dtype=torch.bfloat16, device=dev)
+    v_buf = torch.zeros(64, 8, 128, dtype=torch.bfloat16, device=dev)
+    out = torch.zeros(2, dtype=torch.float32, device=dev)
+    amax = torch.zeros(2, dtype=torch.float32, device=dev)
+    cache_ops.compute_kv_scales(k_buf, v_buf, out=out, amax_out=amax)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            cache_ops.compute_kv_scales(k_buf, v_buf, out=out, amax_out=amax)
+    torch.cuda.current_stream().wait_stream(s)
+    for step in range(4):
+        k = (torch.randn(64, 8, 128, generator=g) * (step + 1)).to(torch.bfloat16)
+        v = (torch.randn(64, 8, 128, generator=g) * 0.1 / (step + 1)).to(torch.bfloat16)
+        k_buf.copy_(k)
+        v_buf.copy_(v)
+        graph.replay()
+        torch.cuda.synchronize()
+        ks, ka = O.amax_scale(raw(k), "bf16")
+        vs, va = O.amax_scale(raw(v), "bf16")
+        assert out.cpu().tolist() == [float(ks), float(vs)], f"replay {step}"
+        assert amax.cpu().tolist() == [float(ka), float(va)], f"replay {step}"
+
+
 # --------------------------------------------------------------------------- #
 # impl_utils / metadata path and graph capture
 # --------------------------------------------------------------------------- #
