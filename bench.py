@@ -26,6 +26,7 @@ Workloads (default fp8_decode_append, config 2 of the benchmark plan):
   copy_blocks        2048 pairs over 61 layers of [8192, 2, 16, 8, 128] bf16
   swap               8192 scattered blocks x 8 layers (4 GiB) D2H + H2D
   kv_scales          config 2's per-tensor K/V scales (amax kernel)
+  swap_sweep         host-link GB/s vs bytes per page, per transport
   hbm_copy           1 GiB device copy (achievable-bandwidth reference and the
                      PMC calibration run)
 """
@@ -358,6 +359,57 @@ def run_swap(args, device):
     print(json.dumps(line), flush=True)
 
 
+def run_swap_sweep(args, device):
+    """Host-link GB/s against bytes per page at a fixed 256 MiB per transfer,
+    scattered pages (every page its own run), both directions, per transport:
+    the MI355X counterpart of the descriptor-size table in copy_engine.py:15-21.
+    `*_GBs` is submit-to-completion wall time (host coalescing included);
+    `*_gpu_GBs` is HIP-event time on the copy stream."""
+    import numpy as np
+    import torch
+
+    from pipeswift_amd import copy_engine
+
+    total = 256 << 20
+    rows = []
+    for page in (4096, 8192, 16384, 32768, 65536, 131072, 262144, 524288):
+        n = total // page
+        cache = torch.empty((1, n + 1, page), dtype=torch.uint8, device=device)
+        rng = np.random.default_rng(page)
+        gpu_ids = rng.permutation(n + 1)[:n]
+        l2_ids = rng.permutation(n)
+        row = {"bytes_per_page": page}
+        for transport in args.transports.split(","):
+            eng = copy_engine.CopyEngine([cache], n + 1, n, transport=transport, timing_events=True)
+            try:
+                for direction in ("store", "load"):
+                    times, gpu_times = [], []
+                    params = eng.store_params if direction == "store" else eng.load_params
+                    for rep in range(3):
+                        torch.cuda.synchronize()
+                        start = torch.cuda.Event(enable_timing=True)
+                        start.record(params.stream)  # ahead of the copy thread's work on that stream
+                        t0 = time.perf_counter()
+                        h = eng.store(gpu_ids, l2_ids) if direction == "store" else eng.load(l2_ids, gpu_ids)
+                        h.wait()
+                        if rep:
+                            times.append(time.perf_counter() - t0)
+                            gpu_times.append(start.elapsed_time(h.event) / 1e3)
+                    row[f"{transport}_{direction}_GBs"] = round(total / min(times) / 1e9, 2)
+                    row[f"{transport}_{direction}_gpu_GBs"] = round(total / min(gpu_times) / 1e9, 2)
+            finally:
+                eng.close()
+        rows.append(row)
+        print(json.dumps(row), file=sys.stderr, flush=True)
+    best = max(min(r[f"{t}_{d}_GBs"] for d in ("store", "load")) for r in rows for t in args.transports.split(","))
+    line = {"metric": "host-link GB/s vs bytes per page (256 MiB scattered transfer)", "value": best, "unit": "GB/s",
+            "n_gpus": 1, "higher_is_better": True, "vs_baseline": None, "dtype": "bytes", "data": "synthetic",
+            "config": {"workload": "swap_sweep", "rows": rows},
+            "roofline": {"bound": "pcie", "achieved": best, "peak": 64.0, "unit": "GB/s", "frac": round(best / 64.0, 4),
+                         "traffic": None}}
+    print(json.dumps(line), flush=True)
+
+
 # --------------------------------------------------------------------------- #
 # CPU baseline: the numpy oracle on a bounded sample of the same workload
 # --------------------------------------------------------------------------- #
@@ -454,6 +506,8 @@ def main():
         return run_swap(args, device)
     elif name == "hbm_copy":
         return run_hbm_copy(args, device)
+    elif name == "swap_sweep":
+        return run_swap_sweep(args, device)
     elif name == "copy_blocks":
         launch, info = setup_copy_blocks(args, device)
         args.graph = min(args.graph, 4)

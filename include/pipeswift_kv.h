@@ -152,14 +152,27 @@ int psk_copy_blocks(void* cache, int64_t num_layers, int64_t layer_stride, int64
  * [0, dst_num_pages) return PSK_E_RANGE before anything is enqueued.
  * PSK_SWAP_BLIT needs `staging`: host memory from psk_host_alloc of at least
  * psk_swap_staging_bytes(num_views, pages) bytes that stays untouched until
- * the enqueued work completes; the other transports ignore it.
- * host pointers must come from psk_host_alloc (mapped pinned memory).
+ * the enqueued work completes, and optionally `desc_dev`, device memory of the
+ * same size: the page tables are then copied there (one async H2D on `stream`)
+ * and read by the kernel from HBM instead of over the host link.  The other
+ * transports ignore both.  Host-tier pointers must come from psk_host_alloc
+ * (mapped pinned memory).
  */
 int psk_swap_blocks(int transport, const uint64_t* src_bases, const uint64_t* dst_bases,
                     const uint64_t* bytes_per_page, int64_t num_views, const int64_t* src_start,
                     const int64_t* dst_start, const int64_t* run_len, int64_t num_runs,
                     int64_t src_num_pages, int64_t dst_num_pages, void* staging,
-                    int64_t staging_bytes, void* stream);
+                    int64_t staging_bytes, void* desc_dev, int64_t desc_dev_bytes, void* stream);
+
+/*
+ * Host-side run coalescing for a page transfer (replaces CopyEngine._coalesce,
+ * copy_engine.py:407-427): pairs (src[i], dst[i]) are ordered by src (stable)
+ * and consecutive pairs whose src and dst both advance by one merge into a run.
+ * Writes the run starts and lengths (arrays of at least n entries) and returns
+ * the number of runs, or a negative status.  Page ids must be non-negative.
+ */
+int64_t psk_coalesce_runs(const int64_t* src, const int64_t* dst, int64_t n, int64_t* run_src,
+                          int64_t* run_dst, int64_t* run_len);
 
 /* Staging bytes PSK_SWAP_BLIT needs for num_views views and num_pages pages. */
 int64_t psk_swap_staging_bytes(int64_t num_views, int64_t num_pages);

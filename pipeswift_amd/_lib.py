@@ -58,9 +58,10 @@ _SIGNATURES = {
     "psk_swap_blocks": (
         _int,
         [_int, _c_uint64_p, _c_uint64_p, _c_uint64_p, _i64, _c_int64_p, _c_int64_p, _c_int64_p, _i64, _i64, _i64,
-         _vp, _i64, _vp],
+         _vp, _i64, _vp, _i64, _vp],
     ),
     "psk_swap_staging_bytes": (_i64, [_i64, _i64]),
+    "psk_coalesce_runs": (_i64, [_c_int64_p, _c_int64_p, _i64, _c_int64_p, _c_int64_p, _c_int64_p]),
     "psk_kv_amax_scale": (
         _int,
         [_vp, _vp, _i64, _i64, _i64, _i64, _int, ctypes.c_float, _vp, _vp, _vp, _i64, _vp],

@@ -131,11 +131,14 @@ class _TransferParams:
         self.dst_limit = dst_limit
         self.max_pages = max_pages
         self.staging = []
+        self.desc_dev = None
         self._slot = 0
 
-    def alloc_staging(self):
+    def alloc_staging(self, device):
         nbytes = int(lib().psk_swap_staging_bytes(self.num_tensors, self.max_pages))
         self.staging = [[_HostBuffer(nbytes), None] for _ in range(_STAGING_SLOTS)]
+        # page tables are copied here before each blit (stream-ordered reuse)
+        self.desc_dev = torch.empty(nbytes, dtype=torch.uint8, device=device)
 
     def next_staging(self):
         """A staging buffer no in-flight transfer still reads."""
@@ -149,6 +152,7 @@ class _TransferParams:
         for buf, _ in self.staging:
             buf.free()
         self.staging = []
+        self.desc_dev = None
 
 
 class CopyHandle:
@@ -181,7 +185,9 @@ class CopyEngine:
     they overlap the forward pass.  Each returns a CopyHandle.
     """
 
-    def __init__(self, gpu_caches, gpu_num_pages, l2_num_pages, transport=None):
+    def __init__(self, gpu_caches, gpu_num_pages, l2_num_pages, transport=None, timing_events=False):
+        """``timing_events`` makes each CopyHandle.event a timing event, so a
+        caller can measure the transfer on the copy stream (benchmarks)."""
         self.closed = False
         self._host_buffers = []
         self.thread = None
@@ -205,10 +211,10 @@ class CopyEngine:
             gpu_views, cpu_views, torch.cuda.Stream(self.device), gpu_num_pages, l2_num_pages, max_pages
         )
         if self._transport_code == _lib.SWAP_BLIT:
-            self.load_params.alloc_staging()
-            self.store_params.alloc_staging()
+            self.load_params.alloc_staging(self.device)
+            self.store_params.alloc_staging(self.device)
         self.thread = threading.Thread(
-            target=self._copy_loop, args=(self.queue, self.device, self._transport_code), daemon=True
+            target=self._copy_loop, args=(self.queue, self.device, self._transport_code, timing_events), daemon=True
         )
         self.thread.start()
 
@@ -321,7 +327,7 @@ class CopyEngine:
                 )
 
     @classmethod
-    def _copy_loop(cls, q, device, transport):
+    def _copy_loop(cls, q, device, transport, timing=False):
         torch.cuda.set_device(device)
         while True:
             item = q.get()
@@ -335,7 +341,7 @@ class CopyEngine:
                         stream.wait_event(wait_event)
                     slot = params.next_staging() if transport == _lib.SWAP_BLIT else None
                     cls._copy_blocks(runs, params, transport, slot)
-                    event = torch.cuda.Event()
+                    event = torch.cuda.Event(enable_timing=timing)
                     event.record(stream)
                     if slot is not None:
                         slot[1] = event
@@ -346,15 +352,21 @@ class CopyEngine:
     @staticmethod
     def _coalesce(src_ids, dst_ids):
         """Merge page pairs that advance together on both tiers into runs
-        (copy_engine.py:407-427).  Returns run starts on both sides and run
-        lengths, in pages."""
-        order = np.argsort(src_ids, kind="stable")
-        src = src_ids[order]
-        dst = dst_ids[order]
-        breaks = (src[1:] != src[:-1] + 1) | (dst[1:] != dst[:-1] + 1)
-        starts = np.flatnonzero(np.concatenate(([True], breaks)))
-        lens = np.diff(np.append(starts, len(src))).astype(np.uint64)
-        return src[starts], dst[starts], lens
+        (copy_engine.py:407-427): order by source (stable), split wherever the
+        source or destination does not step by one.  Native (radix sort in
+        libpipeswift_kv) because the caller waits for it.  Returns run starts
+        on both sides and run lengths, in pages, as uint64 arrays."""
+        src = np.ascontiguousarray(src_ids, dtype=np.int64)
+        dst = np.ascontiguousarray(dst_ids, dtype=np.int64)
+        n = len(src)
+        rs = np.empty(n, dtype=np.int64)
+        rd = np.empty(n, dtype=np.int64)
+        rl = np.empty(n, dtype=np.int64)
+        runs = lib().psk_coalesce_runs(src.ctypes.data_as(_i64p), dst.ctypes.data_as(_i64p), n,
+                                       rs.ctypes.data_as(_i64p), rd.ctypes.data_as(_i64p), rl.ctypes.data_as(_i64p))
+        if runs < 0:
+            check(int(runs), "coalesce page runs")
+        return rs[:runs].astype(np.uint64), rd[:runs].astype(np.uint64), rl[:runs].astype(np.uint64)
 
     @staticmethod
     def _copy_blocks(runs, params, transport, slot=None):
@@ -363,6 +375,8 @@ class CopyEngine:
         if not len(run_len):
             return
         staging, staging_bytes = (slot[0].ptr, slot[0].nbytes) if slot is not None else (None, 0)
+        desc = params.desc_dev
+        desc_ptr, desc_bytes = (desc.data_ptr(), desc.numel()) if (slot is not None and desc is not None) else (None, 0)
         status = lib().psk_swap_blocks(
             transport,
             params.src_bases.ctypes.data_as(_u64p),
@@ -377,6 +391,8 @@ class CopyEngine:
             params.dst_limit,
             staging,
             staging_bytes,
+            desc_ptr,
+            desc_bytes,
             params.stream_handle,
         )
         check(status, "L2 page transfer")

@@ -818,29 +818,36 @@ struct SwapView {
   uint64_t bpb;
 };
 
+// One wave per (page, view) unit, grid-stride over units; each wave moves its
+// page in 64 x B x U byte steps.  Wave granularity keeps small pages (4-16 KiB)
+// from idling most of a workgroup, and the page-id tables are read from device
+// memory (staged there by one H2D copy) rather than over the host link.
 template <int B, int U>
 __global__ void __launch_bounds__(256) blit_pages_kernel(const SwapView* views, const int64_t* src_pages,
                                                          const int64_t* dst_pages, int64_t num_views,
                                                          int64_t num_pages) {
   using V = typename VecT<B>::T;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t waves = int64_t(gridDim.x) * 4;
   const int64_t units = num_views * num_pages;
-  for (int64_t unit = blockIdx.x; unit < units; unit += gridDim.x) {
+  for (int64_t unit = int64_t(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
+       unit < units; unit += waves) {
     const int64_t k = unit / num_views;
     const int64_t vi = unit - k * num_views;
     const SwapView view = views[vi];
     const char* src = reinterpret_cast<const char*>(view.src + uint64_t(src_pages[k]) * view.bpb);
     char* dst = reinterpret_cast<char*>(view.dst + uint64_t(dst_pages[k]) * view.bpb);
     const int64_t nvec = int64_t(view.bpb) / B;
-    for (int64_t base = 0; base < nvec; base += int64_t(blockDim.x) * U) {
+    for (int64_t base = 0; base < nvec; base += kWave * U) {
       V v[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int64_t i = base + int64_t(u) * blockDim.x + threadIdx.x;
+        const int64_t i = base + u * kWave + lane;
         if (i < nvec) v[u] = __builtin_nontemporal_load(reinterpret_cast<const V*>(src) + i);
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int64_t i = base + int64_t(u) * blockDim.x + threadIdx.x;
+        const int64_t i = base + u * kWave + lane;
         if (i < nvec) __builtin_nontemporal_store(v[u], reinterpret_cast<V*>(dst) + i);
       }
     }
@@ -858,6 +865,41 @@ BatchMemcpyFn batch_memcpy_fn() {
     return reinterpret_cast<BatchMemcpyFn>(p);
   }();
   return fn;
+}
+
+// Stable LSD radix sort of indices by non-negative key, 11-bit digits, only as
+// many passes as the largest key needs.  Keys below 2^32 travel packed with
+// their index in one uint64 (key << 32 | index), so every pass is a sequential
+// sweep; larger keys fall back to sorting indices through the key array.
+void radix_order(const int64_t* key, int64_t n, std::vector<uint32_t>& order) {
+  uint64_t maxk = 0;
+  for (int64_t i = 0; i < n; ++i) maxk |= uint64_t(key[i]);
+  order.resize(size_t(n));
+  if (maxk < (uint64_t(1) << 32)) {
+    std::vector<uint64_t> a(static_cast<size_t>(n)), b(static_cast<size_t>(n));
+    for (int64_t i = 0; i < n; ++i) a[size_t(i)] = (uint64_t(key[i]) << 32) | uint64_t(i);
+    for (int shift = 32; shift < 64 && (maxk >> (shift - 32)) != 0; shift += 11) {
+      size_t count[2049] = {0};
+      for (int64_t i = 0; i < n; ++i) ++count[((a[size_t(i)] >> shift) & 2047) + 1];
+      for (int d = 0; d < 2048; ++d) count[d + 1] += count[d];
+      for (int64_t i = 0; i < n; ++i) b[count[(a[size_t(i)] >> shift) & 2047]++] = a[size_t(i)];
+      a.swap(b);
+    }
+    for (int64_t i = 0; i < n; ++i) order[size_t(i)] = uint32_t(a[size_t(i)]);
+    return;
+  }
+  for (int64_t i = 0; i < n; ++i) order[size_t(i)] = uint32_t(i);
+  std::vector<uint32_t> tmp(static_cast<size_t>(n));
+  for (int shift = 0; shift < 64 && (maxk >> shift) != 0; shift += 11) {
+    size_t count[2049] = {0};
+    for (int64_t i = 0; i < n; ++i) ++count[((uint64_t(key[order[size_t(i)]]) >> shift) & 2047) + 1];
+    for (int d = 0; d < 2048; ++d) count[d + 1] += count[d];
+    for (int64_t i = 0; i < n; ++i) {
+      const uint32_t o = order[size_t(i)];
+      tmp[count[(uint64_t(key[o]) >> shift) & 2047]++] = o;
+    }
+    order.swap(tmp);
+  }
 }
 
 int64_t staging_bytes(int64_t num_views, int64_t num_pages) {
@@ -1104,10 +1146,42 @@ int psk_copy_blocks(void* cache, int64_t num_layers, int64_t layer_stride, int64
 
 int64_t psk_swap_staging_bytes(int64_t num_views, int64_t num_pages) { return staging_bytes(num_views, num_pages); }
 
+int64_t psk_coalesce_runs(const int64_t* src, const int64_t* dst, int64_t n, int64_t* run_src, int64_t* run_dst,
+                          int64_t* run_len) {
+  g_err[0] = 0;
+  if (n < 0 || n > int64_t(UINT32_MAX)) return fail(PSK_E_ARG, "page count %lld out of range", (long long)n);
+  if (n == 0) return 0;
+  if (!src || !dst || !run_src || !run_dst || !run_len) return fail(PSK_E_ARG, "NULL array");
+  for (int64_t i = 0; i < n; ++i)
+    if (src[i] < 0 || dst[i] < 0) return fail(PSK_E_RANGE, "negative page id at %lld", (long long)i);
+  std::vector<uint32_t> order;
+  radix_order(src, n, order);
+  int64_t runs = 0;
+  int64_t ps = src[order[0]], pd = dst[order[0]];
+  run_src[0] = ps;
+  run_dst[0] = pd;
+  run_len[0] = 1;
+  for (int64_t i = 1; i < n; ++i) {
+    const int64_t s = src[order[size_t(i)]], d = dst[order[size_t(i)]];
+    if (s == ps + 1 && d == pd + 1) {
+      ++run_len[runs];
+    } else {
+      ++runs;
+      run_src[runs] = s;
+      run_dst[runs] = d;
+      run_len[runs] = 1;
+    }
+    ps = s;
+    pd = d;
+  }
+  return runs + 1;
+}
+
 int psk_swap_blocks(int transport, const uint64_t* src_bases, const uint64_t* dst_bases,
                     const uint64_t* bytes_per_page, int64_t num_views, const int64_t* src_start,
                     const int64_t* dst_start, const int64_t* run_len, int64_t num_runs, int64_t src_num_pages,
-                    int64_t dst_num_pages, void* staging, int64_t staging_bytes_avail, void* stream) {
+                    int64_t dst_num_pages, void* staging, int64_t staging_bytes_avail, void* desc_dev,
+                    int64_t desc_dev_bytes, void* stream) {
   g_err[0] = 0;
   if (num_views < 0 || num_runs < 0) return fail(PSK_E_ARG, "negative view or run count");
   if (num_views == 0 || num_runs == 0) return PSK_OK;
@@ -1187,14 +1261,30 @@ int psk_swap_blocks(int transport, const uint64_t* src_bases, const uint64_t* ds
       sp[k] = src_start[r] + i;
       dp[k] = dst_start[r] + i;
     }
+  // Descriptors go to device memory with one async copy (the staging buffer is
+  // pinned) when a device buffer is given; otherwise the kernel reads them from
+  // the mapped staging buffer directly.
+  const char* desc = base;
+  if (desc_dev) {
+    if (desc_dev_bytes < need) return fail(PSK_E_WORKSPACE, "swap device descriptors need %lld bytes, got %lld",
+                                           (long long)need, (long long)desc_dev_bytes);
+    const size_t used = size_t(reinterpret_cast<char*>(dp + pages) - base);
+    char* dbase = reinterpret_cast<char*>((uintptr_t(desc_dev) + 15) & ~uintptr_t(15));
+    hipError_t e = hipMemcpyAsync(dbase, base, used, hipMemcpyHostToDevice, st);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync (swap descriptors)");
+    desc = dbase;
+  }
+  const SwapView* dviews = reinterpret_cast<const SwapView*>(desc);
+  const int64_t* dsp = reinterpret_cast<const int64_t*>(desc + num_views * int64_t(sizeof(SwapView)));
+  const int64_t* ddp = dsp + pages;
   const int64_t units = num_views * pages;
-  const int64_t grid = units < 4096 ? units : 4096;
+  const int64_t grid = ceil_div(units, 4) < 8192 ? ceil_div(units, 4) : 8192;
   if ((acc & 15) == 0)
-    hipLaunchKernelGGL((blit_pages_kernel<16, 4>), dim3(grid), dim3(256), 0, st, views, sp, dp, num_views, pages);
+    hipLaunchKernelGGL((blit_pages_kernel<16, 4>), dim3(grid), dim3(256), 0, st, dviews, dsp, ddp, num_views, pages);
   else if ((acc & 3) == 0)
-    hipLaunchKernelGGL((blit_pages_kernel<4, 4>), dim3(grid), dim3(256), 0, st, views, sp, dp, num_views, pages);
+    hipLaunchKernelGGL((blit_pages_kernel<4, 4>), dim3(grid), dim3(256), 0, st, dviews, dsp, ddp, num_views, pages);
   else
-    hipLaunchKernelGGL((blit_pages_kernel<1, 4>), dim3(grid), dim3(256), 0, st, views, sp, dp, num_views, pages);
+    hipLaunchKernelGGL((blit_pages_kernel<1, 4>), dim3(grid), dim3(256), 0, st, dviews, dsp, ddp, num_views, pages);
   return check_launch("blit_pages_kernel launch");
 }
 

@@ -57,9 +57,9 @@ def test_swap_range_is_checked_on_the_host():
     s = _lib.i64_array([5])
     d = _lib.i64_array([0])
     n = _lib.i64_array([2])
-    st = lib.psk_swap_blocks(_lib.SWAP_MEMCPY, u, u, b, 1, s, d, n, 1, 6, 10, None, 0, None)
+    st = lib.psk_swap_blocks(_lib.SWAP_MEMCPY, u, u, b, 1, s, d, n, 1, 6, 10, None, 0, None, 0, None)
     assert st == -3 and b"src pages [5, 7)" in lib.psk_last_error()
-    st = lib.psk_swap_blocks(_lib.SWAP_BLIT, u, u, b, 1, d, d, n, 1, 6, 10, None, 0, None)
+    st = lib.psk_swap_blocks(_lib.SWAP_BLIT, u, u, b, 1, d, d, n, 1, 6, 10, None, 0, None, 0, None)
     assert st == -4
     assert lib.psk_swap_staging_bytes(2, 10) >= 2 * 24 + 2 * 10 * 8
 
