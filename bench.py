@@ -27,6 +27,7 @@ Workloads (default fp8_decode_append, config 2 of the benchmark plan):
   swap               8192 scattered blocks x 8 layers (4 GiB) D2H + H2D
   kv_scales          config 2's per-tensor K/V scales (amax kernel)
   swap_sweep         host-link GB/s vs bytes per page, per transport
+  metadata           host us per step of prepare_kv_info (native builder)
   hbm_copy           1 GiB device copy (achievable-bandwidth reference and the
                      PMC calibration run)
 """
@@ -359,6 +360,74 @@ def run_swap(args, device):
     print(json.dumps(line), flush=True)
 
 
+def run_metadata(args, device):
+    """Host time of one step's KV metadata (prepare_kv_info: slot_mapping,
+    page_table, lengths, and their H2D) for config 2 (128 decode sequences,
+    contexts up to 32k) and config 3 (6 sequences, 4096 new tokens), against a
+    per-token Python restatement of the reference's loop (metadata.py:258-295)."""
+    from array import array
+
+    import numpy as np
+    import torch
+
+    from oracle import kv_oracle as O
+    from pipeswift_amd import metadata, workloads
+
+    class Seq:
+        def __init__(self, sid, n, off):
+            self.seq_id, self.token_ids, self.offset = sid, range(n), off
+
+    cases = {}
+    c2 = workloads.config2_fp8_decode()
+    cases["config2_decode"] = ([Seq(b, int(c2.extra["ctx"][b]), int(c2.extra["ctx"][b]) - 1) for b in range(128)],
+                               {b: array("i", c2.extra["tables"][b].tolist()) for b in range(128)}, True)
+    c3 = workloads.config3_chunked()
+    cases["config3_chunked"] = ([Seq(b, int(c3.prefix[b] + c3.chunk[b]), int(c3.prefix[b])) for b in range(6)],
+                                {b: array("i", c3.block_table[b, : int((c3.prefix[b] + c3.chunk[b] + 15) // 16)]
+                                          .tolist()) for b in range(6)}, False)
+
+    def reference_style(seqs, table, ps):
+        slot, rows = [], []
+        width = max(len(table[s.seq_id]) for s in seqs)
+        for s in seqs:
+            row = list(table[s.seq_id])
+            rows.append(row + [0] * (width - len(row)))
+            slot.extend(O.slot_mapping(row, s.offset, len(s.token_ids), ps))
+        pt = torch.from_numpy(np.array(rows, dtype=np.int32)).to(device, non_blocking=True)
+        sm = torch.from_numpy(np.array(slot, dtype=np.int64)).to(device, non_blocking=True)
+        return pt, sm
+
+    out = {}
+    for name, (seqs, table, dec) in cases.items():
+        for _ in range(5):
+            info = metadata.prepare_kv_info(seqs, table, 16, None, None, is_decode=dec, device=device)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        reps = 200
+        for _ in range(reps):
+            info = metadata.prepare_kv_info(seqs, table, 16, None, None, is_decode=dec, device=device)
+        t_ours = (time.perf_counter() - t0) / reps
+        torch.cuda.synchronize()
+        ref_pt, ref_sm = reference_style(seqs, table, 16)
+        torch.cuda.synchronize()
+        assert torch.equal(ref_sm, info.slot_mapping) and torch.equal(ref_pt, info.page_table)
+        t0 = time.perf_counter()
+        rreps = 5
+        for _ in range(rreps):
+            reference_style(seqs, table, 16)
+        t_ref = (time.perf_counter() - t0) / rreps
+        out[name] = {"tokens": int(info.slot_mapping.numel()), "pages_wide": int(info.page_table.shape[1]),
+                     "ours_us": round(t_ours * 1e6, 1), "reference_style_python_us": round(t_ref * 1e6, 1)}
+        print(json.dumps({name: out[name]}), file=sys.stderr, flush=True)
+    line = {"metric": "host us per step for KV metadata (slot_mapping + page_table + H2D)",
+            "value": out["config3_chunked"]["ours_us"], "unit": "us", "n_gpus": 1, "higher_is_better": False,
+            "vs_baseline": None, "dtype": "int64", "data": "synthetic (seeded)",
+            "config": {"workload": "metadata", "cases": out}, "roofline": None,
+            "cpu_baseline": {"value": out["config3_chunked"]["reference_style_python_us"], "unit": "us", "cores": 1,
+                             "kind": "port", "sample": "per-token Python loop restating metadata.py:258-295"}}
+    print(json.dumps(line), flush=True)
+
+
 def run_swap_sweep(args, device):
     """Host-link GB/s against bytes per page at a fixed 256 MiB per transfer,
     scattered pages (every page its own run), both directions, per transport:
@@ -508,6 +577,8 @@ def main():
         return run_hbm_copy(args, device)
     elif name == "swap_sweep":
         return run_swap_sweep(args, device)
+    elif name == "metadata":
+        return run_metadata(args, device)
     elif name == "copy_blocks":
         launch, info = setup_copy_blocks(args, device)
         args.graph = min(args.graph, 4)

@@ -196,6 +196,30 @@ int psk_kv_amax_scale(const void* x0, const void* x1, int64_t rows, int64_t row_
 int64_t psk_kv_amax_workspace_len(void);
 
 /*
+ * Host-side step metadata (replaces the per-token Python loop of
+ * prepare_kv_info, pipeswift/utils/metadata.py:206-348).  For sequence i with
+ * page ids page_table_ptrs[i][0 .. page_table_lens[i]) (int32, host memory),
+ * num_tokens[i] tokens of which offsets[i] are already cached:
+ *   page_table_out[i, :]   the page ids, zero-padded to row_width
+ *   lens_q_out[i]          num_tokens - offset;  cu_seqlens_q_out prefix sums
+ *   lens_kv_out[i]         num_tokens (dcp_deg == 1) or the tokens of the
+ *                          rank's share of the prefix (DCP, metadata.py:246-255)
+ *   slot_mapping_out       for each new position p:
+ *                          page[p / ps] * ps + p % ps (dcp_deg == 1), or with
+ *                          DCP the rank-local slot, -1 for foreign tokens
+ *                          (metadata.py:282-295)
+ * Returns the token count written, or a negative status (a position with no
+ * page returns PSK_E_RANGE, where the reference raises IndexError).
+ */
+int64_t psk_build_kv_metadata(int64_t num_seqs, const uint64_t* page_table_ptrs,
+                              const int64_t* page_table_lens, const int64_t* num_tokens,
+                              const int64_t* offsets, int64_t page_size, int64_t dcp_deg,
+                              int64_t dcp_rank, int64_t dcp_interleave, int is_decode,
+                              int64_t row_width, int32_t* page_table_out, int32_t* cu_seqlens_q_out,
+                              int32_t* lens_q_out, int32_t* lens_kv_out, int64_t* slot_mapping_out,
+                              int64_t slot_capacity);
+
+/*
  * Pinned, device-mapped host memory for the L2 mirror and swap staging
  * (hipHostMalloc).  Allocation happens at set-up, never on the hot path.
  */

@@ -1288,6 +1288,69 @@ int psk_swap_blocks(int transport, const uint64_t* src_bases, const uint64_t* ds
   return check_launch("blit_pages_kernel launch");
 }
 
+int64_t psk_build_kv_metadata(int64_t num_seqs, const uint64_t* page_table_ptrs, const int64_t* page_table_lens,
+                              const int64_t* num_tokens, const int64_t* offsets, int64_t page_size, int64_t dcp_deg,
+                              int64_t dcp_rank, int64_t dcp_interleave, int is_decode, int64_t row_width,
+                              int32_t* page_table_out, int32_t* cu_seqlens_q_out, int32_t* lens_q_out,
+                              int32_t* lens_kv_out, int64_t* slot_mapping_out, int64_t slot_capacity) {
+  g_err[0] = 0;
+  if (num_seqs < 0 || page_size <= 0 || dcp_deg <= 0 || dcp_rank < 0 || dcp_rank >= dcp_deg || dcp_interleave <= 0 ||
+      row_width < 0 || slot_capacity < 0)
+    return fail(PSK_E_ARG, "bad metadata geometry (seqs=%lld page_size=%lld dcp=%lld/%lld interleave=%lld)",
+                (long long)num_seqs, (long long)page_size, (long long)dcp_rank, (long long)dcp_deg,
+                (long long)dcp_interleave);
+  if (dcp_deg > 1 && page_size % dcp_deg) return fail(PSK_E_ARG, "page_size must divide by the DCP degree");
+  if (num_seqs && (!page_table_ptrs || !page_table_lens || !num_tokens || !offsets || !cu_seqlens_q_out ||
+                   !lens_q_out || !lens_kv_out || (row_width && !page_table_out)))
+    return fail(PSK_E_ARG, "NULL array");
+  const int64_t phys = dcp_deg == 1 ? page_size : page_size / dcp_deg;
+  const int64_t stride = dcp_interleave * dcp_deg;
+  int64_t total = 0;
+  cu_seqlens_q_out[0] = 0;
+  for (int64_t i = 0; i < num_seqs; ++i) {
+    const int64_t n = num_tokens[i], off = offsets[i], pages = page_table_lens[i];
+    if (off < 0 || off > n) return fail(PSK_E_ARG, "sequence %lld: offset %lld outside [0, %lld]", (long long)i,
+                                        (long long)off, (long long)n);
+    if (pages > row_width) return fail(PSK_E_ARG, "sequence %lld has %lld pages, row width %lld", (long long)i,
+                                       (long long)pages, (long long)row_width);
+    if (n > 0 && (n - 1) / page_size >= pages)
+      return fail(PSK_E_RANGE, "sequence %lld: position %lld needs page %lld of %lld", (long long)i,
+                  (long long)(n - 1), (long long)((n - 1) / page_size), (long long)pages);
+    const int64_t q = n - off;
+    if (total + q > slot_capacity) return fail(PSK_E_WORKSPACE, "slot_mapping capacity %lld exceeded",
+                                               (long long)slot_capacity);
+    const int32_t* pt = reinterpret_cast<const int32_t*>(uintptr_t(page_table_ptrs[i]));
+    int32_t* row = page_table_out + i * row_width;
+    for (int64_t j = 0; j < pages; ++j) row[j] = pt[j];
+    for (int64_t j = pages; j < row_width; ++j) row[j] = 0;
+    lens_q_out[i] = int32_t(q);
+    if (dcp_deg == 1) {
+      lens_kv_out[i] = int32_t(n);
+      int64_t* out = slot_mapping_out + total;
+      for (int64_t pos = off; pos < n; ++pos) *out++ = int64_t(pt[pos / page_size]) * page_size + pos % page_size;
+    } else {
+      const int64_t prefix = (is_decode && q == 1) ? n : off;
+      int64_t kv = prefix / stride * dcp_interleave;
+      const int64_t rem = prefix % stride;
+      if (rem >= (dcp_rank + 1) * dcp_interleave) kv += dcp_interleave;
+      else if (rem >= dcp_rank * dcp_interleave) kv += rem % dcp_interleave;
+      lens_kv_out[i] = int32_t(kv);
+      int64_t* out = slot_mapping_out + total;
+      for (int64_t pos = off; pos < n; ++pos) {
+        if ((pos / dcp_interleave) % dcp_deg == dcp_rank) {
+          const int64_t local = pos % dcp_interleave + pos / stride * dcp_interleave;
+          *out++ = int64_t(pt[pos / page_size]) * phys + local % phys;
+        } else {
+          *out++ = -1;
+        }
+      }
+    }
+    total += q;
+    cu_seqlens_q_out[i + 1] = int32_t(total);
+  }
+  return total;
+}
+
 int64_t psk_kv_amax_workspace_len(void) { return kAmaxWsLen; }
 
 int psk_kv_amax_scale(const void* x0, const void* x1, int64_t rows, int64_t row_len, int64_t row_stride0,

@@ -43,6 +43,23 @@ def test_prepare_kv_info_matches_oracle(dcp, il):
         assert info.actual_lens_kv.tolist() == kv
 
 
+def test_prepare_kv_info_page_table_containers_and_errors():
+    from array import array
+
+    ps = 16
+    seqs = [Seq(1, 40, 0), Seq(2, 20, 19), Seq(3, 33, 32)]
+    rows = {1: [7, 3, 9], 2: [4, 8], 3: [1, 2, 5]}
+    exp = np.concatenate([O.slot_mapping(rows[s.seq_id], s.offset, len(s.token_ids), ps) for s in seqs])
+    for make in (lambda r: array("i", r), list, lambda r: np.array(r, np.int64), lambda r: torch.tensor(r)):
+        info = metadata.prepare_kv_info(seqs, {k: make(v) for k, v in rows.items()}, ps, None, None, device="cpu")
+        assert np.array_equal(info.slot_mapping.numpy(), exp)
+        assert info.page_table.tolist() == [[7, 3, 9], [4, 8, 0], [1, 2, 5]]
+    with pytest.raises(IndexError, match="needs page 2 of 2"):
+        metadata.prepare_kv_info([Seq(2, 33, 30)], rows, ps, None, None, device="cpu")
+    empty = metadata.prepare_kv_info([Seq(2, 20, 20)], rows, ps, None, None, device="cpu")
+    assert empty.slot_mapping.numel() == 0 and empty.actual_lens_q.tolist() == [0]
+
+
 def test_next_decode_step_metadata():
     ps = 16
     seqs = [Seq(0, 40, 39), Seq(1, 16, 15)]
