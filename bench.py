@@ -428,6 +428,132 @@ def run_metadata(args, device):
     print(json.dumps(line), flush=True)
 
 
+def run_l2_cycle(args, device):
+    """BlockManager's L2 path at config 5b scale: a 8192-page prompt (L=8 layers
+    of [2, 16, 8, 128] bf16, 512 KiB per page, 4 GiB) is stored to L2, evicted
+    from HBM, and restored by a second prompt with the same tokens, on pages
+    drawn from seeded shuffles of both free lists (a churned pool, the case the
+    deadline is priced for, block_manager.py:646-655).  Reports wall time and
+    GB/s of each direction, the deadline the calibrated model set against the
+    time the transfer took, host time of the ledger calls, and the restored
+    bytes' check.  cpu_baseline: the reference's per-page xxhash loop over the
+    same prompt (block_manager.py:678-693) against the native key chain."""
+    from array import array
+    from collections import deque
+
+    import numpy as np
+    import torch
+
+    from oracle import block_ledger as OB
+    from pipeswift_amd.block_manager import BlockManager
+
+    class Seq:
+        def __init__(self, sid, toks):
+            self.seq_id, self.token_ids, self.offset = sid, array("i", toks), 0
+            self.finished, self.l2_load_pending, self.page_hashes, self.l2_probe_resume = False, False, None, None
+
+    L, ps, n = 8, 16, 8192
+    P = n + 2
+    cache = torch.zeros((L, P, 2, ps, 8, 128), dtype=torch.bfloat16, device=device)
+    page_bytes = L * 2 * ps * 8 * 128 * 2
+    t0 = time.perf_counter()
+    m = BlockManager(P, ps, [cache[:, :, 0], cache[:, :, 1]], None, kv_cache_tensor=cache,
+                     l2_cache_gb=n * page_bytes / 1024**3)
+    t_init = time.perf_counter() - t0
+    rng = np.random.default_rng(1005)
+    m.free_page_queue = deque(int(x) for x in rng.permutation(np.arange(1, P)))
+    m.l2_pool.free_page_queue = deque(int(x) for x in rng.permutation(n))
+    prompt = rng.integers(0, 150000, n * ps + 1).tolist()
+    a = Seq(1, prompt)
+    t0 = time.perf_counter()
+    m.allocate_prefill(a)
+    t_alloc = time.perf_counter() - t0
+    table_a = torch.tensor(list(m.kv_page_table[1])[:n], dtype=torch.int64, device=device)
+    flat = cache.view(torch.int16)
+    for l in range(L):  # page j of the prompt holds the value j + l everywhere
+        for j0 in range(0, n, 512):
+            idx = table_a[j0:j0 + 512]
+            v = (torch.arange(j0, j0 + len(idx), device=device, dtype=torch.int16) + l).view(-1, 1, 1, 1, 1)
+            flat[l].index_copy_(0, idx, v.expand(len(idx), 2, ps, 8, 128).contiguous())
+    torch.cuda.synchronize()
+    res = {"init_s (incl. calibrate)": round(t_init, 3), "cost_model": m.l2_cost_model, "views": m.l2_views,
+           "page_bytes": page_bytes, "pages": n}
+
+    m.poll_l2_events(0)
+    t0 = time.perf_counter()
+    m.schedule_l2_stores_for_confirmed_seq(a)
+    t_sched = time.perf_counter() - t0
+    st = m.pending_l2_stores[-1]
+    st["copy"].wait()
+    t_store = time.perf_counter() - t0
+    owed_store = m._l2_owed_s["store"] - 1 * m.l2_step_ms / 1000
+    res["store"] = {"GB/s": n * page_bytes / t_store / 1e9, "wall_ms": 1e3 * t_store,
+                    "host_schedule_ms": 1e3 * t_sched, "runs": st["copy"].num_runs,
+                    "predicted_ms": 1e3 * owed_store, "due_step": st["due_step"]}
+    m.poll_l2_events(st["due_step"])
+    m.deallocate(a)
+    filler = Seq(2, [7] * (ps * (P - 1)))
+    m.allocate_prefill(filler)
+    m.deallocate(filler)
+
+    b = Seq(3, prompt)
+    step = m.l2_step
+    t0 = time.perf_counter()
+    m.allocate_prefill(b)
+    t_alloc_b = time.perf_counter() - t0
+    m.flush_l2_loads()
+    t_flush = time.perf_counter() - t0
+    groups = list(m.pending_l2_loads)
+    for g in groups:
+        g["copy"].wait()
+    t_load = time.perf_counter() - t0
+    owed_load = m._l2_owed_s["load"] - step * m.l2_step_ms / 1000
+    m.poll_l2_events(groups[-1]["due_step"])
+    assert not b.l2_load_pending and b.offset == n * ps
+    table_b = torch.tensor(list(m.kv_page_table[3])[:n], dtype=torch.int64, device=device)
+    ok = True
+    for l in range(L):
+        for j0 in range(0, n, 512):
+            got = flat[l].index_select(0, table_b[j0:j0 + 512])
+            want = (torch.arange(j0, j0 + got.shape[0], device=device, dtype=torch.int16) + l).view(-1, 1, 1, 1, 1)
+            ok = ok and bool((got == want).all())
+    assert ok, "restored pages differ"
+    res["restore"] = {"GB/s": n * page_bytes / t_load / 1e9, "wall_ms": 1e3 * t_load,
+                      "host_allocate_prefill_ms": 1e3 * t_alloc_b, "host_flush_ms": 1e3 * (t_flush - t_alloc_b),
+                      "transfers": len(groups), "runs": sum(g["copy"].num_runs for g in groups),
+                      "predicted_ms": 1e3 * owed_load, "last_due_step": groups[-1]["due_step"] - step}
+    res["bytes_checked"] = True
+
+    # host cost of keying the prompt: native chain against the reference's loop
+    reps = 20
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        m._prompt_page_hashes(Seq(9, prompt))
+    t_native = (time.perf_counter() - t0) / reps
+    oracle_ledger = OB.RefLedger(4, ps)
+    t0 = time.perf_counter()
+    ref_keys = oracle_ledger.prompt_pages(Seq(9, prompt))
+    t_ref = time.perf_counter() - t0
+    assert [h for h, _ in ref_keys] == [h for h, _ in m._prompt_page_hashes(Seq(9, prompt))]
+    res["prompt_keys_ms"] = {"native": 1e3 * t_native, "reference_loop": 1e3 * t_ref, "first_prefill_ms": 1e3 * t_alloc}
+    print(json.dumps(res), file=sys.stderr, flush=True)
+    stg, ldg = res["store"]["GB/s"], res["restore"]["GB/s"]
+    value = 2.0 / (1.0 / stg + 1.0 / ldg)
+    line = {
+        "metric": "L2 offload+restore GB/s through BlockManager (4 GiB each way, 8192 scattered pages)",
+        "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": 1, "warmup": 0,
+        "ms_per_step": res["store"]["wall_ms"] + res["restore"]["wall_ms"], "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bytes", "data": "synthetic (seeded)",
+        "config": {"workload": "l2_cycle (config 5b through BlockManager)", "results": res},
+        "roofline": {"bound": "pcie", "achieved": round(value, 2), "peak": 64.0, "unit": "GB/s",
+                     "frac": round(value / 64.0, 4), "traffic": None},
+        "cpu_baseline": {"value": round(1e3 * t_ref, 2), "unit": "ms to key the 8192-page prompt", "cores": 1,
+                         "kind": "port", "sample": "per-page xxhash loop of block_manager.py:678-693 (oracle)"},
+    }
+    m.l2_copy_engine.close()
+    print(json.dumps(line), flush=True)
+
+
 def run_swap_sweep(args, device):
     """Host-link GB/s against bytes per page at a fixed 256 MiB per transfer,
     scattered pages (every page its own run), both directions, per transport:
@@ -579,6 +705,8 @@ def main():
         return run_swap_sweep(args, device)
     elif name == "metadata":
         return run_metadata(args, device)
+    elif name == "l2_cycle":
+        return run_l2_cycle(args, device)
     elif name == "copy_blocks":
         launch, info = setup_copy_blocks(args, device)
         args.graph = min(args.graph, 4)

@@ -22,6 +22,9 @@
  *   psk_reshape_and_cache     pipeswift/utils/triton_kernels/reshape_and_cache.py:11-135
  *   psk_concat_and_cache_mla  pipeswift/utils/triton_kernels/reshape_and_cache.py:138-229
  *   psk_swap_blocks           pipeswift/utils/copy_engine.py:429-457 (cuMemcpyBatchAsync)
+ *   psk_build_kv_metadata     pipeswift/utils/metadata.py:206-348 (per-token Python loop)
+ *   psk_page_hash_chain,      pipeswift/engine/block_manager.py:220-227, 678-693
+ *   psk_keyed_hash            (xxhash.xxh64 per page; host functions)
  * and build-defined operations that have no reference implementation:
  *   psk_gather_cache          page-table reads done inside attention kernels in the
  *                             reference (pipeswift/llms/layers/attention.py:189-211)
@@ -225,6 +228,26 @@ int64_t psk_build_kv_metadata(int64_t num_seqs, const uint64_t* page_table_ptrs,
  */
 int psk_host_alloc(int64_t bytes, void** ptr);
 int psk_host_free(void* ptr);
+
+/*
+ * Prefix-cache page keys (replaces BlockManager.compute_hash and the per-page
+ * loop of _prompt_page_hashes, pipeswift/engine/block_manager.py:221-227 and
+ * :671-689, which call the xxhash package once per page).  Host code.
+ *
+ * psk_keyed_hash: *key_out = XXH64 (seed 0) of le64(prefix) followed by the
+ * `nbytes` bytes at `data`, or of those bytes alone when has_prefix is 0.
+ *
+ * psk_page_hash_chain: for each full page i of `num_tokens` tokens of
+ * `elem_bytes` bytes, keys_out[i] = psk_keyed_hash(page i, keys_out[i-1]),
+ * with the caller's (prefix, has_prefix) standing in for keys_out[-1].
+ * Returns the number of keys written (num_tokens / page_size), or a negative
+ * status (PSK_E_WORKSPACE when keys_capacity is smaller than that).
+ */
+int psk_keyed_hash(const void* data, int64_t nbytes, uint64_t prefix, int has_prefix,
+                   uint64_t* key_out);
+int64_t psk_page_hash_chain(const void* tokens, int64_t num_tokens, int64_t elem_bytes,
+                            int64_t page_size, uint64_t prefix, int has_prefix,
+                            uint64_t* keys_out, int64_t keys_capacity);
 
 #ifdef __cplusplus
 }

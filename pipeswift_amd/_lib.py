@@ -73,6 +73,8 @@ _SIGNATURES = {
     ),
     "psk_host_alloc": (_int, [_i64, ctypes.POINTER(ctypes.c_void_p)]),
     "psk_host_free": (_int, [_vp]),
+    "psk_keyed_hash": (_int, [_vp, _i64, ctypes.c_uint64, _int, _vp]),
+    "psk_page_hash_chain": (_i64, [_vp, _i64, _i64, _i64, ctypes.c_uint64, _int, _vp, _i64]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)

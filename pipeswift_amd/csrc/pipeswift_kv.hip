@@ -906,6 +906,76 @@ int64_t staging_bytes(int64_t num_views, int64_t num_pages) {
   return num_views * int64_t(sizeof(SwapView)) + 2 * num_pages * int64_t(sizeof(int64_t)) + 64;
 }
 
+// ----------------------------------------------------------------------------
+// XXH64 (Yann Collet's published xxHash64 specification, seed 0), host code.
+// The prefix cache keys every full page by the digest of the previous page's
+// key (8 bytes, little endian) followed by the page's token bytes.
+// ----------------------------------------------------------------------------
+
+constexpr uint64_t kXP1 = 0x9E3779B185EBCA87ull;
+constexpr uint64_t kXP2 = 0xC2B2AE3D27D4EB4Full;
+constexpr uint64_t kXP3 = 0x165667B19E3779F9ull;
+constexpr uint64_t kXP4 = 0x85EBCA77C2B2AE63ull;
+constexpr uint64_t kXP5 = 0x27D4EB2F165667C5ull;
+
+inline uint64_t rotl64(uint64_t x, int r) { return (x << r) | (x >> (64 - r)); }
+
+inline uint64_t load_le64(const uint8_t* p) {
+  uint64_t v;
+  memcpy(&v, p, 8);
+  return v;
+}
+
+inline uint64_t load_le32(const uint8_t* p) {
+  uint32_t v;
+  memcpy(&v, p, 4);
+  return v;
+}
+
+inline uint64_t xxh_lane(uint64_t acc, uint64_t lane) { return rotl64(acc + lane * kXP2, 31) * kXP1; }
+
+inline uint64_t xxh_fold(uint64_t h, uint64_t acc) { return (h ^ xxh_lane(0, acc)) * kXP1 + kXP4; }
+
+uint64_t xxh64(const uint8_t* p, size_t n) {
+  const uint8_t* const end = p + n;
+  uint64_t h;
+  if (n >= 32) {
+    uint64_t a0 = kXP1 + kXP2, a1 = kXP2, a2 = 0, a3 = uint64_t(0) - kXP1;
+    for (; end - p >= 32; p += 32) {
+      a0 = xxh_lane(a0, load_le64(p));
+      a1 = xxh_lane(a1, load_le64(p + 8));
+      a2 = xxh_lane(a2, load_le64(p + 16));
+      a3 = xxh_lane(a3, load_le64(p + 24));
+    }
+    h = rotl64(a0, 1) + rotl64(a1, 7) + rotl64(a2, 12) + rotl64(a3, 18);
+    h = xxh_fold(xxh_fold(xxh_fold(xxh_fold(h, a0), a1), a2), a3);
+  } else {
+    h = kXP5;
+  }
+  h += uint64_t(n);
+  for (; end - p >= 8; p += 8) h = rotl64(h ^ xxh_lane(0, load_le64(p)), 27) * kXP1 + kXP4;
+  if (end - p >= 4) {
+    h = rotl64(h ^ (load_le32(p) * kXP1), 23) * kXP2 + kXP3;
+    p += 4;
+  }
+  for (; p < end; ++p) h = rotl64(h ^ (uint64_t(*p) * kXP5), 11) * kXP1;
+  h ^= h >> 33;
+  h *= kXP2;
+  h ^= h >> 29;
+  h *= kXP3;
+  h ^= h >> 32;
+  return h;
+}
+
+// XXH64 of le64(prefix) || data[0, nbytes), or of the data alone without a prefix.
+// `buf` holds 8 + nbytes bytes of room.
+uint64_t keyed_digest(const uint8_t* data, size_t nbytes, uint64_t prefix, bool has_prefix, uint8_t* buf) {
+  if (!has_prefix) return xxh64(data, nbytes);
+  memcpy(buf, &prefix, 8);  // the host is little endian (x86-64)
+  memcpy(buf + 8, data, nbytes);
+  return xxh64(buf, nbytes + 8);
+}
+
 }  // namespace
 
 // ============================================================================
@@ -1443,6 +1513,36 @@ int psk_host_free(void* ptr) {
   if (!ptr) return PSK_OK;
   hipError_t e = hipHostFree(ptr);
   return e == hipSuccess ? PSK_OK : hip_fail(e, "hipHostFree");
+}
+
+int psk_keyed_hash(const void* data, int64_t nbytes, uint64_t prefix, int has_prefix, uint64_t* key_out) {
+  g_err[0] = 0;
+  if (nbytes < 0 || (nbytes && !data) || !key_out) return fail(PSK_E_ARG, "bad hash input (%lld bytes)", (long long)nbytes);
+  std::vector<uint8_t> buf(has_prefix ? size_t(nbytes) + 8 : 0);
+  *key_out = keyed_digest(static_cast<const uint8_t*>(data), size_t(nbytes), prefix, has_prefix != 0, buf.data());
+  return PSK_OK;
+}
+
+int64_t psk_page_hash_chain(const void* tokens, int64_t num_tokens, int64_t elem_bytes, int64_t page_size,
+                            uint64_t prefix, int has_prefix, uint64_t* keys_out, int64_t keys_capacity) {
+  g_err[0] = 0;
+  if (num_tokens < 0 || elem_bytes <= 0 || page_size <= 0 || (num_tokens && !tokens))
+    return fail(PSK_E_ARG, "bad page-hash geometry (tokens=%lld elem_bytes=%lld page_size=%lld)",
+                (long long)num_tokens, (long long)elem_bytes, (long long)page_size);
+  const int64_t pages = num_tokens / page_size;
+  if (pages > keys_capacity || (pages && !keys_out))
+    return fail(PSK_E_WORKSPACE, "%lld page keys do not fit %lld", (long long)pages, (long long)keys_capacity);
+  const size_t page_bytes = size_t(page_size) * size_t(elem_bytes);
+  std::vector<uint8_t> buf(page_bytes + 8);
+  const uint8_t* src = static_cast<const uint8_t*>(tokens);
+  uint64_t key = prefix;
+  bool chained = has_prefix != 0;
+  for (int64_t i = 0; i < pages; ++i, src += page_bytes) {
+    key = keyed_digest(src, page_bytes, key, chained, buf.data());
+    keys_out[i] = key;
+    chained = true;
+  }
+  return pages;
 }
 
 }  // extern "C"
