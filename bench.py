@@ -127,6 +127,56 @@ def setup_append(args, device, fp8):
     return launch, info
 
 
+def setup_decode_attention(args, device):
+    """One decode step of paged attention over config 2's FP8 cache: 128
+    sequences with log-uniform 128-32768 token contexts in the
+    [65536, 16, 8, 128] E4M3FN cache, 32 query heads (4 per kv head), per-tensor
+    K/V descales.  Algorithmic bytes: every context token's K and V rows of
+    every kv head, the page ids, the bf16 query and the bf16 output."""
+    import torch
+
+    from pipeswift_amd import attention, workloads
+
+    case = workloads.config2_fp8_decode()
+    ctx, tables = case.extra["ctx"], case.extra["tables"]
+    B, H, D, Hq, ps = 128, 8, 128, 32, 16
+    cache = case.cache.to(device)
+    dgen = torch.Generator(device=device).manual_seed(77)
+    for p0 in range(0, cache.shape[0], 4096):  # random FP8 contents, 4096 pages at a time
+        blk = cache[p0: p0 + 4096]
+        blk.copy_((torch.randn(blk.shape, device=device, generator=dgen) * 2.0).to(torch.float8_e4m3fn))
+    W = max(len(t) for t in tables)
+    bt = torch.zeros(B, W, dtype=torch.int32)
+    for b in range(B):
+        bt[b, : len(tables[b])] = tables[b].to(torch.int32)
+    bt = bt.to(device)
+    lens = ctx.to(torch.int32).to(device)
+    R = min(args.rotate, 64)
+    q = (torch.randn(R, B, Hq, D, device=device, generator=dgen) * 2.0).to(torch.bfloat16)
+    scales = torch.tensor([0.01, 0.02], dtype=torch.float32, device=device)
+    out = torch.empty(B, Hq, D, dtype=torch.bfloat16, device=device)
+    ws = torch.empty(attention.workspace_floats(B, Hq, H, W * ps), dtype=torch.float32, device=device)
+    kc, vc = cache[:, 0], cache[:, 1]
+
+    def launch(i):
+        attention.paged_decode_attention(q[i], kc, vc, bt, lens, D ** -0.5, None, scales[0:1], scales[1:2], out=out,
+                                         workspace=ws)
+
+    total = int(ctx.sum())
+    pages = int(sum(len(t) for t in tables))
+    nbytes = total * H * D * 2 + pages * 4 + 2 * B * Hq * D * 2
+    info = {
+        "name": "decode_attention", "kernel": "decode_partial_kernel", "bytes": nbytes, "tokens": B,
+        "dtype": "fp8_e4m3fn",
+        "rotate": R,
+        "config": {"workload": "FP8 paged decode attention (config 2 cache)", "sequences": B, "context_tokens": total,
+                   "kv_heads": H, "q_heads": Hq, "head_dim": D, "block_size": ps, "num_blocks": cache.shape[0],
+                   "split_tokens": "512 (64 splits at 32768)", "descales": "per-tensor K/V"},
+        "cpu": lambda: cpu_decode_attention(kc, vc, bt, ctx, q[0], scales, total * H * D * 2),
+    }
+    return launch, info
+
+
 def setup_kv_scales(args, device):
     """Per-tensor FP8 scales of config 2's K and V (amax / 448), one launch."""
     import torch
@@ -622,6 +672,34 @@ def _raw(t):
     return t.numpy()
 
 
+def cpu_decode_attention(kc, vc, bt, ctx, q, scales, kv_bytes, budget_s=10.0):
+    """The float64 numpy oracle over the first sequences of the batch until the
+    budget is spent; returns (fraction of one launch's K/V bytes processed,
+    seconds, sample)."""
+    import numpy as np
+
+    from oracle import kv_oracle as O
+
+    ks, vs = (float(x) for x in scales.cpu())
+    t0 = time.perf_counter()
+    done = 0
+    nbytes = 0
+    H, D = kc.shape[2], kc.shape[3]
+    while time.perf_counter() - t0 < budget_s and done < len(ctx):
+        n = int(ctx[done])
+        w = (n + 15) // 16
+        pages = bt[done, :w].long()
+        k = _raw(kc[pages].cpu())
+        v = _raw(vc[pages].cpu())
+        O.paged_decode_attention(_raw(q[done: done + 1].cpu()), "bf16", k, v,
+                                 np.arange(w, dtype=np.int32)[None], [n], D ** -0.5, None,
+                                 np.full((1, H), ks, np.float32), np.full((1, H), vs, np.float32))
+        nbytes += n * H * D * 2
+        done += 1
+    el = time.perf_counter() - t0
+    return nbytes / kv_bytes, el, f"float64 numpy oracle over the first {done} of 128 sequences"
+
+
 def cpu_append(case, fp8, budget_s=10.0):
     import numpy as np
 
@@ -693,6 +771,8 @@ def main():
         launch, info = setup_append(args, device, fp8=name.startswith("fp8"))
     elif name == "kv_scales":
         launch, info = setup_kv_scales(args, device)
+    elif name == "decode_attention":
+        launch, info = setup_decode_attention(args, device)
     elif name in ("chunked_append", "gather"):
         launch, info = setup_chunked(args, device, gather=name == "gather")
     elif name in ("mla_prefill", "mla_decode"):

@@ -223,6 +223,45 @@ int64_t psk_build_kv_metadata(int64_t num_seqs, const uint64_t* page_table_ptrs,
                               int64_t slot_capacity);
 
 /*
+ * Paged decode attention over an FP8 E4M3FN KV cache (replaces the reader the
+ * reference calls through vLLM's FA3 fork, pipeswift/llms/layers/attention.py:
+ * 148-187, which takes an FP8 query and per-(sequence, kv head) descales).
+ * One query token per sequence.  For sequence b, query head hq = h*G + g
+ * (G = num_q_heads / num_kv_heads <= 8) and tokens j < seq_lens[b]:
+ *   q~  = e4m3(q[b,hq] / qd)   (q_dtype FP8: q as is)
+ *   s_j = softmax_scale * qd * kd * (q~ . K[j,h])
+ *   out[b,hq] = vd * sum_j softmax(s)_j V[j,h],   lse[hq,b] = log sum_j exp(s_j)
+ * qd/kd/vd = descale[b * stride_b + h * stride_h] (descale_strides holds the
+ * (b, h) strides of q, k, v in that order; a NULL descale is 1.0).
+ * q: [B, Hq, 128] at element strides (q_tok_stride, q_head_stride).
+ * k_cache, v_cache: FP8 [num_blocks, block_size, Hkv, 128]; *_strides are the
+ * (block, row, head) strides in bytes, every one and both bases 16-byte aligned.
+ * Token j of sequence b is row j % block_size of page
+ * block_table[b * block_table_stride + j / block_size]; entries past
+ * block_table_width or outside [0, num_blocks) read as zero rows.
+ * max_seq_len bounds every seq_lens[b] (block_table_width * block_size does).
+ * out: bf16 or f32 at element strides (out_tok_stride, out_head_stride); lse
+ * (fp32, optional) at lse[hq * lse_head_stride + b]; a sequence of length 0
+ * writes zeros and lse = -inf.  workspace: device floats, at least
+ * psk_paged_decode_workspace_len(); no initial contents needed.  Two launches.
+ */
+int psk_paged_decode_attention(const void* q, int64_t q_tok_stride, int64_t q_head_stride, int q_dtype,
+                               const void* k_cache, const void* v_cache, const int64_t* k_strides,
+                               const int64_t* v_strides, const int32_t* block_table,
+                               int64_t block_table_stride, int64_t block_table_width,
+                               const int32_t* seq_lens, int64_t num_seqs, int64_t num_q_heads,
+                               int64_t num_kv_heads, int64_t head_size, int64_t block_size,
+                               int64_t num_blocks, int64_t max_seq_len, float softmax_scale,
+                               const float* q_descale, const float* k_descale,
+                               const float* v_descale, const int64_t* descale_strides, void* out,
+                               int64_t out_tok_stride, int64_t out_head_stride, int out_dtype,
+                               float* lse, int64_t lse_head_stride, float* workspace,
+                               int64_t workspace_len, void* stream);
+
+int64_t psk_paged_decode_workspace_len(int64_t num_seqs, int64_t num_q_heads, int64_t num_kv_heads,
+                                       int64_t max_seq_len);
+
+/*
  * Pinned, device-mapped host memory for the L2 mirror and swap staging
  * (hipHostMalloc).  Allocation happens at set-up, never on the hot path.
  */

@@ -369,3 +369,60 @@ def dcp_kv_len(prefix_len, dcp_deg, dcp_rank, dcp_interleave_size):
     elif rem >= dcp_rank * dcp_interleave_size:
         n += rem % dcp_interleave_size
     return n
+
+
+# --------------------------------------------------------------------------- #
+# paged decode attention over an FP8 cache
+# --------------------------------------------------------------------------- #
+
+
+def paged_decode_attention(q, q_dtype, k_cache, v_cache, block_table, seq_lens, softmax_scale, q_descale=None,
+                           k_descale=None, v_descale=None):
+    """Decode attention of one query token per sequence over an FP8 E4M3FN
+    paged cache, in float64 (the semantics the reference gets from vLLM's FA3
+    fork, pipeswift/llms/layers/attention.py:148-187: FP8 query, descales per
+    (sequence, kv head), here any values instead of the fixed 1.0 of
+    fp8_kv.py:94-103).
+
+    q: raw bits [B, Hq, D] of ``q_dtype`` ("fp8" is used as is, others are
+    quantized as e4m3(q / q_descale)); k_cache, v_cache: uint8 [P, ps, Hkv, D];
+    block_table: int [B, W]; seq_lens: int [B]; descales: float [B, Hkv] or None.
+    Returns (out [B, Hq, D], lse [B, Hq]) as float64; a sequence of length 0
+    gives zeros and lse = -inf.  Table entries outside [0, P) read as zero rows.
+    """
+    q = np.asarray(q)
+    B, Hq, D = q.shape
+    P, ps, Hkv, _ = k_cache.shape
+    G = Hq // Hkv
+    out = np.zeros((B, Hq, D), dtype=np.float64)
+    lse = np.full((B, Hq), -np.inf, dtype=np.float64)
+    ones = np.ones((B, Hkv), dtype=np.float32)
+    qd_all = ones if q_descale is None else np.asarray(q_descale, dtype=np.float32)
+    kd_all = ones if k_descale is None else np.asarray(k_descale, dtype=np.float32)
+    vd_all = ones if v_descale is None else np.asarray(v_descale, dtype=np.float32)
+    for b in range(B):
+        n = int(seq_lens[b])
+        if n == 0:
+            continue
+        j = np.arange(n)
+        pages = np.asarray(block_table[b], dtype=np.int64)[j // ps]
+        ok = (pages >= 0) & (pages < P)
+        rows = j % ps
+        for h in range(Hkv):
+            qd, kd, vd = float(qd_all[b, h]), float(kd_all[b, h]), float(vd_all[b, h])
+            qs = q[b, h * G:(h + 1) * G]
+            if q_dtype == "fp8":
+                qq = e4m3fn_to_f32(qs).astype(np.float64)
+            else:
+                qq = e4m3fn_to_f32(quantize_e4m3(to_f32(qs, q_dtype), qd)).astype(np.float64)
+            K = np.zeros((n, D), dtype=np.float64)
+            V = np.zeros((n, D), dtype=np.float64)
+            K[ok] = e4m3fn_to_f32(k_cache[pages[ok], rows[ok], h]).astype(np.float64)
+            V[ok] = e4m3fn_to_f32(v_cache[pages[ok], rows[ok], h]).astype(np.float64)
+            s = (qq @ K.T) * (float(np.float32(softmax_scale)) * qd * kd)
+            m = s.max(axis=1, keepdims=True)
+            p = np.exp(s - m)
+            den = p.sum(axis=1, keepdims=True)
+            out[b, h * G:(h + 1) * G] = (p @ V) / den * vd
+            lse[b, h * G:(h + 1) * G] = (m + np.log(den))[:, 0]
+    return out, lse

@@ -75,6 +75,12 @@ _SIGNATURES = {
     "psk_host_free": (_int, [_vp]),
     "psk_keyed_hash": (_int, [_vp, _i64, ctypes.c_uint64, _int, _vp]),
     "psk_page_hash_chain": (_i64, [_vp, _i64, _i64, _i64, ctypes.c_uint64, _int, _vp, _i64]),
+    "psk_paged_decode_attention": (
+        _int,
+        [_vp, _i64, _i64, _int, _vp, _vp, _c_int64_p, _c_int64_p, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64,
+         _i64, _i64, ctypes.c_float, _vp, _vp, _vp, _c_int64_p, _vp, _i64, _i64, _int, _vp, _i64, _vp, _i64, _vp],
+    ),
+    "psk_paged_decode_workspace_len": (_i64, [_i64, _i64, _i64, _i64]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)

@@ -1,0 +1,149 @@
+"""Paged decode attention over the FP8 KV cache: the reader of what the append
+writes.
+
+The reference decodes an FP8 cache through vLLM's FA3 fork,
+``flash_attn_varlen_func(q=quantize(query), k, v, max_seqlen_q,
+cu_seqlens_q, max_seqlen_k=None, seqused_k, block_table, softmax_scale,
+causal, fa_version=3, q_descale, k_descale, v_descale)``
+(pipeswift/llms/layers/attention.py:148-187), with every descale 1.0
+(pipeswift/utils/fp8_kv.py:94-103).  ``flash_attn_varlen_func`` here takes the
+same arguments for the decode case (one query token per sequence) and runs
+``psk_paged_decode_attention``: FP8 MFMA for Q K^T, fp32 softmax and P V, and
+descales of any value per (sequence, kv head) -- for instance the per-tensor
+scales ``cache_ops.compute_kv_scales`` gave the append.
+
+Prefill over the paged cache is not covered; ``max_seqlen_q`` must be 1.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from ._lib import check, dtype_code, i64_array, lib, ptr, stream_handle
+
+HEAD_DIM = 128
+MAX_GROUP = 8
+
+_OUT_CODES = {torch.bfloat16: 2, torch.float32: 0}
+
+
+def workspace_floats(num_seqs: int, num_q_heads: int, num_kv_heads: int, max_seq_len: int) -> int:
+    n = int(lib().psk_paged_decode_workspace_len(num_seqs, num_q_heads, num_kv_heads, max_seq_len))
+    if n < 0:
+        check(n, "paged decode workspace")
+    return n
+
+
+def _descale(t: Optional[torch.Tensor], num_seqs: int, num_kv_heads: int, device):
+    """(device pointer, stride over sequences, stride over kv heads) of a
+    descale given as None, a one-element tensor, or a (num_seqs, num_kv_heads)
+    tensor (stride-0 expansions included, as vLLM passes them)."""
+    if t is None:
+        return None, 0, 0
+    assert t.dtype == torch.float32 and t.device == device, "descales are float32 tensors on the query's device"
+    if t.numel() == 1:
+        return t, 0, 0
+    assert t.dim() == 2 and t.shape[0] >= num_seqs and t.shape[1] == num_kv_heads, \
+        f"descale shape {tuple(t.shape)}, want ({num_seqs}, {num_kv_heads})"
+    return t, t.stride(0), t.stride(1)
+
+
+def paged_decode_attention(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    softmax_scale: Optional[float] = None,
+    q_descale: Optional[torch.Tensor] = None,
+    k_descale: Optional[torch.Tensor] = None,
+    v_descale: Optional[torch.Tensor] = None,
+    out: Optional[torch.Tensor] = None,
+    return_softmax_lse: bool = False,
+    max_seq_len: Optional[int] = None,
+    workspace: Optional[torch.Tensor] = None,
+):
+    """One decode step of attention for every sequence.
+
+    q: [B, Hq, 128] (fp8 e4m3fn used as is; bf16/fp16/fp32 quantized as
+    e4m3(q / q_descale), as the reference quantizes its query).
+    k_cache, v_cache: fp8 [num_blocks, block_size, Hkv, 128] (views of the fused
+    [P, 2, ps, H, D] layer are fine).  block_table: int32 [B, W];
+    seq_lens: int32 [B] (``seqused_k``).  Returns out [B, Hq, 128] (bf16 unless
+    ``out`` is given as float32) and, when asked, lse [Hq, B] float32.
+    """
+    assert q.is_cuda and k_cache.is_cuda and v_cache.is_cuda
+    assert q.dim() == 3 and q.shape[2] == HEAD_DIM and q.stride(2) == 1, "q must be [B, Hq, 128] with unit last stride"
+    assert k_cache.dtype == torch.float8_e4m3fn and v_cache.dtype == torch.float8_e4m3fn, "the cache must be fp8 e4m3fn"
+    assert k_cache.dim() == 4 and k_cache.shape == v_cache.shape and k_cache.shape[3] == HEAD_DIM
+    assert k_cache.stride(3) == 1 and v_cache.stride(3) == 1
+    B, Hq, _ = q.shape
+    P, ps, Hkv, _ = k_cache.shape
+    assert Hq % Hkv == 0 and Hq // Hkv <= MAX_GROUP, f"{Hq} query heads over {Hkv} kv heads (at most {MAX_GROUP} per)"
+    assert block_table.dtype == torch.int32 and block_table.dim() == 2 and block_table.stride(1) == 1
+    assert block_table.shape[0] >= B
+    assert seq_lens.dtype == torch.int32 and seq_lens.is_contiguous() and seq_lens.numel() >= B
+    device = q.device
+    if softmax_scale is None:
+        softmax_scale = HEAD_DIM ** -0.5
+    if max_seq_len is None:
+        max_seq_len = block_table.shape[1] * ps  # bounds every sequence, no host sync
+    if out is None:
+        out = torch.empty(B, Hq, HEAD_DIM, dtype=torch.bfloat16, device=device)
+    assert out.dtype in _OUT_CODES and out.shape == (B, Hq, HEAD_DIM) and out.stride(2) == 1
+    lse = torch.empty(Hq, B, dtype=torch.float32, device=device) if return_softmax_lse else None
+    need = workspace_floats(B, Hq, Hkv, max_seq_len)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.float32, device=device)
+    qd, qsb, qsh = _descale(q_descale, B, Hkv, device)
+    kd, ksb, ksh = _descale(k_descale, B, Hkv, device)
+    vd, vsb, vsh = _descale(v_descale, B, Hkv, device)
+    st = lib().psk_paged_decode_attention(
+        q.data_ptr(), q.stride(0), q.stride(1), dtype_code(q.dtype),
+        k_cache.data_ptr(), v_cache.data_ptr(), i64_array(k_cache.stride()[:3]), i64_array(v_cache.stride()[:3]),
+        block_table.data_ptr(), block_table.stride(0), block_table.shape[1], seq_lens.data_ptr(), B, Hq, Hkv,
+        HEAD_DIM, ps, P, int(max_seq_len), float(softmax_scale), ptr(qd), ptr(kd), ptr(vd),
+        i64_array([qsb, qsh, ksb, ksh, vsb, vsh]), out.data_ptr(), out.stride(0), out.stride(1),
+        _OUT_CODES[out.dtype], ptr(lse), B if lse is not None else 0, workspace.data_ptr(), workspace.numel(),
+        stream_handle(device),
+    )
+    check(st, "paged_decode_attention")
+    return (out, lse) if return_softmax_lse else out
+
+
+def flash_attn_varlen_func(
+    q,
+    k,
+    v,
+    max_seqlen_q,
+    cu_seqlens_q,
+    max_seqlen_k=None,
+    seqused_k=None,
+    block_table=None,
+    softmax_scale=None,
+    causal=False,
+    fa_version=3,
+    q_descale=None,
+    k_descale=None,
+    v_descale=None,
+    return_softmax_lse=False,
+    out=None,
+    num_splits=0,
+):
+    """The FA3 entry the reference's ``_fp8_paged_attn`` calls
+    (attention.py:166-184), for decode: q is [total_q, Hq, D] with one token per
+    sequence (``max_seqlen_q == 1``; ``cu_seqlens_q`` then is 0..B and
+    ``causal`` has nothing to mask).  ``max_seqlen_k`` bounds the lengths when
+    given, else the block table's width does.  ``num_splits`` and
+    ``fa_version`` are accepted for signature compatibility; the split is chosen
+    from the length bound."""
+    assert max_seqlen_q == 1, "decode only: one query token per sequence"
+    assert seqused_k is not None and block_table is not None, "paged decode needs seqused_k and block_table"
+    B = seqused_k.shape[0]
+    assert q.shape[0] == B and cu_seqlens_q.shape[0] == B + 1
+    ps = k.shape[1]
+    bound = block_table.shape[1] * ps if max_seqlen_k is None else min(int(max_seqlen_k), block_table.shape[1] * ps)
+    return paged_decode_attention(q, k, v, block_table, seqused_k, softmax_scale, q_descale, k_descale, v_descale,
+                                  out=out, return_softmax_lse=return_softmax_lse, max_seq_len=bound)

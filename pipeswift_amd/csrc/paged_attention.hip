@@ -1,0 +1,538 @@
+// Paged decode attention over the FP8 E4M3FN KV cache for MI355X (gfx950): the
+// reader of what the append writes, with per-(sequence, kv head) descales.
+//
+// For sequence b, query head hq = h * G + g (G query heads per kv head h) and the
+// first seq_lens[b] tokens j of the paged cache:
+//   q~      = e4m3(q[b, hq] / qd)            (an FP8 query is taken as is)
+//   s_j     = softmax_scale * qd * kd * (q~ . K[j, h])
+//   out     = vd * sum_j softmax(s)_j V[j, h]
+//   lse     = log(sum_j exp(s_j))
+// with qd, kd, vd the descales of (b, h).  This is what the reference's decode
+// reads through vLLM's FA3 fork (pipeswift/llms/layers/attention.py:148-187,
+// FP8 query, descales per (sequence, kv head)); there the descales are fixed at
+// 1.0 (pipeswift/utils/fp8_kv.py:94-103).
+//
+// Mapping (head_dim 128, one wave per 16-token tile of one kv head):
+//   * Q K^T is one v_mfma_f32_16x16x32_bf16 chain of 4: the G query heads of
+//     the group are rows (padded to 16), the tile's 16 tokens are columns.  Lane
+//     l loads 32 contiguous bytes of token (l % 16)'s K row at d = 32 * (l / 16)
+//     and the query operand uses the same d permutation.  Both operands are FP8
+//     values converted exactly to bf16 (v_cvt_scalef32_pk_bf16_fp8 at scale 1),
+//     so the products are exact and the sums are fp32.  The FP8 MFMA
+//     (v_mfma_f32_16x16x32_fp8_fp8) is not used: on gfx950 it drops low-order
+//     bits of small products against the largest one (measured: 256 + 31 * 2^-6
+//     sums to 256.375), the accumulation loss the reference's FA3 fork has a
+//     fix for on Hopper (pipeswift/utils/fp8_kv.py:6-13).
+//   * softmax runs in the exp2 domain with a lazily raised running maximum
+//     (raised only when a score exceeds it by 2^8), which keeps the rescaling of
+//     the accumulators off the per-tile path; normalisation is exact.
+//   * P V runs on the VALU in fp32: lane l owns tokens (l / 8) and (l / 8 + 8) of
+//     the tile and d = 16 * (l % 8) .. +16, loaded as one 16-byte vector per
+//     token; FP8 -> fp32 with the native pair convert.  V is never transposed.
+//   * flash-decoding split: a workgroup of 4 waves takes `split` tokens of one
+//     (sequence, kv head); its waves merge through LDS into one partial
+//     (max, sum, accumulator per query head) in the caller's workspace, and a
+//     second kernel merges the partials of a sequence and writes the output.
+//   * loads for tile i + 1 are issued before tile i is computed.
+//
+// C ABI: include/pipeswift_kv.h.  Nothing here allocates or synchronizes.
+
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+
+#include <algorithm>
+#include <cmath>
+
+#include "pipeswift_kv.h"
+#include "psk_common.h"
+
+using namespace psk_detail;
+
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kHead = 128;    // head_dim of the MFMA tiling
+constexpr int kTile = 16;     // tokens per tile (N of the 16x16x32 MFMA)
+constexpr int kWaves = 4;     // waves per workgroup
+constexpr int kMinSplit = 512;
+constexpr int kMaxSplits = 128;
+constexpr float kNegBig = -1.0e30f;  // finite "no token yet" maximum
+constexpr float kLazy = 8.0f;        // raise the running max past 2^8 headroom only
+constexpr int kPageCache = 512;      // page ids of a split staged in LDS
+
+struct DecodeArgs {
+  const char* q;
+  int64_t q_tok_stride;   // bytes
+  int64_t q_head_stride;  // bytes
+  const uint8_t* k;
+  const uint8_t* v;
+  int64_t k_blk, k_row, k_head;  // bytes
+  int64_t v_blk, v_row, v_head;
+  const int32_t* block_table;
+  int64_t bt_stride;
+  int64_t bt_width;
+  const int32_t* seq_lens;
+  int32_t num_blocks;
+  int32_t block_size;
+  int32_t bs_shift;  // log2(block_size) or -1
+  int32_t num_kv_heads;
+  int32_t group;     // query heads per kv head
+  int32_t split;     // tokens per workgroup
+  int32_t max_splits;
+  float scale_log2;  // softmax_scale * log2(e)
+  const float* qd;
+  int64_t qd_b, qd_h;
+  const float* kd;
+  int64_t kd_b, kd_h;
+  const float* vd;
+  int64_t vd_b, vd_h;
+  float* part;       // partials: [B][Hkv][max_splits][G * (kHead + 2)]
+  char* out;
+  int64_t out_tok_stride;   // bytes
+  int64_t out_head_stride;  // bytes
+  float* lse;               // [Hq][lse_head_stride] (entry [hq][b]) or nullptr
+  int64_t lse_head_stride;
+};
+
+__device__ __forceinline__ float descale(const float* p, int64_t sb, int64_t sh, int b, int h) {
+  return p ? p[b * sb + h * sh] : 1.0f;
+}
+
+// Eight E4M3FN bytes (w0 then w1, in byte order) -> eight bf16, exactly: every
+// E4M3FN value is a bf16 value.
+__device__ __forceinline__ bf16x8 e4m3x8_to_bf16(uint32_t w0, uint32_t w1) {
+  const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false);
+  const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true);
+  const bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false);
+  const bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true);
+  return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+__device__ __forceinline__ float bperm(int src_lane, float x) {
+  return __int_as_float(__builtin_amdgcn_ds_bpermute(src_lane << 2, __float_as_int(x)));
+}
+
+__device__ __forceinline__ int page_index(const DecodeArgs& a, int t) {
+  return a.bs_shift >= 0 ? (t >> a.bs_shift) : (t / a.block_size);
+}
+
+// Page id of table entry pi, or -1 past the table's width or out of range.
+__device__ __forceinline__ int32_t checked_page(const DecodeArgs& a, const int32_t* bt_row, int64_t pi) {
+  if (pi >= a.bt_width) return -1;
+  const int32_t p = bt_row[pi];
+  return (p >= 0 && p < a.num_blocks) ? p : -1;
+}
+
+// The page ids a workgroup's split touches, staged once in LDS (entry i holds
+// table entry first + i, -1 when missing); direct reads when they do not fit.
+struct PageIds {
+  const int32_t* lds;
+  const int32_t* bt_row;
+  int first;
+  bool staged;
+};
+
+__device__ __forceinline__ int64_t page_of(const DecodeArgs& a, const PageIds& ids, int t) {
+  const int pi = page_index(a, t);
+  return ids.staged ? int64_t(ids.lds[pi - ids.first]) : int64_t(checked_page(a, ids.bt_row, pi));
+}
+
+__device__ __forceinline__ int64_t row_of(const DecodeArgs& a, int t) {
+  return a.bs_shift >= 0 ? int64_t(t & (a.block_size - 1)) : int64_t(t % a.block_size);
+}
+
+// Tile loads of one lane: K (32 bytes of one token) and V (16 bytes of two tokens).
+struct TileLoads {
+  u32x4 k0, k1, va, vb;
+};
+
+__device__ __forceinline__ TileLoads load_tile(const DecodeArgs& a, const PageIds& ids, int h, int t0, int t_end,
+                                               int lane) {
+  TileLoads r;
+  r.k0 = r.k1 = r.va = r.vb = u32x4(0);
+  const int tk = t0 + (lane & 15);
+  if (tk < t_end) {
+    const int64_t p = page_of(a, ids, tk);
+    if (p >= 0) {
+      const uint8_t* src = a.k + p * a.k_blk + row_of(a, tk) * a.k_row + h * a.k_head + 32 * (lane >> 4);
+      r.k0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
+      r.k1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + 16));
+    }
+  }
+  const int ta = t0 + (lane >> 3), tb = ta + 8;
+  const int64_t dv = 16 * (lane & 7);
+  if (ta < t_end) {
+    const int64_t p = page_of(a, ids, ta);
+    if (p >= 0)
+      r.va = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4*>(a.v + p * a.v_blk + row_of(a, ta) * a.v_row + h * a.v_head + dv));
+  }
+  if (tb < t_end) {
+    const int64_t p = page_of(a, ids, tb);
+    if (p >= 0)
+      r.vb = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4*>(a.v + p * a.v_blk + row_of(a, tb) * a.v_row + h * a.v_head + dv));
+  }
+  return r;
+}
+
+// 32 FP8 query bytes of this lane's MFMA row (query head h*G + lane%16, d from
+// 32 * (lane / 16)); zero rows beyond the group.
+template <int Q_DT>
+__device__ __forceinline__ void load_query(const DecodeArgs& a, int b, int h, float qd, int lane, uint32_t qw[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) qw[i] = 0;
+  const int row = lane & 15;
+  if (row >= a.group) return;
+  const char* src = a.q + b * a.q_tok_stride + int64_t(h * a.group + row) * a.q_head_stride;
+  const int d0 = 32 * (lane >> 4);
+  if constexpr (Q_DT == PSK_DTYPE_FP8_E4M3FN) {
+    const u32x4 lo = *reinterpret_cast<const u32x4*>(src + d0);
+    const u32x4 hi = *reinterpret_cast<const u32x4*>(src + d0 + 16);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      qw[i] = lo[i];
+      qw[4 + i] = hi[i];
+    }
+  } else {
+    constexpr int kEsz = Elt<Q_DT>::kSize;
+    constexpr int E = 16 / kEsz;  // elements per 16-byte load
+    using QC = QuantConv<Q_DT, E>;
+    const QScale qs = make_qscale(qd);
+    uint8_t bytes[32];
+#pragma unroll
+    for (int i = 0; i < 32 / E; ++i) {
+      const typename QC::In x = *reinterpret_cast<const typename QC::In*>(src + (d0 + E * i) * kEsz);
+      const typename QC::Out y = QC::apply(x, qs);
+      __builtin_memcpy(bytes + E * i, &y, E);
+    }
+    __builtin_memcpy(qw, bytes, 32);
+  }
+}
+
+template <int Q_DT, int NG>
+__global__ void __launch_bounds__(kWaves * 64) decode_partial_kernel(DecodeArgs a) {
+  const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int len = a.seq_lens[b];
+  const int t_begin = s * a.split;
+  if (t_begin >= len || s >= a.max_splits) return;  // uniform over the workgroup
+  const int t_end = min(len, t_begin + a.split);
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int G = a.group;
+
+  const float qd = descale(a.qd, a.qd_b, a.qd_h, b, h);
+  const float kd = descale(a.kd, a.kd_b, a.kd_h, b, h);
+  const float sl = a.scale_log2 * qd * kd;
+  uint32_t qw[8];
+  load_query<Q_DT>(a, b, h, qd, lane, qw);
+  const bf16x8 qop[4] = {e4m3x8_to_bf16(qw[0], qw[1]), e4m3x8_to_bf16(qw[2], qw[3]), e4m3x8_to_bf16(qw[4], qw[5]),
+                         e4m3x8_to_bf16(qw[6], qw[7])};
+
+  __shared__ int32_t s_pages[kPageCache];
+  PageIds ids;
+  ids.lds = s_pages;
+  ids.bt_row = a.block_table + b * a.bt_stride;
+  ids.first = page_index(a, t_begin);
+  const int n_ids = page_index(a, t_end - 1) - ids.first + 1;
+  ids.staged = n_ids <= kPageCache;
+  if (ids.staged) {
+    for (int i = threadIdx.x; i < n_ids; i += kWaves * 64) s_pages[i] = checked_page(a, ids.bt_row, ids.first + i);
+    __syncthreads();
+  }
+
+  float m[NG], l[NG], acc[NG][16];
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    m[g] = kNegBig;
+    l[g] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) acc[g][k] = 0.0f;
+  }
+
+  const int stride = kTile * kWaves;
+  const int tv = lane >> 3;
+  int t0 = t_begin + wave * kTile;
+  TileLoads cur;
+  if (t0 < t_end) cur = load_tile(a, ids, h, t0, t_end, lane);
+  for (; t0 < t_end; t0 += stride) {
+    TileLoads nxt;
+    nxt.k0 = nxt.k1 = nxt.va = nxt.vb = u32x4(0);
+    if (t0 + stride < t_end) nxt = load_tile(a, ids, h, t0 + stride, t_end, lane);
+
+    // S[g][t]: lane l, register r holds query row 4*(l/16)+r, token l%16
+    f32x4 sc = {0.0f, 0.0f, 0.0f, 0.0f};
+    sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qop[0], e4m3x8_to_bf16(cur.k0[0], cur.k0[1]), sc, 0, 0, 0);
+    sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qop[1], e4m3x8_to_bf16(cur.k0[2], cur.k0[3]), sc, 0, 0, 0);
+    sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qop[2], e4m3x8_to_bf16(cur.k1[0], cur.k1[1]), sc, 0, 0, 0);
+    sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qop[3], e4m3x8_to_bf16(cur.k1[2], cur.k1[3]), sc, 0, 0, 0);
+
+    // scores of this lane's two tokens for every head of the group
+    const bool va_ok = t0 + tv < t_end, vb_ok = t0 + tv + 8 < t_end;
+    float sa[NG], sb[NG];
+    bool raise = false;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      const float ra = bperm(16 * (g >> 2) + tv, sc[g & 3]);
+      const float rb = bperm(16 * (g >> 2) + tv + 8, sc[g & 3]);
+      sa[g] = va_ok ? ra * sl : -__builtin_inff();
+      sb[g] = vb_ok ? rb * sl : -__builtin_inff();
+      raise |= __builtin_fmaxf(sa[g], sb[g]) > m[g] + kLazy;
+    }
+    if (__any(raise)) {
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        const float mn = __builtin_fmaxf(m[g], __builtin_fmaxf(sa[g], sb[g]));
+        const float c = __builtin_amdgcn_exp2f(m[g] - mn);
+        l[g] *= c;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) acc[g][k] *= c;
+        m[g] = mn;
+      }
+    }
+    float pa[NG], pb[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      pa[g] = __builtin_amdgcn_exp2f(sa[g] - m[g]);
+      pb[g] = __builtin_amdgcn_exp2f(sb[g] - m[g]);
+      l[g] += pa[g] + pb[g];
+    }
+    float fa[16], fb[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x2 a0 = e4m3_unpack2(cur.va[i], false), a1 = e4m3_unpack2(cur.va[i], true);
+      const f32x2 b0 = e4m3_unpack2(cur.vb[i], false), b1 = e4m3_unpack2(cur.vb[i], true);
+      fa[4 * i] = a0.x; fa[4 * i + 1] = a0.y; fa[4 * i + 2] = a1.x; fa[4 * i + 3] = a1.y;
+      fb[4 * i] = b0.x; fb[4 * i + 1] = b0.y; fb[4 * i + 2] = b1.x; fb[4 * i + 3] = b1.y;
+    }
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) acc[g][k] = __builtin_fmaf(pa[g], fa[k], __builtin_fmaf(pb[g], fb[k], acc[g][k]));
+    }
+    cur = nxt;
+  }
+
+  // merge the eight token slots of the wave (lanes differing in bits 3..5)
+#pragma unroll
+  for (int off = 8; off < 64; off <<= 1) {
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      const float mo = __shfl_xor(m[g], off);
+      const float lo = __shfl_xor(l[g], off);
+      const float mn = __builtin_fmaxf(m[g], mo);
+      const float ca = __builtin_amdgcn_exp2f(m[g] - mn), cb = __builtin_amdgcn_exp2f(mo - mn);
+      l[g] = l[g] * ca + lo * cb;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) acc[g][k] = acc[g][k] * ca + __shfl_xor(acc[g][k], off) * cb;
+      m[g] = mn;
+    }
+  }
+
+  // merge the waves through LDS and write this split's partial
+  __shared__ float s_acc[kWaves][NG][kHead];
+  __shared__ float s_m[kWaves][NG], s_l[kWaves][NG];
+  if (lane < 8) {
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) s_acc[wave][g][16 * lane + k] = acc[g][k];
+    }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      s_m[wave][g] = m[g];
+      s_l[wave][g] = l[g];
+    }
+  }
+  __syncthreads();
+  const int rec = G * (kHead + 2);
+  float* part = a.part + ((int64_t(b) * a.num_kv_heads + h) * a.max_splits + s) * rec;
+  for (int i = threadIdx.x; i < G * kHead; i += kWaves * 64) {
+    const int g = i / kHead, d = i % kHead;
+    float mx = s_m[0][g];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) mx = __builtin_fmaxf(mx, s_m[w][g]);
+    float v = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) v += s_acc[w][g][d] * __builtin_amdgcn_exp2f(s_m[w][g] - mx);
+    part[2 * G + i] = v;
+  }
+  if (threadIdx.x < G) {
+    const int g = threadIdx.x;
+    float mx = s_m[0][g];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) mx = __builtin_fmaxf(mx, s_m[w][g]);
+    float sum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) sum += s_l[w][g] * __builtin_amdgcn_exp2f(s_m[w][g] - mx);
+    part[g] = mx;
+    part[G + g] = sum;
+  }
+}
+
+// One workgroup per (kv head, sequence): merge the sequence's partials.
+template <int OUT_DT>
+__global__ void __launch_bounds__(256) decode_combine_kernel(DecodeArgs a) {
+  const int h = blockIdx.x, b = blockIdx.y;
+  const int G = a.group;
+  const int len = a.seq_lens[b];
+  const int n = len > 0 ? min(a.max_splits, (len + a.split - 1) / a.split) : 0;
+  const float vd = descale(a.vd, a.vd_b, a.vd_h, b, h);
+  const int rec = G * (kHead + 2);
+  const float* part = a.part + (int64_t(b) * a.num_kv_heads + h) * a.max_splits * rec;
+  for (int i = threadIdx.x; i < G * kHead; i += blockDim.x) {
+    const int g = i / kHead, d = i % kHead;
+    float mx = kNegBig;
+    for (int s = 0; s < n; ++s) mx = __builtin_fmaxf(mx, part[s * rec + g]);
+    float num = 0.0f, den = 0.0f;
+    for (int s = 0; s < n; ++s) {
+      const float c = __builtin_amdgcn_exp2f(part[s * rec + g] - mx);
+      num += part[s * rec + 2 * G + i] * c;
+      den += part[s * rec + G + g] * c;
+    }
+    const float o = den > 0.0f ? num / den * vd : 0.0f;
+    char* dst = a.out + b * a.out_tok_stride + int64_t(h * G + g) * a.out_head_stride;
+    reinterpret_cast<typename Elt<OUT_DT>::Bits*>(dst)[d] = Elt<OUT_DT>::from_f32(o);
+    if (d == 0 && a.lse) {
+      // natural-log sum of exp(s): 2^mx * den in the exp2 domain
+      a.lse[int64_t(h * G + g) * a.lse_head_stride + b] =
+          den > 0.0f ? (mx + __builtin_log2f(den)) * 0.6931471805599453f : -__builtin_inff();
+    }
+  }
+}
+
+int decode_split(int64_t max_seq_len) {
+  int64_t split = kMinSplit;
+  while (ceil_div(max_seq_len, split) > kMaxSplits) split *= 2;
+  return int(split);
+}
+
+template <int Q_DT>
+void launch_partial(const DecodeArgs& a, dim3 grid, hipStream_t st, int ng) {
+  switch (ng) {
+    case 1: hipLaunchKernelGGL((decode_partial_kernel<Q_DT, 1>), grid, dim3(kWaves * 64), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((decode_partial_kernel<Q_DT, 2>), grid, dim3(kWaves * 64), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((decode_partial_kernel<Q_DT, 4>), grid, dim3(kWaves * 64), 0, st, a); break;
+    default: hipLaunchKernelGGL((decode_partial_kernel<Q_DT, 8>), grid, dim3(kWaves * 64), 0, st, a); break;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t psk_paged_decode_workspace_len(int64_t num_seqs, int64_t num_q_heads, int64_t num_kv_heads,
+                                       int64_t max_seq_len) {
+  if (num_seqs < 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads || max_seq_len < 0) return PSK_E_ARG;
+  const int64_t splits = std::max<int64_t>(1, ceil_div(max_seq_len, decode_split(max_seq_len)));
+  return num_seqs * num_kv_heads * splits * (num_q_heads / num_kv_heads) * (kHead + 2);
+}
+
+int psk_paged_decode_attention(const void* q, int64_t q_tok_stride, int64_t q_head_stride, int q_dtype,
+                               const void* k_cache, const void* v_cache, const int64_t* k_strides,
+                               const int64_t* v_strides, const int32_t* block_table, int64_t block_table_stride,
+                               int64_t block_table_width, const int32_t* seq_lens, int64_t num_seqs,
+                               int64_t num_q_heads, int64_t num_kv_heads, int64_t head_size, int64_t block_size,
+                               int64_t num_blocks, int64_t max_seq_len, float softmax_scale, const float* q_descale,
+                               const float* k_descale, const float* v_descale, const int64_t* descale_strides,
+                               void* out, int64_t out_tok_stride, int64_t out_head_stride, int out_dtype, float* lse,
+                               int64_t lse_head_stride, float* workspace, int64_t workspace_len, void* stream) {
+  g_err[0] = 0;
+  if (num_seqs < 0 || num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads)
+    return fail(PSK_E_ARG, "bad head counts (q %lld, kv %lld)", (long long)num_q_heads, (long long)num_kv_heads);
+  const int64_t G = num_q_heads / num_kv_heads;
+  if (G > 8) return fail(PSK_E_ARG, "at most 8 query heads per kv head (got %lld)", (long long)G);
+  if (head_size != kHead) return fail(PSK_E_ARG, "head_size must be %d (got %lld)", kHead, (long long)head_size);
+  if (block_size <= 0 || num_blocks <= 0 || num_blocks > INT32_MAX || block_table_width <= 0 || max_seq_len < 0 ||
+      max_seq_len > INT32_MAX)
+    return fail(PSK_E_ARG, "bad cache geometry");
+  if (q_dtype != PSK_DTYPE_FP8_E4M3FN && q_dtype != PSK_DTYPE_BF16 && q_dtype != PSK_DTYPE_F16 &&
+      q_dtype != PSK_DTYPE_F32)
+    return fail(PSK_E_DTYPE, "query dtype %d", q_dtype);
+  if (out_dtype != PSK_DTYPE_BF16 && out_dtype != PSK_DTYPE_F32)
+    return fail(PSK_E_DTYPE, "output dtype %d (bf16 or f32)", out_dtype);
+  if (num_seqs == 0) return PSK_OK;
+  if (!q || !k_cache || !v_cache || !k_strides || !v_strides || !block_table || !seq_lens || !out || !workspace)
+    return fail(PSK_E_ARG, "NULL pointer");
+  if (!std::isfinite(softmax_scale)) return fail(PSK_E_ARG, "softmax_scale is not finite");
+  const int qsz = dtype_size(q_dtype);
+  // 16-byte vector loads: every K/V base and stride, and the query rows
+  const uint64_t kv_align[8] = {uint64_t(uintptr_t(k_cache)), uint64_t(uintptr_t(v_cache)), uint64_t(k_strides[0]),
+                                uint64_t(k_strides[1]),       uint64_t(k_strides[2]),       uint64_t(v_strides[0]),
+                                uint64_t(v_strides[1]),       uint64_t(v_strides[2])};
+  if (common_align(kv_align, 8, 16) < 16) return fail(PSK_E_ARG, "K/V caches need 16-byte aligned bases and strides");
+  const uint64_t q_align[3] = {uint64_t(uintptr_t(q)), uint64_t(q_tok_stride * qsz), uint64_t(q_head_stride * qsz)};
+  if (common_align(q_align, 3, 16) < 16) return fail(PSK_E_ARG, "query rows need 16-byte alignment");
+  const int64_t need = psk_paged_decode_workspace_len(num_seqs, num_q_heads, num_kv_heads, max_seq_len);
+  if (workspace_len < need)
+    return fail(PSK_E_WORKSPACE, "workspace of %lld floats, need %lld", (long long)workspace_len, (long long)need);
+
+  DecodeArgs a{};
+  a.q = static_cast<const char*>(q);
+  a.q_tok_stride = q_tok_stride * qsz;
+  a.q_head_stride = q_head_stride * qsz;
+  a.k = static_cast<const uint8_t*>(k_cache);
+  a.v = static_cast<const uint8_t*>(v_cache);
+  a.k_blk = k_strides[0];
+  a.k_row = k_strides[1];
+  a.k_head = k_strides[2];
+  a.v_blk = v_strides[0];
+  a.v_row = v_strides[1];
+  a.v_head = v_strides[2];
+  a.block_table = block_table;
+  a.bt_stride = block_table_stride;
+  a.bt_width = block_table_width;
+  a.seq_lens = seq_lens;
+  a.num_blocks = int32_t(num_blocks);
+  a.block_size = int32_t(block_size);
+  a.bs_shift = log2_exact(block_size);
+  a.num_kv_heads = int32_t(num_kv_heads);
+  a.group = int32_t(G);
+  a.split = decode_split(max_seq_len);
+  a.max_splits = int32_t(std::max<int64_t>(1, ceil_div(max_seq_len, a.split)));
+  a.scale_log2 = softmax_scale * 1.4426950408889634f;
+  const int64_t zero[6] = {0, 0, 0, 0, 0, 0};
+  const int64_t* ds = descale_strides ? descale_strides : zero;
+  a.qd = q_descale;
+  a.qd_b = ds[0];
+  a.qd_h = ds[1];
+  a.kd = k_descale;
+  a.kd_b = ds[2];
+  a.kd_h = ds[3];
+  a.vd = v_descale;
+  a.vd_b = ds[4];
+  a.vd_h = ds[5];
+  a.part = workspace;
+  a.out = static_cast<char*>(out);
+  const int osz = dtype_size(out_dtype);
+  a.out_tok_stride = out_tok_stride * osz;
+  a.out_head_stride = out_head_stride * osz;
+  a.lse = lse;
+  a.lse_head_stride = lse_head_stride;
+
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int ng = G == 1 ? 1 : G == 2 ? 2 : G <= 4 ? 4 : 8;
+  const dim3 grid{unsigned(a.max_splits), unsigned(num_kv_heads), unsigned(num_seqs)};
+  switch (q_dtype) {
+    case PSK_DTYPE_FP8_E4M3FN: launch_partial<PSK_DTYPE_FP8_E4M3FN>(a, grid, st, ng); break;
+    case PSK_DTYPE_BF16: launch_partial<PSK_DTYPE_BF16>(a, grid, st, ng); break;
+    case PSK_DTYPE_F16: launch_partial<PSK_DTYPE_F16>(a, grid, st, ng); break;
+    default: launch_partial<PSK_DTYPE_F32>(a, grid, st, ng); break;
+  }
+  const int st1 = check_launch("decode_partial_kernel launch");
+  if (st1 != PSK_OK) return st1;
+  const dim3 grid2{unsigned(num_kv_heads), unsigned(num_seqs), 1u};
+  if (out_dtype == PSK_DTYPE_BF16)
+    hipLaunchKernelGGL((decode_combine_kernel<PSK_DTYPE_BF16>), grid2, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((decode_combine_kernel<PSK_DTYPE_F32>), grid2, dim3(256), 0, st, a);
+  return check_launch("decode_combine_kernel launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,264 @@
+// Helpers shared by the HIP translation units of libpipeswift_kv: error
+// reporting for the C ABI, vector load/store widths, element conversions and the
+// FP8 E4M3FN quantization used by the append and the attention reader.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "pipeswift_kv.h"
+
+namespace psk_detail {
+
+constexpr int kWave = 64;
+
+// ----------------------------------------------------------------------------
+// error reporting
+// ----------------------------------------------------------------------------
+
+extern thread_local char g_err[512];
+
+inline int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+inline int hip_fail(hipError_t e, const char* what) {
+  snprintf(g_err, sizeof(g_err), "%s: %s (hipError_t %d)", what, hipGetErrorString(e), (int)e);
+  return (int)e;
+}
+
+inline int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? PSK_OK : hip_fail(e, what);
+}
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+inline int dtype_size(int dt) {
+  switch (dt) {
+    case PSK_DTYPE_F32: return 4;
+    case PSK_DTYPE_F16: return 2;
+    case PSK_DTYPE_BF16: return 2;
+    case PSK_DTYPE_FP8_E4M3FN: return 1;
+    default: return 0;
+  }
+}
+
+inline int log2_exact(int64_t v) {
+  if (v <= 0 || (v & (v - 1))) return -1;
+  int s = 0;
+  while ((int64_t(1) << s) < v) ++s;
+  return s;
+}
+
+// Largest power-of-two byte width <= max_bytes dividing every value in vals.
+inline int common_align(const uint64_t* vals, int n, int max_bytes) {
+  uint64_t acc = 0;
+  for (int i = 0; i < n; ++i) acc |= vals[i];
+  int b = max_bytes;
+  while (b > 1 && (acc & uint64_t(b - 1))) b >>= 1;
+  return b;
+}
+
+// ----------------------------------------------------------------------------
+// vectors and element conversions
+// ----------------------------------------------------------------------------
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+template <int B> struct VecT;
+template <> struct VecT<16> { using T = u32x4; };
+template <> struct VecT<8> { using T = u32x2; };
+template <> struct VecT<4> { using T = uint32_t; };
+template <> struct VecT<2> { using T = uint16_t; };
+template <> struct VecT<1> { using T = uint8_t; };
+
+template <int B>
+__device__ __forceinline__ typename VecT<B>::T vload(const char* p) {
+  return *reinterpret_cast<const typename VecT<B>::T*>(p);
+}
+template <int B>
+__device__ __forceinline__ void vstore(char* p, typename VecT<B>::T v) {
+  *reinterpret_cast<typename VecT<B>::T*>(p) = v;
+}
+// Streaming (nontemporal) variants for data touched once per kernel.
+template <int B>
+__device__ __forceinline__ typename VecT<B>::T vload_nt(const char* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const typename VecT<B>::T*>(p));
+}
+template <int B>
+__device__ __forceinline__ void vstore_nt(char* p, typename VecT<B>::T v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<typename VecT<B>::T*>(p));
+}
+
+template <int DT> struct Elt;
+template <> struct Elt<PSK_DTYPE_F32> {
+  using Bits = uint32_t;
+  static constexpr int kSize = 4;
+  __device__ static float to_f32(Bits b) { return __uint_as_float(b); }
+  __device__ static Bits from_f32(float f) { return __float_as_uint(f); }
+};
+template <> struct Elt<PSK_DTYPE_BF16> {
+  using Bits = uint16_t;
+  static constexpr int kSize = 2;
+  __device__ static float to_f32(Bits b) { return __uint_as_float(uint32_t(b) << 16); }
+  // Round to nearest even; NaN becomes the canonical quiet NaN 0x7FC0.
+  __device__ static Bits from_f32(float f) {
+    uint32_t u = __float_as_uint(f);
+    if (__builtin_isnan(f)) return 0x7FC0;
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return Bits(u >> 16);
+  }
+};
+template <> struct Elt<PSK_DTYPE_F16> {
+  using Bits = uint16_t;
+  static constexpr int kSize = 2;
+  __device__ static float to_f32(Bits b) { return float(__builtin_bit_cast(_Float16, b)); }
+  __device__ static Bits from_f32(float f) { return __builtin_bit_cast(Bits, _Float16(f)); }
+};
+
+// OCP E4M3FN byte for a NaN: 0x7F with the sign bit of the input, which is what
+// torch's float -> float8_e4m3fn conversion produces.
+__device__ __forceinline__ uint32_t e4m3_nan_byte(float x) {
+  return ((__float_as_uint(x) >> 24) & 0x80u) | 0x7Fu;
+}
+
+// E4M3FN bytes 0 and 1 (or 2 and 3 with hi) of w -> floats, native conversion.
+__device__ __forceinline__ f32x2 e4m3_unpack2(uint32_t w, bool hi) {
+  return hi ? __builtin_amdgcn_cvt_pk_f32_fp8(int(w), true) : __builtin_amdgcn_cvt_pk_f32_fp8(int(w), false);
+}
+
+// ---- per-tensor scale, prepared once per wave
+
+// x / s must be the correctly rounded IEEE quotient (the oracle divides in
+// fp32).  With r = RN(1/s) computed once per wave, y = RN(x*r) is within an ulp
+// of x/s, the residual e = x - y*s is exact in one FMA and RN(y + e*r) is the
+// correctly rounded quotient (Markstein's theorem) as long as nothing under- or
+// overflows.  For |s| in [2^-80, 2^100) the only cases outside that are:
+//   * |x| < 2^-100: the quotient is below 2^-20 and converts to a signed zero,
+//     so only its sign matters, which copysign(., y) keeps (also for x = +-0);
+//   * y = +-inf or NaN (x infinite, NaN, or the quotient overflows): y itself
+//     is the right input to the clamp.
+// Any other scale (0, inf, NaN, tiny) takes the plain IEEE division.  A scale
+// of exactly 1.0 (the reference's fixed scale) skips the division.
+struct QScale {
+  float s;
+  float r;
+  bool fast;
+};
+
+__device__ __forceinline__ QScale make_qscale(float s) {
+  QScale q;
+  q.s = s;
+  q.r = 1.0f / s;
+  const float a = __builtin_fabsf(s);
+  q.fast = a >= 0x1p-80f && a < 0x1p100f;
+  return q;
+}
+
+// Exact for s == 1.0 as well: r = 1, y = x, e = 0.
+__device__ __forceinline__ float div_fast(float x, const QScale& q) {
+  const float y = x * q.r;
+  const float e = __builtin_fmaf(-y, q.s, x);
+  const float z = __builtin_copysignf(__builtin_fmaf(e, q.r, y), y);
+  return __builtin_fabsf(y) < __builtin_inff() ? z : y;
+}
+
+// ---- conversion policies: In vector (IN_B bytes) -> Out vector (OUT_B bytes)
+
+template <int B>
+struct CopyConv {
+  static constexpr int IN_B = B;
+  static constexpr int OUT_B = B;
+  using In = typename VecT<B>::T;
+  using Out = typename VecT<B>::T;
+  __device__ static Out apply(In v, const QScale&) { return v; }
+  __device__ static Out zero() { return Out(0); }
+};
+
+// E input elements of type IN_DT -> E E4M3FN bytes, q = e4m3(clamp(x / scale)).
+// The clamp is v_med3_f32 (exact for every non-NaN input, +-inf included);
+// the native convert turns NaN into 0xFF, so NaN lanes are patched to torch's
+// 0x7F|sign afterwards (rare path).
+template <int IN_DT, int E>
+struct QuantConv {
+  using EltT = Elt<IN_DT>;
+  static constexpr int IN_B = E * EltT::kSize;
+  static constexpr int OUT_B = E;
+  using In = typename VecT<IN_B>::T;
+  using Out = typename VecT<OUT_B>::T;
+  __device__ static Out apply(In v, const QScale& qs) {
+    typename EltT::Bits e[E];
+    __builtin_memcpy(e, &v, sizeof(v));
+    float f[E];
+    if (__builtin_expect(qs.fast, 1)) {
+#pragma unroll
+      for (int i = 0; i < E; ++i) f[i] = div_fast(EltT::to_f32(e[i]), qs);
+    } else {
+      // scales outside [2^-80, 2^100) (0, inf, NaN, subnormal): IEEE division
+#pragma unroll
+      for (int i = 0; i < E; ++i) f[i] = EltT::to_f32(e[i]) / qs.s;
+    }
+    bool any_nan = false;
+#pragma unroll
+    for (int i = 0; i < E; ++i) any_nan |= __builtin_isnan(f[i]);
+    uint8_t o[E];
+#pragma unroll
+    for (int i = 0; i < E; i += 2) {
+      const float a = __builtin_amdgcn_fmed3f(f[i], -448.0f, 448.0f);
+      const float b = i + 1 < E ? __builtin_amdgcn_fmed3f(f[i + 1], -448.0f, 448.0f) : 0.0f;
+      const uint32_t w = uint32_t(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false));
+      o[i] = uint8_t(w);
+      if (i + 1 < E) o[i + 1] = uint8_t(w >> 8);
+    }
+    if (__builtin_expect(any_nan, 0)) {
+#pragma unroll
+      for (int i = 0; i < E; ++i)
+        if (__builtin_isnan(f[i])) o[i] = uint8_t(e4m3_nan_byte(f[i]));
+    }
+    Out r;
+    __builtin_memcpy(&r, o, sizeof(r));
+    return r;
+  }
+  __device__ static Out zero() { return Out(0); }
+};
+
+// E E4M3FN bytes -> E elements of OUT_DT, y = round(float(q) * scale).
+template <int OUT_DT, int E>
+struct DequantConv {
+  using EltT = Elt<OUT_DT>;
+  static constexpr int IN_B = E;
+  static constexpr int OUT_B = E * EltT::kSize;
+  using In = typename VecT<IN_B>::T;
+  using Out = typename VecT<OUT_B>::T;
+  __device__ static Out apply(In v, const QScale& qs) {
+    uint8_t q[E];
+    __builtin_memcpy(q, &v, sizeof(v));
+    typename EltT::Bits o[E];
+    if constexpr (E == 1) {
+      o[0] = EltT::from_f32(e4m3_unpack2(uint32_t(q[0]), false).x * qs.s);
+    } else {
+#pragma unroll
+      for (int i = 0; i < E; i += 2) {
+        const f32x2 f = e4m3_unpack2(uint32_t(q[i]) | (uint32_t(q[i + 1]) << 8), false);
+        o[i] = EltT::from_f32(f.x * qs.s);
+        o[i + 1] = EltT::from_f32(f.y * qs.s);
+      }
+    }
+    Out r;
+    __builtin_memcpy(&r, o, sizeof(r));
+    return r;
+  }
+  __device__ static Out zero() { return Out(0); }
+};
+
+}  // namespace psk_detail
