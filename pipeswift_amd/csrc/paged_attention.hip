@@ -183,13 +183,7 @@ __device__ __forceinline__ TileLoads load_tile(const DecodeArgs& a, const PageId
 // 32 FP8 query bytes of this lane's MFMA row (query head h*G + lane%16, d from
 // 32 * (lane / 16)); zero rows beyond the group.
 template <int Q_DT>
-__device__ __forceinline__ void load_query(const DecodeArgs& a, int b, int h, float qd, int lane, uint32_t qw[8]) {
-#pragma unroll
-  for (int i = 0; i < 8; ++i) qw[i] = 0;
-  const int row = lane & 15;
-  if (row >= a.group) return;
-  const char* src = a.q + b * a.q_tok_stride + int64_t(h * a.group + row) * a.q_head_stride;
-  const int d0 = 32 * (lane >> 4);
+__device__ __forceinline__ void load_query_as(const char* src, float qd, int d0, uint32_t qw[8]) {
   if constexpr (Q_DT == PSK_DTYPE_FP8_E4M3FN) {
     const u32x4 lo = *reinterpret_cast<const u32x4*>(src + d0);
     const u32x4 hi = *reinterpret_cast<const u32x4*>(src + d0 + 16);
@@ -214,22 +208,144 @@ __device__ __forceinline__ void load_query(const DecodeArgs& a, int b, int h, fl
   }
 }
 
-template <int Q_DT, int NG>
-__global__ void __launch_bounds__(kWaves * 64) decode_partial_kernel(DecodeArgs a) {
+__device__ __forceinline__ void load_query(const DecodeArgs& a, int q_dtype, int b, int h, float qd, int lane,
+                                           uint32_t qw[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) qw[i] = 0;
+  const int row = lane & 15;
+  if (row >= a.group) return;
+  const char* src = a.q + b * a.q_tok_stride + int64_t(h * a.group + row) * a.q_head_stride;
+  const int d0 = 32 * (lane >> 4);
+  switch (q_dtype) {
+    case PSK_DTYPE_FP8_E4M3FN: load_query_as<PSK_DTYPE_FP8_E4M3FN>(src, qd, d0, qw); break;
+    case PSK_DTYPE_BF16: load_query_as<PSK_DTYPE_BF16>(src, qd, d0, qw); break;
+    case PSK_DTYPE_F16: load_query_as<PSK_DTYPE_F16>(src, qd, d0, qw); break;
+    default: load_query_as<PSK_DTYPE_F32>(src, qd, d0, qw); break;
+  }
+}
+
+// Tile addressing when the block size is a power of two >= 16: a 16-token tile
+// (tiles start at multiples of 16) lies in one page, so its page id and row
+// base are wave-uniform and every lane adds a fixed 32-bit offset.
+struct LaneOffsets {
+  uint32_t k, va, vb;
+};
+
+__device__ __forceinline__ TileLoads load_tile_uniform(const DecodeArgs& a, const PageIds& ids, int h, int t0,
+                                                       const LaneOffsets& off) {
+  TileLoads r;
+  const int pi = t0 >> a.bs_shift;
+  const int32_t pid =
+      __builtin_amdgcn_readfirstlane(ids.staged ? ids.lds[pi - ids.first] : checked_page(a, ids.bt_row, pi));
+  if (pid < 0) {
+    r.k0 = r.k1 = r.va = r.vb = u32x4(0);
+    return r;
+  }
+  const int64_t row0 = t0 & (a.block_size - 1);
+  const uint8_t* kb = a.k + int64_t(pid) * a.k_blk + row0 * a.k_row + int64_t(h) * a.k_head;
+  const uint8_t* vb = a.v + int64_t(pid) * a.v_blk + row0 * a.v_row + int64_t(h) * a.v_head;
+  r.k0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kb + off.k));
+  r.k1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kb + off.k + 16));
+  r.va = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vb + off.va));
+  r.vb = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vb + off.vb));
+  return r;
+}
+
+// Running softmax of one lane: per query head of the group the running
+// maximum m (exp2 domain), its lazy threshold mth = m + kLazy, the sum l of
+// exp2(s - m) and the weighted sum acc of the lane's 16 V columns.
+template <int NG>
+struct Softmax {
+  float m[NG], mth[NG], l[NG], acc[NG][16];
+};
+
+// One 16-token tile of one wave.  The MFMA leaves S[g][t] in lane
+// 16 * (g / 4) + t, register g % 4; the scores are scaled (and, in a PARTIAL
+// tile, tokens at or past t_end masked to -inf) there, then each lane pulls the
+// scores of its two tokens.  With NEXT the tile's registers are refilled with
+// the loads of tile t0 + stride as soon as its K and V are consumed, so they fly
+// during the softmax and P V.
+template <int NG, bool PARTIAL, bool NEXT, class Loader>
+__device__ __forceinline__ void attend_step(Softmax<NG>& st, TileLoads& c, const bf16x8 qop[4], float sl, int t0,
+                                            int t_end, int stride, int lane, const Loader& load) {
+  const int tv = lane >> 3;
+  f32x4 sc = {0.0f, 0.0f, 0.0f, 0.0f};
+  sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qop[0], e4m3x8_to_bf16(c.k0[0], c.k0[1]), sc, 0, 0, 0);
+  sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qop[1], e4m3x8_to_bf16(c.k0[2], c.k0[3]), sc, 0, 0, 0);
+  sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qop[2], e4m3x8_to_bf16(c.k1[0], c.k1[1]), sc, 0, 0, 0);
+  sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qop[3], e4m3x8_to_bf16(c.k1[2], c.k1[3]), sc, 0, 0, 0);
+  float fa[16], fb[16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t wa = c.va[i], wb = c.vb[i];
+    if constexpr (PARTIAL) {
+      // rows past t_end may hold anything (a NaN would survive p = 0)
+      wa = t0 + tv < t_end ? wa : 0u;
+      wb = t0 + tv + 8 < t_end ? wb : 0u;
+    }
+    const f32x2 a0 = e4m3_unpack2(wa, false), a1 = e4m3_unpack2(wa, true);
+    const f32x2 b0 = e4m3_unpack2(wb, false), b1 = e4m3_unpack2(wb, true);
+    fa[4 * i] = a0.x;
+    fa[4 * i + 1] = a0.y;
+    fa[4 * i + 2] = a1.x;
+    fa[4 * i + 3] = a1.y;
+    fb[4 * i] = b0.x;
+    fb[4 * i + 1] = b0.y;
+    fb[4 * i + 2] = b1.x;
+    fb[4 * i + 3] = b1.y;
+  }
+  if constexpr (NEXT) c = load(t0 + stride);
+
+  float s4[4];
+  const bool col_ok = !PARTIAL || t0 + (lane & 15) < t_end;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) s4[r] = col_ok ? sc[r] * sl : -__builtin_inff();
+  float sa[NG], sb[NG];
+  bool raise = false;
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    sa[g] = bperm(16 * (g >> 2) + tv, s4[g & 3]);
+    sb[g] = bperm(16 * (g >> 2) + tv + 8, s4[g & 3]);
+    raise |= __builtin_fmaxf(sa[g], sb[g]) > st.mth[g];
+  }
+  if (__any(raise)) {
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      const float mn = __builtin_fmaxf(st.m[g], __builtin_fmaxf(sa[g], sb[g]));
+      const float cr = __builtin_amdgcn_exp2f(st.m[g] - mn);
+      st.l[g] *= cr;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) st.acc[g][k] *= cr;
+      st.m[g] = mn;
+      st.mth[g] = mn + kLazy;
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    const float pa = __builtin_amdgcn_exp2f(sa[g] - st.m[g]);
+    const float pb = __builtin_amdgcn_exp2f(sb[g] - st.m[g]);
+    st.l[g] += pa + pb;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) st.acc[g][k] = __builtin_fmaf(pa, fa[k], __builtin_fmaf(pb, fb[k], st.acc[g][k]));
+  }
+}
+
+template <int NG, bool UNIFORM>
+__global__ void __launch_bounds__(kWaves * 64) decode_partial_kernel(DecodeArgs a, int q_dtype) {
   const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int len = a.seq_lens[b];
   const int t_begin = s * a.split;
   if (t_begin >= len || s >= a.max_splits) return;  // uniform over the workgroup
   const int t_end = min(len, t_begin + a.split);
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
   const int G = a.group;
 
   const float qd = descale(a.qd, a.qd_b, a.qd_h, b, h);
   const float kd = descale(a.kd, a.kd_b, a.kd_h, b, h);
   const float sl = a.scale_log2 * qd * kd;
   uint32_t qw[8];
-  load_query<Q_DT>(a, b, h, qd, lane, qw);
+  load_query(a, q_dtype, b, h, qd, lane, qw);
   const bf16x8 qop[4] = {e4m3x8_to_bf16(qw[0], qw[1]), e4m3x8_to_bf16(qw[2], qw[3]), e4m3x8_to_bf16(qw[4], qw[5]),
                          e4m3x8_to_bf16(qw[6], qw[7])};
 
@@ -245,91 +361,47 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_kernel(DecodeArgs 
     __syncthreads();
   }
 
-  float m[NG], l[NG], acc[NG][16];
+  Softmax<NG> st;
 #pragma unroll
   for (int g = 0; g < NG; ++g) {
-    m[g] = kNegBig;
-    l[g] = 0.0f;
+    st.m[g] = kNegBig;
+    st.mth[g] = kNegBig + kLazy;
+    st.l[g] = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) acc[g][k] = 0.0f;
+    for (int k = 0; k < 16; ++k) st.acc[g][k] = 0.0f;
   }
+  LaneOffsets off;
+  off.k = uint32_t((lane & 15) * a.k_row + 32 * (lane >> 4));
+  off.va = uint32_t((lane >> 3) * a.v_row + 16 * (lane & 7));
+  off.vb = uint32_t(off.va + 8 * a.v_row);
 
+  auto tile = [&](int t) -> TileLoads {
+    if constexpr (UNIFORM) return load_tile_uniform(a, ids, h, t, off);
+    else return load_tile(a, ids, h, t, t_end, lane);
+  };
+  // every tile of a wave but its last lies below t_end
   const int stride = kTile * kWaves;
-  const int tv = lane >> 3;
   int t0 = t_begin + wave * kTile;
-  TileLoads cur;
-  if (t0 < t_end) cur = load_tile(a, ids, h, t0, t_end, lane);
-  for (; t0 < t_end; t0 += stride) {
-    TileLoads nxt;
-    nxt.k0 = nxt.k1 = nxt.va = nxt.vb = u32x4(0);
-    if (t0 + stride < t_end) nxt = load_tile(a, ids, h, t0 + stride, t_end, lane);
-
-    // S[g][t]: lane l, register r holds query row 4*(l/16)+r, token l%16
-    f32x4 sc = {0.0f, 0.0f, 0.0f, 0.0f};
-    sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qop[0], e4m3x8_to_bf16(cur.k0[0], cur.k0[1]), sc, 0, 0, 0);
-    sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qop[1], e4m3x8_to_bf16(cur.k0[2], cur.k0[3]), sc, 0, 0, 0);
-    sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qop[2], e4m3x8_to_bf16(cur.k1[0], cur.k1[1]), sc, 0, 0, 0);
-    sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qop[3], e4m3x8_to_bf16(cur.k1[2], cur.k1[3]), sc, 0, 0, 0);
-
-    // scores of this lane's two tokens for every head of the group
-    const bool va_ok = t0 + tv < t_end, vb_ok = t0 + tv + 8 < t_end;
-    float sa[NG], sb[NG];
-    bool raise = false;
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-      const float ra = bperm(16 * (g >> 2) + tv, sc[g & 3]);
-      const float rb = bperm(16 * (g >> 2) + tv + 8, sc[g & 3]);
-      sa[g] = va_ok ? ra * sl : -__builtin_inff();
-      sb[g] = vb_ok ? rb * sl : -__builtin_inff();
-      raise |= __builtin_fmaxf(sa[g], sb[g]) > m[g] + kLazy;
-    }
-    if (__any(raise)) {
-#pragma unroll
-      for (int g = 0; g < NG; ++g) {
-        const float mn = __builtin_fmaxf(m[g], __builtin_fmaxf(sa[g], sb[g]));
-        const float c = __builtin_amdgcn_exp2f(m[g] - mn);
-        l[g] *= c;
-#pragma unroll
-        for (int k = 0; k < 16; ++k) acc[g][k] *= c;
-        m[g] = mn;
-      }
-    }
-    float pa[NG], pb[NG];
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-      pa[g] = __builtin_amdgcn_exp2f(sa[g] - m[g]);
-      pb[g] = __builtin_amdgcn_exp2f(sb[g] - m[g]);
-      l[g] += pa[g] + pb[g];
-    }
-    float fa[16], fb[16];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const f32x2 a0 = e4m3_unpack2(cur.va[i], false), a1 = e4m3_unpack2(cur.va[i], true);
-      const f32x2 b0 = e4m3_unpack2(cur.vb[i], false), b1 = e4m3_unpack2(cur.vb[i], true);
-      fa[4 * i] = a0.x; fa[4 * i + 1] = a0.y; fa[4 * i + 2] = a1.x; fa[4 * i + 3] = a1.y;
-      fb[4 * i] = b0.x; fb[4 * i + 1] = b0.y; fb[4 * i + 2] = b1.x; fb[4 * i + 3] = b1.y;
-    }
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-#pragma unroll
-      for (int k = 0; k < 16; ++k) acc[g][k] = __builtin_fmaf(pa[g], fa[k], __builtin_fmaf(pb[g], fb[k], acc[g][k]));
-    }
-    cur = nxt;
+  if (t0 < t_end) {
+    TileLoads c = tile(t0);
+    for (; t0 + stride < t_end; t0 += stride)
+      attend_step<NG, false, true>(st, c, qop, sl, t0, t_end, stride, lane, tile);
+    attend_step<NG, true, false>(st, c, qop, sl, t0, t_end, stride, lane, tile);
   }
 
   // merge the eight token slots of the wave (lanes differing in bits 3..5)
 #pragma unroll
-  for (int off = 8; off < 64; off <<= 1) {
+  for (int o = 8; o < 64; o <<= 1) {
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
-      const float mo = __shfl_xor(m[g], off);
-      const float lo = __shfl_xor(l[g], off);
-      const float mn = __builtin_fmaxf(m[g], mo);
-      const float ca = __builtin_amdgcn_exp2f(m[g] - mn), cb = __builtin_amdgcn_exp2f(mo - mn);
-      l[g] = l[g] * ca + lo * cb;
+      const float mo = __shfl_xor(st.m[g], o);
+      const float lo = __shfl_xor(st.l[g], o);
+      const float mn = __builtin_fmaxf(st.m[g], mo);
+      const float ca = __builtin_amdgcn_exp2f(st.m[g] - mn), cb = __builtin_amdgcn_exp2f(mo - mn);
+      st.l[g] = st.l[g] * ca + lo * cb;
 #pragma unroll
-      for (int k = 0; k < 16; ++k) acc[g][k] = acc[g][k] * ca + __shfl_xor(acc[g][k], off) * cb;
-      m[g] = mn;
+      for (int k = 0; k < 16; ++k) st.acc[g][k] = st.acc[g][k] * ca + __shfl_xor(st.acc[g][k], o) * cb;
+      st.m[g] = mn;
     }
   }
 
@@ -340,14 +412,14 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_kernel(DecodeArgs 
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
 #pragma unroll
-      for (int k = 0; k < 16; ++k) s_acc[wave][g][16 * lane + k] = acc[g][k];
+      for (int k = 0; k < 16; ++k) s_acc[wave][g][16 * lane + k] = st.acc[g][k];
     }
   }
   if (lane == 0) {
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
-      s_m[wave][g] = m[g];
-      s_l[wave][g] = l[g];
+      s_m[wave][g] = st.m[g];
+      s_l[wave][g] = st.l[g];
     }
   }
   __syncthreads();
@@ -376,7 +448,9 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_kernel(DecodeArgs 
   }
 }
 
-// One workgroup per (kv head, sequence): merge the sequence's partials.
+// One workgroup per (kv head, sequence): each wave turns a head's split maxima
+// and sums into normalised weights in LDS, then every thread sums a (head,
+// column) over the splits with independent loads.
 template <int OUT_DT>
 __global__ void __launch_bounds__(256) decode_combine_kernel(DecodeArgs a) {
   const int h = blockIdx.x, b = blockIdx.y;
@@ -386,24 +460,47 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(DecodeArgs a) {
   const float vd = descale(a.vd, a.vd_b, a.vd_h, b, h);
   const int rec = G * (kHead + 2);
   const float* part = a.part + (int64_t(b) * a.num_kv_heads + h) * a.max_splits * rec;
+  __shared__ float s_w[kMaxSplits * 8];  // weight of split s for head g at [s * 8 + g]
+  __shared__ float s_lse[8];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int g = wave; g < G; g += 4) {
+    float m0 = kNegBig, m1 = kNegBig, l0 = 0.0f, l1 = 0.0f;
+    if (lane < n) {
+      m0 = part[lane * rec + g];
+      l0 = part[lane * rec + G + g];
+    }
+    if (lane + 64 < n) {
+      m1 = part[(lane + 64) * rec + g];
+      l1 = part[(lane + 64) * rec + G + g];
+    }
+    float mx = __builtin_fmaxf(m0, m1);
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, o));
+    const float w0 = __builtin_amdgcn_exp2f(m0 - mx), w1 = __builtin_amdgcn_exp2f(m1 - mx);
+    float den = l0 * w0 + l1 * w1;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) den += __shfl_xor(den, o);
+    const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+    if (lane < n) s_w[lane * 8 + g] = w0 * inv;
+    if (lane + 64 < n) s_w[(lane + 64) * 8 + g] = w1 * inv;
+    // natural-log sum of exp(s): 2^mx * den in the exp2 domain
+    if (lane == 0) s_lse[g] = den > 0.0f ? (mx + __builtin_log2f(den)) * 0.6931471805599453f : -__builtin_inff();
+  }
+  __syncthreads();
   for (int i = threadIdx.x; i < G * kHead; i += blockDim.x) {
     const int g = i / kHead, d = i % kHead;
-    float mx = kNegBig;
-    for (int s = 0; s < n; ++s) mx = __builtin_fmaxf(mx, part[s * rec + g]);
-    float num = 0.0f, den = 0.0f;
-    for (int s = 0; s < n; ++s) {
-      const float c = __builtin_amdgcn_exp2f(part[s * rec + g] - mx);
-      num += part[s * rec + 2 * G + i] * c;
-      den += part[s * rec + G + g] * c;
+    const float* x = part + 2 * G + i;
+    float o = 0.0f;
+    int sp = 0;
+    for (; sp + 4 <= n; sp += 4) {
+      const float x0 = x[sp * rec], x1 = x[(sp + 1) * rec], x2 = x[(sp + 2) * rec], x3 = x[(sp + 3) * rec];
+      o += x0 * s_w[sp * 8 + g] + x1 * s_w[(sp + 1) * 8 + g] + x2 * s_w[(sp + 2) * 8 + g] +
+           x3 * s_w[(sp + 3) * 8 + g];
     }
-    const float o = den > 0.0f ? num / den * vd : 0.0f;
+    for (; sp < n; ++sp) o += x[sp * rec] * s_w[sp * 8 + g];
     char* dst = a.out + b * a.out_tok_stride + int64_t(h * G + g) * a.out_head_stride;
-    reinterpret_cast<typename Elt<OUT_DT>::Bits*>(dst)[d] = Elt<OUT_DT>::from_f32(o);
-    if (d == 0 && a.lse) {
-      // natural-log sum of exp(s): 2^mx * den in the exp2 domain
-      a.lse[int64_t(h * G + g) * a.lse_head_stride + b] =
-          den > 0.0f ? (mx + __builtin_log2f(den)) * 0.6931471805599453f : -__builtin_inff();
-    }
+    reinterpret_cast<typename Elt<OUT_DT>::Bits*>(dst)[d] = Elt<OUT_DT>::from_f32(o * vd);
+    if (d == 0 && a.lse) a.lse[int64_t(h * G + g) * a.lse_head_stride + b] = s_lse[g];
   }
 }
 
@@ -413,13 +510,14 @@ int decode_split(int64_t max_seq_len) {
   return int(split);
 }
 
-template <int Q_DT>
-void launch_partial(const DecodeArgs& a, dim3 grid, hipStream_t st, int ng) {
+template <bool UNIFORM>
+void launch_partial(const DecodeArgs& a, int q_dtype, dim3 grid, hipStream_t st, int ng) {
+  const dim3 block(kWaves * 64);
   switch (ng) {
-    case 1: hipLaunchKernelGGL((decode_partial_kernel<Q_DT, 1>), grid, dim3(kWaves * 64), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((decode_partial_kernel<Q_DT, 2>), grid, dim3(kWaves * 64), 0, st, a); break;
-    case 4: hipLaunchKernelGGL((decode_partial_kernel<Q_DT, 4>), grid, dim3(kWaves * 64), 0, st, a); break;
-    default: hipLaunchKernelGGL((decode_partial_kernel<Q_DT, 8>), grid, dim3(kWaves * 64), 0, st, a); break;
+    case 1: hipLaunchKernelGGL((decode_partial_kernel<1, UNIFORM>), grid, block, 0, st, a, q_dtype); break;
+    case 2: hipLaunchKernelGGL((decode_partial_kernel<2, UNIFORM>), grid, block, 0, st, a, q_dtype); break;
+    case 4: hipLaunchKernelGGL((decode_partial_kernel<4, UNIFORM>), grid, block, 0, st, a, q_dtype); break;
+    default: hipLaunchKernelGGL((decode_partial_kernel<8, UNIFORM>), grid, block, 0, st, a, q_dtype); break;
   }
 }
 
@@ -519,12 +617,10 @@ int psk_paged_decode_attention(const void* q, int64_t q_tok_stride, int64_t q_he
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int ng = G == 1 ? 1 : G == 2 ? 2 : G <= 4 ? 4 : 8;
   const dim3 grid{unsigned(a.max_splits), unsigned(num_kv_heads), unsigned(num_seqs)};
-  switch (q_dtype) {
-    case PSK_DTYPE_FP8_E4M3FN: launch_partial<PSK_DTYPE_FP8_E4M3FN>(a, grid, st, ng); break;
-    case PSK_DTYPE_BF16: launch_partial<PSK_DTYPE_BF16>(a, grid, st, ng); break;
-    case PSK_DTYPE_F16: launch_partial<PSK_DTYPE_F16>(a, grid, st, ng); break;
-    default: launch_partial<PSK_DTYPE_F32>(a, grid, st, ng); break;
-  }
+  // a 16-token tile stays in one page when the block size is a power of two >= 16
+  const bool uniform = a.bs_shift >= 4 && 16 * std::max(a.k_row, a.v_row) < (int64_t(1) << 31);
+  if (uniform) launch_partial<true>(a, q_dtype, grid, st, ng);
+  else launch_partial<false>(a, q_dtype, grid, st, ng);
   const int st1 = check_launch("decode_partial_kernel launch");
   if (st1 != PSK_OK) return st1;
   const dim3 grid2{unsigned(num_kv_heads), unsigned(num_seqs), 1u};
