@@ -155,12 +155,13 @@ def setup_decode_attention(args, device):
     q = (torch.randn(R, B, Hq, D, device=device, generator=dgen) * 2.0).to(torch.bfloat16)
     scales = torch.tensor([0.01, 0.02], dtype=torch.float32, device=device)
     out = torch.empty(B, Hq, D, dtype=torch.bfloat16, device=device)
-    ws = torch.empty(attention.workspace_floats(B, Hq, H, W * ps), dtype=torch.float32, device=device)
+    ws = torch.empty(attention.workspace_floats(B, Hq, H, W * ps, args.num_splits), dtype=torch.float32,
+                     device=device)
     kc, vc = cache[:, 0], cache[:, 1]
 
     def launch(i):
         attention.paged_decode_attention(q[i], kc, vc, bt, lens, D ** -0.5, None, scales[0:1], scales[1:2], out=out,
-                                         workspace=ws)
+                                         workspace=ws, num_splits=args.num_splits)
 
     total = int(ctx.sum())
     pages = int(sum(len(t) for t in tables))
@@ -171,7 +172,7 @@ def setup_decode_attention(args, device):
         "rotate": R,
         "config": {"workload": "FP8 paged decode attention (config 2 cache)", "sequences": B, "context_tokens": total,
                    "kv_heads": H, "q_heads": Hq, "head_dim": D, "block_size": ps, "num_blocks": cache.shape[0],
-                   "split_tokens": "512 (64 splits at 32768)", "descales": "per-tensor K/V"},
+                   "num_splits": args.num_splits or "auto", "descales": "per-tensor K/V"},
         "cpu": lambda: cpu_decode_attention(kc, vc, bt, ctx, q[0], scales, total * H * D * 2),
     }
     return launch, info
@@ -755,6 +756,7 @@ def main():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--transports", default="blit,memcpy", help="swap workload: transports to compare")
     p.add_argument("--swap-reps", type=int, default=3)
+    p.add_argument("--num-splits", type=int, default=0, help="decode_attention: splits of the longest sequence (0: auto)")
     args = p.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:

@@ -240,6 +240,8 @@ int64_t psk_build_kv_metadata(int64_t num_seqs, const uint64_t* page_table_ptrs,
  * block_table[b * block_table_stride + j / block_size]; entries past
  * block_table_width or outside [0, num_blocks) read as zero rows.
  * max_seq_len bounds every seq_lens[b] (block_table_width * block_size does).
+ * num_splits: how many workgroups share the longest sequence (flash-decoding
+ * split, as FA's num_splits); 0 chooses.  At most 128 splits are used.
  * out: bf16 or f32 at element strides (out_tok_stride, out_head_stride); lse
  * (fp32, optional) at lse[hq * lse_head_stride + b]; a sequence of length 0
  * writes zeros and lse = -inf.  workspace: device floats, at least
@@ -251,7 +253,8 @@ int psk_paged_decode_attention(const void* q, int64_t q_tok_stride, int64_t q_he
                                int64_t block_table_stride, int64_t block_table_width,
                                const int32_t* seq_lens, int64_t num_seqs, int64_t num_q_heads,
                                int64_t num_kv_heads, int64_t head_size, int64_t block_size,
-                               int64_t num_blocks, int64_t max_seq_len, float softmax_scale,
+                               int64_t num_blocks, int64_t max_seq_len, int64_t num_splits,
+                               float softmax_scale,
                                const float* q_descale, const float* k_descale,
                                const float* v_descale, const int64_t* descale_strides, void* out,
                                int64_t out_tok_stride, int64_t out_head_stride, int out_dtype,
@@ -259,7 +262,7 @@ int psk_paged_decode_attention(const void* q, int64_t q_tok_stride, int64_t q_he
                                int64_t workspace_len, void* stream);
 
 int64_t psk_paged_decode_workspace_len(int64_t num_seqs, int64_t num_q_heads, int64_t num_kv_heads,
-                                       int64_t max_seq_len);
+                                       int64_t max_seq_len, int64_t num_splits);
 
 /*
  * Pinned, device-mapped host memory for the L2 mirror and swap staging

@@ -78,9 +78,9 @@ _SIGNATURES = {
     "psk_paged_decode_attention": (
         _int,
         [_vp, _i64, _i64, _int, _vp, _vp, _c_int64_p, _c_int64_p, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64,
-         _i64, _i64, ctypes.c_float, _vp, _vp, _vp, _c_int64_p, _vp, _i64, _i64, _int, _vp, _i64, _vp, _i64, _vp],
+         _i64, _i64, _i64, ctypes.c_float, _vp, _vp, _vp, _c_int64_p, _vp, _i64, _i64, _int, _vp, _i64, _vp, _i64, _vp],
     ),
-    "psk_paged_decode_workspace_len": (_i64, [_i64, _i64, _i64, _i64]),
+    "psk_paged_decode_workspace_len": (_i64, [_i64, _i64, _i64, _i64, _i64]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)

@@ -29,8 +29,8 @@ MAX_GROUP = 8
 _OUT_CODES = {torch.bfloat16: 2, torch.float32: 0}
 
 
-def workspace_floats(num_seqs: int, num_q_heads: int, num_kv_heads: int, max_seq_len: int) -> int:
-    n = int(lib().psk_paged_decode_workspace_len(num_seqs, num_q_heads, num_kv_heads, max_seq_len))
+def workspace_floats(num_seqs: int, num_q_heads: int, num_kv_heads: int, max_seq_len: int, num_splits: int = 0) -> int:
+    n = int(lib().psk_paged_decode_workspace_len(num_seqs, num_q_heads, num_kv_heads, max_seq_len, num_splits))
     if n < 0:
         check(n, "paged decode workspace")
     return n
@@ -64,6 +64,7 @@ def paged_decode_attention(
     return_softmax_lse: bool = False,
     max_seq_len: Optional[int] = None,
     workspace: Optional[torch.Tensor] = None,
+    num_splits: int = 0,
 ):
     """One decode step of attention for every sequence.
 
@@ -73,6 +74,7 @@ def paged_decode_attention(
     [P, 2, ps, H, D] layer are fine).  block_table: int32 [B, W];
     seq_lens: int32 [B] (``seqused_k``).  Returns out [B, Hq, 128] (bf16 unless
     ``out`` is given as float32) and, when asked, lse [Hq, B] float32.
+    ``num_splits``: workgroups per longest sequence (0 chooses), as FA's.
     """
     assert q.is_cuda and k_cache.is_cuda and v_cache.is_cuda
     assert q.dim() == 3 and q.shape[2] == HEAD_DIM and q.stride(2) == 1, "q must be [B, Hq, 128] with unit last stride"
@@ -94,7 +96,7 @@ def paged_decode_attention(
         out = torch.empty(B, Hq, HEAD_DIM, dtype=torch.bfloat16, device=device)
     assert out.dtype in _OUT_CODES and out.shape == (B, Hq, HEAD_DIM) and out.stride(2) == 1
     lse = torch.empty(Hq, B, dtype=torch.float32, device=device) if return_softmax_lse else None
-    need = workspace_floats(B, Hq, Hkv, max_seq_len)
+    need = workspace_floats(B, Hq, Hkv, max_seq_len, num_splits)
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(max(need, 1), dtype=torch.float32, device=device)
     qd, qsb, qsh = _descale(q_descale, B, Hkv, device)
@@ -104,7 +106,7 @@ def paged_decode_attention(
         q.data_ptr(), q.stride(0), q.stride(1), dtype_code(q.dtype),
         k_cache.data_ptr(), v_cache.data_ptr(), i64_array(k_cache.stride()[:3]), i64_array(v_cache.stride()[:3]),
         block_table.data_ptr(), block_table.stride(0), block_table.shape[1], seq_lens.data_ptr(), B, Hq, Hkv,
-        HEAD_DIM, ps, P, int(max_seq_len), float(softmax_scale), ptr(qd), ptr(kd), ptr(vd),
+        HEAD_DIM, ps, P, int(max_seq_len), int(num_splits), float(softmax_scale), ptr(qd), ptr(kd), ptr(vd),
         i64_array([qsb, qsh, ksb, ksh, vsb, vsh]), out.data_ptr(), out.stride(0), out.stride(1),
         _OUT_CODES[out.dtype], ptr(lse), B if lse is not None else 0, workspace.data_ptr(), workspace.numel(),
         stream_handle(device),
@@ -136,9 +138,9 @@ def flash_attn_varlen_func(
     (attention.py:166-184), for decode: q is [total_q, Hq, D] with one token per
     sequence (``max_seqlen_q == 1``; ``cu_seqlens_q`` then is 0..B and
     ``causal`` has nothing to mask).  ``max_seqlen_k`` bounds the lengths when
-    given, else the block table's width does.  ``num_splits`` and
-    ``fa_version`` are accepted for signature compatibility; the split is chosen
-    from the length bound."""
+    given, else the block table's width does.  ``num_splits`` is the
+    flash-decoding split count (0 chooses); ``fa_version`` is accepted for
+    signature compatibility."""
     assert max_seqlen_q == 1, "decode only: one query token per sequence"
     assert seqused_k is not None and block_table is not None, "paged decode needs seqused_k and block_table"
     B = seqused_k.shape[0]
@@ -146,4 +148,5 @@ def flash_attn_varlen_func(
     ps = k.shape[1]
     bound = block_table.shape[1] * ps if max_seqlen_k is None else min(int(max_seqlen_k), block_table.shape[1] * ps)
     return paged_decode_attention(q, k, v, block_table, seqused_k, softmax_scale, q_descale, k_descale, v_descale,
-                                  out=out, return_softmax_lse=return_softmax_lse, max_seq_len=bound)
+                                  out=out, return_softmax_lse=return_softmax_lse, max_seq_len=bound,
+                                  num_splits=num_splits)

@@ -58,11 +58,16 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 constexpr int kHead = 128;    // head_dim of the MFMA tiling
 constexpr int kTile = 16;     // tokens per tile (N of the 16x16x32 MFMA)
 constexpr int kWaves = 4;     // waves per workgroup
-constexpr int kMinSplit = 512;
+constexpr int kMinSplit = 1024;
 constexpr int kMaxSplits = 128;
 constexpr float kNegBig = -1.0e30f;  // finite "no token yet" maximum
 constexpr float kLazy = 8.0f;        // raise the running max past 2^8 headroom only
 constexpr int kPageCache = 512;      // page ids of a split staged in LDS
+constexpr int kRing = 3;             // LDS tile slots per wave (ring kernel)
+constexpr int kRingPages = 1024;     // page ids of a split in the ring kernel
+
+typedef __attribute__((address_space(1))) void gvoid;
+typedef __attribute__((address_space(3))) void lvoid;
 
 struct DecodeArgs {
   const char* q;
@@ -262,12 +267,12 @@ struct Softmax {
 // One 16-token tile of one wave.  The MFMA leaves S[g][t] in lane
 // 16 * (g / 4) + t, register g % 4; the scores are scaled (and, in a PARTIAL
 // tile, tokens at or past t_end masked to -inf) there, then each lane pulls the
-// scores of its two tokens.  With NEXT the tile's registers are refilled with
-// the loads of tile t0 + stride as soon as its K and V are consumed, so they fly
-// during the softmax and P V.
-template <int NG, bool PARTIAL, bool NEXT, class Loader>
+// scores of its two tokens.  `consumed` runs as soon as the tile's K and V
+// registers have been read (the caller starts the next loads there, so they fly
+// during the softmax and P V).
+template <int NG, bool PARTIAL, class Consumed>
 __device__ __forceinline__ void attend_step(Softmax<NG>& st, TileLoads& c, const bf16x8 qop[4], float sl, int t0,
-                                            int t_end, int stride, int lane, const Loader& load) {
+                                            int t_end, int lane, const Consumed& consumed) {
   const int tv = lane >> 3;
   f32x4 sc = {0.0f, 0.0f, 0.0f, 0.0f};
   sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qop[0], e4m3x8_to_bf16(c.k0[0], c.k0[1]), sc, 0, 0, 0);
@@ -294,7 +299,7 @@ __device__ __forceinline__ void attend_step(Softmax<NG>& st, TileLoads& c, const
     fb[4 * i + 2] = b1.x;
     fb[4 * i + 3] = b1.y;
   }
-  if constexpr (NEXT) c = load(t0 + stride);
+  consumed();
 
   float s4[4];
   const bool col_ok = !PARTIAL || t0 + (lane & 15) < t_end;
@@ -327,6 +332,70 @@ __device__ __forceinline__ void attend_step(Softmax<NG>& st, TileLoads& c, const
     st.l[g] += pa + pb;
 #pragma unroll
     for (int k = 0; k < 16; ++k) st.acc[g][k] = __builtin_fmaf(pa, fa[k], __builtin_fmaf(pb, fb[k], st.acc[g][k]));
+  }
+}
+
+// Merge the wave's eight token slots (lanes differing in bits 3..5), then the
+// workgroup's waves through LDS, and write split s's partial record: per
+// query head the maximum, the sum and the 128 weighted V columns.
+template <int NG>
+__device__ __forceinline__ void write_partial(const DecodeArgs& a, Softmax<NG>& st, int b, int h, int s, int lane,
+                                              int wave, float (*s_acc)[NG][kHead]) {
+  const int G = a.group;
+#pragma unroll
+  for (int o = 8; o < 64; o <<= 1) {
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      const float mo = __shfl_xor(st.m[g], o);
+      const float lo = __shfl_xor(st.l[g], o);
+      const float mn = __builtin_fmaxf(st.m[g], mo);
+      const float ca = __builtin_amdgcn_exp2f(st.m[g] - mn), cb = __builtin_amdgcn_exp2f(mo - mn);
+      st.l[g] = st.l[g] * ca + lo * cb;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) st.acc[g][k] = st.acc[g][k] * ca + __shfl_xor(st.acc[g][k], o) * cb;
+      st.m[g] = mn;
+    }
+  }
+
+  // merge the waves through LDS and write this split's partial
+  __shared__ float s_m[kWaves][NG], s_l[kWaves][NG];
+  if (lane < 8) {
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) s_acc[wave][g][16 * lane + k] = st.acc[g][k];
+    }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      s_m[wave][g] = st.m[g];
+      s_l[wave][g] = st.l[g];
+    }
+  }
+  __syncthreads();
+  const int rec = G * (kHead + 2);
+  float* part = a.part + ((int64_t(b) * a.num_kv_heads + h) * a.max_splits + s) * rec;
+  for (int i = threadIdx.x; i < G * kHead; i += kWaves * 64) {
+    const int g = i / kHead, d = i % kHead;
+    float mx = s_m[0][g];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) mx = __builtin_fmaxf(mx, s_m[w][g]);
+    float v = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) v += s_acc[w][g][d] * __builtin_amdgcn_exp2f(s_m[w][g] - mx);
+    part[2 * G + i] = v;
+  }
+  if (threadIdx.x < G) {
+    const int g = threadIdx.x;
+    float mx = s_m[0][g];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) mx = __builtin_fmaxf(mx, s_m[w][g]);
+    float sum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) sum += s_l[w][g] * __builtin_amdgcn_exp2f(s_m[w][g] - mx);
+    part[g] = mx;
+    part[G + g] = sum;
   }
 }
 
@@ -385,67 +454,127 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_kernel(DecodeArgs 
   if (t0 < t_end) {
     TileLoads c = tile(t0);
     for (; t0 + stride < t_end; t0 += stride)
-      attend_step<NG, false, true>(st, c, qop, sl, t0, t_end, stride, lane, tile);
-    attend_step<NG, true, false>(st, c, qop, sl, t0, t_end, stride, lane, tile);
+      attend_step<NG, false>(st, c, qop, sl, t0, t_end, lane, [&] { c = tile(t0 + stride); });
+    attend_step<NG, true>(st, c, qop, sl, t0, t_end, lane, [] {});
   }
 
-  // merge the eight token slots of the wave (lanes differing in bits 3..5)
-#pragma unroll
-  for (int o = 8; o < 64; o <<= 1) {
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-      const float mo = __shfl_xor(st.m[g], o);
-      const float lo = __shfl_xor(st.l[g], o);
-      const float mn = __builtin_fmaxf(st.m[g], mo);
-      const float ca = __builtin_amdgcn_exp2f(st.m[g] - mn), cb = __builtin_amdgcn_exp2f(mo - mn);
-      st.l[g] = st.l[g] * ca + lo * cb;
-#pragma unroll
-      for (int k = 0; k < 16; ++k) st.acc[g][k] = st.acc[g][k] * ca + __shfl_xor(st.acc[g][k], o) * cb;
-      st.m[g] = mn;
-    }
-  }
-
-  // merge the waves through LDS and write this split's partial
   __shared__ float s_acc[kWaves][NG][kHead];
-  __shared__ float s_m[kWaves][NG], s_l[kWaves][NG];
-  if (lane < 8) {
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-#pragma unroll
-      for (int k = 0; k < 16; ++k) s_acc[wave][g][16 * lane + k] = st.acc[g][k];
-    }
-  }
-  if (lane == 0) {
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-      s_m[wave][g] = st.m[g];
-      s_l[wave][g] = st.l[g];
-    }
-  }
+  write_partial<NG>(a, st, b, h, s, lane, wave, s_acc);
+}
+
+// vmcnt <= n, expcnt and lgkmcnt untouched (gfx9 s_waitcnt encoding)
+constexpr int vmcnt_imm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | (((n >> 4) & 3) << 14); }
+
+// The four 16-byte quarters of a ring slot for this lane, read synchronously.
+// Written as one asm block because the compiler, unable to tell which LDS DMA
+// wrote which slot, would otherwise wait for every load in flight before any
+// LDS read; the caller's explicit vmcnt wait orders the slot's DMA before this.
+__device__ __forceinline__ TileLoads ring_read(const u32x4* slot_lane) {
+  const uint32_t addr = (uint32_t)(size_t)(const lvoid*)slot_lane;  // LDS byte offset
+  TileLoads c;
+  asm volatile(
+      "ds_read_b128 %0, %4\n"
+      "ds_read_b128 %1, %4 offset:1024\n"
+      "ds_read_b128 %2, %4 offset:2048\n"
+      "ds_read_b128 %3, %4 offset:3072\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(c.k0), "=&v"(c.k1), "=&v"(c.va), "=&v"(c.vb)
+      : "v"(addr)
+      : "memory");
+  return c;
+}
+
+// Variant for block sizes that are powers of two >= 16 (a tile lies in one
+// page): each wave streams its tiles through a ring of kRing 4 KiB LDS slots
+// filled by global_load_lds_dwordx4, so kRing tiles per wave are in flight
+// without holding registers (12 waves and 36 tiles per CU at 3 workgroups).
+// A slot's four 1 KiB quarters hold K bytes 0-15, K bytes 16-31, V token a and
+// V token b of every lane, lane l at 16 * l.  The vector-memory counter is
+// waited on explicitly: nothing else in the loop uses it.
+template <int NG>
+__global__ void __launch_bounds__(kWaves * 64) decode_partial_ring_kernel(DecodeArgs a, int q_dtype) {
+  const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int len = a.seq_lens[b];
+  const int t_begin = s * a.split;
+  if (t_begin >= len || s >= a.max_splits) return;  // uniform over the workgroup
+  const int t_end = min(len, t_begin + a.split);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+
+  const float qd = descale(a.qd, a.qd_b, a.qd_h, b, h);
+  const float kd = descale(a.kd, a.kd_b, a.kd_h, b, h);
+  const float sl = a.scale_log2 * qd * kd;
+  uint32_t qw[8];
+  load_query(a, q_dtype, b, h, qd, lane, qw);
+  const bf16x8 qop[4] = {e4m3x8_to_bf16(qw[0], qw[1]), e4m3x8_to_bf16(qw[2], qw[3]), e4m3x8_to_bf16(qw[4], qw[5]),
+                         e4m3x8_to_bf16(qw[6], qw[7])};
+
+  // page ids of the split (the host guarantees they fit), then the tile ring
+  __shared__ int32_t s_pages[kRingPages];
+  const int32_t* bt_row = a.block_table + b * a.bt_stride;
+  const int first = t_begin >> a.bs_shift;
+  const int n_ids = ((t_end - 1) >> a.bs_shift) - first + 1;
+  for (int i = threadIdx.x; i < n_ids; i += kWaves * 64) s_pages[i] = checked_page(a, bt_row, first + i);
+  __shared__ __attribute__((aligned(16))) u32x4 s_ring[kWaves][kRing][4][64];
   __syncthreads();
-  const int rec = G * (kHead + 2);
-  float* part = a.part + ((int64_t(b) * a.num_kv_heads + h) * a.max_splits + s) * rec;
-  for (int i = threadIdx.x; i < G * kHead; i += kWaves * 64) {
-    const int g = i / kHead, d = i % kHead;
-    float mx = s_m[0][g];
+  u32x4(*ring)[4][64] = s_ring[wave];
+
+  Softmax<NG> st;
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) mx = __builtin_fmaxf(mx, s_m[w][g]);
-    float v = 0.0f;
+  for (int g = 0; g < NG; ++g) {
+    st.m[g] = kNegBig;
+    st.mth[g] = kNegBig + kLazy;
+    st.l[g] = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) v += s_acc[w][g][d] * __builtin_amdgcn_exp2f(s_m[w][g] - mx);
-    part[2 * G + i] = v;
+    for (int k = 0; k < 16; ++k) st.acc[g][k] = 0.0f;
   }
-  if (threadIdx.x < G) {
-    const int g = threadIdx.x;
-    float mx = s_m[0][g];
-#pragma unroll
-    for (int w = 1; w < kWaves; ++w) mx = __builtin_fmaxf(mx, s_m[w][g]);
-    float sum = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) sum += s_l[w][g] * __builtin_amdgcn_exp2f(s_m[w][g] - mx);
-    part[g] = mx;
-    part[G + g] = sum;
+  const uint32_t off_k = uint32_t((lane & 15) * a.k_row + 32 * (lane >> 4));
+  const uint32_t off_va = uint32_t((lane >> 3) * a.v_row + 16 * (lane & 7));
+  const uint32_t off_vb = uint32_t(off_va + 8 * a.v_row);
+  const int stride = kTile * kWaves;
+  const int t_first = t_begin + wave * kTile;
+  const int n_tiles = t_first < t_end ? (t_end - t_first + stride - 1) / stride : 0;
+
+  // start the loads of tile j into its slot; a missing page reads page 0 (in
+  // bounds) and is zeroed when consumed
+  uint32_t valid = 0;  // bit j % kRing: slot holds a tile on a real page
+  auto issue = [&](int j) {
+    const int t0 = t_first + j * stride;
+    const int32_t raw = __builtin_amdgcn_readfirstlane(s_pages[(t0 >> a.bs_shift) - first]);
+    const int slot = j % kRing;
+    valid = raw >= 0 ? (valid | (1u << slot)) : (valid & ~(1u << slot));
+    const int64_t pid = raw >= 0 ? raw : 0;
+    const int64_t row0 = t0 & (a.block_size - 1);
+    const uint8_t* kb = a.k + pid * a.k_blk + row0 * a.k_row + int64_t(h) * a.k_head;
+    const uint8_t* vb = a.v + pid * a.v_blk + row0 * a.v_row + int64_t(h) * a.v_head;
+    __builtin_amdgcn_global_load_lds((gvoid*)(kb + off_k), (lvoid*)&ring[slot][0][0], 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((gvoid*)(kb + off_k + 16), (lvoid*)&ring[slot][1][0], 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((gvoid*)(vb + off_va), (lvoid*)&ring[slot][2][0], 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((gvoid*)(vb + off_vb), (lvoid*)&ring[slot][3][0], 16, 0, 0);
+  };
+  auto fetch = [&](int j) {
+    // tiles issued after j: min(kRing - 1, n_tiles - 1 - j), four loads each
+    if (j + kRing - 1 < n_tiles) __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 * (kRing - 1)));
+    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    const int slot = j % kRing;
+    TileLoads c = ring_read(&ring[slot][0][lane]);
+    if (!((valid >> slot) & 1u)) c.k0 = c.k1 = c.va = c.vb = u32x4(0);
+    return c;
+  };
+  for (int j = 0; j < kRing && j < n_tiles; ++j) issue(j);
+  if (n_tiles > 0) {
+    int j = 0;
+    for (; j + 1 < n_tiles; ++j) {
+      TileLoads c = fetch(j);
+      attend_step<NG, false>(st, c, qop, sl, t_first + j * stride, t_end, lane, [&] {
+        if (j + kRing < n_tiles) issue(j + kRing);
+      });
+    }
+    TileLoads c = fetch(j);
+    attend_step<NG, true>(st, c, qop, sl, t_first + j * stride, t_end, lane, [] {});
   }
+  __syncthreads();  // every wave is done with the ring: it becomes the merge buffer
+  write_partial<NG>(a, st, b, h, s, lane, wave, reinterpret_cast<float(*)[NG][kHead]>(&s_ring[0][0][0][0]));
 }
 
 // One workgroup per (kv head, sequence): each wave turns a head's split maxima
@@ -504,10 +633,20 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(DecodeArgs a) {
   }
 }
 
-int decode_split(int64_t max_seq_len) {
-  int64_t split = kMinSplit;
+// Tokens per workgroup: num_splits > 0 asks for that many splits of the longest
+// sequence (rounded up to whole 64-token wave strides); 0 picks kMinSplit,
+// doubled until at most kMaxSplits splits cover max_seq_len.
+int decode_split(int64_t max_seq_len, int64_t num_splits) {
+  const int64_t stride = kTile * kWaves;
+  int64_t split;
+  if (num_splits > 0) {
+    split = ceil_div(std::max<int64_t>(max_seq_len, 1), num_splits);
+    split = ceil_div(split, stride) * stride;
+  } else {
+    split = kMinSplit;
+  }
   while (ceil_div(max_seq_len, split) > kMaxSplits) split *= 2;
-  return int(split);
+  return int(std::min<int64_t>(split, INT32_MAX / 2));
 }
 
 template <bool UNIFORM>
@@ -526,9 +665,10 @@ void launch_partial(const DecodeArgs& a, int q_dtype, dim3 grid, hipStream_t st,
 extern "C" {
 
 int64_t psk_paged_decode_workspace_len(int64_t num_seqs, int64_t num_q_heads, int64_t num_kv_heads,
-                                       int64_t max_seq_len) {
-  if (num_seqs < 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads || max_seq_len < 0) return PSK_E_ARG;
-  const int64_t splits = std::max<int64_t>(1, ceil_div(max_seq_len, decode_split(max_seq_len)));
+                                       int64_t max_seq_len, int64_t num_splits) {
+  if (num_seqs < 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads || max_seq_len < 0 || num_splits < 0)
+    return PSK_E_ARG;
+  const int64_t splits = std::max<int64_t>(1, ceil_div(max_seq_len, decode_split(max_seq_len, num_splits)));
   return num_seqs * num_kv_heads * splits * (num_q_heads / num_kv_heads) * (kHead + 2);
 }
 
@@ -537,7 +677,8 @@ int psk_paged_decode_attention(const void* q, int64_t q_tok_stride, int64_t q_he
                                const int64_t* v_strides, const int32_t* block_table, int64_t block_table_stride,
                                int64_t block_table_width, const int32_t* seq_lens, int64_t num_seqs,
                                int64_t num_q_heads, int64_t num_kv_heads, int64_t head_size, int64_t block_size,
-                               int64_t num_blocks, int64_t max_seq_len, float softmax_scale, const float* q_descale,
+                               int64_t num_blocks, int64_t max_seq_len, int64_t num_splits, float softmax_scale,
+                               const float* q_descale,
                                const float* k_descale, const float* v_descale, const int64_t* descale_strides,
                                void* out, int64_t out_tok_stride, int64_t out_head_stride, int out_dtype, float* lse,
                                int64_t lse_head_stride, float* workspace, int64_t workspace_len, void* stream) {
@@ -567,7 +708,8 @@ int psk_paged_decode_attention(const void* q, int64_t q_tok_stride, int64_t q_he
   if (common_align(kv_align, 8, 16) < 16) return fail(PSK_E_ARG, "K/V caches need 16-byte aligned bases and strides");
   const uint64_t q_align[3] = {uint64_t(uintptr_t(q)), uint64_t(q_tok_stride * qsz), uint64_t(q_head_stride * qsz)};
   if (common_align(q_align, 3, 16) < 16) return fail(PSK_E_ARG, "query rows need 16-byte alignment");
-  const int64_t need = psk_paged_decode_workspace_len(num_seqs, num_q_heads, num_kv_heads, max_seq_len);
+  if (num_splits < 0) return fail(PSK_E_ARG, "num_splits %lld", (long long)num_splits);
+  const int64_t need = psk_paged_decode_workspace_len(num_seqs, num_q_heads, num_kv_heads, max_seq_len, num_splits);
   if (workspace_len < need)
     return fail(PSK_E_WORKSPACE, "workspace of %lld floats, need %lld", (long long)workspace_len, (long long)need);
 
@@ -592,7 +734,7 @@ int psk_paged_decode_attention(const void* q, int64_t q_tok_stride, int64_t q_he
   a.bs_shift = log2_exact(block_size);
   a.num_kv_heads = int32_t(num_kv_heads);
   a.group = int32_t(G);
-  a.split = decode_split(max_seq_len);
+  a.split = decode_split(max_seq_len, num_splits);
   a.max_splits = int32_t(std::max<int64_t>(1, ceil_div(max_seq_len, a.split)));
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
   const int64_t zero[6] = {0, 0, 0, 0, 0, 0};
@@ -618,9 +760,19 @@ int psk_paged_decode_attention(const void* q, int64_t q_tok_stride, int64_t q_he
   const int ng = G == 1 ? 1 : G == 2 ? 2 : G <= 4 ? 4 : 8;
   const dim3 grid{unsigned(a.max_splits), unsigned(num_kv_heads), unsigned(num_seqs)};
   // a 16-token tile stays in one page when the block size is a power of two >= 16
-  const bool uniform = a.bs_shift >= 4 && 16 * std::max(a.k_row, a.v_row) < (int64_t(1) << 31);
-  if (uniform) launch_partial<true>(a, q_dtype, grid, st, ng);
-  else launch_partial<false>(a, q_dtype, grid, st, ng);
+  const bool uniform = a.bs_shift >= 4 && 16 * std::max(a.k_row, a.v_row) < (int64_t(1) << 31) &&
+                       a.split / block_size + 1 <= kRingPages;
+  if (uniform) {
+    const dim3 block(kWaves * 64);
+    switch (ng) {
+      case 1: hipLaunchKernelGGL((decode_partial_ring_kernel<1>), grid, block, 0, st, a, q_dtype); break;
+      case 2: hipLaunchKernelGGL((decode_partial_ring_kernel<2>), grid, block, 0, st, a, q_dtype); break;
+      case 4: hipLaunchKernelGGL((decode_partial_ring_kernel<4>), grid, block, 0, st, a, q_dtype); break;
+      default: hipLaunchKernelGGL((decode_partial_ring_kernel<8>), grid, block, 0, st, a, q_dtype); break;
+    }
+  } else {
+    launch_partial<false>(a, q_dtype, grid, st, ng);
+  }
   const int st1 = check_launch("decode_partial_kernel launch");
   if (st1 != PSK_OK) return st1;
   const dim3 grid2{unsigned(num_kv_heads), unsigned(num_seqs), 1u};
