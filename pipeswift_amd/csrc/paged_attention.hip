@@ -117,6 +117,24 @@ __device__ __forceinline__ bf16x8 e4m3x8_to_bf16(uint32_t w0, uint32_t w1) {
   return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
 
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;       // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;       // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7 - i within each 8
+constexpr int kDppRowRor8 = 0x128;   // lane i <- lane (i + 8) % 16 within each row
+
+// P V lane roles.  With replicated query rows (groups of at most 4 heads) lane
+// l owns tokens (l % 8) and (l % 8) + 8 of a tile and V columns 16 * (l / 8) ..
+// +16, so both of its tokens' scores sit in its own 16-lane row.  Otherwise
+// tokens (l / 8) and (l / 8) + 8, columns 16 * (l % 8).
+template <bool REPL>
+__device__ __forceinline__ int token_slot(int lane) { return REPL ? (lane & 7) : (lane >> 3); }
+template <bool REPL>
+__device__ __forceinline__ int column_chunk(int lane) { return REPL ? (lane >> 3) : (lane & 7); }
+
 __device__ __forceinline__ float bperm(int src_lane, float x) {
   return __int_as_float(__builtin_amdgcn_ds_bpermute(src_lane << 2, __float_as_int(x)));
 }
@@ -155,6 +173,7 @@ struct TileLoads {
   u32x4 k0, k1, va, vb;
 };
 
+template <bool REPL>
 __device__ __forceinline__ TileLoads load_tile(const DecodeArgs& a, const PageIds& ids, int h, int t0, int t_end,
                                                int lane) {
   TileLoads r;
@@ -168,8 +187,8 @@ __device__ __forceinline__ TileLoads load_tile(const DecodeArgs& a, const PageId
       r.k1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + 16));
     }
   }
-  const int ta = t0 + (lane >> 3), tb = ta + 8;
-  const int64_t dv = 16 * (lane & 7);
+  const int ta = t0 + token_slot<REPL>(lane), tb = ta + 8;
+  const int64_t dv = 16 * column_chunk<REPL>(lane);
   if (ta < t_end) {
     const int64_t p = page_of(a, ids, ta);
     if (p >= 0)
@@ -213,11 +232,14 @@ __device__ __forceinline__ void load_query_as(const char* src, float qd, int d0,
   }
 }
 
+// rows: MFMA row i holds query head i, or head i % 4 when REPL (groups of at
+// most 4 heads repeated in each of the four row quarters)
+template <bool REPL>
 __device__ __forceinline__ void load_query(const DecodeArgs& a, int q_dtype, int b, int h, float qd, int lane,
                                            uint32_t qw[8]) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) qw[i] = 0;
-  const int row = lane & 15;
+  const int row = REPL ? (lane & 3) : (lane & 15);
   if (row >= a.group) return;
   const char* src = a.q + b * a.q_tok_stride + int64_t(h * a.group + row) * a.q_head_stride;
   const int d0 = 32 * (lane >> 4);
@@ -273,7 +295,8 @@ struct Softmax {
 template <int NG, bool PARTIAL, class Consumed>
 __device__ __forceinline__ void attend_step(Softmax<NG>& st, TileLoads& c, const bf16x8 qop[4], float sl, int t0,
                                             int t_end, int lane, const Consumed& consumed) {
-  const int tv = lane >> 3;
+  constexpr bool REPL = NG <= 4;
+  const int tv = token_slot<REPL>(lane);
   f32x4 sc = {0.0f, 0.0f, 0.0f, 0.0f};
   sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qop[0], e4m3x8_to_bf16(c.k0[0], c.k0[1]), sc, 0, 0, 0);
   sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qop[1], e4m3x8_to_bf16(c.k0[2], c.k0[3]), sc, 0, 0, 0);
@@ -307,10 +330,18 @@ __device__ __forceinline__ void attend_step(Softmax<NG>& st, TileLoads& c, const
   for (int r = 0; r < 4; ++r) s4[r] = col_ok ? sc[r] * sl : -__builtin_inff();
   float sa[NG], sb[NG];
   bool raise = false;
+  const bool low = (lane & 15) < 8;
 #pragma unroll
   for (int g = 0; g < NG; ++g) {
-    sa[g] = bperm(16 * (g >> 2) + tv, s4[g & 3]);
-    sb[g] = bperm(16 * (g >> 2) + tv + 8, s4[g & 3]);
+    if constexpr (REPL) {
+      // this lane's column is one of its tokens; the other is 8 lanes away in the row
+      const float own = s4[g], other = dpp<kDppRowRor8>(s4[g]);
+      sa[g] = low ? own : other;
+      sb[g] = low ? other : own;
+    } else {
+      sa[g] = bperm(16 * (g >> 2) + tv, s4[g & 3]);
+      sb[g] = bperm(16 * (g >> 2) + tv + 8, s4[g & 3]);
+    }
     raise |= __builtin_fmaxf(sa[g], sb[g]) > st.mth[g];
   }
   if (__any(raise)) {
@@ -335,35 +366,62 @@ __device__ __forceinline__ void attend_step(Softmax<NG>& st, TileLoads& c, const
   }
 }
 
-// Merge the wave's eight token slots (lanes differing in bits 3..5), then the
+// One merge step of the running softmax with the partner lane DPP pattern CTRL
+// selects.
+template <int NG, int CTRL>
+__device__ __forceinline__ void merge_slots(Softmax<NG>& st) {
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    const float mo = dpp<CTRL>(st.m[g]);
+    const float lo = dpp<CTRL>(st.l[g]);
+    const float mn = __builtin_fmaxf(st.m[g], mo);
+    const float ca = __builtin_amdgcn_exp2f(st.m[g] - mn), cb = __builtin_amdgcn_exp2f(mo - mn);
+    st.l[g] = st.l[g] * ca + lo * cb;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) st.acc[g][k] = st.acc[g][k] * ca + dpp<CTRL>(st.acc[g][k]) * cb;
+    st.m[g] = mn;
+  }
+}
+
+// Merge the wave's eight token slots, then the
 // workgroup's waves through LDS, and write split s's partial record: per
 // query head the maximum, the sum and the 128 weighted V columns.
 template <int NG>
 __device__ __forceinline__ void write_partial(const DecodeArgs& a, Softmax<NG>& st, int b, int h, int s, int lane,
                                               int wave, float (*s_acc)[NG][kHead]) {
   const int G = a.group;
+  constexpr bool REPL = NG <= 4;
+  if constexpr (REPL) {
+    // token slots are lane bits 0..2: xor 1, xor 2 within quads, then the
+    // other quad of the eight via the half-row mirror
+    merge_slots<NG, kDppXor1>(st);
+    merge_slots<NG, kDppXor2>(st);
+    merge_slots<NG, kDppHalfMirror>(st);
+  } else {
 #pragma unroll
-  for (int o = 8; o < 64; o <<= 1) {
+    for (int o = 8; o < 64; o <<= 1) {
 #pragma unroll
-    for (int g = 0; g < NG; ++g) {
-      const float mo = __shfl_xor(st.m[g], o);
-      const float lo = __shfl_xor(st.l[g], o);
-      const float mn = __builtin_fmaxf(st.m[g], mo);
-      const float ca = __builtin_amdgcn_exp2f(st.m[g] - mn), cb = __builtin_amdgcn_exp2f(mo - mn);
-      st.l[g] = st.l[g] * ca + lo * cb;
+      for (int g = 0; g < NG; ++g) {
+        const float mo = __shfl_xor(st.m[g], o);
+        const float lo = __shfl_xor(st.l[g], o);
+        const float mn = __builtin_fmaxf(st.m[g], mo);
+        const float ca = __builtin_amdgcn_exp2f(st.m[g] - mn), cb = __builtin_amdgcn_exp2f(mo - mn);
+        st.l[g] = st.l[g] * ca + lo * cb;
 #pragma unroll
-      for (int k = 0; k < 16; ++k) st.acc[g][k] = st.acc[g][k] * ca + __shfl_xor(st.acc[g][k], o) * cb;
-      st.m[g] = mn;
+        for (int k = 0; k < 16; ++k) st.acc[g][k] = st.acc[g][k] * ca + __shfl_xor(st.acc[g][k], o) * cb;
+        st.m[g] = mn;
+      }
     }
   }
 
   // merge the waves through LDS and write this split's partial
   __shared__ float s_m[kWaves][NG], s_l[kWaves][NG];
-  if (lane < 8) {
+  if (token_slot<REPL>(lane) == 0) {  // one lane per column chunk holds the merged state
+    const int c = column_chunk<REPL>(lane);
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
 #pragma unroll
-      for (int k = 0; k < 16; ++k) s_acc[wave][g][16 * lane + k] = st.acc[g][k];
+      for (int k = 0; k < 16; ++k) s_acc[wave][g][16 * c + k] = st.acc[g][k];
     }
   }
   if (lane == 0) {
@@ -414,7 +472,7 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_kernel(DecodeArgs 
   const float kd = descale(a.kd, a.kd_b, a.kd_h, b, h);
   const float sl = a.scale_log2 * qd * kd;
   uint32_t qw[8];
-  load_query(a, q_dtype, b, h, qd, lane, qw);
+  load_query<(NG <= 4)>(a, q_dtype, b, h, qd, lane, qw);
   const bf16x8 qop[4] = {e4m3x8_to_bf16(qw[0], qw[1]), e4m3x8_to_bf16(qw[2], qw[3]), e4m3x8_to_bf16(qw[4], qw[5]),
                          e4m3x8_to_bf16(qw[6], qw[7])};
 
@@ -441,12 +499,12 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_kernel(DecodeArgs 
   }
   LaneOffsets off;
   off.k = uint32_t((lane & 15) * a.k_row + 32 * (lane >> 4));
-  off.va = uint32_t((lane >> 3) * a.v_row + 16 * (lane & 7));
+  off.va = uint32_t(token_slot<(NG <= 4)>(lane) * a.v_row + 16 * column_chunk<(NG <= 4)>(lane));
   off.vb = uint32_t(off.va + 8 * a.v_row);
 
   auto tile = [&](int t) -> TileLoads {
     if constexpr (UNIFORM) return load_tile_uniform(a, ids, h, t, off);
-    else return load_tile(a, ids, h, t, t_end, lane);
+    else return load_tile<(NG <= 4)>(a, ids, h, t, t_end, lane);
   };
   // every tile of a wave but its last lies below t_end
   const int stride = kTile * kWaves;
@@ -505,7 +563,7 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_ring_kernel(Decode
   const float kd = descale(a.kd, a.kd_b, a.kd_h, b, h);
   const float sl = a.scale_log2 * qd * kd;
   uint32_t qw[8];
-  load_query(a, q_dtype, b, h, qd, lane, qw);
+  load_query<(NG <= 4)>(a, q_dtype, b, h, qd, lane, qw);
   const bf16x8 qop[4] = {e4m3x8_to_bf16(qw[0], qw[1]), e4m3x8_to_bf16(qw[2], qw[3]), e4m3x8_to_bf16(qw[4], qw[5]),
                          e4m3x8_to_bf16(qw[6], qw[7])};
 
@@ -529,7 +587,7 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_ring_kernel(Decode
     for (int k = 0; k < 16; ++k) st.acc[g][k] = 0.0f;
   }
   const uint32_t off_k = uint32_t((lane & 15) * a.k_row + 32 * (lane >> 4));
-  const uint32_t off_va = uint32_t((lane >> 3) * a.v_row + 16 * (lane & 7));
+  const uint32_t off_va = uint32_t(token_slot<(NG <= 4)>(lane) * a.v_row + 16 * column_chunk<(NG <= 4)>(lane));
   const uint32_t off_vb = uint32_t(off_va + 8 * a.v_row);
   const int stride = kTile * kWaves;
   const int t_first = t_begin + wave * kTile;
