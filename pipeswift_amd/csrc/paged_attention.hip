@@ -58,7 +58,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 constexpr int kHead = 128;    // head_dim of the MFMA tiling
 constexpr int kTile = 16;     // tokens per tile (N of the 16x16x32 MFMA)
 constexpr int kWaves = 4;     // waves per workgroup
-constexpr int kMinSplit = 1024;
+constexpr int kMinSplit = 256;
 constexpr int kMaxSplits = 128;
 constexpr float kNegBig = -1.0e30f;  // finite "no token yet" maximum
 constexpr float kLazy = 8.0f;        // raise the running max past 2^8 headroom only
@@ -459,7 +459,11 @@ __device__ __forceinline__ void write_partial(const DecodeArgs& a, Softmax<NG>& 
 
 template <int NG, bool UNIFORM>
 __global__ void __launch_bounds__(kWaves * 64) decode_partial_kernel(DecodeArgs a, int q_dtype) {
-  const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  // split s of sequence b sits at blockIdx.x = (s + b) % max_splits: workgroups
+  // go round-robin to the 8 XCDs by blockIdx.x (max_splits is the fastest grid
+  // dimension), so the first splits of short sequences spread over all of them
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int s = int((blockIdx.x + unsigned(a.max_splits) - unsigned(b % a.max_splits)) % unsigned(a.max_splits));
   const int len = a.seq_lens[b];
   const int t_begin = s * a.split;
   if (t_begin >= len || s >= a.max_splits) return;  // uniform over the workgroup
@@ -551,7 +555,11 @@ __device__ __forceinline__ TileLoads ring_read(const u32x4* slot_lane) {
 // waited on explicitly: nothing else in the loop uses it.
 template <int NG>
 __global__ void __launch_bounds__(kWaves * 64) decode_partial_ring_kernel(DecodeArgs a, int q_dtype) {
-  const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  // split s of sequence b sits at blockIdx.x = (s + b) % max_splits: workgroups
+  // go round-robin to the 8 XCDs by blockIdx.x (max_splits is the fastest grid
+  // dimension), so the first splits of short sequences spread over all of them
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int s = int((blockIdx.x + unsigned(a.max_splits) - unsigned(b % a.max_splits)) % unsigned(a.max_splits));
   const int len = a.seq_lens[b];
   const int t_begin = s * a.split;
   if (t_begin >= len || s >= a.max_splits) return;  // uniform over the workgroup
@@ -691,18 +699,18 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(DecodeArgs a) {
   }
 }
 
-// Tokens per workgroup: num_splits > 0 asks for that many splits of the longest
-// sequence (rounded up to whole 64-token wave strides); 0 picks kMinSplit,
-// doubled until at most kMaxSplits splits cover max_seq_len.
-int decode_split(int64_t max_seq_len, int64_t num_splits) {
+// Tokens per workgroup.  num_splits > 0 asks for that many splits of the
+// longest sequence; 0 aims at 24 splits of it (measured best for config 2's
+// 128 x 8 sequence-heads), more when there are too few sequence-heads to put
+// ~1536 workgroups on a long context.  Rounded up to whole 64-token wave
+// strides, at least kMinSplit tokens, and doubled until at most kMaxSplits
+// splits cover max_seq_len.
+int decode_split(int64_t max_seq_len, int64_t num_splits, int64_t seq_heads) {
   const int64_t stride = kTile * kWaves;
-  int64_t split;
-  if (num_splits > 0) {
-    split = ceil_div(std::max<int64_t>(max_seq_len, 1), num_splits);
-    split = ceil_div(split, stride) * stride;
-  } else {
-    split = kMinSplit;
-  }
+  int64_t target = num_splits;
+  if (target <= 0) target = std::min<int64_t>(kMaxSplits, std::max<int64_t>(24, ceil_div(1536, std::max<int64_t>(seq_heads, 1))));
+  int64_t split = ceil_div(ceil_div(std::max<int64_t>(max_seq_len, 1), target), stride) * stride;
+  if (num_splits <= 0) split = std::max<int64_t>(split, kMinSplit);
   while (ceil_div(max_seq_len, split) > kMaxSplits) split *= 2;
   return int(std::min<int64_t>(split, INT32_MAX / 2));
 }
@@ -726,7 +734,8 @@ int64_t psk_paged_decode_workspace_len(int64_t num_seqs, int64_t num_q_heads, in
                                        int64_t max_seq_len, int64_t num_splits) {
   if (num_seqs < 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads || max_seq_len < 0 || num_splits < 0)
     return PSK_E_ARG;
-  const int64_t splits = std::max<int64_t>(1, ceil_div(max_seq_len, decode_split(max_seq_len, num_splits)));
+  const int64_t splits =
+      std::max<int64_t>(1, ceil_div(max_seq_len, decode_split(max_seq_len, num_splits, num_seqs * num_kv_heads)));
   return num_seqs * num_kv_heads * splits * (num_q_heads / num_kv_heads) * (kHead + 2);
 }
 
@@ -792,7 +801,7 @@ int psk_paged_decode_attention(const void* q, int64_t q_tok_stride, int64_t q_he
   a.bs_shift = log2_exact(block_size);
   a.num_kv_heads = int32_t(num_kv_heads);
   a.group = int32_t(G);
-  a.split = decode_split(max_seq_len, num_splits);
+  a.split = decode_split(max_seq_len, num_splits, num_seqs * num_kv_heads);
   a.max_splits = int32_t(std::max<int64_t>(1, ceil_div(max_seq_len, a.split)));
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
   const int64_t zero[6] = {0, 0, 0, 0, 0, 0};
