@@ -23,6 +23,8 @@ Workloads (default fp8_decode_append, config 2 of the benchmark plan):
   chunked_append     4096 tokens of Qwen3 K/V (4x128), 32768 blocks
   gather             the chunked case's 6 sequences (prefix + chunk) to rows
   mla_prefill / mla_decode   kv_c 512 + k_pe 64, block 64, 20000 blocks
+  mla_fp8_tiles_prefill / mla_fp8_tiles_decode   the same into 656-byte FP8
+                     entries with one scale per 128-element tile
   copy_blocks        2048 pairs over 61 layers of [8192, 2, 16, 8, 128] bf16
   swap               8192 scattered blocks x 8 layers (4 GiB) D2H + H2D
   kv_scales          config 2's per-tensor K/V scales (amax kernel)
@@ -294,6 +296,40 @@ def setup_mla(args, device, decode):
         "config": {"workload": f"MLA latent append, {'decode' if decode else 'prefill'} (config 4)", "tokens": n,
                    "row": 576, "block_size": ps, "num_blocks": P},
         "cpu": None,
+    }
+
+
+def setup_mla_fp8_tiles(args, device, decode):
+    """Config 4 into the tile-scaled FP8 latent entry (656 bytes per token)."""
+    import torch
+
+    from pipeswift_amd import mla_fp8, workloads
+
+    case = workloads.config4_mla_fp8_tiles(decode=decode)
+    n = case.slot_mapping.shape[0]
+    P, ps = case.cache.shape[0], case.cache.shape[1]
+    R = args.rotate
+    dgen = torch.Generator(device=device).manual_seed(98)
+    latent = torch.empty((R,) + tuple(case.latent.shape), dtype=torch.bfloat16, device=device)
+    latent.normal_(generator=dgen)
+    kv_c = torch.empty((R,) + tuple(case.kv_c.shape), dtype=torch.bfloat16, device=device)
+    kv_c.normal_(generator=dgen)
+    slots = torch.stack([torch.randperm(P * ps, generator=torch.Generator().manual_seed(98 + r))[:n]
+                         for r in range(min(R, 64))]).to(torch.int64).to(device)
+    slots[0].copy_(case.slot_mapping.to(device))
+    cache = case.cache.to(device)
+
+    def launch(i):
+        mla_fp8.concat_and_cache_mla_fp8_tiles(kv_c[i], case.k_pe(latent[i]), cache, slots[i % slots.shape[0]])
+
+    name = "mla_fp8_tiles_decode" if decode else "mla_fp8_tiles_prefill"
+    return launch, {
+        "rotate": R,
+        "name": name, "kernel": "tile_fp8_append_kernel", "bytes": workloads.mla_fp8_tiles_bytes(n),
+        "tokens": n, "dtype": "bf16->fp8_e4m3fn",
+        "config": {"workload": f"MLA latent append into tile-scaled FP8 entries, {'decode' if decode else 'prefill'}"
+                               " (config 4)", "tokens": n, "entry_bytes": 656, "block_size": ps, "num_blocks": P},
+        "cpu": lambda: cpu_mla_fp8_tiles(case),
     }
 
 
@@ -724,6 +760,23 @@ def cpu_append(case, fp8, budget_s=10.0):
     return n, el, f"{n} steps of the numpy oracle append (same inputs and cache geometry)"
 
 
+def cpu_mla_fp8_tiles(case, budget_s=10.0):
+    from oracle import kv_oracle as O
+
+    kv_c, k_pe = _raw(case.kv_c), _raw(case.k_pe())
+    cache = _raw(case.cache).copy()
+    slots = case.slot_mapping.numpy()
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        O.concat_and_cache_mla_tiles(kv_c, k_pe, cache, slots)
+        n += 1
+        el = time.perf_counter() - t0
+        if el > budget_s:
+            break
+    return n, el, f"{n} steps of the numpy oracle tile-scaled FP8 MLA append (same inputs and cache)"
+
+
 def cpu_gather(cc, budget_s=10.0):
     from oracle import kv_oracle as O
 
@@ -779,6 +832,8 @@ def main():
         launch, info = setup_chunked(args, device, gather=name == "gather")
     elif name in ("mla_prefill", "mla_decode"):
         launch, info = setup_mla(args, device, decode=name == "mla_decode")
+    elif name in ("mla_fp8_tiles_prefill", "mla_fp8_tiles_decode"):
+        launch, info = setup_mla_fp8_tiles(args, device, decode=name.endswith("decode"))
     elif name == "swap":
         return run_swap(args, device)
     elif name == "hbm_copy":

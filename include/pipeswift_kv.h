@@ -2,7 +2,8 @@
  * pipeswift_kv.h -- C ABI of the MI355X (gfx950) paged KV-cache data path.
  *
  * One shared library, libpipeswift_kv.so, built with hipcc for gfx950 from
- * pipeswift_amd/csrc/pipeswift_kv.hip.  Every entry point takes plain device
+ * pipeswift_amd/csrc/{pipeswift_kv,paged_attention,mla_fp8_tiles}.hip.  Every
+ * entry point takes plain device
  * pointers, element or byte strides and sizes, a dtype code and a HIP stream
  * handle (hipStream_t passed as void*; NULL is the legacy default stream).
  *
@@ -32,6 +33,13 @@
  *                             (pipeswift/engine/block_manager.py:841-877)
  *   psk_kv_amax_scale         per-tensor FP8 scale; the reference fixes it at 1.0
  *                             (pipeswift/utils/fp8_kv.py:1-3, 75-77)
+ *   psk_paged_decode_attention  decode over the FP8 cache; the reference calls
+ *                             vLLM's FA3 flash_attn_varlen_func for it
+ *                             (pipeswift/llms/layers/attention.py:148-187)
+ *   psk_concat_and_cache_mla_fp8_tiles,  the FP8 MLA entry with per-128-element
+ *   psk_gather_mla_fp8_tiles  tile scales that the reference's MLA reader would
+ *                             need; it rejects FP8 MLA for lack of it
+ *                             (pipeswift/utils/arguments.py:459-467)
  */
 #ifndef PIPESWIFT_KV_H
 #define PIPESWIFT_KV_H
@@ -263,6 +271,47 @@ int psk_paged_decode_attention(const void* q, int64_t q_tok_stride, int64_t q_he
 
 int64_t psk_paged_decode_workspace_len(int64_t num_seqs, int64_t num_q_heads, int64_t num_kv_heads,
                                        int64_t max_seq_len, int64_t num_splits);
+
+/*
+ * FP8 MLA latent entries with one scale per 128-element tile (build-defined;
+ * the entry FlashMLA reads for an FP8 latent cache, which the reference lacks:
+ * pipeswift/utils/arguments.py:459-467 rejects FP8 for MLA models).  An entry
+ * of psk_mla_fp8_tile_entry_bytes(nope_len, rope_len) = nope_len + 4*tiles +
+ * 2*rope_len bytes, tiles = nope_len / 128, holds
+ *   [0, nope_len)                          q_i = e4m3fn_rne(clamp(x_i / s_{i/128}, -448, 448))
+ *   [nope_len, nope_len + 4*tiles)         s_j, float32
+ *   [nope_len + 4*tiles, entry bytes)      the rope part, bf16 bit copies
+ * with s_j = max(amax_j / 448, 2^-126) (IEEE fp32 division), amax_j = max |x_i|
+ * over tile j ignoring NaN; a NaN x_i stores 0x7F|sign.  DeepSeek-V3 (nope 512,
+ * rope 64): 656 bytes.  nope_len: a multiple of 128 up to 8192; rope_len: even,
+ * at most 512.  psk_mla_fp8_tile_entry_bytes returns a negative status for
+ * other sizes.
+ *
+ * psk_concat_and_cache_mla_fp8_tiles: for each token t with a valid slot s (as
+ * psk_reshape_and_cache) the entry at kv_cache + blk*cache_block_stride +
+ * off*cache_page_stride (BYTES) is written from kv_c + t*kv_c_stride and
+ * k_pe + t*k_pe_stride (elements, bf16 only).  kv_c rows must be 16-byte
+ * aligned and entries 4-byte aligned.
+ *
+ * psk_gather_mla_fp8_tiles: as psk_gather_cache over these entries, writing
+ * rows of nope_len + rope_len bf16 or f32 elements at dst + t*dst_row_stride
+ * (BYTES, 16-byte aligned): y_i = round(float(q_i) * s_{i/128}) and the rope
+ * part converted exactly.  Rows with no valid block are zeros.
+ */
+int64_t psk_mla_fp8_tile_entry_bytes(int64_t nope_len, int64_t rope_len);
+int psk_concat_and_cache_mla_fp8_tiles(const void* kv_c, const void* k_pe, void* kv_cache,
+                                       const int64_t* slot_mapping, int64_t num_tokens,
+                                       int64_t nope_len, int64_t rope_len, int64_t kv_c_stride,
+                                       int64_t k_pe_stride, int64_t block_size, int64_t num_blocks,
+                                       int64_t cache_block_stride, int64_t cache_page_stride,
+                                       int in_dtype, void* stream);
+int psk_gather_mla_fp8_tiles(const void* kv_cache, void* dst, const int32_t* block_table,
+                             const int32_t* cu_seq_lens, const int32_t* seq_starts,
+                             int64_t batch_size, int64_t block_table_stride, int64_t num_tokens,
+                             int64_t nope_len, int64_t rope_len, int64_t block_size,
+                             int64_t num_blocks, int64_t cache_block_stride,
+                             int64_t cache_page_stride, int64_t dst_row_stride, int out_dtype,
+                             void* stream);
 
 /*
  * Pinned, device-mapped host memory for the L2 mirror and swap staging

@@ -201,6 +201,89 @@ def concat_and_cache_mla(kv_c, k_pe, kv_cache, slot_mapping, in_dtype="bf16", ca
 
 
 # --------------------------------------------------------------------------- #
+# tile-scaled FP8 MLA entries (build-defined; the scheme the reference names
+# when it rejects FP8 for MLA, pipeswift/utils/arguments.py:459-467)
+# --------------------------------------------------------------------------- #
+
+MLA_TILE = 128
+MLA_MIN_TILE_SCALE = np.float32(2.0 ** -126)
+
+
+def mla_tile_entry_bytes(nope_len, rope_len):
+    """nope_len E4M3 bytes, one float32 scale per 128-element tile, rope_len bf16."""
+    return nope_len + 4 * (nope_len // MLA_TILE) + 2 * rope_len
+
+
+def quantize_mla_tiles(kv_c, k_pe):
+    """kv_c [N, nope] and k_pe [N, rope] bf16 bits -> [N, entry] uint8 entries.
+
+    Tile j of a row: amax_j = max |x| (NaN ignored), s_j = max(amax_j / 448,
+    2^-126) in fp32, q = e4m3fn(clamp(x / s_j, -448, 448)), then the tile
+    scales as float32 and the rope part as bf16 bit copies.  A NaN quotient
+    (a NaN input, or +-inf / inf in a tile holding an infinity) stores 0x7F
+    with the input's sign.
+    """
+    kv_c = np.asarray(kv_c, dtype=np.uint16)
+    k_pe = np.asarray(k_pe, dtype=np.uint16)
+    n, nope = kv_c.shape
+    assert k_pe.ndim == 2 and k_pe.shape[0] == n
+    tiles = nope // MLA_TILE
+    x = bf16_to_f32(kv_c).reshape(n, tiles, MLA_TILE)
+    a = np.abs(x)
+    amax = np.where(np.isnan(a), np.float32(0), a).max(axis=2, initial=np.float32(0)).astype(np.float32)
+    with np.errstate(over="ignore"):
+        s = np.maximum((amax / np.float32(FP8_E4M3_MAX)).astype(np.float32), MLA_MIN_TILE_SCALE)
+    with np.errstate(invalid="ignore", divide="ignore", over="ignore"):
+        y = (x / s[:, :, None]).astype(np.float32)
+    y = np.where(np.isnan(y), np.copysign(np.float32(np.nan), x), np.clip(y, -FP8_E4M3_MAX, FP8_E4M3_MAX))
+    y = y.astype(np.float32)
+    out = np.empty((n, mla_tile_entry_bytes(nope, k_pe.shape[1])), dtype=np.uint8)
+    out[:, :nope] = e4m3fn_from_f32(y).reshape(n, nope)
+    out[:, nope: nope + 4 * tiles] = np.ascontiguousarray(s).view(np.uint8).reshape(n, 4 * tiles)
+    out[:, nope + 4 * tiles:] = np.ascontiguousarray(k_pe).view(np.uint8).reshape(n, -1)
+    return out
+
+
+def dequantize_mla_tiles(entries, nope_len, out_dtype="bf16"):
+    """[N, entry] uint8 -> [N, nope + rope] raw out_dtype bits:
+    y = round(float32(q) * s_tile) for the nope part, the rope part exactly."""
+    entries = np.ascontiguousarray(entries, dtype=np.uint8)
+    n = entries.shape[0]
+    tiles = nope_len // MLA_TILE
+    s = np.ascontiguousarray(entries[:, nope_len: nope_len + 4 * tiles]).view(np.float32).reshape(n, tiles)
+    with np.errstate(invalid="ignore", over="ignore"):
+        y = (e4m3fn_to_f32(entries[:, :nope_len]).reshape(n, tiles, MLA_TILE) * s[:, :, None]).astype(np.float32)
+    rope = np.ascontiguousarray(entries[:, nope_len + 4 * tiles:]).view(np.uint16).reshape(n, -1)
+    nope_out = from_f32(y.reshape(n, nope_len), out_dtype)
+    rope_out = rope if out_dtype == "bf16" else bf16_to_f32(rope).view(np.uint32)
+    return np.concatenate([nope_out, rope_out.astype(nope_out.dtype)], axis=1)
+
+
+def concat_and_cache_mla_tiles(kv_c, k_pe, cache, slot_mapping):
+    """cache [P, ps, entry] uint8: the entry of every valid slot (as the GQA
+    append skips negative and out-of-range slots) = quantize_mla_tiles(row)."""
+    ps = cache.shape[1]
+    tok, blk, off = _slot_parts(slot_mapping, ps, cache.shape[0])
+    cache[blk, off] = quantize_mla_tiles(np.asarray(kv_c)[tok], np.asarray(k_pe)[tok])
+
+
+def gather_mla_tiles(cache, block_table, cu_seq_lens, nope_len, seq_starts=None, out=None, out_dtype="bf16"):
+    """gather_cache over the entries, then dequantize_mla_tiles; rows with no
+    valid block are zeros, rows outside [cu[0], cu[-1]) of ``out`` untouched."""
+    cu = np.asarray(cu_seq_lens, dtype=np.int64)
+    rows = int(cu[-1]) if out is None else out.shape[0]
+    entries = gather_cache(cache, block_table, cu, seq_starts, out=np.zeros((rows, cache.shape[2]), np.uint8),
+                           cache_dtype="fp8")
+    vals = dequantize_mla_tiles(entries, nope_len, out_dtype)
+    if out is None:
+        out = np.zeros_like(vals)
+    written = np.zeros(rows, dtype=bool)
+    written[int(cu[0]): min(int(cu[-1]), rows)] = True
+    out[written] = vals[written]
+    return out
+
+
+# --------------------------------------------------------------------------- #
 # gather (build-defined; vLLM gather_cache convention)
 # --------------------------------------------------------------------------- #
 

@@ -188,6 +188,22 @@ def config4_mla(seed=SEEDS["4"], num_tokens=4096, num_blocks=20000, block_size=6
     return MLACase(latent, kv_c, q_lora, cache, slots.to(torch.int64))
 
 
+def config4_mla_fp8_tiles(decode=False, num_tokens=None, seed=SEEDS["4"]) -> MLACase:
+    """Config 4 with the tile-scaled FP8 latent entry: the same kv_c, k_pe view
+    and slots, a [20000, 64, 656] uint8 cache of seeded bytes, and kv_c rows
+    spread over 2^-8..2^8 in magnitude (with x20 outliers on 1% of elements)
+    so that the per-tile scales differ."""
+    n = num_tokens or (128 if decode else 4096)
+    case = config4_mla(seed=seed, num_tokens=n, decode=decode)
+    g = _gen(seed + 7)
+    mag = torch.exp2(torch.empty(n, 4, 1).uniform_(-8, 8, generator=g)).expand(n, 4, 128).reshape(n, 512)
+    out = torch.rand(n, 512, generator=g) < 0.01
+    kv_c = (case.kv_c.float() * mag * torch.where(out, 20.0, 1.0)).to(torch.bfloat16)
+    P, ps = case.cache.shape[0], case.cache.shape[1]
+    cache = sentinel((P, ps, 656), torch.uint8, seed + 8)
+    return MLACase(case.latent, kv_c, case.q_lora, cache, case.slot_mapping)
+
+
 def config5a_pairs(seed=SEEDS["5a"], num_pairs=2048, num_blocks=8192) -> torch.Tensor:
     """2048 (src, dst) pairs, sources and destinations disjoint (one permutation)."""
     perm = torch.randperm(num_blocks, generator=_gen(seed))
@@ -217,6 +233,11 @@ def gather_bytes(total_tokens, row_elems, cache_size, out_size, num_pages, parts
 
 def mla_bytes(num_tokens, row_elems, in_size, cache_size) -> int:
     return num_tokens * row_elems * (in_size + cache_size) + num_tokens * 8
+
+
+def mla_fp8_tiles_bytes(num_tokens, nope=512, rope=64) -> int:
+    """bf16 kv_c and k_pe read, one tile-scaled FP8 entry written, int64 slot."""
+    return num_tokens * ((nope + rope) * 2 + nope + 4 * (nope // 128) + 2 * rope + 8)
 
 
 def copy_blocks_bytes(num_pairs, num_layers, block_bytes) -> int:

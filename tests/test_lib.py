@@ -50,6 +50,25 @@ def test_argument_errors_return_before_any_device_call():
     assert lib.psk_kv_amax_workspace_len() >= 2
 
 
+def test_mla_fp8_tile_sizes_and_dtypes_are_checked_on_the_host():
+    lib = _lib.lib()
+    assert lib.psk_mla_fp8_tile_entry_bytes(512, 64) == 656
+    assert lib.psk_mla_fp8_tile_entry_bytes(100, 64) == -1
+    assert lib.psk_mla_fp8_tile_entry_bytes(512, 3) == -1
+    assert lib.psk_mla_fp8_tile_entry_bytes(128 * 65, 0) == -1
+    st = lib.psk_concat_and_cache_mla_fp8_tiles(None, None, None, None, 4, 512, 64, 512, 64, 64, 10, 64 * 656, 656,
+                                                1, None)  # fp16 input
+    assert st == -2 and b"bf16" in lib.psk_last_error()
+    st = lib.psk_concat_and_cache_mla_fp8_tiles(None, None, None, None, 4, 512, 64, 512, 64, 64, 10, 64 * 600, 600,
+                                                2, None)  # entry longer than the page stride
+    assert st == -1 and b"656-byte entry" in lib.psk_last_error()
+    assert lib.psk_concat_and_cache_mla_fp8_tiles(None, None, None, None, 0, 512, 64, 512, 64, 64, 10, 64 * 656,
+                                                  656, 2, None) == 0
+    st = lib.psk_gather_mla_fp8_tiles(None, None, None, None, None, 1, 4, 8, 512, 64, 64, 10, 64 * 656, 656,
+                                      576 * 2, 1, None)  # fp16 output
+    assert st == -2
+
+
 def test_swap_range_is_checked_on_the_host():
     lib = _lib.lib()
     u = (ctypes.c_uint64 * 1)(0)
