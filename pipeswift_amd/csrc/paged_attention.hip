@@ -527,21 +527,25 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_kernel(DecodeArgs 
 // vmcnt <= n, expcnt and lgkmcnt untouched (gfx9 s_waitcnt encoding)
 constexpr int vmcnt_imm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | (((n >> 4) & 3) << 14); }
 
-// The four 16-byte quarters of a ring slot for this lane, read synchronously.
+// Cache-policy operand of the ring's loads: nt (streamed once, kept out of L2).
+constexpr int kDmaNontemporal = 2;
+
+// This lane's two K chunks and two V chunks of a ring slot (LDS byte offsets
+// slot + rk0, slot + rk1, slot + rv and slot + rv + 1024), read synchronously.
 // Written as one asm block because the compiler, unable to tell which LDS DMA
 // wrote which slot, would otherwise wait for every load in flight before any
 // LDS read; the caller's explicit vmcnt wait orders the slot's DMA before this.
-__device__ __forceinline__ TileLoads ring_read(const u32x4* slot_lane) {
-  const uint32_t addr = (uint32_t)(size_t)(const lvoid*)slot_lane;  // LDS byte offset
+__device__ __forceinline__ TileLoads ring_read(uint32_t slot, uint32_t rk0, uint32_t rk1, uint32_t rv) {
+  const uint32_t a0 = slot + rk0, a1 = slot + rk1, a2 = slot + rv;
   TileLoads c;
   asm volatile(
       "ds_read_b128 %0, %4\n"
-      "ds_read_b128 %1, %4 offset:1024\n"
-      "ds_read_b128 %2, %4 offset:2048\n"
-      "ds_read_b128 %3, %4 offset:3072\n"
+      "ds_read_b128 %1, %5\n"
+      "ds_read_b128 %2, %6\n"
+      "ds_read_b128 %3, %6 offset:1024\n"
       "s_waitcnt lgkmcnt(0)"
       : "=&v"(c.k0), "=&v"(c.k1), "=&v"(c.va), "=&v"(c.vb)
-      : "v"(addr)
+      : "v"(a0), "v"(a1), "v"(a2)
       : "memory");
   return c;
 }
@@ -550,9 +554,14 @@ __device__ __forceinline__ TileLoads ring_read(const u32x4* slot_lane) {
 // page): each wave streams its tiles through a ring of kRing 4 KiB LDS slots
 // filled by global_load_lds_dwordx4, so kRing tiles per wave are in flight
 // without holding registers (12 waves and 36 tiles per CU at 3 workgroups).
-// A slot's four 1 KiB quarters hold K bytes 0-15, K bytes 16-31, V token a and
-// V token b of every lane, lane l at 16 * l.  The vector-memory counter is
-// waited on explicitly: nothing else in the loop uses it.
+// A slot's four 1 KiB quarters hold the 128-byte head rows of K tokens 0-7,
+// K tokens 8-15, V tokens 0-7 and V tokens 8-15.  Each load instruction reads
+// eight whole rows, eight lanes per row, so every request covers full cache
+// lines; inside a row, 16-byte chunk c of token t sits at 16 * (c ^ (t & 7)),
+// and of K token 8 + t at 16 * (c ^ t ^ 1), so that the sixteen lanes reading
+// one chunk of sixteen tokens (or of eight V tokens) hit distinct LDS banks.
+// The vector-memory counter is waited on explicitly: nothing else in the loop
+// uses it.
 template <int NG>
 __global__ void __launch_bounds__(kWaves * 64) decode_partial_ring_kernel(DecodeArgs a, int q_dtype) {
   // split s of sequence b sits at blockIdx.x = (s + b) % max_splits: workgroups
@@ -594,9 +603,19 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_ring_kernel(Decode
 #pragma unroll
     for (int k = 0; k < 16; ++k) st.acc[g][k] = 0.0f;
   }
-  const uint32_t off_k = uint32_t((lane & 15) * a.k_row + 32 * (lane >> 4));
-  const uint32_t off_va = uint32_t(token_slot<(NG <= 4)>(lane) * a.v_row + 16 * column_chunk<(NG <= 4)>(lane));
-  const uint32_t off_vb = uint32_t(off_va + 8 * a.v_row);
+  // load side: lane l fetches the chunk stored at position l & 7 of row l >> 3
+  const int drow = lane >> 3, dchunk = (lane & 7) ^ (lane >> 3);
+  const uint32_t off_k = uint32_t(drow * a.k_row + 16 * dchunk);
+  const uint32_t off_k8 = uint32_t((8 + drow) * a.k_row + 16 * (dchunk ^ 1));
+  const uint32_t off_v = uint32_t(drow * a.v_row + 16 * dchunk);
+  const uint32_t off_v8 = uint32_t(off_v + 8 * a.v_row);
+  // read side: K bytes 32 * (l >> 4) .. + 32 of token l & 15 (the MFMA's B
+  // operand), V chunk column_chunk(l) of tokens token_slot(l) and + 8
+  const int kt = lane & 15, kc = 2 * (lane >> 4), kx = (kt & 7) ^ (kt >> 3);
+  const uint32_t rk0 = uint32_t(1024 * (kt >> 3) + 128 * (kt & 7) + 16 * (kc ^ kx));
+  const uint32_t rk1 = uint32_t(1024 * (kt >> 3) + 128 * (kt & 7) + 16 * ((kc + 1) ^ kx));
+  const int vt = token_slot<(NG <= 4)>(lane), vc = column_chunk<(NG <= 4)>(lane);
+  const uint32_t rv = uint32_t(2048 + 128 * vt + 16 * (vc ^ vt));
   const int stride = kTile * kWaves;
   const int t_first = t_begin + wave * kTile;
   const int n_tiles = t_first < t_end ? (t_end - t_first + stride - 1) / stride : 0;
@@ -613,17 +632,17 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_ring_kernel(Decode
     const int64_t row0 = t0 & (a.block_size - 1);
     const uint8_t* kb = a.k + pid * a.k_blk + row0 * a.k_row + int64_t(h) * a.k_head;
     const uint8_t* vb = a.v + pid * a.v_blk + row0 * a.v_row + int64_t(h) * a.v_head;
-    __builtin_amdgcn_global_load_lds((gvoid*)(kb + off_k), (lvoid*)&ring[slot][0][0], 16, 0, 0);
-    __builtin_amdgcn_global_load_lds((gvoid*)(kb + off_k + 16), (lvoid*)&ring[slot][1][0], 16, 0, 0);
-    __builtin_amdgcn_global_load_lds((gvoid*)(vb + off_va), (lvoid*)&ring[slot][2][0], 16, 0, 0);
-    __builtin_amdgcn_global_load_lds((gvoid*)(vb + off_vb), (lvoid*)&ring[slot][3][0], 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((gvoid*)(kb + off_k), (lvoid*)&ring[slot][0][0], 16, 0, kDmaNontemporal);
+    __builtin_amdgcn_global_load_lds((gvoid*)(kb + off_k8), (lvoid*)&ring[slot][1][0], 16, 0, kDmaNontemporal);
+    __builtin_amdgcn_global_load_lds((gvoid*)(vb + off_v), (lvoid*)&ring[slot][2][0], 16, 0, kDmaNontemporal);
+    __builtin_amdgcn_global_load_lds((gvoid*)(vb + off_v8), (lvoid*)&ring[slot][3][0], 16, 0, kDmaNontemporal);
   };
   auto fetch = [&](int j) {
     // tiles issued after j: min(kRing - 1, n_tiles - 1 - j), four loads each
     if (j + kRing - 1 < n_tiles) __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 * (kRing - 1)));
     else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     const int slot = j % kRing;
-    TileLoads c = ring_read(&ring[slot][0][lane]);
+    TileLoads c = ring_read((uint32_t)(size_t)(lvoid*)&ring[slot][0][0], rk0, rk1, rv);
     if (!((valid >> slot) & 1u)) c.k0 = c.k1 = c.va = c.vb = u32x4(0);
     return c;
   };
