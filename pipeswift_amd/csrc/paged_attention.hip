@@ -60,6 +60,7 @@ constexpr int kTile = 16;     // tokens per tile (N of the 16x16x32 MFMA)
 constexpr int kWaves = 4;     // waves per workgroup
 constexpr int kMinSplit = 256;
 constexpr int kMaxSplits = 128;
+constexpr int kMaxGroup = 8;   // query heads per kv head
 constexpr float kNegBig = -1.0e30f;  // finite "no token yet" maximum
 constexpr float kLazy = 8.0f;        // raise the running max past 2^8 headroom only
 constexpr int kPageCache = 512;      // page ids of a split staged in LDS
@@ -125,6 +126,7 @@ constexpr int kDppXor1 = 0xB1;       // quad_perm [1,0,3,2]
 constexpr int kDppXor2 = 0x4E;       // quad_perm [2,3,0,1]
 constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7 - i within each 8
 constexpr int kDppRowRor8 = 0x128;   // lane i <- lane (i + 8) % 16 within each row
+constexpr int kDppRowMirror = 0x140;  // lane i <-> 15 - i within each row
 
 // P V lane roles.  With replicated query rows (groups of at most 4 heads) lane
 // l owns tokens (l % 8) and (l % 8) + 8 of a tile and V columns 16 * (l / 8) ..
@@ -662,60 +664,91 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_ring_kernel(Decode
   write_partial<NG>(a, st, b, h, s, lane, wave, reinterpret_cast<float(*)[NG][kHead]>(&s_ring[0][0][0][0]));
 }
 
-// One workgroup per (kv head, sequence): each wave turns a head's split maxima
-// and sums into normalised weights in LDS, then every thread sums a (head,
-// column) over the splits with independent loads.
+// Max and sum over the 64 lanes of a wave, in every lane: four DPP steps
+// inside each 16-lane row, then two swaps across rows.
+__device__ __forceinline__ float wave_max(float v) {
+  v = __builtin_fmaxf(v, dpp<kDppXor1>(v));
+  v = __builtin_fmaxf(v, dpp<kDppXor2>(v));
+  v = __builtin_fmaxf(v, dpp<kDppHalfMirror>(v));
+  v = __builtin_fmaxf(v, dpp<kDppRowMirror>(v));
+  v = __builtin_fmaxf(v, __shfl_xor(v, 16));
+  return __builtin_fmaxf(v, __shfl_xor(v, 32));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp<kDppXor1>(v);
+  v += dpp<kDppXor2>(v);
+  v += dpp<kDppHalfMirror>(v);
+  v += dpp<kDppRowMirror>(v);
+  v += __shfl_xor(v, 16);
+  return v + __shfl_xor(v, 32);
+}
+
+// One workgroup per (kv head, sequence), one wave per query head of the group.
+// Lane s holds split s's maximum and sum (and split s + 64's); the weights
+// come from two wave reductions and reach every lane by readlane.  Each lane
+// sums two output columns over the splits; the columns of the first
+// kCombineChunk splits are loaded together with the maxima, so a sequence of
+// up to kCombineChunk splits costs one round of loads.
+constexpr int kCombineChunk = 16;
+
 template <int OUT_DT>
-__global__ void __launch_bounds__(256) decode_combine_kernel(DecodeArgs a) {
+__global__ void __launch_bounds__(64 * kMaxGroup) decode_combine_kernel(DecodeArgs a) {
   const int h = blockIdx.x, b = blockIdx.y;
   const int G = a.group;
+  const int g = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+  const int lane = threadIdx.x & 63;
   const int len = a.seq_lens[b];
   const int n = len > 0 ? min(a.max_splits, (len + a.split - 1) / a.split) : 0;
   const float vd = descale(a.vd, a.vd_b, a.vd_h, b, h);
   const int rec = G * (kHead + 2);
   const float* part = a.part + (int64_t(b) * a.num_kv_heads + h) * a.max_splits * rec;
-  __shared__ float s_w[kMaxSplits * 8];  // weight of split s for head g at [s * 8 + g]
-  __shared__ float s_lse[8];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int g = wave; g < G; g += 4) {
-    float m0 = kNegBig, m1 = kNegBig, l0 = 0.0f, l1 = 0.0f;
-    if (lane < n) {
-      m0 = part[lane * rec + g];
-      l0 = part[lane * rec + G + g];
-    }
-    if (lane + 64 < n) {
-      m1 = part[(lane + 64) * rec + g];
-      l1 = part[(lane + 64) * rec + G + g];
-    }
-    float mx = __builtin_fmaxf(m0, m1);
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, o));
-    const float w0 = __builtin_amdgcn_exp2f(m0 - mx), w1 = __builtin_amdgcn_exp2f(m1 - mx);
-    float den = l0 * w0 + l1 * w1;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) den += __shfl_xor(den, o);
-    const float inv = den > 0.0f ? 1.0f / den : 0.0f;
-    if (lane < n) s_w[lane * 8 + g] = w0 * inv;
-    if (lane + 64 < n) s_w[(lane + 64) * 8 + g] = w1 * inv;
-    // natural-log sum of exp(s): 2^mx * den in the exp2 domain
-    if (lane == 0) s_lse[g] = den > 0.0f ? (mx + __builtin_log2f(den)) * 0.6931471805599453f : -__builtin_inff();
+  const float* col = part + 2 * G + g * kHead + 2 * lane;
+  using Bits = typename Elt<OUT_DT>::Bits;
+  Bits* dst = reinterpret_cast<Bits*>(a.out + b * a.out_tok_stride + int64_t(h * G + g) * a.out_head_stride);
+  if (n == 0) {  // empty sequence: zeros, lse = -inf
+    dst[2 * lane] = Elt<OUT_DT>::from_f32(0.0f);
+    dst[2 * lane + 1] = Elt<OUT_DT>::from_f32(0.0f);
+    if (lane == 0 && a.lse) a.lse[int64_t(h * G + g) * a.lse_head_stride + b] = -__builtin_inff();
+    return;
   }
-  __syncthreads();
-  for (int i = threadIdx.x; i < G * kHead; i += blockDim.x) {
-    const int g = i / kHead, d = i % kHead;
-    const float* x = part + 2 * G + i;
-    float o = 0.0f;
-    int sp = 0;
-    for (; sp + 4 <= n; sp += 4) {
-      const float x0 = x[sp * rec], x1 = x[(sp + 1) * rec], x2 = x[(sp + 2) * rec], x3 = x[(sp + 3) * rec];
-      o += x0 * s_w[sp * 8 + g] + x1 * s_w[(sp + 1) * 8 + g] + x2 * s_w[(sp + 2) * 8 + g] +
-           x3 * s_w[(sp + 3) * 8 + g];
-    }
-    for (; sp < n; ++sp) o += x[sp * rec] * s_w[sp * 8 + g];
-    char* dst = a.out + b * a.out_tok_stride + int64_t(h * G + g) * a.out_head_stride;
-    reinterpret_cast<typename Elt<OUT_DT>::Bits*>(dst)[d] = Elt<OUT_DT>::from_f32(o * vd);
-    if (d == 0 && a.lse) a.lse[int64_t(h * G + g) * a.lse_head_stride + b] = s_lse[g];
+  float m0 = kNegBig, m1 = kNegBig, l0 = 0.0f, l1 = 0.0f;
+  if (lane < n) {
+    m0 = part[lane * rec + g];
+    l0 = part[lane * rec + G + g];
   }
+  if (lane + 64 < n) {
+    m1 = part[(lane + 64) * rec + g];
+    l1 = part[(lane + 64) * rec + G + g];
+  }
+  f32x2 x[kCombineChunk];
+#pragma unroll
+  for (int i = 0; i < kCombineChunk; ++i)
+    x[i] = *reinterpret_cast<const f32x2*>(col + int64_t(min(i, n - 1)) * rec);
+  const float mx = wave_max(__builtin_fmaxf(m0, m1));
+  const float w0 = __builtin_amdgcn_exp2f(m0 - mx), w1 = __builtin_amdgcn_exp2f(m1 - mx);  // 0 past n
+  const float den = wave_sum(l0 * w0 + l1 * w1);
+  float o0 = 0.0f, o1 = 0.0f;
+  for (int s0 = 0; s0 < n; s0 += kCombineChunk) {
+    if (s0 > 0) {
+#pragma unroll
+      for (int i = 0; i < kCombineChunk; ++i)
+        x[i] = *reinterpret_cast<const f32x2*>(col + int64_t(min(s0 + i, n - 1)) * rec);
+    }
+    const float wsrc = s0 < 64 ? w0 : w1;  // a chunk lies on one side of split 64
+#pragma unroll
+    for (int i = 0; i < kCombineChunk; ++i) {
+      const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wsrc), (s0 + i) & 63));
+      o0 = __builtin_fmaf(x[i].x, w, o0);
+      o1 = __builtin_fmaf(x[i].y, w, o1);
+    }
+  }
+  const float inv = den > 0.0f ? vd / den : 0.0f;
+  dst[2 * lane] = Elt<OUT_DT>::from_f32(o0 * inv);
+  dst[2 * lane + 1] = Elt<OUT_DT>::from_f32(o1 * inv);
+  // natural-log sum of exp(s): 2^mx * den in the exp2 domain
+  if (lane == 0 && a.lse)
+    a.lse[int64_t(h * G + g) * a.lse_head_stride + b] =
+        den > 0.0f ? (mx + __builtin_log2f(den)) * 0.6931471805599453f : -__builtin_inff();
 }
 
 // Tokens per workgroup.  num_splits > 0 asks for that many splits of the
@@ -772,7 +805,7 @@ int psk_paged_decode_attention(const void* q, int64_t q_tok_stride, int64_t q_he
   if (num_seqs < 0 || num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads)
     return fail(PSK_E_ARG, "bad head counts (q %lld, kv %lld)", (long long)num_q_heads, (long long)num_kv_heads);
   const int64_t G = num_q_heads / num_kv_heads;
-  if (G > 8) return fail(PSK_E_ARG, "at most 8 query heads per kv head (got %lld)", (long long)G);
+  if (G > kMaxGroup) return fail(PSK_E_ARG, "at most %d query heads per kv head (got %lld)", kMaxGroup, (long long)G);
   if (head_size != kHead) return fail(PSK_E_ARG, "head_size must be %d (got %lld)", kHead, (long long)head_size);
   if (block_size <= 0 || num_blocks <= 0 || num_blocks > INT32_MAX || block_table_width <= 0 || max_seq_len < 0 ||
       max_seq_len > INT32_MAX)
@@ -863,9 +896,9 @@ int psk_paged_decode_attention(const void* q, int64_t q_tok_stride, int64_t q_he
   if (st1 != PSK_OK) return st1;
   const dim3 grid2{unsigned(num_kv_heads), unsigned(num_seqs), 1u};
   if (out_dtype == PSK_DTYPE_BF16)
-    hipLaunchKernelGGL((decode_combine_kernel<PSK_DTYPE_BF16>), grid2, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((decode_combine_kernel<PSK_DTYPE_BF16>), grid2, dim3(64 * G), 0, st, a);
   else
-    hipLaunchKernelGGL((decode_combine_kernel<PSK_DTYPE_F32>), grid2, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((decode_combine_kernel<PSK_DTYPE_F32>), grid2, dim3(64 * G), 0, st, a);
   return check_launch("decode_combine_kernel launch");
 }
 
