@@ -64,7 +64,7 @@ constexpr int kMaxGroup = 8;   // query heads per kv head
 constexpr float kNegBig = -1.0e30f;  // finite "no token yet" maximum
 constexpr float kLazy = 8.0f;        // raise the running max past 2^8 headroom only
 constexpr int kPageCache = 512;      // page ids of a split staged in LDS
-constexpr int kRing = 3;             // LDS tile slots per wave (ring kernel)
+constexpr int kRing = 2;             // LDS tile slots per wave (ring kernel)
 constexpr int kRingPages = 1024;     // page ids of a split in the ring kernel
 
 typedef __attribute__((address_space(1))) void gvoid;
@@ -555,7 +555,8 @@ __device__ __forceinline__ TileLoads ring_read(uint32_t slot, uint32_t rk0, uint
 // Variant for block sizes that are powers of two >= 16 (a tile lies in one
 // page): each wave streams its tiles through a ring of kRing 4 KiB LDS slots
 // filled by global_load_lds_dwordx4, so kRing tiles per wave are in flight
-// without holding registers (12 waves and 36 tiles per CU at 3 workgroups).
+// without holding registers (16 waves and 32 tiles per CU at 4 workgroups;
+// a third slot per wave, at 3 workgroups per CU, measured 1% slower).
 // A slot's four 1 KiB quarters hold the 128-byte head rows of K tokens 0-7,
 // K tokens 8-15, V tokens 0-7 and V tokens 8-15.  Each load instruction reads
 // eight whole rows, eight lanes per row, so every request covers full cache
@@ -593,6 +594,7 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_ring_kernel(Decode
   const int n_ids = ((t_end - 1) >> a.bs_shift) - first + 1;
   for (int i = threadIdx.x; i < n_ids; i += kWaves * 64) s_pages[i] = checked_page(a, bt_row, first + i);
   __shared__ __attribute__((aligned(16))) u32x4 s_ring[kWaves][kRing][4][64];
+  static_assert(sizeof(s_ring) >= sizeof(float) * kWaves * NG * kHead, "the ring doubles as the merge buffer");
   __syncthreads();
   u32x4(*ring)[4][64] = s_ring[wave];
 
@@ -752,15 +754,16 @@ __global__ void __launch_bounds__(64 * kMaxGroup) decode_combine_kernel(DecodeAr
 }
 
 // Tokens per workgroup.  num_splits > 0 asks for that many splits of the
-// longest sequence; 0 aims at 24 splits of it (measured best for config 2's
-// 128 x 8 sequence-heads), more when there are too few sequence-heads to put
-// ~1536 workgroups on a long context.  Rounded up to whole 64-token wave
+// longest sequence; 0 aims at 20 splits of it (measured best for config 2's
+// 128 x 8 sequence-heads, within 1% from 17 to 20 and up to 20% slower from 31
+// on), more when there are too few sequence-heads to put ~1536 workgroups on a
+// long context.  Rounded up to whole 64-token wave
 // strides, at least kMinSplit tokens, and doubled until at most kMaxSplits
 // splits cover max_seq_len.
 int decode_split(int64_t max_seq_len, int64_t num_splits, int64_t seq_heads) {
   const int64_t stride = kTile * kWaves;
   int64_t target = num_splits;
-  if (target <= 0) target = std::min<int64_t>(kMaxSplits, std::max<int64_t>(24, ceil_div(1536, std::max<int64_t>(seq_heads, 1))));
+  if (target <= 0) target = std::min<int64_t>(kMaxSplits, std::max<int64_t>(20, ceil_div(1536, std::max<int64_t>(seq_heads, 1))));
   int64_t split = ceil_div(ceil_div(std::max<int64_t>(max_seq_len, 1), target), stride) * stride;
   if (num_splits <= 0) split = std::max<int64_t>(split, kMinSplit);
   while (ceil_div(max_seq_len, split) > kMaxSplits) split *= 2;
