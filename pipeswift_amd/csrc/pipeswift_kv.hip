@@ -138,7 +138,7 @@ __global__ void __launch_bounds__(WPB * 64) paged_scatter_kernel(ScatterGeom g, 
     }
     drow[c] = dst + blk * blk_stride + off * page_stride + dst_off;
   }
-  const QScale qs = make_qscale(scale_p ? *scale_p : 1.0f);
+  const QScale qs = make_qscale_uniform(scale_p ? *scale_p : 1.0f);
 
   for (;;) {
 #pragma unroll

@@ -165,6 +165,16 @@ __device__ __forceinline__ QScale make_qscale(float s) {
   return q;
 }
 
+// For a scale that is the same in every lane of the wave.  The range test then
+// becomes a scalar branch: without it the compiler cannot tell that the test is
+// uniform, and evaluates both the fast path and the IEEE divisions for every
+// element, selecting per lane.
+__device__ __forceinline__ QScale make_qscale_uniform(float s) {
+  QScale q = make_qscale(s);
+  q.fast = __builtin_amdgcn_readfirstlane(int(q.fast)) != 0;
+  return q;
+}
+
 // Exact for s == 1.0 as well: r = 1, y = x, e = 0.
 __device__ __forceinline__ float div_fast(float x, const QScale& q) {
   const float y = x * q.r;
@@ -204,7 +214,10 @@ struct QuantConv {
 #pragma unroll
       for (int i = 0; i < E; ++i) f[i] = div_fast(EltT::to_f32(e[i]), qs);
     } else {
-      // scales outside [2^-80, 2^100) (0, inf, NaN, subnormal): IEEE division
+      // scales outside [2^-80, 2^100) (0, inf, NaN, subnormal): IEEE division.
+      // The empty volatile asm keeps this a branch: otherwise the compiler
+      // computes both paths for every element and selects.
+      asm volatile("");
 #pragma unroll
       for (int i = 0; i < E; ++i) f[i] = EltT::to_f32(e[i]) / qs.s;
     }
