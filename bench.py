@@ -28,6 +28,11 @@ Workloads (default fp8_decode_append, config 2 of the benchmark plan):
   copy_blocks        2048 pairs over 61 layers of [8192, 2, 16, 8, 128] bf16
   swap               8192 scattered blocks x 8 layers (4 GiB) D2H + H2D
   kv_scales          config 2's per-tensor K/V scales (amax kernel)
+  decode_attention   one decode step of FP8 paged attention over config 2's
+                     cache (128 sequences, 8 kv heads, 32 query heads)
+  attention_shapes   decode attention on six batch shapes, balanced vs split
+                     schedule
+  l2_cycle           BlockManager store -> evict -> restore of an 8192-page prompt
   swap_sweep         host-link GB/s vs bytes per page, per transport
   metadata           host us per step of prepare_kv_info (native builder)
   hbm_copy           1 GiB device copy (achievable-bandwidth reference and the
@@ -169,7 +174,9 @@ def setup_decode_attention(args, device):
     pages = int(sum(len(t) for t in tables))
     nbytes = total * H * D * 2 + pages * 4 + 2 * B * Hq * D * 2
     info = {
-        "name": "decode_attention", "kernel": "decode_partial_kernel", "bytes": nbytes, "tokens": B,
+        "name": "decode_attention",
+        "kernel": "decode_partial_stream_kernel" if args.num_splits == 0 else "decode_partial_ring_kernel",
+        "bytes": nbytes, "tokens": B,
         "dtype": "fp8_e4m3fn",
         "rotate": R,
         "config": {"workload": "FP8 paged decode attention (config 2 cache)", "sequences": B, "context_tokens": total,
@@ -641,6 +648,74 @@ def run_l2_cycle(args, device):
     print(json.dumps(line), flush=True)
 
 
+def run_attention_shapes(args, device):
+    """Decode attention over several batch shapes, under the balanced schedule
+    (num_splits 0, the default) and under the split schedule at the count the
+    split heuristic would pick; random FP8 pages, shuffled block tables, HIP
+    events around `--steps` eager calls after 5 warmup calls."""
+    import math
+
+    import numpy as np
+    import torch
+
+    from pipeswift_amd import attention
+
+    rng = np.random.default_rng(0)
+    shapes = [
+        ("1 x 131072, 4 kv heads, group 8", 4, 8, [131072]),
+        ("1 x 32768", 8, 4, [32768]),
+        ("8 x 32768", 8, 4, [32768] * 8),
+        ("32 x 8192", 8, 4, [8192] * 32),
+        ("128 log-uniform 128-32768", 8, 4, [int(x) for x in np.exp(rng.uniform(np.log(128), np.log(32768), 128))]),
+        ("64 uniform 1-4096", 8, 4, [int(x) for x in rng.integers(1, 4096, 64)]),
+    ]
+    reps = max(10, min(args.steps, 50))
+    results = []
+    for name, Hkv, G, lens in shapes:
+        B, ps = len(lens), 16
+        g = torch.Generator(device=device).manual_seed(1)
+        pages = [math.ceil(x / ps) for x in lens]
+        P = sum(pages) + 8
+        cache = torch.empty(P, 2, ps, Hkv, 128, dtype=torch.float8_e4m3fn, device=device)
+        cache.view(torch.uint8).random_(0, 120, generator=g)
+        W = max(pages)
+        bt = torch.zeros(B, W, dtype=torch.int32)
+        perm = torch.randperm(P, generator=torch.Generator().manual_seed(2))
+        o = 0
+        for b in range(B):
+            bt[b, : pages[b]] = perm[o: o + pages[b]].to(torch.int32)
+            o += pages[b]
+        bt = bt.to(device)
+        sl = torch.tensor(lens, dtype=torch.int32, device=device)
+        q = torch.randn(B, Hkv * G, 128, device=device, generator=g).to(torch.bfloat16)
+        out = torch.empty(B, Hkv * G, 128, dtype=torch.bfloat16, device=device)
+        kv_bytes = sum(lens) * Hkv * 128 * 2
+        split = min(128, max(20, math.ceil(1536 / (B * Hkv))))
+        row = {"shape": name, "tokens": sum(lens), "kv_bytes": kv_bytes}
+        for label, ns in (("balanced", 0), (f"split_{split}", split)):
+            ws = torch.empty(attention.workspace_floats(B, Hkv * G, Hkv, W * ps, ns), dtype=torch.float32, device=device)
+
+            def call():
+                attention.paged_decode_attention(q, cache[:, 0], cache[:, 1], bt, sl, None, out=out, workspace=ws,
+                                                 num_splits=ns)
+
+            for _ in range(5):
+                call()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                call()
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) / reps * 1e3
+            row[label] = {"us": round(us, 2), "GB/s": round(kv_bytes / us / 1e3, 1)}
+        results.append(row)
+        print(json.dumps(row), file=sys.stderr, flush=True)
+    print(json.dumps({"metric": "decode attention us per call, balanced vs split schedule", "unit": "us",
+                      "calls_per_shape": reps, "shapes": results}), flush=True)
+
+
 def run_swap_sweep(args, device):
     """Host-link GB/s against bytes per page at a fixed 256 MiB per transfer,
     scattered pages (every page its own run), both directions, per transport:
@@ -840,6 +915,8 @@ def main():
         return run_hbm_copy(args, device)
     elif name == "swap_sweep":
         return run_swap_sweep(args, device)
+    elif name == "attention_shapes":
+        return run_attention_shapes(args, device)
     elif name == "metadata":
         return run_metadata(args, device)
     elif name == "l2_cycle":

@@ -248,8 +248,11 @@ int64_t psk_build_kv_metadata(int64_t num_seqs, const uint64_t* page_table_ptrs,
  * block_table[b * block_table_stride + j / block_size]; entries past
  * block_table_width or outside [0, num_blocks) read as zero rows.
  * max_seq_len bounds every seq_lens[b] (block_table_width * block_size does).
- * num_splits: how many workgroups share the longest sequence (flash-decoding
- * split, as FA's num_splits); 0 chooses.  At most 128 splits are used.
+ * num_splits > 0: how many workgroups share the longest sequence (flash-decoding
+ * split, as FA's num_splits; at most 128 are used).  0: the balanced schedule
+ * when the block size is a power of two >= 16 and num_seqs <= 1024 (one
+ * workgroup per resident slot, each taking an equal run of every sequence's
+ * 16-token tiles of one kv head), otherwise an automatic split count.
  * out: bf16 or f32 at element strides (out_tok_stride, out_head_stride); lse
  * (fp32, optional) at lse[hq * lse_head_stride + b]; a sequence of length 0
  * writes zeros and lse = -inf.  workspace: device floats, at least

@@ -8,7 +8,8 @@ causal, fa_version=3, q_descale, k_descale, v_descale)``
 (pipeswift/llms/layers/attention.py:148-187), with every descale 1.0
 (pipeswift/utils/fp8_kv.py:94-103).  ``flash_attn_varlen_func`` here takes the
 same arguments for the decode case (one query token per sequence) and runs
-``psk_paged_decode_attention``: FP8 MFMA for Q K^T, fp32 softmax and P V, and
+``psk_paged_decode_attention``: Q K^T on the bf16 MFMA over exactly converted
+FP8 values (gfx950's FP8 MFMA truncates its sums), fp32 softmax and P V, and
 descales of any value per (sequence, kv head) -- for instance the per-tensor
 scales ``cache_ops.compute_kv_scales`` gave the append.
 
@@ -74,7 +75,10 @@ def paged_decode_attention(
     [P, 2, ps, H, D] layer are fine).  block_table: int32 [B, W];
     seq_lens: int32 [B] (``seqused_k``).  Returns out [B, Hq, 128] (bf16 unless
     ``out`` is given as float32) and, when asked, lse [Hq, B] float32.
-    ``num_splits``: workgroups per longest sequence (0 chooses), as FA's.
+    ``num_splits``: workgroups per longest sequence, as FA's; 0 (default)
+    balances the work instead: one workgroup per resident slot, each streaming
+    an equal run of the batch's 16-token tiles of one kv head across sequence
+    boundaries.
     """
     assert q.is_cuda and k_cache.is_cuda and v_cache.is_cuda
     assert q.dim() == 3 and q.shape[2] == HEAD_DIM and q.stride(2) == 1, "q must be [B, Hq, 128] with unit last stride"
@@ -139,8 +143,8 @@ def flash_attn_varlen_func(
     sequence (``max_seqlen_q == 1``; ``cu_seqlens_q`` then is 0..B and
     ``causal`` has nothing to mask).  ``max_seqlen_k`` bounds the lengths when
     given, else the block table's width does.  ``num_splits`` is the
-    flash-decoding split count (0 chooses); ``fa_version`` is accepted for
-    signature compatibility."""
+    flash-decoding split count (0: the balanced schedule); ``fa_version`` is
+    accepted for signature compatibility."""
     assert max_seqlen_q == 1, "decode only: one query token per sequence"
     assert seqused_k is not None and block_table is not None, "paged decode needs seqused_k and block_table"
     B = seqused_k.shape[0]

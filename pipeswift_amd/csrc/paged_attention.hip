@@ -43,6 +43,8 @@
 
 #include <algorithm>
 #include <cmath>
+#include <map>
+#include <mutex>
 
 #include "pipeswift_kv.h"
 #include "psk_common.h"
@@ -66,6 +68,10 @@ constexpr float kLazy = 8.0f;        // raise the running max past 2^8 headroom 
 constexpr int kPageCache = 512;      // page ids of a split staged in LDS
 constexpr int kRing = 2;             // LDS tile slots per wave (ring kernel)
 constexpr int kRingPages = 1024;     // page ids of a split in the ring kernel
+// Sequences of the balanced schedule: every workgroup scans their lengths
+// (twice) and keeps the prefix in the ring's LDS.
+constexpr int kStreamMaxSeqs = 1024;
+static_assert(kRingPages % (kWaves * 64) == 0, "page ids are staged a whole number per thread");
 
 typedef __attribute__((address_space(1))) void gvoid;
 typedef __attribute__((address_space(3))) void lvoid;
@@ -96,7 +102,10 @@ struct DecodeArgs {
   int64_t kd_b, kd_h;
   const float* vd;
   int64_t vd_b, vd_h;
-  float* part;       // partials: [B][Hkv][max_splits][G * (kHead + 2)]
+  float* part;       // partial records of G * (kHead + 2) floats: [B][Hkv][max_splits] (splits) or
+                     // [(B + stream_wgs) * Hkv] (balanced schedule)
+  int32_t* prefix;   // balanced schedule: tiles before each sequence, [B + 1]
+  int32_t stream_wgs;  // balanced schedule: workgroups per kv head; 0 with splits
   char* out;
   int64_t out_tok_stride;   // bytes
   int64_t out_head_stride;  // bytes
@@ -385,11 +394,11 @@ __device__ __forceinline__ void merge_slots(Softmax<NG>& st) {
   }
 }
 
-// Merge the wave's eight token slots, then the
-// workgroup's waves through LDS, and write split s's partial record: per
-// query head the maximum, the sum and the 128 weighted V columns.
+// Merge the wave's eight token slots, then the workgroup's waves through LDS,
+// and write partial record `rec_idx`: per query head the maximum, the sum and
+// the 128 weighted V columns.
 template <int NG>
-__device__ __forceinline__ void write_partial(const DecodeArgs& a, Softmax<NG>& st, int b, int h, int s, int lane,
+__device__ __forceinline__ void write_partial(const DecodeArgs& a, Softmax<NG>& st, int64_t rec_idx, int lane,
                                               int wave, float (*s_acc)[NG][kHead]) {
   const int G = a.group;
   constexpr bool REPL = NG <= 4;
@@ -435,7 +444,7 @@ __device__ __forceinline__ void write_partial(const DecodeArgs& a, Softmax<NG>& 
   }
   __syncthreads();
   const int rec = G * (kHead + 2);
-  float* part = a.part + ((int64_t(b) * a.num_kv_heads + h) * a.max_splits + s) * rec;
+  float* part = a.part + rec_idx * rec;
   for (int i = threadIdx.x; i < G * kHead; i += kWaves * 64) {
     const int g = i / kHead, d = i % kHead;
     float mx = s_m[0][g];
@@ -523,7 +532,7 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_kernel(DecodeArgs 
   }
 
   __shared__ float s_acc[kWaves][NG][kHead];
-  write_partial<NG>(a, st, b, h, s, lane, wave, s_acc);
+  write_partial<NG>(a, st, (int64_t(b) * a.num_kv_heads + h) * a.max_splits + s, lane, wave, s_acc);
 }
 
 // vmcnt <= n, expcnt and lgkmcnt untouched (gfx9 s_waitcnt encoding)
@@ -552,11 +561,11 @@ __device__ __forceinline__ TileLoads ring_read(uint32_t slot, uint32_t rk0, uint
   return c;
 }
 
-// Variant for block sizes that are powers of two >= 16 (a tile lies in one
-// page): each wave streams its tiles through a ring of kRing 4 KiB LDS slots
-// filled by global_load_lds_dwordx4, so kRing tiles per wave are in flight
-// without holding registers (16 waves and 32 tiles per CU at 4 workgroups;
-// a third slot per wave, at 3 workgroups per CU, measured 1% slower).
+// Block sizes that are powers of two >= 16 (a tile lies in one page): each
+// wave streams its tiles through a ring of kRing 4 KiB LDS slots filled by
+// global_load_lds_dwordx4, so kRing tiles per wave are in flight without
+// holding registers (16 waves and 32 tiles per CU at 4 workgroups; a third
+// slot per wave, at 3 workgroups per CU, measured 1% slower).
 // A slot's four 1 KiB quarters hold the 128-byte head rows of K tokens 0-7,
 // K tokens 8-15, V tokens 0-7 and V tokens 8-15.  Each load instruction reads
 // eight whole rows, eight lanes per row, so every request covers full cache
@@ -565,48 +574,41 @@ __device__ __forceinline__ TileLoads ring_read(uint32_t slot, uint32_t rk0, uint
 // one chunk of sixteen tokens (or of eight V tokens) hit distinct LDS banks.
 // The vector-memory counter is waited on explicitly: nothing else in the loop
 // uses it.
-template <int NG>
-__global__ void __launch_bounds__(kWaves * 64) decode_partial_ring_kernel(DecodeArgs a, int q_dtype) {
-  // split s of sequence b sits at blockIdx.x = (s + b) % max_splits: workgroups
-  // go round-robin to the 8 XCDs by blockIdx.x (max_splits is the fastest grid
-  // dimension), so the first splits of short sequences spread over all of them
-  const int h = blockIdx.y, b = blockIdx.z;
-  const int s = int((blockIdx.x + unsigned(a.max_splits) - unsigned(b % a.max_splits)) % unsigned(a.max_splits));
-  const int len = a.seq_lens[b];
-  const int t_begin = s * a.split;
-  if (t_begin >= len || s >= a.max_splits) return;  // uniform over the workgroup
-  const int t_end = min(len, t_begin + a.split);
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+struct RingLds {
+  u32x4 ring[kWaves][kRing][4][64];
+  int32_t pages[kRingPages];
+};
 
-  const float qd = descale(a.qd, a.qd_b, a.qd_h, b, h);
-  const float kd = descale(a.kd, a.kd_b, a.kd_h, b, h);
-  const float sl = a.scale_log2 * qd * kd;
-  uint32_t qw[8];
-  load_query<(NG <= 4)>(a, q_dtype, b, h, qd, lane, qw);
-  const bf16x8 qop[4] = {e4m3x8_to_bf16(qw[0], qw[1]), e4m3x8_to_bf16(qw[2], qw[3]), e4m3x8_to_bf16(qw[4], qw[5]),
-                         e4m3x8_to_bf16(qw[6], qw[7])};
-
-  // page ids of the split (the host guarantees they fit), then the tile ring
-  __shared__ int32_t s_pages[kRingPages];
+// Tokens [t_begin, t_end) of (sequence b, kv head h) into the running softmax
+// st of this wave (wave w takes tiles t_begin + 16 w + 64 j).  t_begin is a
+// multiple of 16 and the range spans at most kRingPages pages.  Called by every
+// wave of the workgroup: it stages the range's page ids behind a barrier.
+// `overlap` runs while the page-id loads are in flight (a new head's query
+// loads go there, so that both cost one memory latency).
+template <int NG, class Overlap>
+__device__ __forceinline__ void ring_attend(const DecodeArgs& a, Softmax<NG>& st, const bf16x8 (&qop)[4],
+                                            const float& sl, int b, int h, int t_begin, int t_end, int lane,
+                                            int wave, RingLds& lds, const Overlap& overlap) {
+  constexpr int kIdsPerThread = kRingPages / (kWaves * 64);
   const int32_t* bt_row = a.block_table + b * a.bt_stride;
   const int first = t_begin >> a.bs_shift;
   const int n_ids = ((t_end - 1) >> a.bs_shift) - first + 1;
-  for (int i = threadIdx.x; i < n_ids; i += kWaves * 64) s_pages[i] = checked_page(a, bt_row, first + i);
-  __shared__ __attribute__((aligned(16))) u32x4 s_ring[kWaves][kRing][4][64];
-  static_assert(sizeof(s_ring) >= sizeof(float) * kWaves * NG * kHead, "the ring doubles as the merge buffer");
-  __syncthreads();
-  u32x4(*ring)[4][64] = s_ring[wave];
-
-  Softmax<NG> st;
+  __syncthreads();  // the previous range's readers of pages and ring are done
+  int32_t ids[kIdsPerThread];
 #pragma unroll
-  for (int g = 0; g < NG; ++g) {
-    st.m[g] = kNegBig;
-    st.mth[g] = kNegBig + kLazy;
-    st.l[g] = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 16; ++k) st.acc[g][k] = 0.0f;
+  for (int k = 0; k < kIdsPerThread; ++k) {
+    const int i = int(threadIdx.x) + k * kWaves * 64;
+    ids[k] = i < n_ids ? checked_page(a, bt_row, first + i) : -1;
   }
+  overlap();
+#pragma unroll
+  for (int k = 0; k < kIdsPerThread; ++k) {
+    const int i = int(threadIdx.x) + k * kWaves * 64;
+    if (i < n_ids) lds.pages[i] = ids[k];
+  }
+  __syncthreads();
+  u32x4(*ring)[4][64] = lds.ring[wave];
+
   // load side: lane l fetches the chunk stored at position l & 7 of row l >> 3
   const int drow = lane >> 3, dchunk = (lane & 7) ^ (lane >> 3);
   const uint32_t off_k = uint32_t(drow * a.k_row + 16 * dchunk);
@@ -629,7 +631,7 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_ring_kernel(Decode
   uint32_t valid = 0;  // bit j % kRing: slot holds a tile on a real page
   auto issue = [&](int j) {
     const int t0 = t_first + j * stride;
-    const int32_t raw = __builtin_amdgcn_readfirstlane(s_pages[(t0 >> a.bs_shift) - first]);
+    const int32_t raw = __builtin_amdgcn_readfirstlane(lds.pages[(t0 >> a.bs_shift) - first]);
     const int slot = j % kRing;
     valid = raw >= 0 ? (valid | (1u << slot)) : (valid & ~(1u << slot));
     const int64_t pid = raw >= 0 ? raw : 0;
@@ -662,8 +664,162 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_ring_kernel(Decode
     TileLoads c = fetch(j);
     attend_step<NG, true>(st, c, qop, sl, t_first + j * stride, t_end, lane, [] {});
   }
+}
+
+template <int NG>
+__device__ __forceinline__ void softmax_init(Softmax<NG>& st) {
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    st.m[g] = kNegBig;
+    st.mth[g] = kNegBig + kLazy;
+    st.l[g] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) st.acc[g][k] = 0.0f;
+  }
+}
+
+// Query operands and the score scale of (sequence b, kv head h).
+template <int NG>
+__device__ __forceinline__ float load_head(const DecodeArgs& a, int q_dtype, int b, int h, int lane, bf16x8 qop[4]) {
+  const float qd = descale(a.qd, a.qd_b, a.qd_h, b, h);
+  const float kd = descale(a.kd, a.kd_b, a.kd_h, b, h);
+  uint32_t qw[8];
+  load_query<(NG <= 4)>(a, q_dtype, b, h, qd, lane, qw);
+  qop[0] = e4m3x8_to_bf16(qw[0], qw[1]);
+  qop[1] = e4m3x8_to_bf16(qw[2], qw[3]);
+  qop[2] = e4m3x8_to_bf16(qw[4], qw[5]);
+  qop[3] = e4m3x8_to_bf16(qw[6], qw[7]);
+  return a.scale_log2 * qd * kd;
+}
+
+// One workgroup per (split, kv head, sequence) (an explicit num_splits).
+template <int NG>
+__global__ void __launch_bounds__(kWaves * 64) decode_partial_ring_kernel(DecodeArgs a, int q_dtype) {
+  // split s of sequence b sits at blockIdx.x = (s + b) % max_splits: workgroups
+  // go round-robin to the 8 XCDs by blockIdx.x (max_splits is the fastest grid
+  // dimension), so the first splits of short sequences spread over all of them
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int s = int((blockIdx.x + unsigned(a.max_splits) - unsigned(b % a.max_splits)) % unsigned(a.max_splits));
+  const int len = a.seq_lens[b];
+  const int t_begin = s * a.split;
+  if (t_begin >= len || s >= a.max_splits) return;  // uniform over the workgroup
+  const int t_end = min(len, t_begin + a.split);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+  __shared__ RingLds lds;
+  static_assert(sizeof(lds.ring) >= sizeof(float) * kWaves * NG * kHead, "the ring doubles as the merge buffer");
+  bf16x8 qop[4];
+  float sl = 0.0f;
+  Softmax<NG> st;
+  softmax_init(st);
+  // the host keeps a split within kRingPages pages
+  ring_attend<NG>(a, st, qop, sl, b, h, t_begin, t_end, lane, wave, lds,
+                  [&] { sl = load_head<NG>(a, q_dtype, b, h, lane, qop); });
   __syncthreads();  // every wave is done with the ring: it becomes the merge buffer
-  write_partial<NG>(a, st, b, h, s, lane, wave, reinterpret_cast<float(*)[NG][kHead]>(&s_ring[0][0][0][0]));
+  write_partial<NG>(a, st, (int64_t(b) * a.num_kv_heads + h) * a.max_splits + s, lane, wave,
+                    reinterpret_cast<float(*)[NG][kHead]>(&lds.ring[0][0][0][0]));
+}
+
+// Balanced schedule.  Per kv head the work is the list of units (sequence b,
+// 16-token tile t), T = sum of tiles_b = ceil(len_b / 16) in all.  Run j of
+// head h takes head h's units [T j / M, T (j+1) / M), M = min(grid / Hkv, T), whatever sequences they belong to: every workgroup streams the same
+// number of tiles, the grid (one workgroup per resident slot) ends together,
+// and the Hkv workgroups of one j walk the same tokens of the same pages at
+// the same time (a token's kv heads share its cache rows).  Workgroup
+// j * Hkv + h runs (h, j): the heads of one run are dispatched together.  Each maximal run
+// of one sequence inside the range gives one partial record, at index
+// (b + j) * Hkv + h: the records of one (b, h) come from consecutive j, Hkv
+// apart.  Workgroup 0 also stores the tiles prefix (prefix[b] = tiles before
+// b) after the records for the combine.
+__device__ __forceinline__ int tiles_of(int len) { return len > 0 ? (len + kTile - 1) / kTile : 0; }
+
+template <int NG>
+__global__ void __launch_bounds__(kWaves * 64) decode_partial_stream_kernel(DecodeArgs a, int q_dtype, int num_seqs) {
+  const int w = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+  const int Hkv = a.num_kv_heads;
+  __shared__ RingLds lds;
+  static_assert(sizeof(lds.ring) >= sizeof(float) * kWaves * NG * kHead, "the ring doubles as the merge buffer");
+  static_assert(sizeof(lds.ring) / sizeof(int32_t) > kStreamMaxSeqs, "the ring holds the tiles prefix");
+
+  // tiles prefix over the sequences, scanned in the ring (free until the first tile)
+  int32_t* pref = reinterpret_cast<int32_t*>(&lds.ring[0][0][0][0]);
+  __shared__ int32_t s_scan[kWaves * 64];
+  const int tid = threadIdx.x, nt = kWaves * 64;
+  const int chunk = (num_seqs + nt - 1) / nt;
+  int sum = 0;
+  for (int i = 0; i < chunk; ++i) {
+    const int b = tid * chunk + i;
+    if (b < num_seqs) sum += tiles_of(a.seq_lens[b]);
+  }
+  s_scan[tid] = sum;
+  __syncthreads();
+  for (int o = 1; o < nt; o <<= 1) {
+    const int v = tid >= o ? s_scan[tid - o] : 0;
+    __syncthreads();
+    s_scan[tid] += v;
+    __syncthreads();
+  }
+  int run = tid > 0 ? s_scan[tid - 1] : 0;
+  for (int i = 0; i < chunk; ++i) {
+    const int b = tid * chunk + i;
+    if (b < num_seqs) {
+      pref[b] = run;
+      run += tiles_of(a.seq_lens[b]);
+    }
+  }
+  if (tid == nt - 1) pref[num_seqs] = s_scan[nt - 1];
+  __syncthreads();
+  const int64_t T = pref[num_seqs];
+  if (w == 0) {
+    for (int i = tid; i <= num_seqs; i += nt) a.prefix[i] = pref[i];
+  }
+  // no more runs than units, so that no range is empty and the records of one
+  // (b, h) stay consecutive; the other workgroups leave
+  const int h = w % Hkv, j = w / Hkv;
+  const int64_t M = min<int64_t>(gridDim.x / Hkv, T);
+  if (j >= M) return;  // uniform over the workgroup
+  int64_t u = T * j / M;
+  const int64_t u_end = T * (j + 1) / M;
+  // last b with pref[b] <= u (sequences without tiles share their successor's
+  // prefix; the search lands on the one that owns unit u)
+  int lo = 0, hi = num_seqs - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (pref[mid] <= u) lo = mid; else hi = mid - 1;
+  }
+  int b = lo;
+  int t = int(u - pref[b]);
+  // ring_attend's first barrier orders these prefix reads before the ring is refilled
+
+  // tokens per page staging: at most kRingPages pages from any 16-aligned start
+  const int piece = int(std::min<int64_t>(int64_t(kRingPages - 1) << a.bs_shift, INT32_MAX / 2)) & ~(kTile * kWaves - 1);
+  while (u < u_end && b < num_seqs) {
+    const int len = a.seq_lens[b];
+    const int tb = tiles_of(len);
+    const int n = int(min<int64_t>(tb - t, u_end - u));
+    bf16x8 qop[4];
+    float sl = 0.0f;
+    Softmax<NG> st;
+    softmax_init(st);
+    const int t_end = min(len, (t + n) * kTile);
+    for (int t0 = t * kTile; t0 < t_end; t0 += piece) {
+      const bool head = t0 == t * kTile;
+      ring_attend<NG>(a, st, qop, sl, b, h, t0, min(t_end, t0 + piece), lane, wave, lds, [&] {
+        if (head) sl = load_head<NG>(a, q_dtype, b, h, lane, qop);
+      });
+    }
+    __syncthreads();  // every wave is done with the ring: it becomes the merge buffer
+    write_partial<NG>(a, st, (int64_t(b) + j) * Hkv + h, lane, wave,
+                      reinterpret_cast<float(*)[NG][kHead]>(&lds.ring[0][0][0][0]));
+    u += n;
+    t += n;
+    if (t == tb) {
+      t = 0;
+      do ++b; while (b < num_seqs && a.seq_lens[b] <= 0);
+    }
+  }
 }
 
 // Max and sum over the 64 lanes of a wave, in every lane: four DPP steps
@@ -686,11 +842,12 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // One workgroup per (kv head, sequence), one wave per query head of the group.
-// Lane s holds split s's maximum and sum (and split s + 64's); the weights
-// come from two wave reductions and reach every lane by readlane.  Each lane
-// sums two output columns over the splits; the columns of the first
-// kCombineChunk splits are loaded together with the maxima, so a sequence of
-// up to kCombineChunk splits costs one round of loads.
+// The records are taken 64 at a time: lane s holds record s's maximum and sum,
+// two wave reductions (with an online rescale across chunks) give the weights,
+// and readlane hands each weight to every lane.  Each lane sums two output
+// columns over the records; the columns of the first kCombineChunk records of
+// a chunk are loaded together with its maxima, so up to kCombineChunk records
+// cost one round of loads.
 constexpr int kCombineChunk = 16;
 
 template <int OUT_DT>
@@ -699,51 +856,67 @@ __global__ void __launch_bounds__(64 * kMaxGroup) decode_combine_kernel(DecodeAr
   const int G = a.group;
   const int g = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
   const int lane = threadIdx.x & 63;
-  const int len = a.seq_lens[b];
-  const int n = len > 0 ? min(a.max_splits, (len + a.split - 1) / a.split) : 0;
-  const float vd = descale(a.vd, a.vd_b, a.vd_h, b, h);
   const int rec = G * (kHead + 2);
-  const float* part = a.part + (int64_t(b) * a.num_kv_heads + h) * a.max_splits * rec;
+  int64_t first = 0;  // index of the first record of (b, h)
+  int64_t rs = rec;   // floats between consecutive records of (b, h)
+  int n = 0;          // records of (b, h)
+  if (a.stream_wgs > 0) {
+    // run j of head h took units [T j / M, T (j+1) / M); unit u belongs to run
+    // j(u) = ((u + 1) M - 1) / T, and b owns units [p0, p0 + tiles)
+    const int64_t p0 = a.prefix[b], tiles = a.prefix[b + 1] - p0;
+    if (tiles > 0) {
+      const int64_t T = a.prefix[gridDim.y];
+      const int64_t M = min<int64_t>(a.stream_wgs, T);  // as the partial kernel caps it
+      const int64_t j0 = ((p0 + 1) * M - 1) / T, j1 = ((p0 + tiles) * M - 1) / T;
+      first = (int64_t(b) + j0) * a.num_kv_heads + h;
+      rs = int64_t(a.num_kv_heads) * rec;
+      n = int(j1 - j0 + 1);
+    }
+  } else {
+    const int len = a.seq_lens[b];
+    n = len > 0 ? min(a.max_splits, (len + a.split - 1) / a.split) : 0;
+    first = (int64_t(b) * a.num_kv_heads + h) * a.max_splits;
+  }
+  const float vd = descale(a.vd, a.vd_b, a.vd_h, b, h);
+  const float* part = a.part + first * rec;
   const float* col = part + 2 * G + g * kHead + 2 * lane;
   using Bits = typename Elt<OUT_DT>::Bits;
   Bits* dst = reinterpret_cast<Bits*>(a.out + b * a.out_tok_stride + int64_t(h * G + g) * a.out_head_stride);
-  if (n == 0) {  // empty sequence: zeros, lse = -inf
-    dst[2 * lane] = Elt<OUT_DT>::from_f32(0.0f);
-    dst[2 * lane + 1] = Elt<OUT_DT>::from_f32(0.0f);
-    if (lane == 0 && a.lse) a.lse[int64_t(h * G + g) * a.lse_head_stride + b] = -__builtin_inff();
-    return;
-  }
-  float m0 = kNegBig, m1 = kNegBig, l0 = 0.0f, l1 = 0.0f;
-  if (lane < n) {
-    m0 = part[lane * rec + g];
-    l0 = part[lane * rec + G + g];
-  }
-  if (lane + 64 < n) {
-    m1 = part[(lane + 64) * rec + g];
-    l1 = part[(lane + 64) * rec + G + g];
-  }
-  f32x2 x[kCombineChunk];
-#pragma unroll
-  for (int i = 0; i < kCombineChunk; ++i)
-    x[i] = *reinterpret_cast<const f32x2*>(col + int64_t(min(i, n - 1)) * rec);
-  const float mx = wave_max(__builtin_fmaxf(m0, m1));
-  const float w0 = __builtin_amdgcn_exp2f(m0 - mx), w1 = __builtin_amdgcn_exp2f(m1 - mx);  // 0 past n
-  const float den = wave_sum(l0 * w0 + l1 * w1);
-  float o0 = 0.0f, o1 = 0.0f;
-  for (int s0 = 0; s0 < n; s0 += kCombineChunk) {
-    if (s0 > 0) {
-#pragma unroll
-      for (int i = 0; i < kCombineChunk; ++i)
-        x[i] = *reinterpret_cast<const f32x2*>(col + int64_t(min(s0 + i, n - 1)) * rec);
+  float mx = kNegBig, den = 0.0f, o0 = 0.0f, o1 = 0.0f;
+  for (int c0 = 0; c0 < n; c0 += 64) {
+    const int cnt = min(64, n - c0);
+    float m = kNegBig, l = 0.0f;
+    if (lane < cnt) {
+      m = part[int64_t(c0 + lane) * rs + g];
+      l = part[int64_t(c0 + lane) * rs + G + g];
     }
-    const float wsrc = s0 < 64 ? w0 : w1;  // a chunk lies on one side of split 64
+    f32x2 x[kCombineChunk];
 #pragma unroll
-    for (int i = 0; i < kCombineChunk; ++i) {
-      const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wsrc), (s0 + i) & 63));
-      o0 = __builtin_fmaf(x[i].x, w, o0);
-      o1 = __builtin_fmaf(x[i].y, w, o1);
+    for (int i = 0; i < kCombineChunk; ++i)
+      x[i] = *reinterpret_cast<const f32x2*>(col + int64_t(c0 + min(i, cnt - 1)) * rs);
+    const float cm = __builtin_fmaxf(mx, wave_max(m));
+    const float c = __builtin_amdgcn_exp2f(mx - cm);
+    den *= c;
+    o0 *= c;
+    o1 *= c;
+    mx = cm;
+    const float wl = __builtin_amdgcn_exp2f(m - cm);  // 0 past cnt
+    den += wave_sum(l * wl);
+    for (int s0 = 0; s0 < cnt; s0 += kCombineChunk) {
+      if (s0 > 0) {
+#pragma unroll
+        for (int i = 0; i < kCombineChunk; ++i)
+          x[i] = *reinterpret_cast<const f32x2*>(col + int64_t(c0 + min(s0 + i, cnt - 1)) * rs);
+      }
+#pragma unroll
+      for (int i = 0; i < kCombineChunk; ++i) {
+        const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), s0 + i));
+        o0 = __builtin_fmaf(x[i].x, w, o0);
+        o1 = __builtin_fmaf(x[i].y, w, o1);
+      }
     }
   }
+  // no records (an empty sequence): zeros and lse = -inf
   const float inv = den > 0.0f ? vd / den : 0.0f;
   dst[2 * lane] = Elt<OUT_DT>::from_f32(o0 * inv);
   dst[2 * lane + 1] = Elt<OUT_DT>::from_f32(o1 * inv);
@@ -770,6 +943,44 @@ int decode_split(int64_t max_seq_len, int64_t num_splits, int64_t seq_heads) {
   return int(std::min<int64_t>(split, INT32_MAX / 2));
 }
 
+// Workgroups of the balanced schedule on the current device: one per slot that
+// can be resident at once (CUs x occupancy of the kernel instantiation).
+template <int NG>
+int64_t stream_wgs_for() {
+  static std::mutex mu;
+  static std::map<int, int64_t> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(dev);
+  if (it != cache.end()) return it->second;
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_partial_stream_kernel<NG>, kWaves * 64, 0) !=
+          hipSuccess)
+    return 0;
+  const int64_t n = int64_t(cus) * std::max(per_cu, 1);
+  cache[dev] = n;
+  return n;
+}
+
+int64_t stream_wgs(int ng) {
+  switch (ng) {
+    case 1: return stream_wgs_for<1>();
+    case 2: return stream_wgs_for<2>();
+    case 4: return stream_wgs_for<4>();
+    default: return stream_wgs_for<8>();
+  }
+}
+
+int group_ng(int64_t G) { return G == 1 ? 1 : G == 2 ? 2 : G <= 4 ? 4 : 8; }
+
+// Workgroups per kv head of the balanced schedule.
+int64_t stream_runs(int ng, int64_t num_kv_heads) {
+  const int64_t slots = stream_wgs(ng);
+  return slots > 0 ? std::max<int64_t>(1, slots / num_kv_heads) : 0;
+}
+
 template <bool UNIFORM>
 void launch_partial(const DecodeArgs& a, int q_dtype, dim3 grid, hipStream_t st, int ng) {
   const dim3 block(kWaves * 64);
@@ -787,11 +998,19 @@ extern "C" {
 
 int64_t psk_paged_decode_workspace_len(int64_t num_seqs, int64_t num_q_heads, int64_t num_kv_heads,
                                        int64_t max_seq_len, int64_t num_splits) {
-  if (num_seqs < 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads || max_seq_len < 0 || num_splits < 0)
+  if (num_seqs < 0 || num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads || max_seq_len < 0 ||
+      num_splits < 0)
     return PSK_E_ARG;
+  const int64_t G = num_q_heads / num_kv_heads;
+  const int64_t rec = G * (kHead + 2);
   const int64_t splits =
       std::max<int64_t>(1, ceil_div(max_seq_len, decode_split(max_seq_len, num_splits, num_seqs * num_kv_heads)));
-  return num_seqs * num_kv_heads * splits * (num_q_heads / num_kv_heads) * (kHead + 2);
+  int64_t need = num_seqs * num_kv_heads * splits * rec;
+  if (num_splits == 0 && num_seqs <= kStreamMaxSeqs && G <= kMaxGroup) {
+    // the balanced schedule: a record per (sequence, kv head) and per workgroup, then the tiles prefix
+    need = std::max(need, (num_seqs + stream_runs(group_ng(G), num_kv_heads)) * num_kv_heads * rec + num_seqs + 1);
+  }
+  return need;
 }
 
 int psk_paged_decode_attention(const void* q, int64_t q_tok_stride, int64_t q_head_stride, int q_dtype,
@@ -879,12 +1098,24 @@ int psk_paged_decode_attention(const void* q, int64_t q_tok_stride, int64_t q_he
   a.lse_head_stride = lse_head_stride;
 
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int ng = G == 1 ? 1 : G == 2 ? 2 : G <= 4 ? 4 : 8;
+  const int ng = group_ng(G);
   const dim3 grid{unsigned(a.max_splits), unsigned(num_kv_heads), unsigned(num_seqs)};
   // a 16-token tile stays in one page when the block size is a power of two >= 16
-  const bool uniform = a.bs_shift >= 4 && 16 * std::max(a.k_row, a.v_row) < (int64_t(1) << 31) &&
-                       a.split / block_size + 1 <= kRingPages;
-  if (uniform) {
+  const bool ring = a.bs_shift >= 4 && 16 * std::max(a.k_row, a.v_row) < (int64_t(1) << 31);
+  const int64_t runs = ring && num_splits == 0 && num_seqs <= kStreamMaxSeqs ? stream_runs(ng, num_kv_heads) : 0;
+  const bool uniform = ring && a.split / block_size + 1 <= kRingPages;
+  if (runs > 0) {
+    a.stream_wgs = int32_t(runs);
+    a.prefix = reinterpret_cast<int32_t*>(workspace + (num_seqs + runs) * num_kv_heads * G * (kHead + 2));
+    const dim3 sgrid{unsigned(runs * num_kv_heads), 1u, 1u}, block(kWaves * 64);
+    const int ns = int(num_seqs);
+    switch (ng) {
+      case 1: hipLaunchKernelGGL((decode_partial_stream_kernel<1>), sgrid, block, 0, st, a, q_dtype, ns); break;
+      case 2: hipLaunchKernelGGL((decode_partial_stream_kernel<2>), sgrid, block, 0, st, a, q_dtype, ns); break;
+      case 4: hipLaunchKernelGGL((decode_partial_stream_kernel<4>), sgrid, block, 0, st, a, q_dtype, ns); break;
+      default: hipLaunchKernelGGL((decode_partial_stream_kernel<8>), sgrid, block, 0, st, a, q_dtype, ns); break;
+    }
+  } else if (uniform) {
     const dim3 block(kWaves * 64);
     switch (ng) {
       case 1: hipLaunchKernelGGL((decode_partial_ring_kernel<1>), grid, block, 0, st, a, q_dtype); break;

@@ -38,7 +38,7 @@ def _check(got, exp, vmax, bf16):
     assert (err <= tol).all(), f"max err {err.max():.3e} at {np.unravel_index(err.argmax(), err.shape)}"
 
 
-def _case(dev, seed, B, Hq, Hkv, ps, P, lens, q_dtype, out_dtype, descales, W=None, bad_ids=False):
+def _case(dev, seed, B, Hq, Hkv, ps, P, lens, q_dtype, out_dtype, descales, W=None, bad_ids=False, num_splits=0):
     g = torch.Generator().manual_seed(seed)
     fused = torch.zeros(P, 2, ps, Hkv, 128, dtype=torch.float8_e4m3fn)
     fused[:, 0] = _fp8((P, ps, Hkv, 128), 2.0, g)
@@ -64,7 +64,7 @@ def _case(dev, seed, B, Hq, Hkv, ps, P, lens, q_dtype, out_dtype, descales, W=No
     scale = 128 ** -0.5
     got, lse = attention.paged_decode_attention(
         q.to(dev), fd[:, 0], fd[:, 1], bt.to(dev), lens.to(dev), scale,
-        *[d.to(dev) if d is not None else None for d in ds], out=out, return_softmax_lse=True)
+        *[d.to(dev) if d is not None else None for d in ds], out=out, return_softmax_lse=True, num_splits=num_splits)
     npd = [None if d is None else np.broadcast_to(d.numpy().reshape(-1, 1) if d.numel() == 1 else d.numpy(),
                                                   (B, Hkv)) for d in ds]
     exp, lse_exp = O.paged_decode_attention(raw(q), q_dtype, raw(fused[:, 0]), raw(fused[:, 1]), bt.numpy(),
@@ -95,6 +95,30 @@ LENS = [0, 1, 15, 16, 17, 100, 513, 1500, 2049]
 )
 def test_decode_attention_matches_oracle(dev, Hq, Hkv, ps, q_dtype, out_dtype, descales):
     _case(dev, 11 + Hq + ps, len(LENS), Hq, Hkv, ps, 700, LENS, q_dtype, out_dtype, descales)
+
+
+@pytest.mark.parametrize("num_splits", [0, 1, 3, 40])
+def test_balanced_and_split_schedules(dev, num_splits):
+    """num_splits 0 is the balanced schedule (every workgroup an equal run of
+    (sequence, kv head, tile) units across sequence boundaries); an explicit
+    count splits each sequence, as FA's num_splits."""
+    _case(dev, 21, len(LENS), 8, 2, 16, 700, LENS, "bf16", torch.float32, "per_seq_head", num_splits=num_splits)
+
+
+@pytest.mark.parametrize("B,Hkv,long_len", [(300, 1, 40000), (2, 4, 0), (1025, 2, 3000)])
+def test_balanced_schedule_skewed_batches(dev, B, Hkv, long_len):
+    """Many short sequences (zeros included) around one long one: workgroups
+    span many sequences, and the long sequence's records come from hundreds of
+    workgroups (the combine takes them 64 at a time).  (2, 4, 0): fewer units
+    than workgroups.  1025 sequences: more than the balanced schedule takes, so
+    the split schedule runs."""
+    rng = np.random.default_rng(B)
+    lens = rng.integers(0, 40, B).tolist()
+    lens[B // 3] = long_len if long_len else 1
+    lens[0] = 0
+    P = max(64, sum(-(-x // 16) for x in lens) + 16)
+    print(f"skewed: B={B} Hkv={Hkv} long={long_len} pages={P}", flush=True)
+    _case(dev, 31 + B, B, 4 * Hkv, Hkv, 16, P, lens, "bf16", torch.float32, None)
 
 
 def test_decode_attention_bad_page_ids_read_as_zero_rows(dev):
