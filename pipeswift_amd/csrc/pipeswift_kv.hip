@@ -209,6 +209,57 @@ int launch_scatter_shape(ScatterGeom g, const ScatterPart& p0, const ScatterPart
   return check_launch("paged_scatter_kernel launch");
 }
 
+// Decode-sized appends (< 1024 tokens, power-of-two block size, flat rows of
+// at most 512 vectors): the time is latency, so everything the wave needs sits
+// in one padding-free argument block that arrives in one round of scalar
+// loads (the general kernel's two part structs make the compiler split its
+// argument loads into two dependent rounds).  One wave per (token, part,
+// slice); the part is the wave number's low bit and every wave of the exact
+// grid is valid, so the row load is issued before any argument-dependent
+// branch.
+struct SmallAppend {
+  const int64_t* slots;
+  uint64_t num_slots;       // num_blocks * block_size; slot >= num_slots (or < 0) is skipped
+  int64_t blk_stride;       // bytes, shared by both parts
+  int64_t page_stride;      // bytes, shared by both parts
+  const char* src[2];
+  char* dst[2];             // cache base + the part's byte offset within a slot row
+  const float* scale[2];    // FP8 scale per part, nullptr for 1.0
+  int64_t src_stride[2];    // bytes between input token rows
+  int32_t vecs[2];          // vectors in each part's row
+  int32_t bs_shift;         // log2(block_size)
+  int32_t slice_shift;      // log2(slices per row); slices * 64 >= vecs
+};
+
+template <class C>
+__global__ void __launch_bounds__(64) paged_append_small_kernel(SmallAppend a) {
+  const int lane = threadIdx.x;
+  const uint32_t wave = blockIdx.x;
+  const int part = int(wave & 1u);
+  const uint32_t rest = wave >> 1;
+  const int slice = int(rest & ((1u << a.slice_shift) - 1u));
+  const int64_t t = int64_t(rest >> a.slice_shift);
+  const int i = slice * kWave + lane;
+  // selects, not a[part]: an indexed kernel argument is fetched with vector loads
+  const char* src = part ? a.src[1] : a.src[0];
+  char* dst = part ? a.dst[1] : a.dst[0];
+  const float* sp = part ? a.scale[1] : a.scale[0];
+  const int64_t src_stride = part ? a.src_stride[1] : a.src_stride[0];
+  const int vecs = part ? a.vecs[1] : a.vecs[0];
+  const bool act = i < vecs;
+  // every lane loads (lanes past the row re-read its last vector), so no
+  // branch delays the row load behind the argument loads
+  const int il = act ? i : vecs - 1;
+  const typename C::In v = vload_nt<C::IN_B>(src + t * src_stride + int64_t(il) * C::IN_B);
+  const int64_t slot = a.slots[t];
+  const QScale qs = make_qscale_uniform(sp ? *sp : 1.0f);
+  if (act && uint64_t(slot) < a.num_slots) {
+    char* drow = dst + (slot >> a.bs_shift) * a.blk_stride +
+                 (slot & ((int64_t(1) << a.bs_shift) - 1)) * a.page_stride;
+    vstore_nt<C::OUT_B>(drow + int64_t(i) * C::OUT_B, C::apply(v, qs));
+  }
+}
+
 bool part_flat(const ScatterPart& p, int out_b) { return p.nseg == 1 && p.inner_stride == out_b; }
 
 template <class C>
@@ -217,6 +268,27 @@ int launch_scatter(const ScatterGeom& g, const ScatterPart& p0, const ScatterPar
   const ScatterShape sh = scatter_shape(g.num_tokens, total);
   const bool fast = g.bs_shift >= 0 && part_flat(p0, C::OUT_B) && (g.nparts == 1 || part_flat(p1, C::OUT_B));
   if (!fast) return launch_scatter_shape<C, 1, 2, false, 4>(g, p0, p1, sh.ch == 1 ? sh.slice_shift : 0, st);
+  if (sh.ch == 1 && g.nparts == 2 && total <= 8 * kWave && p0.blk_stride == p1.blk_stride &&
+      p0.page_stride == p1.page_stride && g.num_tokens <= INT32_MAX / 16) {
+    SmallAppend a;
+    a.slots = g.slots;
+    a.num_slots = uint64_t(g.num_slots);
+    a.blk_stride = p0.blk_stride;
+    a.page_stride = p0.page_stride;
+    const ScatterPart* pp[2] = {&p0, &p1};
+    for (int k = 0; k < 2; ++k) {
+      a.src[k] = pp[k]->src;
+      a.dst[k] = pp[k]->dst + pp[k]->dst_off;
+      a.scale[k] = pp[k]->scale;
+      a.src_stride[k] = pp[k]->src_stride;
+      a.vecs[k] = pp[k]->seg_vecs;
+    }
+    a.bs_shift = g.bs_shift;
+    a.slice_shift = sh.slice_shift;
+    const int64_t grid = (g.num_tokens * 2) << sh.slice_shift;
+    hipLaunchKernelGGL((paged_append_small_kernel<C>), dim3(grid), dim3(kWave), 0, st, a);
+    return check_launch("paged_append_small_kernel launch");
+  }
   if (sh.ch == 1) return launch_scatter_shape<C, 1, 1, true, 1>(g, p0, p1, sh.slice_shift, st);
   return launch_scatter_shape<C, 4, 2, true, 4>(g, p0, p1, sh.slice_shift, st);
 }

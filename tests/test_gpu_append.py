@@ -50,7 +50,8 @@ def test_append_other_dtypes(dev, dtype):
     assert np.array_equal(got, exp)
 
 
-@pytest.mark.parametrize("heads,head_size,block_size", [(32, 128, 16), (1, 64, 128), (4, 96, 12), (2, 40, 7)])
+@pytest.mark.parametrize("heads,head_size,block_size",
+                         [(32, 128, 16), (12, 128, 32), (1, 64, 128), (4, 96, 12), (2, 40, 7), (64, 128, 16)])
 def test_append_shapes(dev, heads, head_size, block_size):
     case = workloads.config1_append(seed=heads + head_size, num_tokens=257, num_blocks=97, block_size=block_size,
                                     heads=heads, head_size=head_size, q_size=head_size * heads)
