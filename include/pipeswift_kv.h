@@ -144,7 +144,9 @@ int psk_gather_cache(const void* src0, const void* src1, void* dst0, void* dst1,
  *     = bytes at cache + l*layer_stride + s*block_stride        (strides in bytes)
  * Pairs with s or d outside [0, num_blocks) are skipped.  Snapshot semantics
  * hold when destinations are unique and disjoint from sources (the host layer
- * checks this); otherwise overlapping pairs race.
+ * checks this); otherwise overlapping pairs race.  Limits: num_layers <= 65535
+ * and num_pairs <= 2^24 (one workgroup per (pair, layer) on a 2-D grid);
+ * larger calls return PSK_E_ARG.
  */
 int psk_copy_blocks(void* cache, int64_t num_layers, int64_t layer_stride, int64_t block_stride,
                     int64_t block_bytes, int64_t num_blocks, const int64_t* block_mapping,
