@@ -375,53 +375,108 @@ struct GatherGeom {
   int32_t nparts;
 };
 
-template <class C, int CH, int U>
+template <class C, int CH, int U, bool POW2>
 __global__ void __launch_bounds__(256) paged_gather_kernel(GatherGeom g) {
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t wave = int64_t(blockIdx.x) * (blockDim.x / kWave) +
                        __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
   const int part = g.nparts == 2 ? int(wave & 1) : 0;
   const int64_t t0 = (g.nparts == 2 ? (wave >> 1) : wave) * CH;
-  if (t0 >= g.num_tokens) return;
   const char* src = part ? g.src1 : g.src0;
   char* dst = part ? g.dst1 : g.dst0;
+  // Branch-free up to the row loads (a wave past the last token runs with
+  // every row predicated off): each branch would start a new block and
+  // split the argument and lookup loads into dependent rounds.
   QScale qs;
-  qs.s = g.scale ? *g.scale : 1.0f;
-  qs.r = 0.0f;
-  qs.fast = false;
-
-  // Sequence of the first token: largest b in [0, batch] with cu[b] <= t0.
-  int lo = 0, hi = int(g.batch);
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (int64_t(g.cu[mid]) <= t0) lo = mid; else hi = mid - 1;
+  {
+    const float sv = *(g.scale ? g.scale : reinterpret_cast<const float*>(g.cu));
+    qs.s = g.scale ? sv : 1.0f;
+    qs.r = 0.0f;
+    qs.fast = false;
   }
-  int b = lo;
 
-  const char* srow[CH];
-  char* drow[CH];
-  bool rd[CH], wr[CH];
+  // Sequence lookup without a chain of dependent loads.  The lanes hold a
+  // window of 64 sequences k = wbase + lane: cu[k], cu[k+1] and seq_starts[k]
+  // (clamped loads, lanes past the batch hold an end of INT32_MAX).  Token t
+  // belongs to sequence wbase + n, n = the number of window entries with
+  // cu[k+1] <= t (a ballot); its cu[b] and start come from lane n.  The first
+  // window is loaded unconditionally; a batch of more than 64 sequences whose
+  // token lies beyond it places the window with one 64-wide probe of cu[64j].
+  // A later token of the chunk past the window takes the scalar walk.
+  const int32_t* sp = g.starts ? g.starts : g.cu;
+  const int64_t last = g.batch > 0 ? g.batch - 1 : 0;
+  int64_t wbase = 0;
+  int64_t kw = lane;
+  int64_t cu_lo = g.cu[kw < g.batch ? kw : g.batch];
+  int64_t cu_hi = g.cu[kw < g.batch ? kw + 1 : g.batch];
+  int32_t st = sp[kw < last ? kw : last];
+  if (g.batch > kWave && t0 >= int64_t(__builtin_amdgcn_readlane(int(cu_hi), kWave - 1))) {
+    const int64_t k = (int64_t(lane) + 1) * kWave;
+    const int64_t c = g.cu[k <= g.batch ? k : g.batch];
+    wbase = int64_t(__popcll(__ballot(k <= g.batch && c <= t0))) * kWave;
+    kw = wbase + lane;
+    cu_lo = g.cu[kw < g.batch ? kw : g.batch];
+    cu_hi = g.cu[kw < g.batch ? kw + 1 : g.batch];
+    st = sp[kw < last ? kw : last];
+  }
+  if (kw >= g.batch) cu_hi = INT32_MAX;
+  if (!g.starts) st = 0;
+  const int64_t cu0 = g.cu[0];
+
+  int64_t bseq[CH], pos[CH];
+  int nwin[CH];
+  bool slow = false;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     const int64_t t = t0 + c;
-    while (b < g.batch && t >= int64_t(g.cu[b + 1])) ++b;
-    wr[c] = t < g.num_tokens && b < g.batch && t >= int64_t(g.cu[0]);
-    int64_t blk = -1, off = 0;
-    if (wr[c]) {
-      const int64_t p = (g.starts ? int64_t(g.starts[b]) : 0) + t - int64_t(g.cu[b]);
-      int64_t page;
-      if (g.bs_shift >= 0) {
-        page = p >> g.bs_shift;
-        off = p & (g.block_size - 1);
-      } else {
-        page = p / g.block_size;
-        off = p - page * g.block_size;
-      }
-      if (p >= 0 && page < g.bt_stride) blk = g.block_table[int64_t(b) * g.bt_stride + page];
+    const int n = __popcll(__ballot(cu_hi <= t));
+    nwin[c] = n;
+    slow |= n == kWave;
+    const int nl = n < kWave ? n : kWave - 1;
+    bseq[c] = wbase + n;
+    pos[c] = int64_t(__builtin_amdgcn_readlane(st, nl)) + t - int64_t(__builtin_amdgcn_readlane(int(cu_lo), nl));
+  }
+  if (slow) {  // a token of this chunk lies past the window: walk on from its end
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      if (nwin[c] != kWave) continue;
+      const int64_t t = t0 + c;
+      int64_t b = wbase + kWave;
+      while (b < g.batch && t >= int64_t(g.cu[b + 1])) ++b;
+      bseq[c] = b;
+      pos[c] = b < g.batch ? (g.starts ? int64_t(g.starts[b]) : 0) + t - int64_t(g.cu[b]) : 0;
     }
-    rd[c] = wr[c] && blk >= 0 && blk < g.num_blocks;
-    srow[c] = src + blk * g.blk_stride + off * g.page_stride;
-    drow[c] = dst + t * g.dst_stride;
+  }
+
+  // Block-table reads through an always-valid pointer, the value passed
+  // through readfirstlane before the select: a select between a loaded value
+  // and a constant makes LLVM put the load behind a branch, and the branches
+  // would split the CH reads into dependent rounds.
+  __amdgpu_buffer_rsrc_t rin[CH], rout[CH];
+  const uint32_t in_bytes = uint32_t(g.row_vecs) * C::IN_B;
+  const uint32_t out_bytes = uint32_t(g.row_vecs) * C::OUT_B;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int64_t t = t0 + c;
+    const int64_t p = pos[c];
+    int64_t page, off;
+    if (POW2) {
+      page = p >> g.bs_shift;
+      off = p & ((int64_t(1) << g.bs_shift) - 1);
+    } else {
+      page = p / g.block_size;
+      off = p - page * g.block_size;
+    }
+    const bool wr = t < g.num_tokens && bseq[c] < g.batch && t >= cu0;
+    const bool look = wr && p >= 0 && page < g.bt_stride;
+    const int32_t* bp = look ? g.block_table + bseq[c] * g.bt_stride + page : g.cu;
+    const int64_t v = __builtin_amdgcn_readfirstlane(*bp);
+    const int64_t blk = look ? v : int64_t(-1);
+    const bool rd = blk >= 0 && blk < g.num_blocks;
+    // rows that must not be read come back as zeros; rows past the batch are
+    // not written
+    rin[c] = make_rsrc(src + blk * g.blk_stride + off * g.page_stride, rd ? in_bytes : 0u);
+    rout[c] = make_rsrc(dst + t * g.dst_stride, wr ? out_bytes : 0u);
   }
 
   const int total = g.row_vecs;
@@ -430,34 +485,50 @@ __global__ void __launch_bounds__(256) paged_gather_kernel(GatherGeom g) {
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int i = base + u * kWave + lane;
-        if (rd[c] && i < total) v[c][u] = vload_nt<C::IN_B>(srow[c] + int64_t(i) * C::IN_B);
-      }
+      for (int u = 0; u < U; ++u)
+        v[c][u] = BufIO<C::IN_B>::load(rin[c], uint32_t(base + u * kWave + lane) * C::IN_B);
     }
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int i = base + u * kWave + lane;
-        if (wr[c] && i < total)
-          vstore_nt<C::OUT_B>(drow[c] + int64_t(i) * C::OUT_B, rd[c] ? C::apply(v[c][u], qs) : C::zero());
-      }
+      for (int u = 0; u < U; ++u)
+        BufIO<C::OUT_B>::store(C::apply(v[c][u], qs), rout[c], uint32_t(base + u * kWave + lane) * C::OUT_B);
+    }
+  }
+}
+
+template <class C, bool POW2>
+void launch_gather_pow2(const GatherGeom& g, hipStream_t st) {
+  if (g.num_tokens < 4096) {
+    const int64_t waves = g.num_tokens * g.nparts;
+    const int threads = g.num_tokens <= 1024 ? 64 : 256;
+    hipLaunchKernelGGL((paged_gather_kernel<C, 1, 2, POW2>), dim3(ceil_div(waves, threads / kWave)), dim3(threads),
+                       0, st, g);
+  } else {
+    // About 2 KiB of cache per wave: one token of a row over 64 vectors (two
+    // vectors per lane, looping beyond), two tokens of a 1 KiB row, four of a
+    // smaller one.  Measured on config 3's 1 KiB rows: 118.5 us at two tokens
+    // per wave, 123 at four, 133 at sixteen, 135 at one.
+    const int64_t in_row = int64_t(g.row_vecs) * C::IN_B;
+    if (g.row_vecs > kWave) {
+      const int64_t waves = g.num_tokens * g.nparts;
+      hipLaunchKernelGGL((paged_gather_kernel<C, 1, 2, POW2>), dim3(ceil_div(waves, 4)), dim3(256), 0, st, g);
+    } else if (in_row >= 1024) {
+      const int64_t waves = ceil_div(g.num_tokens, 2) * g.nparts;
+      hipLaunchKernelGGL((paged_gather_kernel<C, 2, 1, POW2>), dim3(ceil_div(waves, 4)), dim3(256), 0, st, g);
+    } else {
+      const int64_t waves = ceil_div(g.num_tokens, 4) * g.nparts;
+      hipLaunchKernelGGL((paged_gather_kernel<C, 4, 1, POW2>), dim3(ceil_div(waves, 4)), dim3(256), 0, st, g);
     }
   }
 }
 
 template <class C>
 int launch_gather(const GatherGeom& g, hipStream_t st) {
-  if (g.num_tokens < 4096) {
-    const int64_t waves = g.num_tokens * g.nparts;
-    const int threads = g.num_tokens <= 1024 ? 64 : 256;
-    hipLaunchKernelGGL((paged_gather_kernel<C, 1, 2>), dim3(ceil_div(waves, threads / kWave)), dim3(threads), 0,
-                       st, g);
-  } else {
-    const int64_t waves = ceil_div(g.num_tokens, 4) * g.nparts;
-    hipLaunchKernelGGL((paged_gather_kernel<C, 4, 2>), dim3(ceil_div(waves, 4)), dim3(256), 0, st, g);
-  }
+  if (g.bs_shift >= 0)
+    launch_gather_pow2<C, true>(g, st);
+  else
+    launch_gather_pow2<C, false>(g, st);
   return check_launch("paged_gather_kernel launch");
 }
 

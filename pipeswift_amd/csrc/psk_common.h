@@ -100,6 +100,37 @@ __device__ __forceinline__ void vstore_nt(char* p, typename VecT<B>::T v) {
   __builtin_nontemporal_store(v, reinterpret_cast<typename VecT<B>::T*>(p));
 }
 
+// ---- buffer (V#) loads and stores: an access at or beyond num_records bytes
+// of the descriptor returns zeros (loads) or is dropped (stores), so a row
+// that must not be touched gets num_records = 0 instead of a branch.
+// Dword 3 is the gfx9-family raw-buffer format word; aux 2 = nontemporal.
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t num_records) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, int(num_records), 0x00020000);
+}
+
+template <int B> struct BufIO;
+template <> struct BufIO<16> {
+  __device__ static u32x4 load(__amdgpu_buffer_rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2); }
+  __device__ static void store(u32x4 v, __amdgpu_buffer_rsrc_t r, uint32_t off) { __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, 2); }
+};
+template <> struct BufIO<8> {
+  __device__ static u32x2 load(__amdgpu_buffer_rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 2); }
+  __device__ static void store(u32x2 v, __amdgpu_buffer_rsrc_t r, uint32_t off) { __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, 2); }
+};
+template <> struct BufIO<4> {
+  __device__ static uint32_t load(__amdgpu_buffer_rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 2); }
+  __device__ static void store(uint32_t v, __amdgpu_buffer_rsrc_t r, uint32_t off) { __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, 2); }
+};
+template <> struct BufIO<2> {
+  __device__ static uint16_t load(__amdgpu_buffer_rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 2); }
+  __device__ static void store(uint16_t v, __amdgpu_buffer_rsrc_t r, uint32_t off) { __builtin_amdgcn_raw_buffer_store_b16(v, r, off, 0, 2); }
+};
+template <> struct BufIO<1> {
+  __device__ static uint8_t load(__amdgpu_buffer_rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b8(r, off, 0, 2); }
+  __device__ static void store(uint8_t v, __amdgpu_buffer_rsrc_t r, uint32_t off) { __builtin_amdgcn_raw_buffer_store_b8(v, r, off, 0, 2); }
+};
+
 template <int DT> struct Elt;
 template <> struct Elt<PSK_DTYPE_F32> {
   using Bits = uint32_t;

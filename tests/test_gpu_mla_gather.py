@@ -160,3 +160,36 @@ def test_gather_many_sequences_and_tail_untouched(dev):
     exp = np.full((T, H, D), raw(torch.full((1,), 3, dtype=torch.bfloat16))[0], np.uint16)
     O.gather_cache(raw(cache), bt.numpy(), cu.numpy(), out=exp)
     assert np.array_equal(raw(out), exp)
+
+
+@pytest.mark.parametrize("ps,H,D,with_starts", [(16, 8, 128, True), (12, 4, 128, True), (16, 2, 64, False),
+                                                (5, 1, 64, True)])
+def test_gather_many_sequences_kv_variants(dev, ps, H, D, with_starts):
+    """Hundreds of sequences over 4096+ tokens (the four-tokens-per-wave launch
+    and its sequence windows), K and V in one launch, page-aligned and
+    unaligned seq_starts, power-of-two and other block sizes, 2 KiB rows."""
+    g = torch.Generator().manual_seed(38 + ps + H)
+    P = 4096
+    kc = workloads.sentinel((P, ps, H, D), torch.bfloat16, 39)
+    vc = workloads.sentinel((P, ps, H, D), torch.bfloat16, 40)
+    B = 230
+    lens = torch.randint(0, 60, (B,), generator=g)
+    lens[::17] = 0
+    cu = torch.zeros(B + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(lens, 0)
+    starts = torch.randint(0, 3 * ps, (B,), generator=g).to(torch.int32) if with_starts else None
+    W = (60 + 3 * ps) // ps + 2
+    bt = torch.randint(0, P, (B, W), generator=g, dtype=torch.int32)
+    bt[3, 1] = P + 5  # out of range -> zero rows
+    T = int(cu[-1]) + 9
+    assert T >= 4096
+    out_k = torch.full((T, H, D), 3, dtype=torch.bfloat16, device=dev)
+    out_v = torch.full((T, H, D), 3, dtype=torch.bfloat16, device=dev)
+    cache_ops.gather_cache(kc.to(dev), out_k, bt.to(dev), cu.to(dev), src_cache_v=vc.to(dev), dst_v=out_v,
+                           seq_starts=None if starts is None else starts.to(dev))
+    fill = raw(torch.full((1,), 3, dtype=torch.bfloat16))[0]
+    for cache, out in ((kc, out_k), (vc, out_v)):
+        exp = np.full((T, H, D), fill, np.uint16)
+        O.gather_cache(raw(cache), bt.numpy(), cu.numpy(), seq_starts=None if starts is None else starts.numpy(),
+                       out=exp)
+        assert np.array_equal(raw(out), exp)
