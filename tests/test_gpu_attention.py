@@ -91,6 +91,9 @@ LENS = [0, 1, 15, 16, 17, 100, 513, 1500, 2049]
         (10, 2, 32, "bf16", torch.float32, "per_seq_head"),
         (16, 2, 64, "fp8", torch.float32, "per_seq_head"),
         (6, 2, 24, "bf16", torch.bfloat16, None),
+        (32, 8, 16, "fp8", torch.bfloat16, "per_seq_head"),
+        (8, 8, 32, "bf16", torch.float32, None),
+        (12, 6, 16, "bf16", torch.float32, "scalar"),
     ],
 )
 def test_decode_attention_matches_oracle(dev, Hq, Hkv, ps, q_dtype, out_dtype, descales):
