@@ -14,7 +14,10 @@ The JSON line carries:
   value            algorithmic HBM GB/s (bytes the kernel must move / time)
   roofline         the same per launch against MI355X's 8 TB/s peak, plus the
                    HBM traffic measured with rocprofv3 PMC counters (committed
-                   under profiles/), when present
+                   under profiles/), when present, and the fraction of the
+                   best device copy measured on this box in the same run
+                   (`achievable`, copy_blocks_kernel over 1 GiB)
+  wall_us_per_call_eager  host wall time per eager Python call (no graph)
   cpu_baseline     the numpy oracle timed on this host on a bounded sample
 
 Workloads (default fp8_decode_append, config 2 of the benchmark plan):
@@ -118,7 +121,7 @@ def setup_append(args, device, fp8):
     nbytes = workloads.append_bytes(case.num_valid, N, case.num_heads, case.head_size, 2, 1 if fp8 else 2)
     info = {
         "name": "fp8_decode_append" if fp8 else "bf16_append",
-        "kernel": "paged_scatter_kernel",
+        "kernel": "paged_append_small_kernel",  # the launch for batches under 1024 tokens
         "bytes": nbytes,
         "tokens": case.num_valid,
         "dtype": "fp8_e4m3fn" if fp8 else "bf16",
@@ -175,7 +178,8 @@ def setup_decode_attention(args, device):
     nbytes = total * H * D * 2 + pages * 4 + 2 * B * Hq * D * 2
     info = {
         "name": "decode_attention",
-        "kernel": "decode_partial_stream_kernel" if args.num_splits == 0 else "decode_partial_ring_kernel",
+        # the head-parallel balanced schedule from 8 sequences up, the split schedule for an explicit count
+        "kernel": "decode_partial_heads_kernel" if args.num_splits == 0 else "decode_partial_ring_kernel",
         "bytes": nbytes, "tokens": B,
         "dtype": "fp8_e4m3fn",
         "rotate": R,
@@ -298,7 +302,8 @@ def setup_mla(args, device, decode):
     nbytes = workloads.mla_bytes(n, 576, 2, 2)
     return launch, {
         "rotate": R,
-        "name": "mla_decode" if decode else "mla_prefill", "kernel": "paged_scatter_kernel", "bytes": nbytes,
+        "name": "mla_decode" if decode else "mla_prefill",
+        "kernel": "paged_append_small_kernel" if decode else "paged_scatter_kernel", "bytes": nbytes,
         "tokens": n, "dtype": "bf16",
         "config": {"workload": f"MLA latent append, {'decode' if decode else 'prefill'} (config 4)", "tokens": n,
                    "row": 576, "block_size": ps, "num_blocks": P},
@@ -362,6 +367,31 @@ def setup_copy_blocks(args, device):
                    "block_bytes": 65536},
         "cpu": None,
     }
+
+
+def measure_device_copy(device, reps=10):
+    """GB/s (read + write) of the best device copy on this box: copy_blocks_kernel
+    over 16384 contiguous 64 KiB blocks, 1 GiB each way.  The achievable
+    reference of the roofline next to the 8 TB/s spec."""
+    import torch
+
+    from pipeswift_amd import cache_ops
+
+    stack = torch.empty((1, 2 * 16384, 65536), dtype=torch.uint8, device=device)
+    pairs = torch.stack([torch.arange(16384), torch.arange(16384) + 16384], 1).to(torch.int64).to(device)
+    for _ in range(3):
+        cache_ops.copy_blocks(stack, pairs, validate=False)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        cache_ops.copy_blocks(stack, pairs, validate=False)
+    e1.record()
+    torch.cuda.synchronize()
+    gbs = 2 * (1 << 30) / (e0.elapsed_time(e1) / 1e3 / reps) / 1e9
+    del stack
+    torch.cuda.empty_cache()
+    return gbs
 
 
 def run_hbm_copy(args, device):
@@ -971,6 +1001,19 @@ def main():
     per_launch_s = ms / 1e3 / done
     achieved = info["bytes"] / per_launch_s / 1e9
 
+    # host wall time per eager call (Python shim, argument checks, launch), the
+    # figure a caller that does not capture graphs sees
+    eager_n = max(1, min(200, args.steps))
+    with torch.cuda.stream(stream):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(eager_n):
+            launch(i % R)
+        torch.cuda.synchronize()
+        eager_us = (time.perf_counter() - t0) / eager_n * 1e6
+
+    achievable = measure_device_copy(device)
+
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
@@ -1010,7 +1053,10 @@ def main():
             "bytes_per_launch": info["bytes"],
             "us_per_launch": round(per_launch_s * 1e6, 3),
             "traffic": traffic,
+            "achievable": round(achievable, 1),
+            "frac_of_achievable": round(achieved / achievable, 5),
         },
+        "wall_us_per_call_eager": round(eager_us, 2),
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -580,12 +580,22 @@ __device__ __forceinline__ TileLoads ring_read(uint32_t slot, uint32_t rk0, uint
 // one chunk of sixteen tokens (or of eight V tokens) hit distinct LDS banks.
 // The vector-memory counter is waited on explicitly: nothing else in the loop
 // uses it.
-template <int W>
+template <int W, int R = kRing>
 struct RingLdsT {
-  u32x4 ring[W][kRing][4][64];
+  u32x4 ring[W][R][4][64];
   int32_t pages[kRingPages];
 };
 using RingLds = RingLdsT<kWaves>;
+
+// s_waitcnt vmcnt(n) for a run-time n < 16 (the immediate must be a constant)
+__device__ __forceinline__ void wait_vmcnt(int n) {
+  switch (n) {
+    case 0: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
+    case 4: __builtin_amdgcn_s_waitcnt(vmcnt_imm(4)); break;
+    case 8: __builtin_amdgcn_s_waitcnt(vmcnt_imm(8)); break;
+    default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(12)); break;
+  }
+}
 
 // Tokens [t_begin, t_end) of (sequence b, kv head h) into the running softmax
 // st of this wave, which takes tiles t_begin + 16 phase + 16 P j (phase < P).
@@ -594,10 +604,11 @@ using RingLds = RingLdsT<kWaves>;
 // heads may differ): it stages the range's page ids behind a barrier.
 // `overlap` runs while the page-id loads are in flight (a new head's query
 // loads go there, so that both cost one memory latency).
-template <int NG, int W, int P, class Overlap>
+template <int NG, int W, int P, int R, class Overlap>
 __device__ __forceinline__ void ring_attend(const DecodeArgs& a, Softmax<NG>& st, const bf16x8 (&qop)[4],
                                             const float& sl, int b, int h, int t_begin, int t_end, int lane,
-                                            int wave, int phase, RingLdsT<W>& lds, const Overlap& overlap) {
+                                            int wave, int phase, RingLdsT<W, R>& lds, const Overlap& overlap) {
+  static_assert(R >= 2 && R <= 4, "ring of 2 to 4 tiles per wave");
   constexpr int kIdsPerThread = kRingPages / (W * 64);
   static_assert(kRingPages % (W * 64) == 0, "page ids are staged a whole number per thread");
   const int32_t* bt_row = a.block_table + b * a.bt_stride;
@@ -638,11 +649,11 @@ __device__ __forceinline__ void ring_attend(const DecodeArgs& a, Softmax<NG>& st
 
   // start the loads of tile j into its slot; a missing page reads page 0 (in
   // bounds) and is zeroed when consumed
-  uint32_t valid = 0;  // bit j % kRing: slot holds a tile on a real page
+  uint32_t valid = 0;  // bit j % R: slot holds a tile on a real page
   auto issue = [&](int j) {
     const int t0 = t_first + j * stride;
     const int32_t raw = __builtin_amdgcn_readfirstlane(lds.pages[(t0 >> a.bs_shift) - first]);
-    const int slot = j % kRing;
+    const int slot = j % R;
     valid = raw >= 0 ? (valid | (1u << slot)) : (valid & ~(1u << slot));
     const int64_t pid = raw >= 0 ? raw : 0;
     const int64_t row0 = t0 & (a.block_size - 1);
@@ -654,21 +665,21 @@ __device__ __forceinline__ void ring_attend(const DecodeArgs& a, Softmax<NG>& st
     __builtin_amdgcn_global_load_lds((gvoid*)(vb + off_v8), (lvoid*)&ring[slot][3][0], 16, 0, kDmaNontemporal);
   };
   auto fetch = [&](int j) {
-    // tiles issued after j: min(kRing - 1, n_tiles - 1 - j), four loads each
-    if (j + kRing - 1 < n_tiles) __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 * (kRing - 1)));
-    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-    const int slot = j % kRing;
+    // tiles issued after j: min(R - 1, n_tiles - 1 - j), four loads each
+    if (j + R - 1 < n_tiles) __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 * (R - 1)));
+    else wait_vmcnt(4 * (n_tiles - 1 - j));
+    const int slot = j % R;
     TileLoads c = ring_read((uint32_t)(size_t)(lvoid*)&ring[slot][0][0], rk0, rk1, rv);
     if (!((valid >> slot) & 1u)) c.k0 = c.k1 = c.va = c.vb = u32x4(0);
     return c;
   };
-  for (int j = 0; j < kRing && j < n_tiles; ++j) issue(j);
+  for (int j = 0; j < R && j < n_tiles; ++j) issue(j);
   if (n_tiles > 0) {
     int j = 0;
     for (; j + 1 < n_tiles; ++j) {
       TileLoads c = fetch(j);
       attend_step<NG, false>(st, c, qop, sl, t_first + j * stride, t_end, lane, [&] {
-        if (j + kRing < n_tiles) issue(j + kRing);
+        if (j + R < n_tiles) issue(j + R);
       });
     }
     TileLoads c = fetch(j);
@@ -723,7 +734,7 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_ring_kernel(Decode
   Softmax<NG> st;
   softmax_init(st);
   // the host keeps a split within kRingPages pages
-  ring_attend<NG, kWaves, kWaves>(a, st, qop, sl, b, h, t_begin, t_end, lane, wave, wave, lds,
+  ring_attend<NG, kWaves, kWaves, kRing>(a, st, qop, sl, b, h, t_begin, t_end, lane, wave, wave, lds,
                                   [&] { sl = load_head<NG>(a, q_dtype, b, h, lane, qop); });
   __syncthreads();  // every wave is done with the ring: it becomes the merge buffer
   write_partial<NG>(a, st, (int64_t(b) * a.num_kv_heads + h) * a.max_splits + s, lane, wave,
@@ -816,7 +827,7 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_stream_kernel(Deco
     const int t_end = min(len, (t + n) * kTile);
     for (int t0 = t * kTile; t0 < t_end; t0 += piece) {
       const bool head = t0 == t * kTile;
-      ring_attend<NG, kWaves, kWaves>(a, st, qop, sl, b, h, t0, min(t_end, t0 + piece), lane, wave, wave, lds, [&] {
+      ring_attend<NG, kWaves, kWaves, kRing>(a, st, qop, sl, b, h, t0, min(t_end, t0 + piece), lane, wave, wave, lds, [&] {
         if (head) sl = load_head<NG>(a, q_dtype, b, h, lane, qop);
       });
     }
@@ -844,6 +855,9 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_stream_kernel(Deco
 // (NHG = Hkv / HG); records and the tiles prefix are laid out as in the
 // per-head balanced schedule, so the same combine reads them.
 constexpr int kHeadWaves = 8;
+// LDS tile slots per wave.  At one workgroup per CU deeper rings cost no
+// occupancy, but measured slower on config 2: 250 us at three, 252 at four.
+constexpr int kHeadRing = 2;
 
 // Merge this wave's token slots and, with P phases per head, the P waves of
 // each head through LDS; write head h's partial record rec_idx.
@@ -928,7 +942,7 @@ __global__ void __launch_bounds__(kHeadWaves * 64) decode_partial_heads_kernel(D
   const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
   const int Hkv = a.num_kv_heads;
   const int NHG = Hkv / HG;
-  __shared__ RingLdsT<W> lds;
+  __shared__ RingLdsT<W, kHeadRing> lds;
   __shared__ float s_m[W][NG], s_l[W][NG];
   static_assert(sizeof(lds.ring) >= sizeof(float) * W * NG * kHead, "the ring doubles as the merge buffer");
   static_assert(sizeof(lds.ring) / sizeof(int32_t) > kStreamMaxSeqs, "the ring holds the tiles prefix");
@@ -993,7 +1007,7 @@ __global__ void __launch_bounds__(kHeadWaves * 64) decode_partial_heads_kernel(D
     const int t_end = min(len, (t + n) * kTile);
     for (int t0 = t * kTile; t0 < t_end; t0 += piece) {
       const bool head = t0 == t * kTile;
-      ring_attend<NG, W, P>(a, st, qop, sl, b, h, t0, min(t_end, t0 + piece), lane, wave, phase, lds, [&] {
+      ring_attend<NG, W, P, kHeadRing>(a, st, qop, sl, b, h, t0, min(t_end, t0 + piece), lane, wave, phase, lds, [&] {
         if (head) sl = load_head<NG>(a, q_dtype, b, h, lane, qop);
       });
     }
