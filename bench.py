@@ -19,6 +19,9 @@ The JSON line carries:
                    (`achievable`, copy_blocks_kernel over 1 GiB)
   wall_us_per_call_eager  host wall time per eager Python call (no graph)
   cpu_baseline     the numpy oracle timed on this host on a bounded sample
+  cpu_torch        the reference's CPU path (torch index_put_ / index_select on
+                   host tensors of the same layout) on all host threads and on
+                   one, for the appends and the gather
 
 Workloads (default fp8_decode_append, config 2 of the benchmark plan):
   fp8_decode_append  128 seqs x 1 token, 8x128 bf16 -> E4M3FN, 65536 blocks
@@ -133,6 +136,7 @@ def setup_append(args, device, fp8):
             "scale": "per-tensor from amax" if fp8 else None,
         },
         "cpu": lambda: cpu_append(case, fp8),
+        "cpu_torch": lambda: torch_cpu_append(case, fp8),
     }
     return launch, info
 
@@ -251,6 +255,7 @@ def setup_chunked(args, device, gather):
             "config": {"workload": "chunked_append (config 3)", "tokens": N, "kv_heads": a.num_heads,
                        "head_dim": a.head_size, "block_size": ps, "num_blocks": P, "sequences": len(cc.chunk)},
             "cpu": lambda: cpu_append(a, False),
+            "cpu_torch": lambda: torch_cpu_append(a, False),
         }
     T = int(cc.cu_seq_lens[-1])
     bt = cc.block_table.to(device)
@@ -272,6 +277,7 @@ def setup_chunked(args, device, gather):
                    "kv_heads": a.num_heads, "head_dim": a.head_size, "block_size": ps, "num_blocks": P,
                    "pages": pages},
         "cpu": lambda: cpu_gather(cc),
+        "cpu_torch": lambda: torch_cpu_gather(cc),
     }
 
 
@@ -898,6 +904,71 @@ def cpu_gather(cc, budget_s=10.0):
     return n / 2.0, el, f"{n} K-only numpy oracle gathers (counted as {n / 2:.1f} K+V steps)"
 
 
+def _timed(fn, budget_s):
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el > budget_s:
+            return n, el
+
+
+def torch_cpu_append(case, fp8, budget_s=3.0):
+    """The reference's CPU path for the append (as the north star names it): torch
+    index_put_ of the valid tokens' K and V rows into host caches of the same
+    strided [P, 2, ps, H, D] layout, after fp8_kv.quantize (fp8_kv.py:75-77,
+    x / scale clamped to +-448, then float8_e4m3fn) for an FP8 cache."""
+    import torch
+
+    key, value = case.key(), case.value()
+    slots = case.slot_mapping
+    valid = slots >= 0
+    ps = case.cache.shape[2]
+    blk, off = slots[valid] // ps, slots[valid] % ps
+    kv, vv = key[valid], value[valid]
+    cache = torch.zeros(tuple(case.cache.shape), dtype=torch.float8_e4m3fn if fp8 else torch.bfloat16)
+    kc, vc = cache[:, 0], cache[:, 1]
+    ks = vs = None
+    if fp8:
+        from oracle import kv_oracle as O
+
+        ks, _ = O.amax_scale(_raw(key), "bf16")
+        vs, _ = O.amax_scale(_raw(value), "bf16")
+
+    def step():
+        if fp8:
+            kc.index_put_((blk, off), (kv.float() / ks).clamp(-448.0, 448.0).to(torch.float8_e4m3fn))
+            vc.index_put_((blk, off), (vv.float() / vs).clamp(-448.0, 448.0).to(torch.float8_e4m3fn))
+        else:
+            kc.index_put_((blk, off), kv)
+            vc.index_put_((blk, off), vv)
+
+    return _timed(step, budget_s)
+
+
+def torch_cpu_gather(cc, budget_s=3.0):
+    """torch on the host for the gather: index_select of each sequence's pages of
+    the K and V caches, reshaped to rows and cut to the sequence's tokens."""
+    import torch
+
+    kc, vc = cc.append.cache[:, 0], cc.append.cache[:, 1]
+    cu = cc.cu_seq_lens.tolist()
+    ps = kc.shape[1]
+    tables = []
+    for b in range(len(cu) - 1):
+        n = cu[b + 1] - cu[b]
+        tables.append((cc.block_table[b, : (n + ps - 1) // ps].long(), n))
+
+    def step():
+        for t, n in tables:
+            torch.index_select(kc, 0, t).reshape(-1, *kc.shape[2:])[:n].contiguous()
+            torch.index_select(vc, 0, t).reshape(-1, *vc.shape[2:])[:n].contiguous()
+
+    return _timed(step, budget_s)
+
+
 # --------------------------------------------------------------------------- #
 # main
 # --------------------------------------------------------------------------- #
@@ -1027,6 +1098,18 @@ def main():
                "sample": f"{sample}; {el:.1f} s on 1 thread of {_cpu_model()} ({os.cpu_count()} cpus visible)",
                "tokens_per_s": info["tokens"] * n / el}
 
+    cpu_torch = None
+    if not args.no_cpu_baseline and info.get("cpu_torch") is not None:
+        threads = os.cpu_count() or 1
+        torch.set_num_threads(threads)
+        n, el = info["cpu_torch"]()
+        torch.set_num_threads(1)
+        n1, el1 = info["cpu_torch"]()
+        cpu_torch = {"value": info["bytes"] * n / el / 1e9, "unit": "GB/s", "threads": threads,
+                     "value_1thread": info["bytes"] * n1 / el1 / 1e9,
+                     "what": "the reference's CPU path: torch index_put_/index_select on host tensors of the same "
+                             f"layout, {n} steps in {el:.1f} s on {threads} threads, {n1} in {el1:.1f} s on 1"}
+
     line = {
         "metric": "achieved HBM GB/s (% of MI355X peak) + tokens/s for paged KV append/FP8 quant",
         "value": round(achieved, 2),
@@ -1058,6 +1141,7 @@ def main():
         },
         "wall_us_per_call_eager": round(eager_us, 2),
         "cpu_baseline": cpu,
+        "cpu_torch": cpu_torch,
     }
     print(json.dumps(line), flush=True)
 
