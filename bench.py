@@ -915,11 +915,12 @@ def _timed(fn, budget_s):
             return n, el
 
 
-def torch_cpu_append(case, fp8, budget_s=3.0):
+def torch_cpu_append_step(case, fp8):
     """The reference's CPU path for the append (as the north star names it): torch
     index_put_ of the valid tokens' K and V rows into host caches of the same
     strided [P, 2, ps, H, D] layout, after fp8_kv.quantize (fp8_kv.py:75-77,
-    x / scale clamped to +-448, then float8_e4m3fn) for an FP8 cache."""
+    x / scale clamped to +-448, then float8_e4m3fn) for an FP8 cache.  Returns
+    (step, cache)."""
     import torch
 
     key, value = case.key(), case.value()
@@ -945,12 +946,18 @@ def torch_cpu_append(case, fp8, budget_s=3.0):
             kc.index_put_((blk, off), kv)
             vc.index_put_((blk, off), vv)
 
+    return step, cache
+
+
+def torch_cpu_append(case, fp8, budget_s=3.0):
+    step, _ = torch_cpu_append_step(case, fp8)
     return _timed(step, budget_s)
 
 
-def torch_cpu_gather(cc, budget_s=3.0):
+def torch_cpu_gather_step(cc):
     """torch on the host for the gather: index_select of each sequence's pages of
-    the K and V caches, reshaped to rows and cut to the sequence's tokens."""
+    the K and V caches, reshaped to rows and cut to the sequence's tokens.
+    Returns (step, outputs), outputs filled by the last step as [K rows, V rows]."""
     import torch
 
     kc, vc = cc.append.cache[:, 0], cc.append.cache[:, 1]
@@ -960,12 +967,20 @@ def torch_cpu_gather(cc, budget_s=3.0):
     for b in range(len(cu) - 1):
         n = cu[b + 1] - cu[b]
         tables.append((cc.block_table[b, : (n + ps - 1) // ps].long(), n))
+    out = [None, None]
 
     def step():
+        k_rows, v_rows = [], []
         for t, n in tables:
-            torch.index_select(kc, 0, t).reshape(-1, *kc.shape[2:])[:n].contiguous()
-            torch.index_select(vc, 0, t).reshape(-1, *vc.shape[2:])[:n].contiguous()
+            k_rows.append(torch.index_select(kc, 0, t).reshape(-1, *kc.shape[2:])[:n])
+            v_rows.append(torch.index_select(vc, 0, t).reshape(-1, *vc.shape[2:])[:n])
+        out[0], out[1] = torch.cat(k_rows), torch.cat(v_rows)
 
+    return step, out
+
+
+def torch_cpu_gather(cc, budget_s=3.0):
+    step, _ = torch_cpu_gather_step(cc)
     return _timed(step, budget_s)
 
 

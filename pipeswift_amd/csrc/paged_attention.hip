@@ -754,21 +754,14 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_ring_kernel(Decode
 // b) after the records for the combine.
 __device__ __forceinline__ int tiles_of(int len) { return len > 0 ? (len + kTile - 1) / kTile : 0; }
 
-template <int NG>
-__global__ void __launch_bounds__(kWaves * 64) decode_partial_stream_kernel(DecodeArgs a, int q_dtype, int num_seqs) {
-  const int w = blockIdx.x;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
-  const int Hkv = a.num_kv_heads;
-  __shared__ RingLds lds;
-  static_assert(sizeof(lds.ring) >= sizeof(float) * kWaves * NG * kHead, "the ring doubles as the merge buffer");
-  static_assert(sizeof(lds.ring) / sizeof(int32_t) > kStreamMaxSeqs, "the ring holds the tiles prefix");
-
-  // tiles prefix over the sequences, scanned in the ring (free until the first tile)
-  int32_t* pref = reinterpret_cast<int32_t*>(&lds.ring[0][0][0][0]);
-  __shared__ int32_t s_scan[kWaves * 64];
-  const int tid = threadIdx.x, nt = kWaves * 64;
-  const int chunk = (num_seqs + nt - 1) / nt;
+// Tiles prefix of the batch in LDS (pref[b] = tiles before sequence b,
+// pref[num_seqs] = all tiles), by the NT threads of the workgroup; returns the
+// total.  `store` also writes it to a.prefix for the combine.
+template <int NT>
+__device__ __forceinline__ int64_t scan_tiles(const DecodeArgs& a, int num_seqs, int32_t* pref, int32_t* s_scan,
+                                              bool store) {
+  const int tid = threadIdx.x;
+  const int chunk = (num_seqs + NT - 1) / NT;
   int sum = 0;
   for (int i = 0; i < chunk; ++i) {
     const int b = tid * chunk + i;
@@ -776,7 +769,7 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_stream_kernel(Deco
   }
   s_scan[tid] = sum;
   __syncthreads();
-  for (int o = 1; o < nt; o <<= 1) {
+  for (int o = 1; o < NT; o <<= 1) {
     const int v = tid >= o ? s_scan[tid - o] : 0;
     __syncthreads();
     s_scan[tid] += v;
@@ -790,12 +783,28 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_stream_kernel(Deco
       run += tiles_of(a.seq_lens[b]);
     }
   }
-  if (tid == nt - 1) pref[num_seqs] = s_scan[nt - 1];
+  if (tid == NT - 1) pref[num_seqs] = s_scan[NT - 1];
   __syncthreads();
-  const int64_t T = pref[num_seqs];
-  if (w == 0) {
-    for (int i = tid; i <= num_seqs; i += nt) a.prefix[i] = pref[i];
+  if (store) {
+    for (int i = tid; i <= num_seqs; i += NT) a.prefix[i] = pref[i];
   }
+  return pref[num_seqs];
+}
+
+template <int NG>
+__global__ void __launch_bounds__(kWaves * 64) decode_partial_stream_kernel(DecodeArgs a, int q_dtype, int num_seqs) {
+  const int w = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+  const int Hkv = a.num_kv_heads;
+  __shared__ RingLds lds;
+  static_assert(sizeof(lds.ring) >= sizeof(float) * kWaves * NG * kHead, "the ring doubles as the merge buffer");
+  static_assert(sizeof(lds.ring) / sizeof(int32_t) > kStreamMaxSeqs, "the ring holds the tiles prefix");
+
+  // tiles prefix over the sequences, scanned in the ring (free until the first tile)
+  int32_t* pref = reinterpret_cast<int32_t*>(&lds.ring[0][0][0][0]);
+  __shared__ int32_t s_scan[kWaves * 64];
+  const int64_t T = scan_tiles<kWaves * 64>(a, num_seqs, pref, s_scan, w == 0);
   // no more runs than units, so that no range is empty and the records of one
   // (b, h) stay consecutive; the other workgroups leave
   const int h = w % Hkv, j = w / Hkv;
@@ -950,35 +959,7 @@ __global__ void __launch_bounds__(kHeadWaves * 64) decode_partial_heads_kernel(D
   // tiles prefix over the sequences, scanned in the ring (free until the first tile)
   int32_t* pref = reinterpret_cast<int32_t*>(&lds.ring[0][0][0][0]);
   __shared__ int32_t s_scan[W * 64];
-  const int tid = threadIdx.x, nt = W * 64;
-  const int chunk = (num_seqs + nt - 1) / nt;
-  int sum = 0;
-  for (int i = 0; i < chunk; ++i) {
-    const int b = tid * chunk + i;
-    if (b < num_seqs) sum += tiles_of(a.seq_lens[b]);
-  }
-  s_scan[tid] = sum;
-  __syncthreads();
-  for (int o = 1; o < nt; o <<= 1) {
-    const int v = tid >= o ? s_scan[tid - o] : 0;
-    __syncthreads();
-    s_scan[tid] += v;
-    __syncthreads();
-  }
-  int run = tid > 0 ? s_scan[tid - 1] : 0;
-  for (int i = 0; i < chunk; ++i) {
-    const int b = tid * chunk + i;
-    if (b < num_seqs) {
-      pref[b] = run;
-      run += tiles_of(a.seq_lens[b]);
-    }
-  }
-  if (tid == nt - 1) pref[num_seqs] = s_scan[nt - 1];
-  __syncthreads();
-  const int64_t T = pref[num_seqs];
-  if (w == 0) {
-    for (int i = tid; i <= num_seqs; i += nt) a.prefix[i] = pref[i];
-  }
+  const int64_t T = scan_tiles<W * 64>(a, num_seqs, pref, s_scan, w == 0);
   const int hg = w % NHG, j = w / NHG;
   const int h = hg * HG + wave % HG, phase = wave / HG;
   const int64_t M = min<int64_t>(gridDim.x / NHG, T);
