@@ -133,13 +133,26 @@ def dtype_code(dtype: torch.dtype) -> int:
         raise AssertionError(f"unsupported dtype {dtype}") from None
 
 
+# torch's raw accessor of the current stream (what its generated kernels call):
+# 0.05 us against 1.7 us for torch.cuda.current_stream(device).cuda_stream, which
+# builds a Stream object per call.  The public call is the fallback.
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_handle(device: torch.device) -> int:
+    if _raw_stream is not None:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        return _raw_stream(idx)
     return torch.cuda.current_stream(device).cuda_stream
 
 
+_I64x4 = ctypes.c_int64 * 4
+
+
 def i64_array(values) -> ctypes.Array:
-    vals = [int(v) for v in values]
-    return (ctypes.c_int64 * len(vals))(*vals)
+    if len(values) == 4:
+        return _I64x4(*values)
+    return (ctypes.c_int64 * len(values))(*values)
 
 
 def ptr(t) -> int:
