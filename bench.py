@@ -371,7 +371,8 @@ def setup_copy_blocks(args, device):
         "dtype": "bf16",
         "config": {"workload": "copy_blocks (config 5a)", "pairs": 2048, "layers": L, "num_blocks": P,
                    "block_bytes": 65536},
-        "cpu": None,
+        "cpu": lambda: cpu_copy_blocks(nbytes),
+        "cpu_torch": lambda: torch_cpu_copy_blocks(nbytes),
     }
 
 
@@ -984,6 +985,42 @@ def torch_cpu_gather(cc, budget_s=3.0):
     return _timed(step, budget_s)
 
 
+def _copy_blocks_sample(P=256, n=128, L=61):
+    """A bounded host sample of config 5a: L layers of P 64 KiB blocks, n disjoint
+    pairs (about 1 GiB of host stack, 0.5 GB moved per step)."""
+    import torch
+
+    g = torch.Generator().manual_seed(1005)
+    stack = torch.randint(-32768, 32767, (L, P, 2, 16, 8, 128), generator=g, dtype=torch.int16)
+    perm = torch.randperm(P, generator=g)
+    pairs = torch.stack([perm[:n], perm[n: 2 * n]], 1)
+    moved = L * n * 65536 * 2 + n * 16
+    return stack, pairs, moved
+
+
+def cpu_copy_blocks(full_bytes, budget_s=10.0):
+    from oracle import kv_oracle as O
+
+    stack, pairs, moved = _copy_blocks_sample()
+    st, m = stack.numpy(), pairs.numpy()
+    n, el = _timed(lambda: O.copy_blocks(st, m), budget_s)
+    return n * moved / full_bytes, el, (f"{n} numpy oracle snapshot copies of 128 pairs x 61 layers of a 256-block "
+                                        f"host stack ({moved / 1e9:.2f} GB each), scaled to config 5a's bytes")
+
+
+def torch_cpu_copy_blocks(full_bytes, budget_s=3.0):
+    """The host path the survey names for copy_blocks: a snapshot index copy
+    stack[:, dst] = stack[:, src].clone() on a bounded sample."""
+    stack, pairs, moved = _copy_blocks_sample()
+    src, dst = pairs[:, 0], pairs[:, 1]
+
+    def step():
+        stack[:, dst] = stack[:, src].clone()
+
+    n, el = _timed(step, budget_s)
+    return n * moved / full_bytes, el
+
+
 # --------------------------------------------------------------------------- #
 # main
 # --------------------------------------------------------------------------- #
@@ -1122,8 +1159,9 @@ def main():
         n1, el1 = info["cpu_torch"]()
         cpu_torch = {"value": info["bytes"] * n / el / 1e9, "unit": "GB/s", "threads": threads,
                      "value_1thread": info["bytes"] * n1 / el1 / 1e9,
-                     "what": "the reference's CPU path: torch index_put_/index_select on host tensors of the same "
-                             f"layout, {n} steps in {el:.1f} s on {threads} threads, {n1} in {el1:.1f} s on 1"}
+                     "what": "the reference's CPU path: torch index_put_/index_select (copy_blocks: a snapshot "
+                             f"index copy) on host tensors of the same layout, {n:.3g} steps in {el:.1f} s on "
+                             f"{threads} threads, {n1:.3g} in {el1:.1f} s on 1"}
 
     line = {
         "metric": "achieved HBM GB/s (% of MI355X peak) + tokens/s for paged KV append/FP8 quant",
