@@ -476,6 +476,32 @@ def run_swap(args, device):
     best = max(results, key=lambda t: min(results[t]["store"]["GB/s"], results[t]["load"]["GB/s"]))
     st, ld = results[best]["store"]["GB/s"], results[best]["load"]["GB/s"]
     value = 2.0 / (1.0 / st + 1.0 / ld)  # both directions, harmonic mean
+
+    # achievable host link: one contiguous 1 GiB copy each way between device
+    # memory and pinned host memory; and a pinned host-to-host copy as the
+    # reference point for a path with no CPU analog
+    del cache
+    torch.cuda.empty_cache()
+    n = 1 << 30
+    dev_buf = torch.empty(n, dtype=torch.uint8, device=device)
+    host_a = torch.empty(n, dtype=torch.uint8, pin_memory=True)
+    host_b = torch.empty(n, dtype=torch.uint8, pin_memory=True)
+    host_a.fill_(3)
+
+    def timed_copy(dst, src, reps=5):
+        dst.copy_(src, non_blocking=True)
+        torch.cuda.synchronize()
+        t = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            dst.copy_(src, non_blocking=True)
+            torch.cuda.synchronize()
+            t.append(time.perf_counter() - t0)
+        return n / float(np.median(t)) / 1e9
+
+    link = {"D2H": timed_copy(host_a, dev_buf), "H2D": timed_copy(dev_buf, host_a)}
+    link_hm = 2.0 / (1.0 / link["D2H"] + 1.0 / link["H2D"])
+    host_copy = timed_copy(host_b, host_a)
     line = {
         "metric": "swap_blocks host-link GB/s (D2H store + H2D load, 4 GiB each way)",
         "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.swap_reps, "warmup": 1,
@@ -485,7 +511,11 @@ def run_swap(args, device):
         "config": {"workload": "swap_blocks (config 5b)", "blocks": len(gpu_ids), "layers": L,
                    "bytes_per_block_layer": 65536, "transport": best, "all_transports": results},
         "roofline": {"bound": "pcie", "achieved": round(value, 2), "peak": 64.0, "unit": "GB/s",
-                     "frac": round(value / 64.0, 4), "traffic": None},
+                     "frac": round(value / 64.0, 4), "traffic": None,
+                     "achievable": round(link_hm, 2), "frac_of_achievable": round(value / link_hm, 4),
+                     "achievable_each_way": {k: round(v, 2) for k, v in link.items()},
+                     "achievable_how": "one contiguous 1 GiB copy each way, device <-> pinned host"},
+        "host_to_host_pinned_copy_GBs": round(host_copy, 2),
         "cpu_baseline": None,
     }
     print(json.dumps(line), flush=True)
