@@ -251,6 +251,17 @@ def compute_kv_scales(
     if amax_out is not None:
         assert amax_out.dtype == torch.float32 and amax_out.numel() >= k and amax_out.device == device
     ws = amax_workspace(device)
+    if k == 2 and rows * row_len == 0:
+        # Empty tensors have NULL data, and a NULL second tensor means "key
+        # only" to the C entry: one single-tensor call per output (scale 1.0).
+        for j, t in enumerate(tensors):
+            status = lib().psk_kv_amax_scale(
+                ptr(t), None, rows, row_len, strides[j], strides[j], dtype_code(key.dtype), float(qmax),
+                out.data_ptr() + 4 * j, None if amax_out is None else amax_out.data_ptr() + 4 * j,
+                ptr(ws), ws.numel(), stream_handle(device),
+            )
+            check(status, "compute_kv_scales")
+        return out
     status = lib().psk_kv_amax_scale(
         ptr(key), ptr(value), rows, row_len, strides[0], strides[-1], dtype_code(key.dtype), float(qmax),
         ptr(out), ptr(amax_out), ptr(ws), ws.numel(), stream_handle(device),

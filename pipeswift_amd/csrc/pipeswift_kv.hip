@@ -1388,7 +1388,8 @@ int psk_kv_amax_scale(const void* x0, const void* x1, int64_t rows, int64_t row_
   const int sz = dtype_size(dtype);
   if (!sz || dtype == PSK_DTYPE_FP8_E4M3FN) return fail(PSK_E_DTYPE, "amax input must be bf16, fp16 or fp32");
   if (!(qmax > 0.0f)) return fail(PSK_E_ARG, "qmax must be positive");
-  if (!x0 || !scale_out || !workspace) return fail(PSK_E_ARG, "NULL pointer");
+  // an empty tensor (NULL data) reads nothing: its amax is 0 and its scale 1.0
+  if ((!x0 && rows * row_len > 0) || !scale_out || !workspace) return fail(PSK_E_ARG, "NULL pointer");
   if (workspace_len < kAmaxWsLen)
     return fail(PSK_E_WORKSPACE, "amax workspace needs %lld uint32 words, got %lld", (long long)kAmaxWsLen,
                 (long long)workspace_len);
