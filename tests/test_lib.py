@@ -48,6 +48,15 @@ def test_argument_errors_return_before_any_device_call():
         _lib.check(lib.psk_gather_cache(None, None, None, None, None, None, None, 1, 1, 1, 0, 16, 8, 1, 1, 1,
                                         2, 2, None, None), "gather")
     assert lib.psk_kv_amax_workspace_len() >= 2
+    # copy_blocks' grid limits: one workgroup per (pair, layer) on a 2-D grid
+    fake = 1 << 20  # never dereferenced: the checks return first
+    st = lib.psk_copy_blocks(fake, 70000, 65536, 65536, 65536, 4, fake, 8, None)
+    assert st == -1 and b"num_layers 70000 exceeds 65535" in lib.psk_last_error()
+    st = lib.psk_copy_blocks(fake, 2, 65536, 65536, 65536, 4, fake, (1 << 24) + 1, None)
+    assert st == -1 and b"exceeds 2^24" in lib.psk_last_error()
+    st = lib.psk_copy_blocks(fake, 2, 65536, 1024, 65536, 4, fake, 8, None)
+    assert st == -1 and b"exceeds block_stride" in lib.psk_last_error()
+    assert lib.psk_copy_blocks(None, 2, 65536, 65536, 65536, 4, None, 0, None) == 0  # no pairs: no-op
 
 
 def test_mla_fp8_tile_sizes_and_dtypes_are_checked_on_the_host():
