@@ -718,8 +718,10 @@ def run_l2_cycle(args, device):
 def run_attention_shapes(args, device):
     """Decode attention over several batch shapes, under the balanced schedule
     (num_splits 0, the default) and under the split schedule at the count the
-    split heuristic would pick; random FP8 pages, shuffled block tables, HIP
-    events around `--steps` eager calls after 5 warmup calls."""
+    split heuristic would pick; random FP8 pages, shuffled block tables.  `us`
+    is the device time per call, from HIP events around graph replays of 10
+    calls; `eager_us` is the same around eager calls, which includes the host
+    time of the Python call where that exceeds the device time."""
     import math
 
     import numpy as np
@@ -766,17 +768,36 @@ def run_attention_shapes(args, device):
                 attention.paged_decode_attention(q, cache[:, 0], cache[:, 1], bt, sl, None, out=out, workspace=ws,
                                                  num_splits=ns)
 
-            for _ in range(5):
-                call()
-            torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            for _ in range(reps):
-                call()
-            e1.record()
-            torch.cuda.synchronize()
-            us = e0.elapsed_time(e1) / reps * 1e3
-            row[label] = {"us": round(us, 2), "GB/s": round(kv_bytes / us / 1e3, 1)}
+            stream = torch.cuda.Stream(device)
+            with torch.cuda.stream(stream):
+                for _ in range(5):
+                    call()
+                stream.synchronize()
+                # eager: host time per call included (small shapes are host bound)
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for _ in range(reps):
+                    call()
+                e1.record(stream)
+                torch.cuda.synchronize()
+                eager_us = e0.elapsed_time(e1) / reps * 1e3
+                # graph replay: the device time per call
+                per_graph = 10
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, stream=stream):
+                    for _ in range(per_graph):
+                        call()
+                graph.replay()
+                stream.synchronize()
+                n_rep = max(1, reps // per_graph)
+                e0.record(stream)
+                for _ in range(n_rep):
+                    graph.replay()
+                e1.record(stream)
+                torch.cuda.synchronize()
+                us = e0.elapsed_time(e1) / (n_rep * per_graph) * 1e3
+                del graph
+            row[label] = {"us": round(us, 2), "GB/s": round(kv_bytes / us / 1e3, 1), "eager_us": round(eager_us, 2)}
         results.append(row)
         print(json.dumps(row), file=sys.stderr, flush=True)
     print(json.dumps({"metric": "decode attention us per call, balanced vs split schedule", "unit": "us",
