@@ -1023,20 +1023,26 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v + __shfl_xor(v, 32);
 }
 
-// One workgroup per (kv head, sequence), one wave per query head of the group.
-// The records are taken 64 at a time: lane s holds record s's maximum and sum,
-// two wave reductions (with an online rescale across chunks) give the weights,
-// and readlane hands each weight to every lane.  Each lane sums two output
-// columns over the records; the columns of the first kCombineChunk records of
-// a chunk are loaded together with its maxima, so up to kCombineChunk records
-// cost one round of loads.
+// One workgroup per (kv head, sequence), S waves per query head of the group
+// (S = blockDim / (64 G), chosen by the host from the records a sequence is
+// expected to have): wave (g, s) takes the s-th of S equal stretches of the
+// records.  The records are taken 64 at a time: lane r holds record r's
+// maximum and sum, two wave reductions (with an online rescale across chunks)
+// give the weights, and readlane hands each weight to every lane.  Each lane
+// sums two output columns over the records; the columns of the first
+// kCombineChunk records of a chunk are loaded together with its maxima, so up
+// to kCombineChunk records cost one round of loads.  With S > 1 the S partial
+// states of a head merge through LDS and wave (g, 0) writes the output.
 constexpr int kCombineChunk = 16;
+constexpr int kCombineMaxWaves = 16;
 
 template <int OUT_DT>
-__global__ void __launch_bounds__(64 * kMaxGroup) decode_combine_kernel(DecodeArgs a) {
+__global__ void __launch_bounds__(64 * kCombineMaxWaves) decode_combine_kernel(DecodeArgs a) {
   const int h = blockIdx.x, b = blockIdx.y;
   const int G = a.group;
-  const int g = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+  const int w = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+  const int S = int(blockDim.x) / (64 * G);
+  const int g = w % G, sidx = w / G;
   const int lane = threadIdx.x & 63;
   const int rec = G * (kHead + 2);
   int64_t first = 0;  // index of the first record of (b, h)
@@ -1065,8 +1071,9 @@ __global__ void __launch_bounds__(64 * kMaxGroup) decode_combine_kernel(DecodeAr
   using Bits = typename Elt<OUT_DT>::Bits;
   Bits* dst = reinterpret_cast<Bits*>(a.out + b * a.out_tok_stride + int64_t(h * G + g) * a.out_head_stride);
   float mx = kNegBig, den = 0.0f, o0 = 0.0f, o1 = 0.0f;
-  for (int c0 = 0; c0 < n; c0 += 64) {
-    const int cnt = min(64, n - c0);
+  const int r_end = int(int64_t(n) * (sidx + 1) / S);
+  for (int c0 = int(int64_t(n) * sidx / S); c0 < r_end; c0 += 64) {
+    const int cnt = min(64, r_end - c0);
     float m = kNegBig, l = 0.0f;
     if (lane < cnt) {
       m = part[int64_t(c0 + lane) * rs + g];
@@ -1097,6 +1104,32 @@ __global__ void __launch_bounds__(64 * kMaxGroup) decode_combine_kernel(DecodeAr
         o1 = __builtin_fmaf(x[i].y, w, o1);
       }
     }
+  }
+  if (S > 1) {
+    // merge the S stretches of each head (a stretch without records holds
+    // mx = kNegBig and zero sums, which weigh nothing)
+    __shared__ float s_mx[kCombineMaxWaves], s_den[kCombineMaxWaves];
+    __shared__ f32x2 s_o[kCombineMaxWaves][64];
+    if (lane == 0) {
+      s_mx[w] = mx;
+      s_den[w] = den;
+    }
+    s_o[w][lane] = f32x2{o0, o1};
+    __syncthreads();
+    if (sidx != 0) return;
+    float m_all = mx;
+    for (int t = 1; t < S; ++t) m_all = __builtin_fmaxf(m_all, s_mx[g + G * t]);
+    den = 0.0f;
+    o0 = 0.0f;
+    o1 = 0.0f;
+    for (int t = 0; t < S; ++t) {
+      const float c = __builtin_amdgcn_exp2f(s_mx[g + G * t] - m_all);
+      den += s_den[g + G * t] * c;
+      const f32x2 o = s_o[g + G * t][lane];
+      o0 += o.x * c;
+      o1 += o.y * c;
+    }
+    mx = m_all;
   }
   // no records (an empty sequence): zeros and lse = -inf
   const float inv = den > 0.0f ? vd / den : 0.0f;
@@ -1395,10 +1428,16 @@ int psk_paged_decode_attention(const void* q, int64_t q_tok_stride, int64_t q_he
   const int st1 = check_launch("decode_partial_kernel launch");
   if (st1 != PSK_OK) return st1;
   const dim3 grid2{unsigned(num_kv_heads), unsigned(num_seqs), 1u};
+  // waves per query head in the combine: one per 64 records a sequence is
+  // expected to have (the balanced schedule spreads runs / sequences + 1 on
+  // average; the split schedule at most max_splits), at most 16 / G
+  const int64_t recs = runs > 0 ? runs / num_seqs + 1 : a.max_splits;
+  const int64_t waves_g = std::max<int64_t>(1, std::min<int64_t>(kCombineMaxWaves / G, ceil_div(recs, 64)));
+  const dim3 block2{unsigned(64 * G * waves_g), 1u, 1u};
   if (out_dtype == PSK_DTYPE_BF16)
-    hipLaunchKernelGGL((decode_combine_kernel<PSK_DTYPE_BF16>), grid2, dim3(64 * G), 0, st, a);
+    hipLaunchKernelGGL((decode_combine_kernel<PSK_DTYPE_BF16>), grid2, block2, 0, st, a);
   else
-    hipLaunchKernelGGL((decode_combine_kernel<PSK_DTYPE_F32>), grid2, dim3(64 * G), 0, st, a);
+    hipLaunchKernelGGL((decode_combine_kernel<PSK_DTYPE_F32>), grid2, block2, 0, st, a);
   return check_launch("decode_combine_kernel launch");
 }
 

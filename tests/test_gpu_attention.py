@@ -278,3 +278,12 @@ def test_flash_attn_varlen_func_matches_direct_call(dev):
     assert torch.equal(a, b)
     with pytest.raises(AssertionError):
         attention.flash_attn_varlen_func(q, fd[:, 0], fd[:, 1], 2, None, seqused_k=lens, block_table=bt)
+
+
+@pytest.mark.parametrize("Hq,Hkv,length", [(8, 2, 20000), (64, 8, 9000), (3, 1, 33000)])
+def test_single_long_sequence_combine_waves(dev, Hq, Hkv, length):
+    """One sequence spread over every run of the balanced schedule: hundreds of
+    records per (sequence, kv head), merged by several combine waves per query
+    head (up to 1024 threads for groups of 8)."""
+    P = -(-length // 16) + 8
+    _case(dev, 61 + Hkv, 1, Hq, Hkv, 16, P, [length], "bf16", torch.float32, "per_seq_head")
