@@ -253,8 +253,9 @@ int64_t psk_build_kv_metadata(int64_t num_seqs, const uint64_t* page_table_ptrs,
  * num_splits > 0: how many workgroups share the longest sequence (flash-decoding
  * split, as FA's num_splits; at most 128 are used).  0: the balanced schedule
  * when the block size is a power of two >= 16 and num_seqs <= 1024 (one
- * workgroup per resident slot, each taking an equal run of every sequence's
- * 16-token tiles of one kv head), otherwise an automatic split count.
+ * workgroup per resident slot, each taking an equal share of the batch's
+ * 16-token tiles across sequence boundaries, a sequence start priced as
+ * extra tiles), otherwise an automatic split count.
  * out: bf16 or f32 at element strides (out_tok_stride, out_head_stride); lse
  * (fp32, optional) at lse[hq * lse_head_stride + b]; a sequence of length 0
  * writes zeros and lse = -inf.  workspace: device floats, at least

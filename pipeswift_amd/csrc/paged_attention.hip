@@ -104,8 +104,9 @@ struct DecodeArgs {
   int64_t vd_b, vd_h;
   float* part;       // partial records of G * (kHead + 2) floats: [B][Hkv][max_splits] (splits) or
                      // [(B + stream_wgs) * Hkv] (balanced schedule)
-  int32_t* prefix;   // balanced schedule: tiles before each sequence, [B + 1]
+  int32_t* prefix;   // balanced schedule: units before each sequence, [B + 1]
   int32_t stream_wgs;  // balanced schedule: workgroups per kv head; 0 with splits
+  int32_t seq_units;   // balanced schedule: units that stand for the start of a sequence
   char* out;
   int64_t out_tok_stride;   // bytes
   int64_t out_head_stride;  // bytes
@@ -741,31 +742,47 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_ring_kernel(Decode
                     reinterpret_cast<float(*)[NG][kHead]>(&lds.ring[0][0][0][0]));
 }
 
-// Balanced schedule.  Per kv head the work is the list of units (sequence b,
-// 16-token tile t), T = sum of tiles_b = ceil(len_b / 16) in all.  Run j of
-// head h takes head h's units [T j / M, T (j+1) / M), M = min(grid / Hkv, T), whatever sequences they belong to: every workgroup streams the same
-// number of tiles, the grid (one workgroup per resident slot) ends together,
+// Balanced schedule.  Per kv head the work is a list of units: for each
+// sequence b with tokens, seq_units units that carry no work (the cost of
+// starting a sequence) and then its 16-token tiles t, ceil(len_b / 16) of
+// them; T units in all.  Run j of head h takes head h's units
+// [T j / M, T (j+1) / M), M = min(grid / Hkv, T), whatever sequences they
+// belong to: every workgroup gets the same cost in tiles and sequence starts,
+// the grid (one workgroup per resident slot) ends together,
 // and the Hkv workgroups of one j walk the same tokens of the same pages at
 // the same time (a token's kv heads share its cache rows).  Workgroup
 // j * Hkv + h runs (h, j): the heads of one run are dispatched together.  Each maximal run
 // of one sequence inside the range gives one partial record, at index
 // (b + j) * Hkv + h: the records of one (b, h) come from consecutive j, Hkv
-// apart.  Workgroup 0 also stores the tiles prefix (prefix[b] = tiles before
+// apart.  Workgroup 0 also stores the units prefix (prefix[b] = units before
 // b) after the records for the combine.
 __device__ __forceinline__ int tiles_of(int len) { return len > 0 ? (len + kTile - 1) / kTile : 0; }
 
-// Tiles prefix of the batch in LDS (pref[b] = tiles before sequence b,
-// pref[num_seqs] = all tiles), by the NT threads of the workgroup; returns the
-// total.  `store` also writes it to a.prefix for the combine.
+// Units of sequence b in the balanced schedule: its tiles, after a.seq_units
+// units that carry no work and stand for the fixed cost of starting a
+// sequence (page-id staging, query loads, the partial record), so that a run
+// over many short sequences takes fewer tiles.
+__device__ __forceinline__ int units_of(const DecodeArgs& a, int len) {
+  return len > 0 ? tiles_of(len) + a.seq_units : 0;
+}
+
+// Units prefix of the batch in LDS (pref[b] = units before sequence b,
+// pref[num_seqs] = all units), by the NT threads of the workgroup; returns the
+// total.  `store` also writes it to a.prefix for the combine; `lens`, when
+// given, receives a copy of the sequence lengths.
 template <int NT>
 __device__ __forceinline__ int64_t scan_tiles(const DecodeArgs& a, int num_seqs, int32_t* pref, int32_t* s_scan,
-                                              bool store) {
+                                              bool store, int32_t* lens = nullptr) {
   const int tid = threadIdx.x;
   const int chunk = (num_seqs + NT - 1) / NT;
   int sum = 0;
   for (int i = 0; i < chunk; ++i) {
     const int b = tid * chunk + i;
-    if (b < num_seqs) sum += tiles_of(a.seq_lens[b]);
+    if (b < num_seqs) {
+      const int len = a.seq_lens[b];
+      if (lens) lens[b] = len;
+      sum += units_of(a, len);
+    }
   }
   s_scan[tid] = sum;
   __syncthreads();
@@ -780,7 +797,7 @@ __device__ __forceinline__ int64_t scan_tiles(const DecodeArgs& a, int num_seqs,
     const int b = tid * chunk + i;
     if (b < num_seqs) {
       pref[b] = run;
-      run += tiles_of(a.seq_lens[b]);
+      run += units_of(a, lens ? lens[b] : a.seq_lens[b]);
     }
   }
   if (tid == NT - 1) pref[num_seqs] = s_scan[NT - 1];
@@ -791,6 +808,20 @@ __device__ __forceinline__ int64_t scan_tiles(const DecodeArgs& a, int num_seqs,
   return pref[num_seqs];
 }
 
+// The sequence b that owns unit u (the last with pref[b] <= u: sequences
+// without units share their successor's prefix) and the tile t of b that unit
+// u stands for, negative inside b's leading units.
+__device__ __forceinline__ void seek_unit(const int32_t* pref, int num_seqs, int seq_units, int64_t u, int& b,
+                                          int& t) {
+  int lo = 0, hi = num_seqs - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (pref[mid] <= u) lo = mid; else hi = mid - 1;
+  }
+  b = lo;
+  t = int(u - pref[b]) - seq_units;
+}
+
 template <int NG>
 __global__ void __launch_bounds__(kWaves * 64) decode_partial_stream_kernel(DecodeArgs a, int q_dtype, int num_seqs) {
   const int w = blockIdx.x;
@@ -799,9 +830,9 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_stream_kernel(Deco
   const int Hkv = a.num_kv_heads;
   __shared__ RingLds lds;
   static_assert(sizeof(lds.ring) >= sizeof(float) * kWaves * NG * kHead, "the ring doubles as the merge buffer");
-  static_assert(sizeof(lds.ring) / sizeof(int32_t) > kStreamMaxSeqs, "the ring holds the tiles prefix");
+  static_assert(sizeof(lds.ring) / sizeof(int32_t) > kStreamMaxSeqs, "the ring holds the units prefix");
 
-  // tiles prefix over the sequences, scanned in the ring (free until the first tile)
+  // units prefix over the sequences, scanned in the ring (free until the first tile)
   int32_t* pref = reinterpret_cast<int32_t*>(&lds.ring[0][0][0][0]);
   __shared__ int32_t s_scan[kWaves * 64];
   const int64_t T = scan_tiles<kWaves * 64>(a, num_seqs, pref, s_scan, w == 0);
@@ -812,20 +843,19 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_stream_kernel(Deco
   if (j >= M) return;  // uniform over the workgroup
   int64_t u = T * j / M;
   const int64_t u_end = T * (j + 1) / M;
-  // last b with pref[b] <= u (sequences without tiles share their successor's
-  // prefix; the search lands on the one that owns unit u)
-  int lo = 0, hi = num_seqs - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (pref[mid] <= u) lo = mid; else hi = mid - 1;
-  }
-  int b = lo;
-  int t = int(u - pref[b]);
+  int b, t;
+  seek_unit(pref, num_seqs, a.seq_units, u, b, t);
   // ring_attend's first barrier orders these prefix reads before the ring is refilled
 
   // tokens per page staging: at most kRingPages pages from any 16-aligned start
   const int piece = int(std::min<int64_t>(int64_t(kRingPages - 1) << a.bs_shift, INT32_MAX / 2)) & ~(kTile * kWaves - 1);
   while (u < u_end && b < num_seqs) {
+    if (t < 0) {  // leading units of b: no work
+      const int skip = int(min<int64_t>(-t, u_end - u));
+      u += skip;
+      t += skip;
+      if (u >= u_end) break;
+    }
     const int len = a.seq_lens[b];
     const int tb = tiles_of(len);
     const int n = int(min<int64_t>(tb - t, u_end - u));
@@ -846,7 +876,7 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_stream_kernel(Deco
     u += n;
     t += n;
     if (t == tb) {
-      t = 0;
+      t = -a.seq_units;
       do ++b; while (b < num_seqs && a.seq_lens[b] <= 0);
     }
   }
@@ -861,7 +891,7 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_stream_kernel(Deco
 // each of eight workgroups on eight XCDs requesting its own slice: a
 // read-only probe of config 2's pages streams 6.9 TB/s that way against 5.9
 // for head slices.  Workgroup j * NHG + hg serves run j of head group hg
-// (NHG = Hkv / HG); records and the tiles prefix are laid out as in the
+// (NHG = Hkv / HG); records and the units prefix are laid out as in the
 // per-head balanced schedule, so the same combine reads them.
 constexpr int kHeadWaves = 8;
 // LDS tile slots per wave.  At one workgroup per CU deeper rings cost no
@@ -954,31 +984,30 @@ __global__ void __launch_bounds__(kHeadWaves * 64) decode_partial_heads_kernel(D
   __shared__ RingLdsT<W, kHeadRing> lds;
   __shared__ float s_m[W][NG], s_l[W][NG];
   static_assert(sizeof(lds.ring) >= sizeof(float) * W * NG * kHead, "the ring doubles as the merge buffer");
-  static_assert(sizeof(lds.ring) / sizeof(int32_t) > kStreamMaxSeqs, "the ring holds the tiles prefix");
 
-  // tiles prefix over the sequences, scanned in the ring (free until the first tile)
-  int32_t* pref = reinterpret_cast<int32_t*>(&lds.ring[0][0][0][0]);
+  // units prefix and lengths of the sequences, kept in LDS for the whole run
+  __shared__ int32_t s_pref[kStreamMaxSeqs + 1], s_len[kStreamMaxSeqs];
   __shared__ int32_t s_scan[W * 64];
-  const int64_t T = scan_tiles<W * 64>(a, num_seqs, pref, s_scan, w == 0);
+  const int64_t T = scan_tiles<W * 64>(a, num_seqs, s_pref, s_scan, w == 0, s_len);
   const int hg = w % NHG, j = w / NHG;
   const int h = hg * HG + wave % HG, phase = wave / HG;
   const int64_t M = min<int64_t>(gridDim.x / NHG, T);
   if (j >= M) return;  // uniform over the workgroup
   int64_t u = T * j / M;
   const int64_t u_end = T * (j + 1) / M;
-  int lo = 0, hi = num_seqs - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (pref[mid] <= u) lo = mid; else hi = mid - 1;
-  }
-  int b = lo;
-  int t = int(u - pref[b]);
-  // ring_attend's first barrier orders these prefix reads before the ring is refilled
+  int b, t;
+  seek_unit(s_pref, num_seqs, a.seq_units, u, b, t);
 
   // page-id staging pieces: at most kRingPages pages, whole multiples of every phase stride
   const int piece = int(std::min<int64_t>(int64_t(kRingPages - 1) << a.bs_shift, INT32_MAX / 2)) & ~(kTile * W - 1);
   while (u < u_end && b < num_seqs) {
-    const int len = a.seq_lens[b];
+    if (t < 0) {  // leading units of b: no work
+      const int skip = int(min<int64_t>(-t, u_end - u));
+      u += skip;
+      t += skip;
+      if (u >= u_end) break;
+    }
+    const int len = s_len[b];
     const int tb = tiles_of(len);
     const int n = int(min<int64_t>(tb - t, u_end - u));
     bf16x8 qop[4];
@@ -998,8 +1027,8 @@ __global__ void __launch_bounds__(kHeadWaves * 64) decode_partial_heads_kernel(D
     u += n;
     t += n;
     if (t == tb) {
-      t = 0;
-      do ++b; while (b < num_seqs && a.seq_lens[b] <= 0);
+      t = -a.seq_units;
+      do ++b; while (b < num_seqs && s_len[b] <= 0);
     }
   }
 }
@@ -1050,12 +1079,14 @@ __global__ void __launch_bounds__(64 * kCombineMaxWaves) decode_combine_kernel(D
   int n = 0;          // records of (b, h)
   if (a.stream_wgs > 0) {
     // run j of head h took units [T j / M, T (j+1) / M); unit u belongs to run
-    // j(u) = ((u + 1) M - 1) / T, and b owns units [p0, p0 + tiles)
-    const int64_t p0 = a.prefix[b], tiles = a.prefix[b + 1] - p0;
-    if (tiles > 0) {
+    // j(u) = ((u + 1) M - 1) / T, and b owns units [p0, p0 + units), of which
+    // the first seq_units carry no work: the runs of its tiles wrote records
+    const int64_t p0 = a.prefix[b], units = a.prefix[b + 1] - p0;
+    if (units > 0) {
       const int64_t T = a.prefix[gridDim.y];
       const int64_t M = min<int64_t>(a.stream_wgs, T);  // as the partial kernel caps it
-      const int64_t j0 = ((p0 + 1) * M - 1) / T, j1 = ((p0 + tiles) * M - 1) / T;
+      const int64_t u0 = p0 + a.seq_units, u1 = p0 + units - 1;  // first and last tile units
+      const int64_t j0 = ((u0 + 1) * M - 1) / T, j1 = ((u1 + 1) * M - 1) / T;
       first = (int64_t(b) + j0) * a.num_kv_heads + h;
       rs = int64_t(a.num_kv_heads) * rec;
       n = int(j1 - j0 + 1);
@@ -1261,6 +1292,17 @@ int64_t stream_runs(int ng, int64_t num_kv_heads) {
 // 128 sequences 244 us against 266).
 constexpr int64_t kHeadsMinSeqs = 8;
 
+// Units that stand for the fixed cost of starting a sequence in a run (see
+// units_of), per schedule.
+#ifndef PSK_HEADS_SEQ_UNITS
+#define PSK_HEADS_SEQ_UNITS 8
+#endif
+#ifndef PSK_STREAM_SEQ_UNITS
+#define PSK_STREAM_SEQ_UNITS 0
+#endif
+constexpr int kHeadsSeqUnits = PSK_HEADS_SEQ_UNITS;
+constexpr int kStreamSeqUnits = PSK_STREAM_SEQ_UNITS;
+
 // Runs per workgroup family of the balanced schedule for this batch.
 int64_t balanced_runs(int ng, int64_t num_seqs, int64_t num_kv_heads) {
   return num_seqs >= kHeadsMinSeqs ? heads_runs(ng, num_kv_heads) : stream_runs(ng, num_kv_heads);
@@ -1292,7 +1334,7 @@ int64_t psk_paged_decode_workspace_len(int64_t num_seqs, int64_t num_q_heads, in
       std::max<int64_t>(1, ceil_div(max_seq_len, decode_split(max_seq_len, num_splits, num_seqs * num_kv_heads)));
   int64_t need = num_seqs * num_kv_heads * splits * rec;
   if (num_splits == 0 && num_seqs <= kStreamMaxSeqs && G <= kMaxGroup) {
-    // the balanced schedule: a record per (sequence, kv head) and per workgroup, then the tiles prefix
+    // the balanced schedule: a record per (sequence, kv head) and per workgroup, then the units prefix
     need = std::max(need,
                     (num_seqs + balanced_runs(group_ng(G), num_seqs, num_kv_heads)) * num_kv_heads * rec + num_seqs + 1);
   }
@@ -1394,6 +1436,7 @@ int psk_paged_decode_attention(const void* q, int64_t q_tok_stride, int64_t q_he
   const bool uniform = ring && a.split / block_size + 1 <= kRingPages;
   if (runs > 0) {
     a.stream_wgs = int32_t(runs);
+    a.seq_units = heads ? kHeadsSeqUnits : kStreamSeqUnits;
     a.prefix = reinterpret_cast<int32_t*>(workspace + (num_seqs + runs) * num_kv_heads * G * (kHead + 2));
     const int ns = int(num_seqs);
     if (heads) {
