@@ -1052,26 +1052,28 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v + __shfl_xor(v, 32);
 }
 
-// One workgroup per (kv head, sequence), S waves per query head of the group
-// (S = blockDim / (64 G), chosen by the host from the records a sequence is
-// expected to have): wave (g, s) takes the s-th of S equal stretches of the
-// records.  The records are taken 64 at a time: lane r holds record r's
+// One workgroup per (query head h G + g, sequence), S waves (S = blockDim /
+// 64, chosen by the host from the records a sequence is expected to have, one
+// wave per kCombineChunk of them): wave s takes the s-th of S equal stretches
+// of the records.  The records are taken 64 at a time: lane r holds record r's
 // maximum and sum, two wave reductions (with an online rescale across chunks)
 // give the weights, and readlane hands each weight to every lane.  Each lane
 // sums two output columns over the records; the columns of the first
-// kCombineChunk records of a chunk are loaded together with its maxima, so up
-// to kCombineChunk records cost one round of loads.  With S > 1 the S partial
-// states of a head merge through LDS and wave (g, 0) writes the output.
+// kCombineChunk records of a chunk are loaded together with its maxima, so a
+// stretch of up to kCombineChunk records costs one round of loads.  With
+// S > 1 the S partial states merge through LDS and wave 0 writes the output.
+// A workgroup per query head rather than per kv head spreads a single long
+// sequence's records over G times the CUs.
 constexpr int kCombineChunk = 16;
 constexpr int kCombineMaxWaves = 16;
 
 template <int OUT_DT>
 __global__ void __launch_bounds__(64 * kCombineMaxWaves) decode_combine_kernel(DecodeArgs a) {
-  const int h = blockIdx.x, b = blockIdx.y;
   const int G = a.group;
+  const int h = int(blockIdx.x) / G, g = int(blockIdx.x) - h * G, b = blockIdx.y;
   const int w = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
-  const int S = int(blockDim.x) / (64 * G);
-  const int g = w % G, sidx = w / G;
+  const int S = int(blockDim.x) / 64;
+  const int sidx = w;
   const int lane = threadIdx.x & 63;
   const int rec = G * (kHead + 2);
   int64_t first = 0;  // index of the first record of (b, h)
@@ -1137,8 +1139,8 @@ __global__ void __launch_bounds__(64 * kCombineMaxWaves) decode_combine_kernel(D
     }
   }
   if (S > 1) {
-    // merge the S stretches of each head (a stretch without records holds
-    // mx = kNegBig and zero sums, which weigh nothing)
+    // merge the S stretches (a stretch without records holds mx = kNegBig and
+    // zero sums, which weigh nothing)
     __shared__ float s_mx[kCombineMaxWaves], s_den[kCombineMaxWaves];
     __shared__ f32x2 s_o[kCombineMaxWaves][64];
     if (lane == 0) {
@@ -1149,14 +1151,14 @@ __global__ void __launch_bounds__(64 * kCombineMaxWaves) decode_combine_kernel(D
     __syncthreads();
     if (sidx != 0) return;
     float m_all = mx;
-    for (int t = 1; t < S; ++t) m_all = __builtin_fmaxf(m_all, s_mx[g + G * t]);
+    for (int t = 1; t < S; ++t) m_all = __builtin_fmaxf(m_all, s_mx[t]);
     den = 0.0f;
     o0 = 0.0f;
     o1 = 0.0f;
     for (int t = 0; t < S; ++t) {
-      const float c = __builtin_amdgcn_exp2f(s_mx[g + G * t] - m_all);
-      den += s_den[g + G * t] * c;
-      const f32x2 o = s_o[g + G * t][lane];
+      const float c = __builtin_amdgcn_exp2f(s_mx[t] - m_all);
+      den += s_den[t] * c;
+      const f32x2 o = s_o[t][lane];
       o0 += o.x * c;
       o1 += o.y * c;
     }
@@ -1470,13 +1472,14 @@ int psk_paged_decode_attention(const void* q, int64_t q_tok_stride, int64_t q_he
   }
   const int st1 = check_launch("decode_partial_kernel launch");
   if (st1 != PSK_OK) return st1;
-  const dim3 grid2{unsigned(num_kv_heads), unsigned(num_seqs), 1u};
-  // waves per query head in the combine: one per 64 records a sequence is
-  // expected to have (the balanced schedule spreads runs / sequences + 1 on
-  // average; the split schedule at most max_splits), at most 16 / G
+  const dim3 grid2{unsigned(num_q_heads), unsigned(num_seqs), 1u};
+  // waves per query head in the combine: one per kCombineChunk records a
+  // sequence is expected to have (the balanced schedule spreads runs /
+  // sequences + 1 on average; the split schedule at most max_splits), at most
+  // kCombineMaxWaves
   const int64_t recs = runs > 0 ? runs / num_seqs + 1 : a.max_splits;
-  const int64_t waves_g = std::max<int64_t>(1, std::min<int64_t>(kCombineMaxWaves / G, ceil_div(recs, 64)));
-  const dim3 block2{unsigned(64 * G * waves_g), 1u, 1u};
+  const int64_t waves = std::max<int64_t>(1, std::min<int64_t>(kCombineMaxWaves, ceil_div(recs, kCombineChunk)));
+  const dim3 block2{unsigned(64 * waves), 1u, 1u};
   if (out_dtype == PSK_DTYPE_BF16)
     hipLaunchKernelGGL((decode_combine_kernel<PSK_DTYPE_BF16>), grid2, block2, 0, st, a);
   else
