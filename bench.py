@@ -17,6 +17,9 @@ The JSON line carries:
                    under profiles/), when present, and the fraction of the
                    best device copy measured on this box in the same run
                    (`achievable`, copy_blocks_kernel over 1 GiB)
+  copy_floor       for workloads under 64 MB: device us of the HIP runtime's
+                   contiguous copy of the same bytes at the same size, timed
+                   the same way (vs_launch > 1: the kernel beats that copy)
   wall_us_per_call_eager  host wall time per eager Python call (no graph)
   cpu_baseline     the numpy oracle timed on this host on a bounded sample
   cpu_torch        the reference's CPU path (torch index_put_ / index_select on
@@ -399,6 +402,48 @@ def measure_device_copy(device, reps=10):
     del stack
     torch.cuda.empty_cache()
     return gbs
+
+
+def measure_copy_floor(device, nbytes, G=64):
+    """Device microseconds of the HIP runtime's own contiguous copy (torch
+    ``copy_``) moving the same bytes as one launch (nbytes / 2 each way), over
+    rotated buffer pairs (a working set of at least 1 GiB, above the Infinity
+    Cache) replayed from HIP graphs of G copies, as the kernels are timed: the
+    floor of a plain copy at this size, for the microsecond workloads."""
+    import torch
+
+    each = max(16, (nbytes // 2) // 16 * 16)
+    n = int(min(512, max(16, math.ceil((1 << 30) / (2 * each)))))
+    src = torch.zeros(n, each, dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+    G = min(G, n)
+    stream = torch.cuda.Stream(device)
+    graphs = []
+    with torch.cuda.stream(stream):
+        for i in range(min(n, 8)):
+            dst[i].copy_(src[i])
+        stream.synchronize()
+        for gi in range(max(1, min(n // G, 8))):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                for j in range(G):
+                    k = (gi * G + j) % n
+                    dst[k].copy_(src[k])
+            graphs.append(g)
+        for g in graphs:
+            g.replay()
+        stream.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 4 * len(graphs)
+        e0.record(stream)
+        for r in range(reps):
+            graphs[r % len(graphs)].replay()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (reps * G)
+    del graphs, src, dst
+    torch.cuda.empty_cache()
+    return us
 
 
 def run_hbm_copy(args, device):
@@ -1187,6 +1232,8 @@ def main():
         eager_us = (time.perf_counter() - t0) / eager_n * 1e6
 
     achievable = measure_device_copy(device)
+    # microsecond workloads: the runtime's copy of the same bytes at the same size
+    copy_floor = measure_copy_floor(device, info["bytes"]) if info["bytes"] < (64 << 20) else None
 
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
@@ -1242,6 +1289,12 @@ def main():
             "traffic": traffic,
             "achievable": round(achievable, 1),
             "frac_of_achievable": round(achieved / achievable, 5),
+        },
+        "copy_floor": None if copy_floor is None else {
+            "us": round(copy_floor, 3),
+            "vs_launch": round(copy_floor / (per_launch_s * 1e6), 4),
+            "how": "torch copy_ (the HIP runtime's device copy) of the same bytes, half each way, over rotated "
+                   "buffer pairs (>= 1 GiB) replayed from HIP graphs of 64 copies",
         },
         "wall_us_per_call_eager": round(eager_us, 2),
         "cpu_baseline": cpu,
