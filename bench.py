@@ -218,7 +218,7 @@ def setup_kv_scales(args, device):
 
     nbytes = 2 * case.qkv.shape[0] * case.num_heads * case.head_size * 2
     return launch, {
-        "name": "kv_scales", "kernel": "amax_scale_kernel", "bytes": nbytes, "tokens": case.qkv.shape[0],
+        "name": "kv_scales", "kernel": "amax_partial_kernel + amax_finalize_kernel", "bytes": nbytes, "tokens": case.qkv.shape[0],
         "dtype": "bf16",
         "config": {"workload": "FP8 per-tensor scale from amax, config 2 K and V", "tokens": case.qkv.shape[0]},
         "cpu": None,
