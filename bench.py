@@ -231,7 +231,10 @@ def setup_chunked(args, device, gather):
     from pipeswift_amd import cache_ops, workloads
     from pipeswift_amd.reshape_and_cache import reshape_and_cache_flash
 
-    cc = workloads.config3_chunked()
+    # --block-size: the sensitivity run at a larger page (the same token
+    # capacity: num_blocks scaled down)
+    ps_arg = args.block_size
+    cc = workloads.config3_chunked(block_size=ps_arg, num_blocks=32768 * 16 // ps_arg)
     a = cc.append
     P, ps = a.cache.shape[0], a.cache.shape[2]
     cache = a.cache.to(device)
@@ -255,7 +258,7 @@ def setup_chunked(args, device, gather):
         return launch, {
             "name": "chunked_append", "kernel": "paged_scatter_kernel", "bytes": nbytes, "tokens": N,
             "dtype": "bf16",
-            "config": {"workload": "chunked_append (config 3)", "tokens": N, "kv_heads": a.num_heads,
+            "config": {"workload": "chunked_append (config 3)" + ("" if ps == 16 else f", block size {ps}"), "tokens": N, "kv_heads": a.num_heads,
                        "head_dim": a.head_size, "block_size": ps, "num_blocks": P, "sequences": len(cc.chunk)},
             "cpu": lambda: cpu_append(a, False),
             "cpu_torch": lambda: torch_cpu_append(a, False),
@@ -276,7 +279,7 @@ def setup_chunked(args, device, gather):
     return launch, {
         "name": "gather", "kernel": "paged_gather_kernel", "bytes": nbytes, "tokens": T, "dtype": "bf16",
         "rotate": R,
-        "config": {"workload": "block gather (config 3)", "tokens": T, "sequences": len(cc.chunk),
+        "config": {"workload": "block gather (config 3)" + ("" if ps == 16 else f", block size {ps}"), "tokens": T, "sequences": len(cc.chunk),
                    "kv_heads": a.num_heads, "head_dim": a.head_size, "block_size": ps, "num_blocks": P,
                    "pages": pages},
         "cpu": lambda: cpu_gather(cc),
@@ -1134,6 +1137,8 @@ def main():
     p.add_argument("--transports", default="blit,memcpy", help="swap workload: transports to compare")
     p.add_argument("--swap-reps", type=int, default=3)
     p.add_argument("--num-splits", type=int, default=0, help="decode_attention: splits of the longest sequence (0: auto)")
+    p.add_argument("--block-size", type=int, default=16,
+                   help="chunked_append / gather: page size (16 is config 3; 128 is its sensitivity run)")
     args = p.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:

@@ -193,3 +193,29 @@ def test_gather_many_sequences_kv_variants(dev, ps, H, D, with_starts):
         O.gather_cache(raw(cache), bt.numpy(), cu.numpy(), seq_starts=None if starts is None else starts.numpy(),
                        out=exp)
         assert np.array_equal(raw(out), exp)
+
+
+def test_config3_block_size_128_append_then_gather(dev):
+    """Config 3's sensitivity run: the same chunked prefill at 128-token pages
+    (4096 blocks, the same slot capacity), append then gather, against the
+    oracle and as a round trip."""
+    cc = workloads.config3_chunked(block_size=128, num_blocks=4096)
+    a = cc.append
+    print(f"config3 ps=128: chunks={cc.chunk.tolist()} prefix={cc.prefix.tolist()} T={int(cc.cu_seq_lens[-1])}",
+          flush=True)
+    qd = a.qkv.to(dev)
+    cache_d = a.cache.to(dev)
+    reshape_and_cache_flash(a.key(qd), a.value(qd), cache_d[:, 0], cache_d[:, 1], a.slot_mapping.to(dev))
+    exp = raw(a.cache).copy()
+    O.reshape_and_cache(raw(a.key()), raw(a.value()), exp[:, 0], exp[:, 1], a.slot_mapping.numpy())
+    assert np.array_equal(raw(cache_d), exp)
+    T = int(cc.cu_seq_lens[-1])
+    out_k = torch.empty(T, a.num_heads, a.head_size, dtype=torch.bfloat16, device=dev)
+    out_v = torch.empty_like(out_k)
+    cache_ops.gather_cache(cache_d[:, 0], out_k, cc.block_table.to(dev), cc.cu_seq_lens.to(dev),
+                           src_cache_v=cache_d[:, 1], dst_v=out_v)
+    assert np.array_equal(raw(out_k), O.gather_cache(exp[:, 0], cc.block_table.numpy(), cc.cu_seq_lens.numpy()))
+    assert np.array_equal(raw(out_v), O.gather_cache(exp[:, 1], cc.block_table.numpy(), cc.cu_seq_lens.numpy()))
+    cu = cc.cu_seq_lens.numpy()
+    rows = [raw(out_v)[cu[b] + int(cc.prefix[b]): cu[b + 1]] for b in range(len(cc.chunk))]
+    assert np.array_equal(np.concatenate(rows), raw(a.value()))
