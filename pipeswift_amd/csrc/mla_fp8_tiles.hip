@@ -38,25 +38,41 @@ constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
 constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7 - i within each 8
 constexpr int kDppRowMirror = 0x140;   // lane i <-> 15 - i within each 16
 
-// Max over the 16 lanes of a DPP row; every lane of the row gets it.
-__device__ __forceinline__ float row16_max(float v) {
-  v = __builtin_fmaxf(v, dpp<kDppXor1>(v));
-  v = __builtin_fmaxf(v, dpp<kDppXor2>(v));
-  v = __builtin_fmaxf(v, dpp<kDppHalfMirror>(v));
-  return __builtin_fmaxf(v, dpp<kDppRowMirror>(v));
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
+  return uint32_t(__builtin_amdgcn_update_dpp(0, int(x), CTRL, 0xF, 0xF, false));
 }
 
-// max |x| over 8 bf16 elements, NaN ignored (it never wins the max).
-__device__ __forceinline__ float amax8(u32x4 x) {
-  float m = 0.0f;
+// Max over the 16 lanes of a DPP row; every lane of the row gets it.  On the
+// bits of non-negative floats (no NaN), whose integer order is their order.
+__device__ __forceinline__ uint32_t row16_max_bits(uint32_t v) {
+  v = max(v, dpp_u32<kDppXor1>(v));
+  v = max(v, dpp_u32<kDppXor2>(v));
+  v = max(v, dpp_u32<kDppHalfMirror>(v));
+  return max(v, dpp_u32<kDppRowMirror>(v));
+}
+
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// max |x| over 8 bf16 elements as float32 bits, NaN ignored (it never wins
+// the max).  The magnitudes are 15-bit integers whose order is the order of
+// |x| up to +inf (0x7F80); NaNs sort above it.  Packed 16-bit maxima take two
+// elements per instruction, and only a lane whose maximum is a NaN pattern
+// takes the element-wise pass that skips NaNs.
+__device__ __forceinline__ uint32_t amax8_bits(u32x4 x) {
+  u16x2 m2 = {0, 0};
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float lo = __builtin_fabsf(__uint_as_float(x[i] << 16));
-    const float hi = __builtin_fabsf(__uint_as_float(x[i] & 0xFFFF0000u));
-    m = __builtin_isnan(lo) ? m : __builtin_fmaxf(m, lo);
-    m = __builtin_isnan(hi) ? m : __builtin_fmaxf(m, hi);
+  for (int i = 0; i < 4; ++i) m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(u16x2, x[i] & 0x7FFF7FFFu));
+  uint32_t m = m2[0] > m2[1] ? m2[0] : m2[1];
+  if (__builtin_expect(m > 0x7F80u, 0)) {
+    m = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t v = (x[i >> 1] >> (16 * (i & 1))) & 0x7FFFu;
+      m = (v <= 0x7F80u && v > m) ? v : m;
+    }
   }
-  return m;
+  return m << 16;
 }
 
 // s = max(amax / 448, 2^-126) with the correctly rounded quotient.  From 2^-90
@@ -133,10 +149,12 @@ __global__ void __launch_bounds__(kWaves * 64) tile_fp8_append_kernel(TileAppend
       if (active) x = vload_nt<16>(src + int64_t(e) * 2);
     }
     // every lane takes part in the row max (inactive rows reduce zeros)
-    const float s = tile_scale(row16_max(amax8(x)));
+    const float s = tile_scale(__uint_as_float(row16_max_bits(amax8_bits(x))));
     if (active) {
+      // on the fast path s is finite and at least amax / 448, so no element is
+      // infinite and no quotient overflows: the bounded division applies
       const QScale qs = make_qscale(s);
-      u32x2 q = QuantConv<PSK_DTYPE_BF16, 8>::apply(x, qs);
+      u32x2 q = QuantConv<PSK_DTYPE_BF16, 8, true>::apply(x, qs);
       if (__builtin_expect(__builtin_isinf(s), 0)) {
         // A tile holding an infinity has s = inf, and +-inf / inf is a NaN
         // whose sign the division does not define: store 0x7F with the sign

@@ -206,11 +206,16 @@ __device__ __forceinline__ QScale make_qscale_uniform(float s) {
   return q;
 }
 
-// Exact for s == 1.0 as well: r = 1, y = x, e = 0.
+// Exact for s == 1.0 as well: r = 1, y = x, e = 0.  BOUNDED: the caller
+// knows that y is finite or NaN (x is never infinite on this path and |x / s|
+// cannot overflow, as for a tile divided by its own amax / 448), so the
+// select that passes an infinite y through is left out.
+template <bool BOUNDED = false>
 __device__ __forceinline__ float div_fast(float x, const QScale& q) {
   const float y = x * q.r;
   const float e = __builtin_fmaf(-y, q.s, x);
   const float z = __builtin_copysignf(__builtin_fmaf(e, q.r, y), y);
+  if constexpr (BOUNDED) return z;  // a NaN y gives a NaN z with y's sign
   return __builtin_fabsf(y) < __builtin_inff() ? z : y;
 }
 
@@ -230,7 +235,7 @@ struct CopyConv {
 // The clamp is v_med3_f32 (exact for every non-NaN input, +-inf included);
 // the native convert turns NaN into 0xFF, so NaN lanes are patched to torch's
 // 0x7F|sign afterwards (rare path).
-template <int IN_DT, int E>
+template <int IN_DT, int E, bool BOUNDED = false>
 struct QuantConv {
   using EltT = Elt<IN_DT>;
   static constexpr int IN_B = E * EltT::kSize;
@@ -243,7 +248,7 @@ struct QuantConv {
     float f[E];
     if (__builtin_expect(qs.fast, 1)) {
 #pragma unroll
-      for (int i = 0; i < E; ++i) f[i] = div_fast(EltT::to_f32(e[i]), qs);
+      for (int i = 0; i < E; ++i) f[i] = div_fast<BOUNDED>(EltT::to_f32(e[i]), qs);
     } else {
       // scales outside [2^-80, 2^100) (0, inf, NaN, subnormal): IEEE division.
       // The empty volatile asm keeps this a branch: otherwise the compiler
