@@ -786,6 +786,8 @@ def run_attention_shapes(args, device):
         ("128 log-uniform 128-32768", 8, 4, [int(x) for x in np.exp(rng.uniform(np.log(128), np.log(32768), 128))]),
         ("64 uniform 1-4096", 8, 4, [int(x) for x in rng.integers(1, 4096, 64)]),
     ]
+    # group 8 (64 query heads over 8 kv heads, Llama-3-70B class) on two of them
+    shapes += [("128 log-uniform 128-32768, group 8", 8, 8, shapes[4][3]), ("32 x 8192, group 8", 8, 8, [8192] * 32)]
     reps = max(10, min(args.steps, 50))
     results = []
     for name, Hkv, G, lens in shapes:

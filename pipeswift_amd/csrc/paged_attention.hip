@@ -26,9 +26,14 @@
 //   * softmax runs in the exp2 domain with a lazily raised running maximum
 //     (raised only when a score exceeds it by 2^8), which keeps the rescaling of
 //     the accumulators off the per-tile path; normalisation is exact.
-//   * P V runs on the VALU in fp32: lane l owns tokens (l / 8) and (l / 8 + 8) of
-//     the tile and d = 16 * (l % 8) .. +16, loaded as one 16-byte vector per
-//     token; FP8 -> fp32 with the native pair convert.  V is never transposed.
+//   * P V: in the balanced schedules (the default) on the matrix cores, with
+//     S^T = K Q^T so that each lane holds one head's scores of four tokens (the
+//     P operand), V^T read from LDS by ds_read_b64_tr_b8, and P split into
+//     bf16 hi + lo (relative error 2^-17 per weight, fp32 sums); see "P V on
+//     the matrix cores" below.  In the split schedule and for block sizes that
+//     are not powers of two, on the VALU in fp32: lane l owns tokens (l / 8)
+//     and (l / 8 + 8) of the tile and d = 16 * (l % 8) .. +16, loaded as one
+//     16-byte vector per token; FP8 -> fp32 with the native pair convert.
 //   * flash-decoding split: a workgroup of 4 waves takes `split` tokens of one
 //     (sequence, kv head); its waves merge through LDS into one partial
 //     (max, sum, accumulator per query head) in the caller's workspace, and a
@@ -43,6 +48,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 #include <map>
 #include <mutex>
 
@@ -425,30 +431,12 @@ __device__ __forceinline__ void merge_lanes(Softmax<NG>& st) {
   }
 }
 
+// The LDS merge of a workgroup's kWaves per-wave states (s_acc, s_m, s_l) into
+// partial record rec_idx.
 template <int NG>
-__device__ __forceinline__ void write_partial(const DecodeArgs& a, Softmax<NG>& st, int64_t rec_idx, int lane,
-                                              int wave, float (*s_acc)[NG][kHead]) {
+__device__ __forceinline__ void merge_write(const DecodeArgs& a, int64_t rec_idx, float (*s_acc)[NG][kHead],
+                                            float (*s_m)[NG], float (*s_l)[NG]) {
   const int G = a.group;
-  constexpr bool REPL = NG <= 4;
-  merge_lanes<NG>(st);
-
-  // merge the waves through LDS and write this split's partial
-  __shared__ float s_m[kWaves][NG], s_l[kWaves][NG];
-  if (token_slot<REPL>(lane) == 0) {  // one lane per column chunk holds the merged state
-    const int c = column_chunk<REPL>(lane);
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-#pragma unroll
-      for (int k = 0; k < 16; ++k) s_acc[wave][g][16 * c + k] = st.acc[g][k];
-    }
-  }
-  if (lane == 0) {
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-      s_m[wave][g] = st.m[g];
-      s_l[wave][g] = st.l[g];
-    }
-  }
   __syncthreads();
   const int rec = G * (kHead + 2);
   float* part = a.part + rec_idx * rec;
@@ -473,6 +461,33 @@ __device__ __forceinline__ void write_partial(const DecodeArgs& a, Softmax<NG>& 
     part[g] = mx;
     part[G + g] = sum;
   }
+}
+
+template <int NG>
+__device__ __forceinline__ void write_partial(const DecodeArgs& a, Softmax<NG>& st, int64_t rec_idx, int lane,
+                                              int wave, float (*s_acc)[NG][kHead]) {
+  const int G = a.group;
+  constexpr bool REPL = NG <= 4;
+  merge_lanes<NG>(st);
+
+  // merge the waves through LDS and write this split's partial
+  __shared__ float s_m[kWaves][NG], s_l[kWaves][NG];
+  if (token_slot<REPL>(lane) == 0) {  // one lane per column chunk holds the merged state
+    const int c = column_chunk<REPL>(lane);
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) s_acc[wave][g][16 * c + k] = st.acc[g][k];
+    }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      s_m[wave][g] = st.m[g];
+      s_l[wave][g] = st.l[g];
+    }
+  }
+  merge_write<NG>(a, rec_idx, s_acc, s_m, s_l);
 }
 
 template <int NG, bool UNIFORM>
@@ -588,6 +603,197 @@ struct RingLdsT {
 };
 using RingLds = RingLdsT<kWaves>;
 
+// ---- P V on the matrix cores ----
+//
+// Q K^T is computed transposed, S^T = K Q^T (the same four MFMAs with the
+// operands swapped): lane l then holds the scores of query head g = l % 16 for
+// the four tokens 4 (l / 16) .. +3 of the tile, which is exactly the A operand
+// (row g, k = those four tokens) of v_mfma_f32_16x16x16_bf16 for P V.  The B
+// operand, V^T (column d, the same four tokens), comes from the ring slot by
+// ds_read_b64_tr_b8: in each 16-lane group, result lane i's byte j is byte
+// i & 7 of the 8-byte row that source lane 2 j + (i >> 3) addressed.  Source
+// lane r of group s addresses token 4 s + ((r >> 1) & 3), bytes 8 (r & 1) ..
+// +8 of a 16-byte column chunk, the chunk of block 2 k for r < 8 and of block
+// 2 k + 1 otherwise; so one read gives lane l the four tokens of column
+// 16 b + l % 16 for two column blocks b (its low and high dword).  P is split
+// into bf16 hi + lo (p - hi is exact in fp32 and rounds to bf16 again), so the
+// products carry ~16 significant bits of p and the sums are fp32: the same
+// accuracy class as fp32 FMAs, with the FMAs off the VALU.  Each lane keeps
+// one head's running max and its share of the sum; the MFMA accumulates O
+// over all of the wave's tokens, so no lane merge is needed for O.
+struct SoftmaxM {
+  float m, mth, l;  // head lane % 16: running max (exp2 domain), lazy threshold, this lane's part of the sum
+  f32x4 o[8];       // O[4 (lane / 16) + r][16 b + lane % 16] = o[b][r]
+};
+
+__device__ __forceinline__ void softmax_init(SoftmaxM& st) {
+  st.m = kNegBig;
+  st.mth = kNegBig + kLazy;
+  st.l = 0.0f;
+#pragma unroll
+  for (int b = 0; b < 8; ++b) st.o[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+}
+
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+// Byte offsets (from a ring slot) of this lane's four transposed-read rows:
+// V token 4 s + ((r >> 1) & 3), chunk 2 k (r < 8) or 2 k + 1, half r & 1,
+// with the slot's XOR swizzle (chunk c of token t at 16 (c ^ (t & 7))).
+__device__ __forceinline__ void pv_offsets(int lane, uint32_t (&off)[4]) {
+  const int r = lane & 15, s = lane >> 4;
+  const int tok = 4 * s + ((r >> 1) & 3);
+  const uint32_t row = uint32_t(2048 + 1024 * (tok >> 3) + 128 * (tok & 7) + 8 * (r & 1));
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int c = 2 * k + (r >= 8 ? 1 : 0);
+    off[k] = row + uint32_t(16 * (c ^ (tok & 7)));
+  }
+}
+
+// K (as ring_read) and the eight V^T operand words of a slot, read
+// synchronously in one asm block (see ring_read for why).
+__device__ __forceinline__ void ring_read_pv(uint32_t slot, uint32_t rk0, uint32_t rk1, const uint32_t (&off)[4],
+                                             u32x4& k0, u32x4& k1, uint32_t (&vw)[8]) {
+  i32x2 t0, t1, t2, t3;
+  asm volatile(
+      "ds_read_b128 %0, %6\n"
+      "ds_read_b128 %1, %7\n"
+      "ds_read_b64_tr_b8 %2, %8\n"
+      "ds_read_b64_tr_b8 %3, %9\n"
+      "ds_read_b64_tr_b8 %4, %10\n"
+      "ds_read_b64_tr_b8 %5, %11\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(k0), "=&v"(k1), "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3)
+      : "v"(slot + rk0), "v"(slot + rk1), "v"(slot + off[0]), "v"(slot + off[1]), "v"(slot + off[2]),
+        "v"(slot + off[3])
+      : "memory");
+  vw[0] = uint32_t(t0[0]);
+  vw[1] = uint32_t(t0[1]);
+  vw[2] = uint32_t(t1[0]);
+  vw[3] = uint32_t(t1[1]);
+  vw[4] = uint32_t(t2[0]);
+  vw[5] = uint32_t(t2[1]);
+  vw[6] = uint32_t(t3[0]);
+  vw[7] = uint32_t(t3[1]);
+}
+
+// One 16-token tile of one wave on the matrix cores.  vw: V^T words (byte j =
+// token 4 (lane / 16) + j of column 16 b + lane % 16), zero for a missing page;
+// G query heads of the group are rows 0 .. G-1.
+template <bool PARTIAL, class Consumed>
+__device__ __forceinline__ void attend_step_pv(SoftmaxM& st, const u32x4& k0, const u32x4& k1,
+                                               const uint32_t (&vw)[8], const bf16x8 qop[4], float sl, int t0,
+                                               int t_end, int G, int lane, const Consumed& consumed) {
+  f32x4 sc = {0.0f, 0.0f, 0.0f, 0.0f};
+  sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(e4m3x8_to_bf16(k0[0], k0[1]), qop[0], sc, 0, 0, 0);
+  sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(e4m3x8_to_bf16(k0[2], k0[3]), qop[1], sc, 0, 0, 0);
+  sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(e4m3x8_to_bf16(k1[0], k1[1]), qop[2], sc, 0, 0, 0);
+  sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(e4m3x8_to_bf16(k1[2], k1[3]), qop[3], sc, 0, 0, 0);
+  consumed();
+
+  const int g = lane & 15, tq = 4 * (lane >> 4);
+  float s4[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const bool ok = g < G && (!PARTIAL || t0 + tq + r < t_end);
+    s4[r] = ok ? sc[r] * sl : -__builtin_inff();
+  }
+  float mx = __builtin_fmaxf(__builtin_fmaxf(s4[0], s4[1]), __builtin_fmaxf(s4[2], s4[3]));
+  mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16));
+  mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32));  // head g's tile max, in its four lanes
+  if (__any(mx > st.mth)) {
+    const float mn = __builtin_fmaxf(st.m, mx);
+    const float c = __builtin_amdgcn_exp2f(st.m - mn);
+    st.l *= c;
+    st.m = mn;
+    st.mth = mn + kLazy;
+    // O row 4 (lane / 16) + r takes its head's factor from that head's lane
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float cr = bperm(tq + r, c);
+#pragma unroll
+      for (int b = 0; b < 8; ++b) st.o[b][r] *= cr;
+    }
+  }
+  float p[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(s4[r] - st.m);
+  st.l += (p[0] + p[1]) + (p[2] + p[3]);
+  const bf16x4 hi = {(__bf16)p[0], (__bf16)p[1], (__bf16)p[2], (__bf16)p[3]};
+  const bf16x4 lo = {(__bf16)(p[0] - (float)hi[0]), (__bf16)(p[1] - (float)hi[1]), (__bf16)(p[2] - (float)hi[2]),
+                     (__bf16)(p[3] - (float)hi[3])};
+  uint32_t vmask = 0xFFFFFFFFu;
+  if constexpr (PARTIAL) {
+    // tokens at or past t_end may hold anything (a NaN would survive p = 0)
+    const int n_ok = t_end - (t0 + tq);
+    vmask = n_ok >= 4 ? 0xFFFFFFFFu : n_ok <= 0 ? 0u : (0xFFFFFFFFu >> (32 - 8 * n_ok));
+  }
+#pragma unroll
+  for (int b = 0; b < 8; ++b) {
+    const uint32_t w = vw[b] & vmask;
+    const bf16x2 v01 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false);
+    const bf16x2 v23 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true);
+    const bf16x4 vb = {v01[0], v01[1], v23[0], v23[1]};
+    st.o[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, hi), __builtin_bit_cast(s16x4, vb),
+                                                        st.o[b], 0, 0, 0);
+    st.o[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, lo), __builtin_bit_cast(s16x4, vb),
+                                                        st.o[b], 0, 0, 0);
+  }
+}
+
+// The wave's record of a P V-on-MFMA state: head g's sum over its four lanes,
+// then either stored directly (record at `part`) or stashed in LDS for a
+// cross-wave merge.
+__device__ __forceinline__ void finish_sum(SoftmaxM& st) {
+  st.l += __shfl_xor(st.l, 16);
+  st.l += __shfl_xor(st.l, 32);
+}
+
+__device__ __forceinline__ void write_record_pv(const SoftmaxM& st, float* part, int G, int lane) {
+  const int g = lane & 15, q = lane >> 4;
+  if (q == 0 && g < G) {
+    part[g] = st.m;
+    part[G + g] = st.l;
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int gr = 4 * q + r;
+    if (gr < G) {
+#pragma unroll
+      for (int b = 0; b < 8; ++b) part[2 * G + gr * kHead + 16 * b + g] = st.o[b][r];
+    }
+  }
+}
+
+template <int NG>
+__device__ __forceinline__ void stash_pv(const SoftmaxM& st, float (*s_acc)[NG][kHead], float (*s_m)[NG],
+                                         float (*s_l)[NG], int wave, int lane) {
+  const int g = lane & 15, q = lane >> 4;
+  if (q == 0 && g < NG) {
+    s_m[wave][g] = st.m;
+    s_l[wave][g] = st.l;
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int gr = 4 * q + r;
+    if (gr < NG) {
+#pragma unroll
+      for (int b = 0; b < 8; ++b) s_acc[wave][gr][16 * b + g] = st.o[b][r];
+    }
+  }
+}
+
+template <int NG>
+__device__ __forceinline__ void write_partial(const DecodeArgs& a, SoftmaxM& st, int64_t rec_idx, int lane, int wave,
+                                              float (*s_acc)[NG][kHead]) {
+  finish_sum(st);
+  __shared__ float s_m[kWaves][NG], s_l[kWaves][NG];
+  stash_pv<NG>(st, s_acc, s_m, s_l, wave, lane);
+  merge_write<NG>(a, rec_idx, s_acc, s_m, s_l);
+}
+
 // s_waitcnt vmcnt(n) for a run-time n < 16 (the immediate must be a constant)
 __device__ __forceinline__ void wait_vmcnt(int n) {
   switch (n) {
@@ -605,8 +811,8 @@ __device__ __forceinline__ void wait_vmcnt(int n) {
 // heads may differ): it stages the range's page ids behind a barrier.
 // `overlap` runs while the page-id loads are in flight (a new head's query
 // loads go there, so that both cost one memory latency).
-template <int NG, int W, int P, int R, class Overlap>
-__device__ __forceinline__ void ring_attend(const DecodeArgs& a, Softmax<NG>& st, const bf16x8 (&qop)[4],
+template <int NG, int W, int P, int R, class ST, class Overlap>
+__device__ __forceinline__ void ring_attend(const DecodeArgs& a, ST& st, const bf16x8 (&qop)[4],
                                             const float& sl, int b, int h, int t_begin, int t_end, int lane,
                                             int wave, int phase, RingLdsT<W, R>& lds, const Overlap& overlap) {
   static_assert(R >= 2 && R <= 4, "ring of 2 to 4 tiles per wave");
@@ -675,16 +881,50 @@ __device__ __forceinline__ void ring_attend(const DecodeArgs& a, Softmax<NG>& st
     return c;
   };
   for (int j = 0; j < R && j < n_tiles; ++j) issue(j);
-  if (n_tiles > 0) {
-    int j = 0;
-    for (; j + 1 < n_tiles; ++j) {
-      TileLoads c = fetch(j);
-      attend_step<NG, false>(st, c, qop, sl, t_first + j * stride, t_end, lane, [&] {
-        if (j + R < n_tiles) issue(j + R);
-      });
+  if constexpr (std::is_same_v<ST, SoftmaxM>) {
+    uint32_t off[4];
+    pv_offsets(lane, off);
+    const int G = a.group;
+    struct PvTile {
+      u32x4 k0, k1;
+      uint32_t vw[8];
+    };
+    auto fetch_pv = [&](int j) {
+      if (j + R - 1 < n_tiles) __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 * (R - 1)));
+      else wait_vmcnt(4 * (n_tiles - 1 - j));
+      const int slot = j % R;
+      PvTile c;
+      ring_read_pv((uint32_t)(size_t)(lvoid*)&ring[slot][0][0], rk0, rk1, off, c.k0, c.k1, c.vw);
+      if (!((valid >> slot) & 1u)) {
+        c.k0 = c.k1 = u32x4(0);
+#pragma unroll
+        for (int b = 0; b < 8; ++b) c.vw[b] = 0u;
+      }
+      return c;
+    };
+    if (n_tiles > 0) {
+      int j = 0;
+      for (; j + 1 < n_tiles; ++j) {
+        PvTile c = fetch_pv(j);
+        attend_step_pv<false>(st, c.k0, c.k1, c.vw, qop, sl, t_first + j * stride, t_end, G, lane, [&] {
+          if (j + R < n_tiles) issue(j + R);
+        });
+      }
+      PvTile c = fetch_pv(j);
+      attend_step_pv<true>(st, c.k0, c.k1, c.vw, qop, sl, t_first + j * stride, t_end, G, lane, [] {});
     }
-    TileLoads c = fetch(j);
-    attend_step<NG, true>(st, c, qop, sl, t_first + j * stride, t_end, lane, [] {});
+  } else {
+    if (n_tiles > 0) {
+      int j = 0;
+      for (; j + 1 < n_tiles; ++j) {
+        TileLoads c = fetch(j);
+        attend_step<NG, false>(st, c, qop, sl, t_first + j * stride, t_end, lane, [&] {
+          if (j + R < n_tiles) issue(j + R);
+        });
+      }
+      TileLoads c = fetch(j);
+      attend_step<NG, true>(st, c, qop, sl, t_first + j * stride, t_end, lane, [] {});
+    }
   }
 }
 
@@ -700,13 +940,15 @@ __device__ __forceinline__ void softmax_init(Softmax<NG>& st) {
   }
 }
 
-// Query operands and the score scale of (sequence b, kv head h).
-template <int NG>
+// Query operands and the score scale of (sequence b, kv head h).  REPL: rows
+// replicated in the four row quarters (the VALU P V path for groups of at
+// most 4 heads); otherwise row i is query head i.
+template <int NG, bool REPL = (NG <= 4)>
 __device__ __forceinline__ float load_head(const DecodeArgs& a, int q_dtype, int b, int h, int lane, bf16x8 qop[4]) {
   const float qd = descale(a.qd, a.qd_b, a.qd_h, b, h);
   const float kd = descale(a.kd, a.kd_b, a.kd_h, b, h);
   uint32_t qw[8];
-  load_query<(NG <= 4)>(a, q_dtype, b, h, qd, lane, qw);
+  load_query<REPL>(a, q_dtype, b, h, qd, lane, qw);
   qop[0] = e4m3x8_to_bf16(qw[0], qw[1]);
   qop[1] = e4m3x8_to_bf16(qw[2], qw[3]);
   qop[2] = e4m3x8_to_bf16(qw[4], qw[5]);
@@ -822,6 +1064,15 @@ __device__ __forceinline__ void seek_unit(const int32_t* pref, int num_seqs, int
   t = int(u - pref[b]) - seq_units;
 }
 
+// P V on the matrix cores in the balanced schedules' kernels (the VALU path
+// stays for the split schedule and non-power-of-two block sizes).
+#ifndef PSK_PV_MFMA
+#define PSK_PV_MFMA 1
+#endif
+constexpr bool kPvMfma = PSK_PV_MFMA != 0;
+template <int NG>
+using BalancedState = std::conditional_t<kPvMfma, SoftmaxM, Softmax<NG>>;
+
 template <int NG>
 __global__ void __launch_bounds__(kWaves * 64) decode_partial_stream_kernel(DecodeArgs a, int q_dtype, int num_seqs) {
   const int w = blockIdx.x;
@@ -861,13 +1112,13 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_stream_kernel(Deco
     const int n = int(min<int64_t>(tb - t, u_end - u));
     bf16x8 qop[4];
     float sl = 0.0f;
-    Softmax<NG> st;
+    BalancedState<NG> st;
     softmax_init(st);
     const int t_end = min(len, (t + n) * kTile);
     for (int t0 = t * kTile; t0 < t_end; t0 += piece) {
       const bool head = t0 == t * kTile;
       ring_attend<NG, kWaves, kWaves, kRing>(a, st, qop, sl, b, h, t0, min(t_end, t0 + piece), lane, wave, wave, lds, [&] {
-        if (head) sl = load_head<NG>(a, q_dtype, b, h, lane, qop);
+        if (head) sl = load_head<NG, !kPvMfma && (NG <= 4)>(a, q_dtype, b, h, lane, qop);
       });
     }
     __syncthreads();  // every wave is done with the ring: it becomes the merge buffer
@@ -897,6 +1148,7 @@ constexpr int kHeadWaves = 8;
 // LDS tile slots per wave.  At one workgroup per CU deeper rings cost no
 // occupancy, but measured slower on config 2: 250 us at three, 252 at four.
 constexpr int kHeadRing = 2;
+
 
 // Merge this wave's token slots and, with P phases per head, the P waves of
 // each head through LDS; write head h's partial record rec_idx.
@@ -971,6 +1223,44 @@ __device__ __forceinline__ void write_partial_heads(const DecodeArgs& a, Softmax
   }
 }
 
+template <int NG, int HG, int P>
+__device__ __forceinline__ void write_partial_heads(const DecodeArgs& a, SoftmaxM& st, int64_t rec_idx, int lane,
+                                                    int wave, float (*s_acc)[NG][kHead], float (*s_m)[NG],
+                                                    float (*s_l)[NG]) {
+  const int G = a.group;
+  finish_sum(st);
+  float* part = a.part + rec_idx * (G * (kHead + 2));
+  if constexpr (P == 1) {
+    write_record_pv(st, part, G, lane);
+  } else {
+    stash_pv<NG>(st, s_acc, s_m, s_l, wave, lane);
+    __syncthreads();
+    if (wave < HG) {  // phase 0 of head `wave` writes the merged record
+      for (int i = lane; i < G * kHead; i += 64) {
+        const int g = i / kHead, d = i % kHead;
+        float mx = s_m[wave][g];
+#pragma unroll
+        for (int p = 1; p < P; ++p) mx = __builtin_fmaxf(mx, s_m[wave + HG * p][g]);
+        float v = 0.0f;
+#pragma unroll
+        for (int p = 0; p < P; ++p) v += s_acc[wave + HG * p][g][d] * __builtin_amdgcn_exp2f(s_m[wave + HG * p][g] - mx);
+        part[2 * G + i] = v;
+      }
+      if (lane < G) {
+        const int g = lane;
+        float mx = s_m[wave][g];
+#pragma unroll
+        for (int p = 1; p < P; ++p) mx = __builtin_fmaxf(mx, s_m[wave + HG * p][g]);
+        float sum = 0.0f;
+#pragma unroll
+        for (int p = 0; p < P; ++p) sum += s_l[wave + HG * p][g] * __builtin_amdgcn_exp2f(s_m[wave + HG * p][g] - mx);
+        part[g] = mx;
+        part[G + g] = sum;
+      }
+    }
+  }
+}
+
 template <int NG, int HG>
 __global__ void __launch_bounds__(kHeadWaves * 64) decode_partial_heads_kernel(DecodeArgs a, int q_dtype,
                                                                               int num_seqs) {
@@ -1012,13 +1302,13 @@ __global__ void __launch_bounds__(kHeadWaves * 64) decode_partial_heads_kernel(D
     const int n = int(min<int64_t>(tb - t, u_end - u));
     bf16x8 qop[4];
     float sl = 0.0f;
-    Softmax<NG> st;
+    BalancedState<NG> st;
     softmax_init(st);
     const int t_end = min(len, (t + n) * kTile);
     for (int t0 = t * kTile; t0 < t_end; t0 += piece) {
       const bool head = t0 == t * kTile;
       ring_attend<NG, W, P, kHeadRing>(a, st, qop, sl, b, h, t0, min(t_end, t0 + piece), lane, wave, phase, lds, [&] {
-        if (head) sl = load_head<NG>(a, q_dtype, b, h, lane, qop);
+        if (head) sl = load_head<NG, !kPvMfma && (NG <= 4)>(a, q_dtype, b, h, lane, qop);
       });
     }
     if constexpr (P > 1) __syncthreads();  // every wave is done with the ring: it becomes the merge buffer
