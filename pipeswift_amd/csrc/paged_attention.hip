@@ -26,12 +26,12 @@
 //   * softmax runs in the exp2 domain with a lazily raised running maximum
 //     (raised only when a score exceeds it by 2^8), which keeps the rescaling of
 //     the accumulators off the per-tile path; normalisation is exact.
-//   * P V: in the balanced schedules (the default) on the matrix cores, with
-//     S^T = K Q^T so that each lane holds one head's scores of four tokens (the
-//     P operand), V^T read from LDS by ds_read_b64_tr_b8, and P split into
-//     bf16 hi + lo (relative error 2^-17 per weight, fp32 sums); see "P V on
-//     the matrix cores" below.  In the split schedule and for block sizes that
-//     are not powers of two, on the VALU in fp32: lane l owns tokens (l / 8)
+//   * P V: for power-of-two block sizes >= 16 (every ring-based kernel) on the
+//     matrix cores, with S^T = K Q^T so that each lane holds one head's scores
+//     of four tokens (the P operand), V^T read from LDS by ds_read_b64_tr_b8,
+//     and P split into bf16 hi + lo (relative error 2^-17 per weight, fp32
+//     sums); see "P V on the matrix cores" below.  For other block sizes
+//     (decode_partial_kernel), on the VALU in fp32: lane l owns tokens (l / 8)
 //     and (l / 8 + 8) of the tile and d = 16 * (l % 8) .. +16, loaded as one
 //     16-byte vector per token; FP8 -> fp32 with the native pair convert.
 //   * flash-decoding split: a workgroup of 4 waves takes `split` tokens of one
@@ -956,6 +956,15 @@ __device__ __forceinline__ float load_head(const DecodeArgs& a, int q_dtype, int
   return a.scale_log2 * qd * kd;
 }
 
+// P V on the matrix cores in the kernels built on ring_attend (the VALU path
+// stays for block sizes that are not powers of two, decode_partial_kernel).
+#ifndef PSK_PV_MFMA
+#define PSK_PV_MFMA 1
+#endif
+constexpr bool kPvMfma = PSK_PV_MFMA != 0;
+template <int NG>
+using BalancedState = std::conditional_t<kPvMfma, SoftmaxM, Softmax<NG>>;
+
 // One workgroup per (split, kv head, sequence) (an explicit num_splits).
 template <int NG>
 __global__ void __launch_bounds__(kWaves * 64) decode_partial_ring_kernel(DecodeArgs a, int q_dtype) {
@@ -974,11 +983,11 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_ring_kernel(Decode
   static_assert(sizeof(lds.ring) >= sizeof(float) * kWaves * NG * kHead, "the ring doubles as the merge buffer");
   bf16x8 qop[4];
   float sl = 0.0f;
-  Softmax<NG> st;
+  BalancedState<NG> st;
   softmax_init(st);
   // the host keeps a split within kRingPages pages
   ring_attend<NG, kWaves, kWaves, kRing>(a, st, qop, sl, b, h, t_begin, t_end, lane, wave, wave, lds,
-                                  [&] { sl = load_head<NG>(a, q_dtype, b, h, lane, qop); });
+                                  [&] { sl = load_head<NG, !kPvMfma && (NG <= 4)>(a, q_dtype, b, h, lane, qop); });
   __syncthreads();  // every wave is done with the ring: it becomes the merge buffer
   write_partial<NG>(a, st, (int64_t(b) * a.num_kv_heads + h) * a.max_splits + s, lane, wave,
                     reinterpret_cast<float(*)[NG][kHead]>(&lds.ring[0][0][0][0]));
@@ -1063,15 +1072,6 @@ __device__ __forceinline__ void seek_unit(const int32_t* pref, int num_seqs, int
   b = lo;
   t = int(u - pref[b]) - seq_units;
 }
-
-// P V on the matrix cores in the balanced schedules' kernels (the VALU path
-// stays for the split schedule and non-power-of-two block sizes).
-#ifndef PSK_PV_MFMA
-#define PSK_PV_MFMA 1
-#endif
-constexpr bool kPvMfma = PSK_PV_MFMA != 0;
-template <int NG>
-using BalancedState = std::conditional_t<kPvMfma, SoftmaxM, Softmax<NG>>;
 
 template <int NG>
 __global__ void __launch_bounds__(kWaves * 64) decode_partial_stream_kernel(DecodeArgs a, int q_dtype, int num_seqs) {

@@ -3,7 +3,7 @@ over the FP8 cache.
 
 Tolerances (floating point).  The products q~ k are exact (bf16 MFMA over
 exactly converted FP8 values), and each 128-term score is summed in fp32.
-P V (balanced schedules) multiplies V, exact in bf16, by p split into bf16
+P V (power-of-two pages) multiplies V, exact in bf16, by p split into bf16
 hi + lo, which carries p to a relative 2^-17 -- far inside the bounds below,
 as are the fp32 sums of either P V path:
 |ds| <~ 128 * 2^-24 * sum|q~ k| * scale * qd * kd, about 1e-4 at these
