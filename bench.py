@@ -185,7 +185,7 @@ def setup_decode_attention(args, device):
     nbytes = total * H * D * 2 + pages * 4 + 2 * B * Hq * D * 2
     info = {
         "name": "decode_attention",
-        # the head-parallel balanced schedule from 8 sequences up, the split schedule for an explicit count
+        # the head-parallel balanced schedule from 2 sequences up, the split schedule for an explicit count
         "kernel": "decode_partial_heads_kernel" if args.num_splits == 0 else "decode_partial_ring_kernel",
         "bytes": nbytes, "tokens": B,
         "dtype": "fp8_e4m3fn",

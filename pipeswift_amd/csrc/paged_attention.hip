@@ -1577,12 +1577,14 @@ int64_t stream_runs(int ng, int64_t num_kv_heads) {
   return slots > 0 ? std::max<int64_t>(1, slots / num_kv_heads) : 0;
 }
 
-// The head-parallel schedule from kHeadsMinSeqs sequences up; below that the
-// per-head schedule, whose 4-wave workgroups put twice the waves on a single
-// long sequence (measured: 1 x 32768 tokens 29.9 us per-head against 43.4;
-// from 8 sequences up the head-parallel one is level or faster, config 2's
-// 128 sequences 244 us against 266).
-constexpr int64_t kHeadsMinSeqs = 8;
+// The head-parallel schedule from kHeadsMinSeqs sequences up; a single
+// sequence takes the per-head schedule, whose 4-wave workgroups put more waves
+// on it.  Measured with P V on the matrix cores: from 2 sequences the
+// head-parallel schedule is faster (2 x 32768 tokens 32.8 us against 35.1,
+// 4 x 16384 32.5 against 34.8, 7 mixed 27.5 against 30.8, 3 skewed 45.5
+// against 52.4; 6 x 2048 at group 8 20.9 against 19.3), config 2's 128
+// sequences 223 us against 266 before it.
+constexpr int64_t kHeadsMinSeqs = 2;
 
 // Units that stand for the fixed cost of starting a sequence in a run (see
 // units_of), per schedule.
