@@ -290,3 +290,25 @@ def test_single_long_sequence_combine_waves(dev, Hq, Hkv, length):
     head (up to 1024 threads for groups of 8)."""
     P = -(-length // 16) + 8
     _case(dev, 61 + Hkv, 1, Hq, Hkv, 16, P, [length], "bf16", torch.float32, "per_seq_head")
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_decode_attention_random_shapes(dev, seed):
+    """Seeded random batches for the matrix-core P V path: group sizes 1-8,
+    power-of-two pages 16-64 (the ring kernels), 1-40 sequences (per-head and
+    head-parallel schedules, and the split schedule on every third case),
+    lengths 0-3000 with ragged last tiles, fp8 and bf16 queries, descales."""
+    rng = np.random.default_rng(1000 + seed)
+    G = int(rng.integers(1, 9))
+    Hkv = int(rng.choice([1, 2, 4, 8]))
+    ps = int(rng.choice([16, 32, 64]))
+    B = int(rng.choice([1, 2, 3, 7, 8, 13, 40]))
+    lens = rng.integers(0, 3000, B).tolist()
+    lens[int(rng.integers(0, B))] = int(rng.integers(1, 3000))  # at least one non-empty sequence
+    P = max(64, sum(-(-x // ps) for x in lens) + 8)
+    q_dtype = "fp8" if seed % 2 else "bf16"
+    out_dtype = torch.float32 if seed % 4 < 2 else torch.bfloat16
+    descales = [None, "scalar", "per_seq_head"][seed % 3]
+    num_splits = 0 if seed % 3 else int(rng.integers(1, 24))
+    print(f"random {seed}: G={G} Hkv={Hkv} ps={ps} B={B} splits={num_splits} {q_dtype}", flush=True)
+    _case(dev, 2000 + seed, B, G * Hkv, Hkv, ps, P, lens, q_dtype, out_dtype, descales, num_splits=num_splits)
