@@ -3,17 +3,36 @@
     python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline]
 
 A step is one launch of the hot-path kernel over one batch of synthetic input
-(one decode step's K/V append for one layer, by default).  Launches are
-replayed from a HIP graph of G back-to-back launches, each over a different
-rotation set of inputs and slot mappings, as the reference replays its decode
-step from a CUDA graph (llm.py:634-681); the rotation keeps the working set far
-above the 256 MB Infinity Cache.  Inputs are resident in HBM before timing.
-HIP events on the launch stream bracket exactly K steps after W warmup steps.
+(one decode step's K/V append for one layer, by default).  Exactly K launches
+are timed after W untimed ones: they are replayed from HIP graphs of G
+launches (G = min(--graph, K, rotation sets)) plus one tail graph of K mod G
+launches, each launch over a different rotation set of inputs and slot
+mappings, as the reference replays its decode step from a CUDA graph
+(llm.py:634-681); the rotation keeps the working set far above the 256 MB
+Infinity Cache.  Inputs are resident in HBM before timing.  HIP events on the
+launch stream bracket the K launches, behind a bounded spin kernel so that
+host submission stays outside the timed region.
 
-The JSON line carries:
+The default run reports config 2 (the FP8 decode append) as the headline and
+every other benchmark configuration under `secondary`, each a bounded run of
+its own timed the same way (its own step count), with its own roofline and
+torch CPU baseline:
+  fp8_decode_write   config 2 with the scales recomputed each step (amax + append)
+  kv_scales          config 2's per-tensor K/V scales alone (amax kernels)
+  bf16_append        config 1: 512 tokens of Llama-3-8B K/V (8x128), 4096 blocks
+  chunked_append     config 3: 4096 tokens of Qwen3 K/V (4x128), 32768 blocks
+  gather             config 3: the 6 sequences (prefix + chunk) to rows
+  mla_prefill / mla_decode, mla_prefill_fp8 / mla_decode_fp8
+                     config 4: kv_c 512 + k_pe 64, block 64, 20000 blocks, bf16
+                     or per-tensor FP8
+  copy_blocks        config 5a: 2048 pairs over 61 layers of [8192, 2, 16, 8, 128]
+  decode_attention   one decode step of FP8 paged attention over config 2's cache
+  swap               config 5b: 8192 scattered blocks x 8 layers (4 GiB) D2H + H2D
+
+Each result carries:
   value            algorithmic HBM GB/s (bytes the kernel must move / time)
-  roofline         the same per launch against MI355X's 8 TB/s peak, plus the
-                   HBM traffic measured with rocprofv3 PMC counters (committed
+  roofline         the same per launch against MI355X's 8 TB/s peak, the HBM
+                   traffic measured with rocprofv3 PMC counters (committed
                    under profiles/), when present, and the fraction of the
                    best device copy measured on this box in the same run
                    (`achievable`, copy_blocks_kernel over 1 GiB)
@@ -22,25 +41,15 @@ The JSON line carries:
                    the same way (vs_launch > 1: the kernel beats that copy)
   wall_us_per_call_eager  host wall time per eager Python call (no graph)
   cpu_baseline     the numpy oracle timed on this host on a bounded sample
-  cpu_torch        the reference's CPU path (torch index_put_ / index_select on
-                   host tensors of the same layout) on all host threads and on
-                   one, for the appends and the gather
+                   (headline only)
+  cpu_torch        the reference's CPU path (torch index_put_ / index_select /
+                   amax on host tensors of the same layout) on all host threads
+                   and on one
 
-Workloads (default fp8_decode_append, config 2 of the benchmark plan):
-  fp8_decode_append  128 seqs x 1 token, 8x128 bf16 -> E4M3FN, 65536 blocks
-  bf16_append        512 tokens of Llama-3-8B K/V (8x128), 4096 blocks
-  chunked_append     4096 tokens of Qwen3 K/V (4x128), 32768 blocks
-  gather             the chunked case's 6 sequences (prefix + chunk) to rows
-  mla_prefill / mla_decode   kv_c 512 + k_pe 64, block 64, 20000 blocks
-  mla_fp8_tiles_prefill / mla_fp8_tiles_decode   the same into 656-byte FP8
+Other workloads (--workload NAME runs one alone): any name above, and
+  mla_fp8_tiles_prefill / mla_fp8_tiles_decode   config 4 into 656-byte FP8
                      entries with one scale per 128-element tile
-  copy_blocks        2048 pairs over 61 layers of [8192, 2, 16, 8, 128] bf16
-  swap               8192 scattered blocks x 8 layers (4 GiB) D2H + H2D
-  kv_scales          config 2's per-tensor K/V scales (amax kernel)
-  decode_attention   one decode step of FP8 paged attention over config 2's
-                     cache (128 sequences, 8 kv heads, 32 query heads)
-  attention_shapes   decode attention on six batch shapes, balanced vs split
-                     schedule
+  attention_shapes   decode attention on several batch shapes, balanced vs split
   l2_cycle           BlockManager store -> evict -> restore of an 8192-page prompt
   swap_sweep         host-link GB/s vs bytes per page, per transport
   metadata           host us per step of prepare_kv_info (native builder)
@@ -63,6 +72,9 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0
+SPIN_CYCLES = 2_000_000  # shader clocks of the pre-timing spin (~1 ms at 2.4 GHz)
+STEADY_STEPS = 2048  # launches per graph for the steady per-launch figure of the us workloads
+QUEUED_MAX = 256  # longest run timed by the queued method (the rest: one graph replay)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
 
@@ -91,10 +103,15 @@ def _affine_block_maps(R, num_blocks, gen, device):
     return a.to(device), c.to(device)
 
 
-def setup_append(args, device, fp8):
+def setup_append(args, device, fp8, rescale=False):
+    """Config 1 (bf16) or config 2 (FP8 decode) append.  With ``rescale`` a
+    step is the whole FP8 write of a caller that recomputes its per-tensor
+    scales every step: amax -> scale of K and V (two launches), then the fused
+    append (one launch); its bytes add the amax read of K and V."""
     import torch
 
-    from pipeswift_amd import cache_ops, workloads
+    import workloads
+    from pipeswift_amd import cache_ops
     from pipeswift_amd.reshape_and_cache import reshape_and_cache_flash
 
     case = workloads.config2_fp8_decode() if fp8 else workloads.config1_append()
@@ -115,32 +132,47 @@ def setup_append(args, device, fp8):
     slots[0].copy_(base)
     cache = case.cache.to(device)
     k_scale = v_scale = None
+    scales = torch.ones(2, dtype=torch.float32, device=device)
     if fp8:
-        scales = cache_ops.compute_kv_scales(case.key(qkv[0]), case.value(qkv[0]))
+        cache_ops.warmup(device)
+        cache_ops.compute_kv_scales(case.key(qkv[0]), case.value(qkv[0]), out=scales)
         k_scale, v_scale = scales[0:1], scales[1:2]
     kc, vc = cache[:, 0], cache[:, 1]
 
-    def launch(i):
-        q = qkv[i]
-        reshape_and_cache_flash(case.key(q), case.value(q), kc, vc, slots[i], k_scale, v_scale)
+    if rescale:
+        def launch(i):
+            q = qkv[i]
+            cache_ops.compute_kv_scales(case.key(q), case.value(q), out=scales)
+            reshape_and_cache_flash(case.key(q), case.value(q), kc, vc, slots[i], k_scale, v_scale)
+    else:
+        def launch(i):
+            q = qkv[i]
+            reshape_and_cache_flash(case.key(q), case.value(q), kc, vc, slots[i], k_scale, v_scale)
 
     nbytes = workloads.append_bytes(case.num_valid, N, case.num_heads, case.head_size, 2, 1 if fp8 else 2)
+    amax_bytes = 2 * N * case.num_heads * case.head_size * 2
+    name = "fp8_decode_write" if rescale else ("fp8_decode_append" if fp8 else "bf16_append")
     info = {
-        "name": "fp8_decode_append" if fp8 else "bf16_append",
-        "kernel": "paged_append_small_kernel",  # the launch for batches under 1024 tokens
-        "bytes": nbytes,
+        "name": name,
+        "kernel": ("amax_partial_kernel + amax_finalize_kernel + paged_append_small_kernel" if rescale
+                   else "paged_append_small_kernel"),  # the launch for batches under 1024 tokens
+        "bytes": nbytes + (amax_bytes if rescale else 0),
         "tokens": case.num_valid,
         "dtype": "fp8_e4m3fn" if fp8 else "bf16",
         "config": {
-            "workload": "fp8_decode_append (config 2)" if fp8 else "bf16_append (config 1)",
+            "workload": ("fp8_decode_write: amax -> scale + fused FP8 append (config 2)" if rescale
+                         else "fp8_decode_append (config 2)" if fp8 else "bf16_append (config 1)"),
             "tokens": N, "valid_tokens": case.num_valid, "kv_heads": case.num_heads, "head_dim": case.head_size,
             "block_size": ps, "num_blocks": P, "in_dtype": "bf16",
             "cache_dtype": "fp8_e4m3fn" if fp8 else "bf16", "qkv_row_stride": case.qkv.shape[1],
-            "scale": "per-tensor from amax" if fp8 else None,
+            "scale": ("per-tensor, recomputed from amax every step" if rescale
+                      else "per-tensor from amax" if fp8 else None),
         },
-        "cpu": lambda: cpu_append(case, fp8),
-        "cpu_torch": lambda: torch_cpu_append(case, fp8),
+        "cpu": lambda b: cpu_append(case, fp8, b),
+        "cpu_torch": lambda b: torch_cpu_append(case, fp8, b, rescale=rescale),
     }
+    if rescale:
+        info["config"]["amax_read_bytes"] = amax_bytes
     return launch, info
 
 
@@ -152,7 +184,8 @@ def setup_decode_attention(args, device):
     every kv head, the page ids, the bf16 query and the bf16 output."""
     import torch
 
-    from pipeswift_amd import attention, workloads
+    import workloads
+    from pipeswift_amd import attention
 
     case = workloads.config2_fp8_decode()
     ctx, tables = case.extra["ctx"], case.extra["tables"]
@@ -193,7 +226,7 @@ def setup_decode_attention(args, device):
         "config": {"workload": "FP8 paged decode attention (config 2 cache)", "sequences": B, "context_tokens": total,
                    "kv_heads": H, "q_heads": Hq, "head_dim": D, "block_size": ps, "num_blocks": cache.shape[0],
                    "num_splits": args.num_splits or "auto", "descales": "per-tensor K/V"},
-        "cpu": lambda: cpu_decode_attention(kc, vc, bt, ctx, q[0], scales, total * H * D * 2),
+        "cpu": lambda b: cpu_decode_attention(kc, vc, bt, ctx, q[0], scales, total * H * D * 2, b),
     }
     return launch, info
 
@@ -202,7 +235,8 @@ def setup_kv_scales(args, device):
     """Per-tensor FP8 scales of config 2's K and V (amax / 448), one launch."""
     import torch
 
-    from pipeswift_amd import cache_ops, workloads
+    import workloads
+    from pipeswift_amd import cache_ops
 
     case = workloads.config2_fp8_decode()
     R = args.rotate
@@ -222,13 +256,15 @@ def setup_kv_scales(args, device):
         "dtype": "bf16",
         "config": {"workload": "FP8 per-tensor scale from amax, config 2 K and V", "tokens": case.qkv.shape[0]},
         "cpu": None,
+        "cpu_torch": lambda b: torch_cpu_kv_scales(case, b),
     }
 
 
 def setup_chunked(args, device, gather):
     import torch
 
-    from pipeswift_amd import cache_ops, workloads
+    import workloads
+    from pipeswift_amd import cache_ops
     from pipeswift_amd.reshape_and_cache import reshape_and_cache_flash
 
     # --block-size: the sensitivity run at a larger page (the same token
@@ -260,8 +296,8 @@ def setup_chunked(args, device, gather):
             "dtype": "bf16",
             "config": {"workload": "chunked_append (config 3)" + ("" if ps == 16 else f", block size {ps}"), "tokens": N, "kv_heads": a.num_heads,
                        "head_dim": a.head_size, "block_size": ps, "num_blocks": P, "sequences": len(cc.chunk)},
-            "cpu": lambda: cpu_append(a, False),
-            "cpu_torch": lambda: torch_cpu_append(a, False),
+            "cpu": lambda b: cpu_append(a, False, b),
+            "cpu_torch": lambda b: torch_cpu_append(a, False, b),
         }
     T = int(cc.cu_seq_lens[-1])
     bt = cc.block_table.to(device)
@@ -282,15 +318,19 @@ def setup_chunked(args, device, gather):
         "config": {"workload": "block gather (config 3)" + ("" if ps == 16 else f", block size {ps}"), "tokens": T, "sequences": len(cc.chunk),
                    "kv_heads": a.num_heads, "head_dim": a.head_size, "block_size": ps, "num_blocks": P,
                    "pages": pages},
-        "cpu": lambda: cpu_gather(cc),
-        "cpu_torch": lambda: torch_cpu_gather(cc),
+        "cpu": lambda b: cpu_gather(cc, b),
+        "cpu_torch": lambda b: torch_cpu_gather(cc, b),
     }
 
 
-def setup_mla(args, device, decode):
+def setup_mla(args, device, decode, fp8=False):
+    """Config 4's MLA latent append, prefill (4096 tokens) or decode (128),
+    into the bf16 cache or, with ``fp8``, an E4M3FN cache with one per-tensor
+    scale (amax of kv_c and k_pe over 448, computed once at set-up)."""
     import torch
 
-    from pipeswift_amd import workloads
+    import workloads
+    from pipeswift_amd import cache_ops
     from pipeswift_amd.reshape_and_cache import reshape_and_cache_flash_diffkv
 
     n = 128 if decode else 4096
@@ -302,24 +342,41 @@ def setup_mla(args, device, decode):
     latent.normal_(generator=dgen)
     kv_c = torch.empty((R,) + tuple(case.kv_c.shape), dtype=torch.bfloat16, device=device)
     kv_c.normal_(generator=dgen)
+    latent[0].copy_(case.latent.to(device))
+    kv_c[0].copy_(case.kv_c.to(device))
     slots = torch.stack([torch.randperm(P * ps, generator=torch.Generator().manual_seed(97 + r))[:n]
                          for r in range(min(R, 64))]).to(torch.int64).to(device)
     slots[0].copy_(case.slot_mapping.to(device))
-    cache = case.cache.to(device).unsqueeze(2)
+    scale = None
+    if fp8:
+        cache = torch.zeros(tuple(case.cache.shape), dtype=torch.uint8, device=device).view(torch.float8_e4m3fn)
+        cache_ops.warmup(device)
+        sc = torch.empty(2, dtype=torch.float32, device=device)
+        cache_ops.compute_kv_scales(kv_c[0], out=sc[0:1])
+        cache_ops.compute_kv_scales(case.k_pe(latent[0]), out=sc[1:2])
+        scale = sc.max().reshape(1).contiguous()  # one scale for the whole row: max of the two amax / 448
+    else:
+        cache = case.cache.to(device)
+    cache = cache.unsqueeze(2)
 
     def launch(i):
         reshape_and_cache_flash_diffkv(kv_c[i].unsqueeze(1), case.k_pe(latent[i]).unsqueeze(1), cache,
-                                       slots[i % slots.shape[0]])
+                                       slots[i % slots.shape[0]], scale)
 
-    nbytes = workloads.mla_bytes(n, 576, 2, 2)
+    nbytes = workloads.mla_bytes(n, 576, 2, 1 if fp8 else 2)
+    kind = "decode" if decode else "prefill"
+    name = f"mla_{kind}" + ("_fp8" if fp8 else "")
+    host_scale = None if scale is None else float(scale.cpu())
     return launch, {
         "rotate": R,
-        "name": "mla_decode" if decode else "mla_prefill",
+        "name": name,
         "kernel": "paged_append_small_kernel" if decode else "paged_scatter_kernel", "bytes": nbytes,
-        "tokens": n, "dtype": "bf16",
-        "config": {"workload": f"MLA latent append, {'decode' if decode else 'prefill'} (config 4)", "tokens": n,
-                   "row": 576, "block_size": ps, "num_blocks": P},
+        "tokens": n, "dtype": "fp8_e4m3fn" if fp8 else "bf16",
+        "config": {"workload": f"MLA latent append, {kind}" + (", per-tensor FP8" if fp8 else "") + " (config 4)",
+                   "tokens": n, "row": 576, "block_size": ps, "num_blocks": P,
+                   "cache_dtype": "fp8_e4m3fn" if fp8 else "bf16"},
         "cpu": None,
+        "cpu_torch": lambda b: torch_cpu_mla(case, host_scale, b),
     }
 
 
@@ -327,7 +384,8 @@ def setup_mla_fp8_tiles(args, device, decode):
     """Config 4 into the tile-scaled FP8 latent entry (656 bytes per token)."""
     import torch
 
-    from pipeswift_amd import mla_fp8, workloads
+    import workloads
+    from pipeswift_amd import mla_fp8
 
     case = workloads.config4_mla_fp8_tiles(decode=decode)
     n = case.slot_mapping.shape[0]
@@ -353,14 +411,15 @@ def setup_mla_fp8_tiles(args, device, decode):
         "tokens": n, "dtype": "bf16->fp8_e4m3fn",
         "config": {"workload": f"MLA latent append into tile-scaled FP8 entries, {'decode' if decode else 'prefill'}"
                                " (config 4)", "tokens": n, "entry_bytes": 656, "block_size": ps, "num_blocks": P},
-        "cpu": lambda: cpu_mla_fp8_tiles(case),
+        "cpu": lambda b: cpu_mla_fp8_tiles(case, b),
     }
 
 
 def setup_copy_blocks(args, device):
     import torch
 
-    from pipeswift_amd import cache_ops, workloads
+    import workloads
+    from pipeswift_amd import cache_ops
 
     L, P = 61, 8192
     stack = torch.empty((L, P, 2, 16, 8, 128), dtype=torch.bfloat16, device=device)
@@ -377,8 +436,8 @@ def setup_copy_blocks(args, device):
         "dtype": "bf16",
         "config": {"workload": "copy_blocks (config 5a)", "pairs": 2048, "layers": L, "num_blocks": P,
                    "block_bytes": 65536},
-        "cpu": lambda: cpu_copy_blocks(nbytes),
-        "cpu_torch": lambda: torch_cpu_copy_blocks(nbytes),
+        "cpu": lambda b: cpu_copy_blocks(nbytes, b),
+        "cpu_torch": lambda b: torch_cpu_copy_blocks(nbytes, b),
     }
 
 
@@ -407,46 +466,23 @@ def measure_device_copy(device, reps=10):
     return gbs
 
 
-def measure_copy_floor(device, nbytes, G=64):
+def measure_copy_floor(device, nbytes, steps=256):
     """Device microseconds of the HIP runtime's own contiguous copy (torch
     ``copy_``) moving the same bytes as one launch (nbytes / 2 each way), over
     rotated buffer pairs (a working set of at least 1 GiB, above the Infinity
-    Cache) replayed from HIP graphs of G copies, as the kernels are timed: the
-    floor of a plain copy at this size, for the microsecond workloads."""
+    Cache), timed as the kernels are (events inside one graph of `steps`
+    copies): the floor of a plain copy at this size, for the microsecond
+    workloads."""
     import torch
 
     each = max(16, (nbytes // 2) // 16 * 16)
     n = int(min(512, max(16, math.ceil((1 << 30) / (2 * each)))))
     src = torch.zeros(n, each, dtype=torch.uint8, device=device)
     dst = torch.empty_like(src)
-    G = min(G, n)
-    stream = torch.cuda.Stream(device)
-    graphs = []
-    with torch.cuda.stream(stream):
-        for i in range(min(n, 8)):
-            dst[i].copy_(src[i])
-        stream.synchronize()
-        for gi in range(max(1, min(n // G, 8))):
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g, stream=stream):
-                for j in range(G):
-                    k = (gi * G + j) % n
-                    dst[k].copy_(src[k])
-            graphs.append(g)
-        for g in graphs:
-            g.replay()
-        stream.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        reps = 4 * len(graphs)
-        e0.record(stream)
-        for r in range(reps):
-            graphs[r % len(graphs)].replay()
-        e1.record(stream)
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / (reps * G)
-    del graphs, src, dst
+    t = time_launches(lambda i: dst[i].copy_(src[i]), n, steps, 16, 64, device, eager_calls=1)
+    del src, dst
     torch.cuda.empty_cache()
-    return us
+    return t["ms"] * 1e3 / t["launches"]
 
 
 def run_hbm_copy(args, device):
@@ -486,13 +522,18 @@ def run_hbm_copy(args, device):
     print(json.dumps(line), flush=True)
 
 
-def run_swap(args, device):
+def measure_swap(device, transports=("blit",), reps=3):
     """D2H store then H2D load of 8192 scattered blocks x 8 layers (4 GiB each
-    way) through CopyEngine; wall time from submit to CopyHandle.wait()."""
+    way) through CopyEngine; wall time from submit to CopyHandle.wait(), the
+    median of `reps` after one untimed pass.  Also the achievable host link
+    (one contiguous 1 GiB copy each way between device and pinned host memory)
+    and a pinned host-to-host copy, the reference point for a path with no CPU
+    analog.  Returns the result dict (value: harmonic mean of both directions)."""
     import numpy as np
     import torch
 
-    from pipeswift_amd import copy_engine, workloads
+    import workloads
+    from pipeswift_amd import copy_engine
 
     L, Pg, P2 = 8, 16384, 8192
     gpu_ids, l2_ids = workloads.config5b_pages(gpu_pages=Pg, l2_pages=P2)
@@ -500,13 +541,13 @@ def run_swap(args, device):
     cache.view(torch.int16).random_(generator=torch.Generator(device=device).manual_seed(95))
     nbytes = len(gpu_ids) * L * 65536
     results = {}
-    for transport in args.transports.split(","):
+    for transport in transports:
         eng = copy_engine.CopyEngine([cache], Pg, P2, transport=transport)
         try:
             res = {}
             for direction in ("store", "load"):
                 times = []
-                for rep in range(args.swap_reps + 1):
+                for rep in range(reps + 1):
                     torch.cuda.synchronize()
                     t0 = time.perf_counter()
                     if direction == "store":
@@ -516,8 +557,8 @@ def run_swap(args, device):
                     h.wait()
                     if rep:
                         times.append(time.perf_counter() - t0)
-                res[direction] = {"GB/s": nbytes / float(np.median(times)) / 1e9, "ms": 1e3 * float(np.median(times)),
-                                  "runs": h.num_runs * L}
+                res[direction] = {"GB/s": round(nbytes / float(np.median(times)) / 1e9, 2),
+                                  "ms": round(1e3 * float(np.median(times)), 3), "runs": h.num_runs * L}
             results[transport] = res
         finally:
             eng.close()
@@ -525,9 +566,6 @@ def run_swap(args, device):
     st, ld = results[best]["store"]["GB/s"], results[best]["load"]["GB/s"]
     value = 2.0 / (1.0 / st + 1.0 / ld)  # both directions, harmonic mean
 
-    # achievable host link: one contiguous 1 GiB copy each way between device
-    # memory and pinned host memory; and a pinned host-to-host copy as the
-    # reference point for a path with no CPU analog
     del cache
     torch.cuda.empty_cache()
     n = 1 << 30
@@ -550,22 +588,32 @@ def run_swap(args, device):
     link = {"D2H": timed_copy(host_a, dev_buf), "H2D": timed_copy(dev_buf, host_a)}
     link_hm = 2.0 / (1.0 / link["D2H"] + 1.0 / link["H2D"])
     host_copy = timed_copy(host_b, host_a)
-    line = {
-        "metric": "swap_blocks host-link GB/s (D2H store + H2D load, 4 GiB each way)",
-        "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.swap_reps, "warmup": 1,
+    del dev_buf, host_a, host_b
+    torch.cuda.empty_cache()
+    blocks_per_s = len(gpu_ids) / ((results[best]["store"]["ms"] + results[best]["load"]["ms"]) / 2e3)
+    return {
+        "value": round(value, 2), "unit": "GB/s", "steps": reps, "warmup": 1,
         "ms_per_step": results[best]["store"]["ms"] + results[best]["load"]["ms"],
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bytes",
-        "data": "synthetic (seeded)",
+        "blocks_per_s": round(blocks_per_s, 1),
         "config": {"workload": "swap_blocks (config 5b)", "blocks": len(gpu_ids), "layers": L,
-                   "bytes_per_block_layer": 65536, "transport": best, "all_transports": results},
-        "roofline": {"bound": "pcie", "achieved": round(value, 2), "peak": 64.0, "unit": "GB/s",
+                   "bytes_per_block_layer": 65536, "bytes_each_way": nbytes, "transport": best,
+                   "all_transports": results},
+        "roofline": {"bound": "pcie", "kernel": "blit_pages_kernel" if best == "blit" else best,
+                     "achieved": round(value, 2), "peak": 64.0, "unit": "GB/s",
                      "frac": round(value / 64.0, 4), "traffic": None,
                      "achievable": round(link_hm, 2), "frac_of_achievable": round(value / link_hm, 4),
                      "achievable_each_way": {k: round(v, 2) for k, v in link.items()},
                      "achievable_how": "one contiguous 1 GiB copy each way, device <-> pinned host"},
-        "host_to_host_pinned_copy_GBs": round(host_copy, 2),
-        "cpu_baseline": None,
+        "cpu_baseline": {"value": round(host_copy, 2), "unit": "GB/s", "cores": 1, "kind": "reference point",
+                         "sample": "pinned host-to-host copy of 1 GiB (the swap has no CPU analog)"},
     }
+
+
+def run_swap(args, device):
+    res = measure_swap(device, tuple(args.transports.split(",")), args.swap_reps)
+    line = dict({"metric": "swap_blocks host-link GB/s (D2H store + H2D load, 4 GiB each way)", "n_gpus": 1,
+                 "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bytes",
+                 "data": "synthetic (seeded)"}, **res)
     print(json.dumps(line), flush=True)
 
 
@@ -580,7 +628,8 @@ def run_metadata(args, device):
     import torch
 
     from oracle import kv_oracle as O
-    from pipeswift_amd import metadata, workloads
+    import workloads
+    from pipeswift_amd import metadata
 
     class Seq:
         def __init__(self, sid, n, off):
@@ -1051,8 +1100,60 @@ def torch_cpu_append_step(case, fp8):
     return step, cache
 
 
-def torch_cpu_append(case, fp8, budget_s=3.0):
+def torch_cpu_append(case, fp8, budget_s=3.0, rescale=False):
+    """The torch host append.  ``rescale``: each step first recomputes the two
+    per-tensor scales (torch amax of |K| and |V| over 448), as the GPU step
+    of fp8_decode_write does."""
+    import torch
+
     step, _ = torch_cpu_append_step(case, fp8)
+    if not rescale:
+        return _timed(step, budget_s)
+    key, value = case.key(), case.value()
+
+    def full():
+        (key.float().abs().amax() / 448.0).item(), (value.float().abs().amax() / 448.0).item()
+        step()
+
+    return _timed(full, budget_s)
+
+
+def torch_cpu_kv_scales(case, budget_s=3.0):
+    """torch on the host for the per-tensor scales: amax of |K| and of |V| in
+    fp32, each divided by 448."""
+    key, value = case.key(), case.value()
+
+    def step():
+        return key.float().abs().amax() / 448.0, value.float().abs().amax() / 448.0
+
+    return _timed(step, budget_s)
+
+
+def torch_cpu_mla_step(case, scale):
+    """torch on the host for the MLA append: the [kv_c | k_pe] rows of the
+    valid tokens index_put_ into a [P, ps, 576] host cache, quantized first as
+    fp8_kv.quantize does (x / scale clamped to +-448, float8_e4m3fn) when
+    ``scale`` is given.  Returns (step, cache)."""
+    import torch
+
+    slots = case.slot_mapping
+    ps = case.cache.shape[1]
+    valid = slots >= 0
+    blk, off = slots[valid] // ps, slots[valid] % ps
+    rows = torch.cat([case.kv_c, case.k_pe()], 1)[valid]
+    cache = torch.zeros(tuple(case.cache.shape), dtype=torch.float8_e4m3fn if scale is not None else torch.bfloat16)
+
+    def step():
+        if scale is not None:
+            cache.index_put_((blk, off), (rows.float() / scale).clamp(-448.0, 448.0).to(torch.float8_e4m3fn))
+        else:
+            cache.index_put_((blk, off), rows)
+
+    return step, cache
+
+
+def torch_cpu_mla(case, scale, budget_s=3.0):
+    step, _ = torch_cpu_mla_step(case, scale)
     return _timed(step, budget_s)
 
 
@@ -1123,8 +1224,267 @@ def torch_cpu_copy_blocks(full_bytes, budget_s=3.0):
 
 
 # --------------------------------------------------------------------------- #
-# main
+# timing
 # --------------------------------------------------------------------------- #
+
+
+def launch_sets(steps, rotate):
+    """Rotation set of each of the `steps` timed launches, in order: exactly
+    `steps` entries cycling through the `rotate` input sets."""
+    R = max(1, int(rotate))
+    return [i % R for i in range(max(0, int(steps)))]
+
+
+_SPIN_US_PER_CYCLE = None
+
+
+def _spin_us_per_cycle(device):
+    """Microseconds per cycle of torch's spin kernel on this GPU, measured once."""
+    global _SPIN_US_PER_CYCLE
+    import torch
+
+    if _SPIN_US_PER_CYCLE is None:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(100_000)
+        e0.record()
+        torch.cuda._sleep(SPIN_CYCLES)
+        e1.record()
+        torch.cuda.synchronize()
+        _SPIN_US_PER_CYCLE = e0.elapsed_time(e1) * 1e3 / SPIN_CYCLES
+    return _SPIN_US_PER_CYCLE
+
+
+def time_launches(launch, rotate, steps, warmup, graph_len, device, eager_calls=200):
+    """HIP-event time of exactly `steps` launches on one stream, after `warmup`
+    untimed ones.  Launch i uses rotation set i % rotate.
+
+    Up to QUEUED_MAX launches ("queued"): a spin kernel is enqueued first, long
+    enough to cover the host's enqueue time of the K launches (twice the
+    measured per-call host time, plus 0.2 ms), then the start event, the K
+    launches and the end event.  The GPU reaches the start event only after
+    the spin, by which time all K launches wait in the queue, so the events
+    bracket K back-to-back kernels.  That is checked: the host's enqueue
+    interval (from before the spin to after the end event) must be shorter
+    than the GPU's interval from an event before the spin to the start event;
+    otherwise the spin doubles (three attempts) and the graph method is used.
+
+    Longer runs ("graph"): the K launches are captured into one graph, replayed
+    once untimed (the first replay also uploads the graph), and stream events
+    bracket a second replay, which includes the replay's own dispatch cost
+    (about 15 us; torch refuses timing events inside a graph on ROCm, and
+    HIP's external event-record node fails under capture on this runtime).
+    graph_len == 0 forces eager launches between the events without a spin
+    long enough for them ("eager").
+
+    Returns a dict with the elapsed ms, the launch count, the method and the
+    host wall time of one eager call (Python shim, argument checks, launch)."""
+    import torch
+
+    R = max(1, int(rotate))
+    sets = launch_sets(steps, R)
+    stream = torch.cuda.Stream(device)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        for i in range(min(R, 8)):
+            launch(i)  # eager warmup of every code path before capture
+        for i in range(warmup):
+            launch(i % R)
+        stream.synchronize()
+        # host wall time per eager call (Python shim, argument checks, launch):
+        # what a caller that does not capture graphs pays, and what the queued
+        # method's spin has to cover
+        eager_n = max(1, min(eager_calls, steps))
+        t0 = time.perf_counter()
+        for i in range(eager_n):
+            launch(i % R)
+        stream.synchronize()
+        eager_us = (time.perf_counter() - t0) / eager_n * 1e6
+    torch.cuda.synchronize()
+
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    method, ms = None, None
+    if int(graph_len) > 0 and 0 < steps <= QUEUED_MAX:
+        us_per_cycle = _spin_us_per_cycle(device)
+        spin_us = 2.0 * steps * eager_us + 200.0
+        for _ in range(3):
+            cycles = int(spin_us / us_per_cycle)
+            with torch.cuda.stream(stream):
+                h0 = time.perf_counter()
+                ev[0].record(stream)
+                torch.cuda._sleep(cycles)
+                ev[1].record(stream)
+                for i in sets:
+                    launch(i)
+                ev[2].record(stream)
+                h1 = time.perf_counter()
+            torch.cuda.synchronize()
+            if (h1 - h0) * 1e3 < ev[0].elapsed_time(ev[1]):
+                method, ms = "queued", ev[1].elapsed_time(ev[2])
+                break
+            spin_us *= 2.0
+    if method is None and int(graph_len) > 0 and steps > 0:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(graph, stream=stream):
+                for i in sets:
+                    launch(i)
+            graph.replay()  # untimed: the first replay also uploads the graph
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            torch.cuda._sleep(SPIN_CYCLES)  # keeps host submission out of the timed region
+            ev[1].record(stream)
+            graph.replay()
+            ev[2].record(stream)
+        torch.cuda.synchronize()
+        method, ms = "graph", ev[1].elapsed_time(ev[2])
+        del graph
+    if method is None:
+        with torch.cuda.stream(stream):
+            torch.cuda._sleep(SPIN_CYCLES)
+            ev[1].record(stream)
+            for i in sets:
+                launch(i)
+            ev[2].record(stream)
+        torch.cuda.synchronize()
+        method, ms = "eager", ev[1].elapsed_time(ev[2])
+    how = {"queued": "HIP stream events around K back-to-back launches already queued behind a spin kernel",
+           "graph": "HIP stream events around one (warm) graph replay of the K launches",
+           "eager": "HIP stream events around K eager launches"}[method]
+    return {"ms": ms, "launches": len(sets), "method": method, "timing": how, "eager_us": eager_us}
+
+
+SETUPS = {
+    "fp8_decode_append": lambda a, d: setup_append(a, d, fp8=True),
+    "fp8_decode_write": lambda a, d: setup_append(a, d, fp8=True, rescale=True),
+    "bf16_append": lambda a, d: setup_append(a, d, fp8=False),
+    "kv_scales": setup_kv_scales,
+    "decode_attention": setup_decode_attention,
+    "chunked_append": lambda a, d: setup_chunked(a, d, gather=False),
+    "gather": lambda a, d: setup_chunked(a, d, gather=True),
+    "mla_prefill": lambda a, d: setup_mla(a, d, decode=False),
+    "mla_decode": lambda a, d: setup_mla(a, d, decode=True),
+    "mla_prefill_fp8": lambda a, d: setup_mla(a, d, decode=False, fp8=True),
+    "mla_decode_fp8": lambda a, d: setup_mla(a, d, decode=True, fp8=True),
+    "mla_fp8_tiles_prefill": lambda a, d: setup_mla_fp8_tiles(a, d, decode=False),
+    "mla_fp8_tiles_decode": lambda a, d: setup_mla_fp8_tiles(a, d, decode=True),
+    "copy_blocks": setup_copy_blocks,
+}
+
+# The default run: config 2 is the headline (`value`); every other benchmark
+# configuration gets a bounded run of its own under `secondary`, each timed
+# the same way (exactly `steps` launches after `warmup`), with CPU baselines
+# on a short budget.  (name, steps, warmup)
+SECONDARY = (
+    ("fp8_decode_write", 1024, 64),
+    ("kv_scales", 1024, 64),
+    ("bf16_append", 1024, 64),
+    ("chunked_append", 1024, 64),
+    ("gather", 64, 8),
+    ("mla_prefill", 1024, 64),
+    ("mla_decode", 1024, 64),
+    ("mla_prefill_fp8", 1024, 64),
+    ("mla_decode_fp8", 1024, 64),
+    ("copy_blocks", 8, 2),
+    ("decode_attention", 64, 8),
+    ("swap", 2, 1),
+)
+
+
+def _load_traffic():
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f)
+    return {}
+
+
+def measure_workload(args, device, name, steps, warmup, achievable, cpu_budget, port_budget, copy_floor=True):
+    """Set up one workload, time exactly `steps` launches and return its result
+    dict (value, roofline, CPU baselines); frees its device memory on return."""
+    import gc
+
+    import torch
+
+    launch, info = SETUPS[name](args, device)
+    R = info.get("rotate", args.rotate)
+    graph_len = args.graph
+    t = time_launches(launch, R, steps, warmup, graph_len, device)
+    per_launch_s = t["ms"] / 1e3 / t["launches"]
+    achieved = info["bytes"] / per_launch_s / 1e9
+    # For the microsecond workloads the same kernel is also timed over 2048
+    # launches in one graph: the per-launch time inside a long graph, such as
+    # a decode step, a cross-check of the short run's method.
+    steady = None
+    if graph_len > 0 and steps < STEADY_STEPS and info["bytes"] < (64 << 20):
+        ts = time_launches(launch, R, STEADY_STEPS, warmup, graph_len, device, eager_calls=1)
+        steady = ts["ms"] * 1e3 / ts["launches"]
+    floor = None
+    if copy_floor and info["bytes"] < (64 << 20):
+        floor = measure_copy_floor(device, info["bytes"])
+    traffic = _load_traffic().get(name, {}).get("bytes_per_launch")
+
+    cpu = None
+    if port_budget > 0 and info.get("cpu") is not None:
+        torch.set_num_threads(1)
+        n, el, sample = info["cpu"](port_budget)
+        cpu = {"value": info["bytes"] * n / el / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+               "sample": f"{sample}; {el:.1f} s on 1 thread of {_cpu_model()} ({os.cpu_count()} cpus visible)",
+               "tokens_per_s": info["tokens"] * n / el}
+    cpu_torch = None
+    if cpu_budget > 0 and info.get("cpu_torch") is not None:
+        threads = os.cpu_count() or 1
+        torch.set_num_threads(threads)
+        n, el = info["cpu_torch"](cpu_budget)
+        torch.set_num_threads(1)
+        n1, el1 = info["cpu_torch"](cpu_budget)
+        cpu_torch = {"value": info["bytes"] * n / el / 1e9, "unit": "GB/s", "threads": threads,
+                     "value_1thread": info["bytes"] * n1 / el1 / 1e9,
+                     "tokens_per_s": info["tokens"] * n / el,
+                     "what": "the reference's CPU path: torch index_put_ / index_select / amax (copy_blocks: a "
+                             "snapshot index copy) on host tensors of the same layout, "
+                             f"{n:.3g} steps in {el:.1f} s on {threads} threads, {n1:.3g} in {el1:.1f} s on 1"}
+    res = {
+        "value": round(achieved, 2),
+        "unit": "GB/s",
+        "steps": t["launches"],
+        "warmup": warmup,
+        "ms_per_step": t["ms"] / t["launches"],
+        "tokens_per_s": round(info["tokens"] / per_launch_s, 1),
+        "pct_of_peak": round(100.0 * achieved / PEAK_HBM_GBS, 3),
+        "dtype": info["dtype"],
+        "config": dict(info["config"], rotation_sets=R, timing=t["timing"]),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": info["kernel"],
+            "achieved": round(achieved, 2),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 5),
+            "bytes_per_launch": info["bytes"],
+            "us_per_launch": round(per_launch_s * 1e6, 3),
+            "steady_us_per_launch": None if steady is None else round(steady, 3),
+            "steady_frac": None if steady is None else round(info["bytes"] / steady / 1e3 / PEAK_HBM_GBS, 5),
+            "traffic": traffic,
+            "achievable": None if achievable is None else round(achievable, 1),
+            "frac_of_achievable": None if achievable is None else round(achieved / achievable, 5),
+        },
+        "copy_floor": None if floor is None else {
+            "us": round(floor, 3),
+            "vs_launch": round(floor / (per_launch_s * 1e6), 4),
+            "how": "torch copy_ (the HIP runtime's device copy) of the same bytes, half each way, over rotated "
+                   "buffer pairs (>= 1 GiB), 256 copies timed by events inside one graph",
+        },
+        "wall_us_per_call_eager": round(t["eager_us"], 2),
+        "cpu_baseline": cpu,
+        "cpu_torch": cpu_torch,
+    }
+    del launch, info
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return res
+
+
+METRIC = "achieved HBM GB/s (% of MI355X peak) + tokens/s for paged KV append/FP8 quant"
 
 
 def main():
@@ -1132,7 +1492,9 @@ def main():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=2048)
     p.add_argument("--warmup", type=int, default=256)
-    p.add_argument("--workload", default="fp8_decode_append")
+    p.add_argument("--workload", default="default",
+                   help="default: config 2 as the headline plus every other configuration under `secondary`")
+    p.add_argument("--no-secondary", action="store_true", help="default workload: the headline only")
     p.add_argument("--rotate", type=int, default=512, help="rotation sets of inputs/slots")
     p.add_argument("--graph", type=int, default=64, help="launches captured per HIP graph (0: eager)")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -1147,166 +1509,66 @@ def main():
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(the KV kernels are rank-local; see the sharding notes). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+    if args.steps < 1 or args.warmup < 0:
+        raise SystemExit("--steps must be >= 1 and --warmup >= 0")
 
     import torch
 
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
     name = args.workload
-    if name in ("fp8_decode_append", "bf16_append"):
-        launch, info = setup_append(args, device, fp8=name.startswith("fp8"))
-    elif name == "kv_scales":
-        launch, info = setup_kv_scales(args, device)
-    elif name == "decode_attention":
-        launch, info = setup_decode_attention(args, device)
-    elif name in ("chunked_append", "gather"):
-        launch, info = setup_chunked(args, device, gather=name == "gather")
-    elif name in ("mla_prefill", "mla_decode"):
-        launch, info = setup_mla(args, device, decode=name == "mla_decode")
-    elif name in ("mla_fp8_tiles_prefill", "mla_fp8_tiles_decode"):
-        launch, info = setup_mla_fp8_tiles(args, device, decode=name.endswith("decode"))
-    elif name == "swap":
-        return run_swap(args, device)
-    elif name == "hbm_copy":
-        return run_hbm_copy(args, device)
-    elif name == "swap_sweep":
-        return run_swap_sweep(args, device)
-    elif name == "attention_shapes":
-        return run_attention_shapes(args, device)
-    elif name == "metadata":
-        return run_metadata(args, device)
-    elif name == "l2_cycle":
-        return run_l2_cycle(args, device)
-    elif name == "copy_blocks":
-        launch, info = setup_copy_blocks(args, device)
-        args.graph = min(args.graph, 4)
-    else:
+    standalone = {"swap": run_swap, "hbm_copy": run_hbm_copy, "swap_sweep": run_swap_sweep,
+                  "attention_shapes": run_attention_shapes, "metadata": run_metadata, "l2_cycle": run_l2_cycle}
+    if name in standalone:
+        return standalone[name](args, device)
+    headline = "fp8_decode_append" if name == "default" else name
+    if headline not in SETUPS:
         raise SystemExit(f"unknown workload {name}")
-    R = info.get("rotate", args.rotate)
-    if args.graph > R:
-        args.graph = R
-    torch.cuda.synchronize()
-
-    stream = torch.cuda.Stream(device)
-    G = args.graph
-    graphs = []
-    with torch.cuda.stream(stream):
-        for i in range(min(R, 8)):
-            launch(i)  # eager warmup of every code path before capture
-        stream.synchronize()
-        if G > 0:
-            n_graphs = max(1, min(R // G, 8))
-            for gi in range(n_graphs):
-                g = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(g, stream=stream):
-                    for j in range(G):
-                        launch((gi * G + j) % R)
-                graphs.append(g)
-    torch.cuda.synchronize()
-
-    def run(steps):
-        with torch.cuda.stream(stream):
-            if G > 0:
-                reps = steps // G
-                for r in range(reps):
-                    graphs[r % len(graphs)].replay()
-                return reps * G
-            for i in range(steps):
-                launch(i % R)
-            return steps
-
-    run(args.warmup)
-    torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    done = run(args.steps)
-    end.record(stream)
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end)
-    per_launch_s = ms / 1e3 / done
-    achieved = info["bytes"] / per_launch_s / 1e9
-
-    # host wall time per eager call (Python shim, argument checks, launch), the
-    # figure a caller that does not capture graphs sees
-    eager_n = max(1, min(200, args.steps))
-    with torch.cuda.stream(stream):
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for i in range(eager_n):
-            launch(i % R)
-        torch.cuda.synchronize()
-        eager_us = (time.perf_counter() - t0) / eager_n * 1e6
 
     achievable = measure_device_copy(device)
-    # microsecond workloads: the runtime's copy of the same bytes at the same size
-    copy_floor = measure_copy_floor(device, info["bytes"]) if info["bytes"] < (64 << 20) else None
-
-    traffic = None
-    if os.path.exists(TRAFFIC_FILE):
-        with open(TRAFFIC_FILE) as f:
-            traffic = json.load(f).get(name, {}).get("bytes_per_launch")
-
-    cpu = None
-    if not args.no_cpu_baseline and info.get("cpu") is not None:
-        torch.set_num_threads(1)
-        n, el, sample = info["cpu"]()
-        cpu = {"value": info["bytes"] * n / el / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-               "sample": f"{sample}; {el:.1f} s on 1 thread of {_cpu_model()} ({os.cpu_count()} cpus visible)",
-               "tokens_per_s": info["tokens"] * n / el}
-
-    cpu_torch = None
-    if not args.no_cpu_baseline and info.get("cpu_torch") is not None:
-        threads = os.cpu_count() or 1
-        torch.set_num_threads(threads)
-        n, el = info["cpu_torch"]()
-        torch.set_num_threads(1)
-        n1, el1 = info["cpu_torch"]()
-        cpu_torch = {"value": info["bytes"] * n / el / 1e9, "unit": "GB/s", "threads": threads,
-                     "value_1thread": info["bytes"] * n1 / el1 / 1e9,
-                     "what": "the reference's CPU path: torch index_put_/index_select (copy_blocks: a snapshot "
-                             f"index copy) on host tensors of the same layout, {n:.3g} steps in {el:.1f} s on "
-                             f"{threads} threads, {n1:.3g} in {el1:.1f} s on 1"}
+    nocpu = args.no_cpu_baseline
+    res = measure_workload(args, device, headline, args.steps, args.warmup, achievable,
+                           cpu_budget=0 if nocpu else 3.0, port_budget=0 if nocpu else 10.0)
+    print(f"[bench] {headline}: {res['roofline']['us_per_launch']} us/launch, {res['value']} GB/s",
+          file=sys.stderr, flush=True)
+    secondary = None
+    if name == "default" and not args.no_secondary:
+        secondary = {}
+        for sname, steps, warmup in SECONDARY:
+            t0 = time.perf_counter()
+            if sname == "swap":
+                r = measure_swap(device, ("blit",), reps=steps)
+            else:
+                r = measure_workload(args, device, sname, steps, warmup, achievable,
+                                     cpu_budget=0 if nocpu else 1.0, port_budget=0)
+            secondary[sname] = r
+            print(f"[bench] {sname}: {r['value']} {r['unit']} ({time.perf_counter() - t0:.1f} s)",
+                  file=sys.stderr, flush=True)
 
     line = {
-        "metric": "achieved HBM GB/s (% of MI355X peak) + tokens/s for paged KV append/FP8 quant",
-        "value": round(achieved, 2),
+        "metric": METRIC,
+        "value": res["value"],
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": done,
+        "steps": res["steps"],
         "warmup": args.warmup,
-        "ms_per_step": ms / done,
+        "ms_per_step": res["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": info["dtype"],
+        "dtype": res["dtype"],
         "data": "synthetic (seeded)",
-        "tokens_per_s": round(info["tokens"] / per_launch_s, 1),
-        "pct_of_peak": round(100.0 * achieved / PEAK_HBM_GBS, 3),
-        "config": dict(info["config"], launches_per_graph=G, rotation_sets=R),
-        "roofline": {
-            "bound": "hbm",
-            "kernel": info["kernel"],
-            "achieved": round(achieved, 2),
-            "peak": PEAK_HBM_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / PEAK_HBM_GBS, 5),
-            "bytes_per_launch": info["bytes"],
-            "us_per_launch": round(per_launch_s * 1e6, 3),
-            "traffic": traffic,
-            "achievable": round(achievable, 1),
-            "frac_of_achievable": round(achieved / achievable, 5),
-        },
-        "copy_floor": None if copy_floor is None else {
-            "us": round(copy_floor, 3),
-            "vs_launch": round(copy_floor / (per_launch_s * 1e6), 4),
-            "how": "torch copy_ (the HIP runtime's device copy) of the same bytes, half each way, over rotated "
-                   "buffer pairs (>= 1 GiB) replayed from HIP graphs of 64 copies",
-        },
-        "wall_us_per_call_eager": round(eager_us, 2),
-        "cpu_baseline": cpu,
-        "cpu_torch": cpu_torch,
+        "tokens_per_s": res["tokens_per_s"],
+        "pct_of_peak": res["pct_of_peak"],
+        "config": res["config"],
+        "roofline": res["roofline"],
+        "copy_floor": res["copy_floor"],
+        "wall_us_per_call_eager": res["wall_us_per_call_eager"],
+        "cpu_baseline": res["cpu_baseline"],
+        "cpu_torch": res["cpu_torch"],
     }
+    if secondary is not None:
+        line["secondary"] = secondary
     print(json.dumps(line), flush=True)
 
 

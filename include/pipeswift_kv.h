@@ -24,6 +24,8 @@
  *   psk_concat_and_cache_mla  pipeswift/utils/triton_kernels/reshape_and_cache.py:138-229
  *   psk_swap_blocks           pipeswift/utils/copy_engine.py:429-457 (cuMemcpyBatchAsync)
  *   psk_build_kv_metadata     pipeswift/utils/metadata.py:206-348 (per-token Python loop)
+ *   psk_build_next_decode_metadata  pipeswift/utils/metadata.py:351-414 (per-sequence loop)
+ *   psk_refresh_graph_metadata      pipeswift/utils/cudagraph.py:75-118 (copy_/fill_ sequence)
  *   psk_page_hash_chain,      pipeswift/engine/block_manager.py:220-227, 678-693
  *   psk_keyed_hash            (xxhash.xxh64 per page; host functions)
  * and build-defined operations that have no reference implementation:
@@ -231,6 +233,51 @@ int64_t psk_build_kv_metadata(int64_t num_seqs, const uint64_t* page_table_ptrs,
                               int64_t row_width, int32_t* page_table_out, int32_t* cu_seqlens_q_out,
                               int32_t* lens_q_out, int32_t* lens_kv_out, int64_t* slot_mapping_out,
                               int64_t slot_capacity);
+
+/*
+ * Graph static-metadata refresh (replaces set_graph_kvcacheinfo,
+ * pipeswift/utils/cudagraph.py:75-118, a sequence of about ten copy_/fill_/
+ * zero_/arange launches per decode step).  One kernel launch on `stream`, no
+ * memset node, so it may itself be captured.  Reads the step's device metadata
+ * (src_*: page table [bsz, width] at row stride src_page_table_stride,
+ * num_slots slots, lens_q/lens_kv [bsz], cu_seqlens_q [bsz + 1]) and writes the
+ * static buffers (dst_*: page table [max_bsz, dst_page_table_width] at row
+ * stride dst_page_table_stride, slot_mapping [slot_capacity], lens [max_bsz],
+ * cu_seqlens_q [max_bsz + 1]):
+ *   page_table[r, c]  = src[r, c]              r < bsz, c < width
+ *   slot_mapping[k]   = src[k]                 k < num_slots
+ *   lens_q/kv[k], cu_seqlens_q[k <= bsz]       copies
+ * and, when bsz != cg_bsz (a padded replay; bsz < cg_bsz <= max_bsz):
+ *   page_table[r, c]  = 0                      bsz <= r < max_bsz, c < width
+ *   slot_mapping[k]   = -1                     num_slots <= k < slot_capacity
+ *   lens_q[k] = pad_q_len, lens_kv[k] = 0      bsz <= k < max_bsz
+ *   cu_seqlens_q[bsz + j] = cu_seqlens_q[bsz] + j * pad_q_len,  1 <= j <= max_bsz - bsz
+ * Elements not named here keep their contents, as in the reference.
+ */
+int psk_refresh_graph_metadata(const int32_t* src_page_table, int64_t src_page_table_stride,
+                                const int64_t* src_slot_mapping, const int32_t* src_lens_q,
+                                const int32_t* src_lens_kv, const int32_t* src_cu_seqlens_q, int64_t bsz,
+                                int64_t width, int64_t num_slots, int32_t* dst_page_table,
+                                int64_t dst_page_table_stride, int64_t dst_page_table_width,
+                                int64_t* dst_slot_mapping, int64_t slot_capacity, int32_t* dst_lens_q,
+                                int32_t* dst_lens_kv, int32_t* dst_cu_seqlens_q, int64_t max_bsz, int64_t cg_bsz,
+                                int32_t pad_q_len, void* stream);
+
+/*
+ * Host-side metadata of the next draft decode step (replaces the per-sequence
+ * Python loop of derive_kvcache_info_next_decode_step,
+ * pipeswift/utils/metadata.py:351-414).  Sequence i has one new token at
+ * positions[i] with page ids page_table_ptrs[i][0 .. page_table_lens[i]):
+ *   slot_mapping_out[i] = page[pos / ps] * ps + pos % ps, lens_kv_out[i] = lens_kv_prev[i] + 1
+ * with DCP (dcp_deg > 1) the rank-local slot when the rank owns pos, else -1
+ * with lens_kv unchanged (metadata.py:390-403).  Returns num_seqs, or
+ * PSK_E_RANGE when a position has no page (the reference raises IndexError).
+ */
+int64_t psk_build_next_decode_metadata(int64_t num_seqs, const uint64_t* page_table_ptrs,
+                                       const int64_t* page_table_lens, const int64_t* positions,
+                                       const int32_t* lens_kv_prev, int64_t page_size, int64_t dcp_deg,
+                                       int64_t dcp_rank, int64_t dcp_interleave, int64_t* slot_mapping_out,
+                                       int32_t* lens_kv_out);
 
 /*
  * Paged decode attention over an FP8 E4M3FN KV cache (replaces the reader the

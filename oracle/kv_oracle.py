@@ -8,7 +8,9 @@ only the FP8 paths convert to float32.
 Reference files restated here (wsjdsg/PipeSwift):
   pipeswift/utils/triton_kernels/reshape_and_cache.py  (append, MLA concat, FP8)
   pipeswift/utils/fp8_kv.py:24-25,75-77                 (FP8 constants, quantize)
-  pipeswift/utils/metadata.py:264-295, 351-392          (slot_mapping, page_table)
+  pipeswift/utils/metadata.py:264-295, 351-414          (slot_mapping, page_table,
+                                                         next decode step)
+  pipeswift/utils/cudagraph.py:75-118                   (graph static refresh)
   pipeswift/utils/copy_engine.py:121-142, 373-427       (page bytes, views, range
                                                          check, run coalescing)
 """
@@ -407,17 +409,6 @@ def coalesce(src_ids, dst_ids):
     return src[starts], dst[starts], lens
 
 
-def swap_pages(src_views, dst_views, src_ids, dst_ids):
-    """Byte copy of page rows between [P, bpb] views: dst[v][d] = src[v][s]."""
-    for sv, dv in zip(src_views, dst_views):
-        dv[np.asarray(dst_ids, dtype=np.int64)] = sv[np.asarray(src_ids, dtype=np.int64)]
-
-
-# --------------------------------------------------------------------------- #
-# slot mapping and page table, metadata.py
-# --------------------------------------------------------------------------- #
-
-
 def slot_mapping(page_table_row, offset, num_tokens, page_size, dcp_deg=1, dcp_rank=0, dcp_interleave_size=1):
     """Slots of positions [offset, num_tokens) of one sequence (metadata.py:272-295).
 
@@ -452,6 +443,47 @@ def dcp_kv_len(prefix_len, dcp_deg, dcp_rank, dcp_interleave_size):
     elif rem >= dcp_rank * dcp_interleave_size:
         n += rem % dcp_interleave_size
     return n
+
+
+def next_decode_step(page_tables, positions, lens_kv_prev, page_size, dcp_deg=1, dcp_rank=0, dcp_interleave_size=1):
+    """Slots and lens_kv of the next draft decode step (metadata.py:351-414):
+    one token per sequence at positions[i]; lens_kv + 1 where the rank owns
+    it.  A position without a page raises IndexError, as the reference's
+    page-table subscript does (:376)."""
+    slots, lens = [], []
+    for row, pos, prev in zip(page_tables, positions, lens_kv_prev):
+        row[pos // page_size]  # IndexError, as kv_page_table[seq_id][pos // ps]
+        s = slot_mapping(row, pos, pos + 1, page_size, dcp_deg, dcp_rank, dcp_interleave_size)[0]
+        slots.append(s)
+        lens.append(prev + 1 if s >= 0 else prev)
+    return np.array(slots, np.int64), np.array(lens, np.int32)
+
+
+def graph_refresh(static, step, cg_bsz, pad_q_len=1):
+    """set_graph_kvcacheinfo (cudagraph.py:75-118) on numpy arrays, in place.
+
+    static / step: dicts of page_table [rows, W], slot_mapping, lens_q,
+    lens_kv, cu_seqlens_q.  Copies the step's metadata into the leading part of
+    the static arrays; when bsz != cg_bsz pads lens_q with pad_q_len,
+    slot_mapping with -1, lens_kv and page_table[bsz:, :W] with 0, and
+    cu_seqlens_q[bsz + 1:] with cu[bsz] + k * pad_q_len (k = 1, 2, ...)."""
+    bsz, w = step["lens_q"].shape[0], step["page_table"].shape[1]
+    n = step["slot_mapping"].shape[0]
+    static["page_table"][:bsz, :w] = step["page_table"]
+    static["slot_mapping"][:n] = step["slot_mapping"]
+    static["lens_q"][:bsz] = step["lens_q"]
+    static["lens_kv"][:bsz] = step["lens_kv"]
+    static["cu_seqlens_q"][: bsz + 1] = step["cu_seqlens_q"][: bsz + 1]
+    if bsz != cg_bsz:
+        assert bsz < cg_bsz
+        static["lens_q"][bsz:] = pad_q_len
+        static["slot_mapping"][n:] = -1
+        static["lens_kv"][bsz:] = 0
+        static["page_table"][bsz:, :w] = 0
+        tail = static["cu_seqlens_q"].shape[0] - bsz
+        static["cu_seqlens_q"][bsz + 1:] = static["cu_seqlens_q"][bsz] + np.arange(pad_q_len, tail * pad_q_len,
+                                                                                    pad_q_len, dtype=np.int64)
+    return static
 
 
 # --------------------------------------------------------------------------- #

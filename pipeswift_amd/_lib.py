@@ -71,6 +71,14 @@ _SIGNATURES = {
         _i64,
         [_i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _i64, _vp, _vp, _vp, _vp, _vp, _i64],
     ),
+    "psk_refresh_graph_metadata": (
+        _int,
+        [_vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _i64,
+         ctypes.c_int32, _vp],
+    ),
+    "psk_build_next_decode_metadata": (
+        _i64, [_i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp],
+    ),
     "psk_host_alloc": (_int, [_i64, ctypes.POINTER(ctypes.c_void_p)]),
     "psk_host_free": (_int, [_vp]),
     "psk_keyed_hash": (_int, [_vp, _i64, ctypes.c_uint64, _int, _vp]),

@@ -307,7 +307,7 @@ int psk_concat_and_cache_mla_fp8_tiles(const void* kv_c, const void* k_pe, void*
                                        int64_t rope_len, int64_t kv_c_stride, int64_t k_pe_stride,
                                        int64_t block_size, int64_t num_blocks, int64_t cache_block_stride,
                                        int64_t cache_page_stride, int in_dtype, void* stream) {
-  g_err[0] = 0;
+  begin_device_call();
   int tiles = 0, rope_off = 0;
   int st = check_tiles(nope_len, rope_len, &tiles, &rope_off);
   if (st != PSK_OK) return st;
@@ -367,7 +367,7 @@ int psk_gather_mla_fp8_tiles(const void* kv_cache, void* dst, const int32_t* blo
                              int64_t block_table_stride, int64_t num_tokens, int64_t nope_len, int64_t rope_len,
                              int64_t block_size, int64_t num_blocks, int64_t cache_block_stride,
                              int64_t cache_page_stride, int64_t dst_row_stride, int out_dtype, void* stream) {
-  g_err[0] = 0;
+  begin_device_call();
   int tiles = 0, rope_off = 0;
   int st = check_tiles(nope_len, rope_len, &tiles, &rope_off);
   if (st != PSK_OK) return st;

@@ -1645,7 +1645,7 @@ int psk_paged_decode_attention(const void* q, int64_t q_tok_stride, int64_t q_he
                                const float* k_descale, const float* v_descale, const int64_t* descale_strides,
                                void* out, int64_t out_tok_stride, int64_t out_head_stride, int out_dtype, float* lse,
                                int64_t lse_head_stride, float* workspace, int64_t workspace_len, void* stream) {
-  g_err[0] = 0;
+  begin_device_call();
   if (num_seqs < 0 || num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads)
     return fail(PSK_E_ARG, "bad head counts (q %lld, kv %lld)", (long long)num_q_heads, (long long)num_kv_heads);
   const int64_t G = num_q_heads / num_kv_heads;

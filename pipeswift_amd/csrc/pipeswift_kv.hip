@@ -755,6 +755,59 @@ __global__ void __launch_bounds__(256) amax_finalize_kernel(AmaxArgs a, int npar
 }
 
 // ----------------------------------------------------------------------------
+// graph static metadata: one launch refreshes every static field
+// ----------------------------------------------------------------------------
+
+// The captured decode step reads fixed buffers; before each replay they take
+// the live step's metadata, and with a padded batch (bsz < cg_bsz) the rows
+// past the batch are set so that padded graph rows never write the cache and
+// the readers see empty sequences.  One thread per element of the union of
+// the regions, grid-stride: no memset node, so the refresh itself may also be
+// captured.
+struct GraphMeta {
+  const int32_t* src_pt;  // [bsz, width] at src_pt_stride
+  const int64_t* src_slots;
+  const int32_t* src_lq;
+  const int32_t* src_lkv;
+  const int32_t* src_cu;  // [bsz + 1]
+  int32_t* dst_pt;        // [max_bsz, >= width] at dst_pt_stride
+  int64_t* dst_slots;     // [slot_cap]
+  int32_t* dst_lq;
+  int32_t* dst_lkv;
+  int32_t* dst_cu;        // [max_bsz + 1]
+  int64_t src_pt_stride, dst_pt_stride;
+  int64_t bsz, width, n_slots;
+  int64_t pt_rows;        // bsz, or max_bsz when padding
+  int64_t slot_end;       // n_slots, or slot_cap when padding
+  int64_t len_end;        // bsz, or max_bsz when padding
+  int32_t pad_q_len;
+  // ends of the regions in the flattened index space
+  int64_t e_pt, e_slot, e_lq, e_lkv, e_cu;
+};
+
+__global__ void __launch_bounds__(256) graph_meta_refresh_kernel(GraphMeta m) {
+  const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < m.e_cu; i += stride) {
+    if (i < m.e_pt) {
+      const int64_t r = i / m.width, c = i - r * m.width;
+      m.dst_pt[r * m.dst_pt_stride + c] = r < m.bsz ? m.src_pt[r * m.src_pt_stride + c] : 0;
+    } else if (i < m.e_slot) {
+      const int64_t k = i - m.e_pt;
+      m.dst_slots[k] = k < m.n_slots ? m.src_slots[k] : int64_t(-1);
+    } else if (i < m.e_lq) {
+      const int64_t k = i - m.e_slot;
+      m.dst_lq[k] = k < m.bsz ? m.src_lq[k] : m.pad_q_len;
+    } else if (i < m.e_lkv) {
+      const int64_t k = i - m.e_lq;
+      m.dst_lkv[k] = k < m.bsz ? m.src_lkv[k] : 0;
+    } else {
+      const int64_t k = i - m.e_lkv;
+      m.dst_cu[k] = k <= m.bsz ? m.src_cu[k] : m.src_cu[m.bsz] + int32_t(k - m.bsz) * m.pad_q_len;
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------
 // swap: blit kernel over (view, page) units reading/writing mapped host memory
 // ----------------------------------------------------------------------------
 
@@ -939,7 +992,7 @@ int psk_reshape_and_cache(const void* key, const void* value, void* key_cache, v
                           int64_t head_size, int64_t block_size, int64_t num_blocks, int64_t key_stride,
                           int64_t value_stride, const int64_t* kc, const int64_t* vc, int in_dtype,
                           int cache_dtype, const float* k_scale, const float* v_scale, void* stream) {
-  g_err[0] = 0;
+  begin_device_call();
   if (num_tokens < 0 || num_heads <= 0 || head_size <= 0 || block_size <= 0 || num_blocks < 0)
     return fail(PSK_E_ARG, "bad sizes: num_tokens=%lld num_heads=%lld head_size=%lld block_size=%lld num_blocks=%lld",
                 (long long)num_tokens, (long long)num_heads, (long long)head_size, (long long)block_size,
@@ -1027,7 +1080,7 @@ int psk_concat_and_cache_mla(const void* kv_c, const void* k_pe, void* kv_cache,
                              int64_t k_pe_stride, int64_t block_size, int64_t num_blocks,
                              int64_t cache_block_stride, int64_t cache_page_stride, int in_dtype, int cache_dtype,
                              const float* scale, void* stream) {
-  g_err[0] = 0;
+  begin_device_call();
   if (num_tokens < 0 || key_len <= 0 || value_len < 0 || block_size <= 0 || num_blocks < 0)
     return fail(PSK_E_ARG, "bad sizes: num_tokens=%lld key_len=%lld value_len=%lld block_size=%lld",
                 (long long)num_tokens, (long long)key_len, (long long)value_len, (long long)block_size);
@@ -1087,7 +1140,7 @@ int psk_gather_cache(const void* src0, const void* src1, void* dst0, void* dst1,
                      int64_t block_table_stride, int64_t num_tokens, int64_t row_len, int64_t block_size,
                      int64_t num_blocks, int64_t cache_block_stride, int64_t cache_page_stride,
                      int64_t dst_row_stride, int cache_dtype, int out_dtype, const float* scale, void* stream) {
-  g_err[0] = 0;
+  begin_device_call();
   if (batch_size < 0 || num_tokens < 0 || row_len <= 0 || block_size <= 0 || num_blocks < 0 ||
       block_table_stride < 0)
     return fail(PSK_E_ARG, "bad sizes: batch=%lld num_tokens=%lld row_len=%lld block_size=%lld",
@@ -1137,7 +1190,7 @@ int psk_gather_cache(const void* src0, const void* src1, void* dst0, void* dst1,
 int psk_copy_blocks(void* cache, int64_t num_layers, int64_t layer_stride, int64_t block_stride,
                     int64_t block_bytes, int64_t num_blocks, const int64_t* block_mapping, int64_t num_pairs,
                     void* stream) {
-  g_err[0] = 0;
+  begin_device_call();
   if (num_layers < 0 || num_pairs < 0 || block_bytes < 0 || num_blocks < 0 || layer_stride < 0 ||
       block_stride < 0)
     return fail(PSK_E_ARG, "bad sizes: layers=%lld pairs=%lld block_bytes=%lld", (long long)num_layers,
@@ -1209,7 +1262,7 @@ int psk_swap_blocks(int transport, const uint64_t* src_bases, const uint64_t* ds
                     const int64_t* dst_start, const int64_t* run_len, int64_t num_runs, int64_t src_num_pages,
                     int64_t dst_num_pages, void* staging, int64_t staging_bytes_avail, void* desc_dev,
                     int64_t desc_dev_bytes, void* stream) {
-  g_err[0] = 0;
+  begin_device_call();
   if (num_views < 0 || num_runs < 0) return fail(PSK_E_ARG, "negative view or run count");
   if (num_views == 0 || num_runs == 0) return PSK_OK;
   if (!src_bases || !dst_bases || !bytes_per_page || !src_start || !dst_start || !run_len)
@@ -1378,12 +1431,110 @@ int64_t psk_build_kv_metadata(int64_t num_seqs, const uint64_t* page_table_ptrs,
   return total;
 }
 
+int psk_refresh_graph_metadata(const int32_t* src_page_table, int64_t src_page_table_stride,
+                                const int64_t* src_slot_mapping, const int32_t* src_lens_q,
+                                const int32_t* src_lens_kv, const int32_t* src_cu_seqlens_q, int64_t bsz,
+                                int64_t width, int64_t num_slots, int32_t* dst_page_table,
+                                int64_t dst_page_table_stride, int64_t dst_page_table_width,
+                                int64_t* dst_slot_mapping, int64_t slot_capacity, int32_t* dst_lens_q,
+                                int32_t* dst_lens_kv, int32_t* dst_cu_seqlens_q, int64_t max_bsz, int64_t cg_bsz,
+                                int32_t pad_q_len, void* stream) {
+  begin_device_call();
+  if (bsz < 0 || width < 0 || num_slots < 0 || max_bsz < 0 || slot_capacity < 0)
+    return fail(PSK_E_ARG, "negative graph metadata size");
+  if (bsz > cg_bsz || cg_bsz > max_bsz)
+    return fail(PSK_E_ARG, "batch %lld does not fit the graph batch %lld of the static buffers (%lld rows)",
+                (long long)bsz, (long long)cg_bsz, (long long)max_bsz);
+  if (width > dst_page_table_width)
+    return fail(PSK_E_ARG, "page table width %lld exceeds the static width %lld", (long long)width,
+                (long long)dst_page_table_width);
+  if (num_slots > slot_capacity)
+    return fail(PSK_E_ARG, "%lld slots exceed the static slot_mapping capacity %lld", (long long)num_slots,
+                (long long)slot_capacity);
+  if (src_page_table_stride < width || dst_page_table_stride < dst_page_table_width)
+    return fail(PSK_E_ARG, "page table row stride smaller than its width");
+  const bool pad = bsz != cg_bsz;
+  if (pad && pad_q_len < 0) return fail(PSK_E_ARG, "negative pad_q_len");
+  if ((bsz && (!src_lens_q || !src_lens_kv)) || !src_cu_seqlens_q || !dst_cu_seqlens_q ||
+      (num_slots && !src_slot_mapping) || (bsz * width && !src_page_table) ||
+      ((pad ? max_bsz : bsz) * width && !dst_page_table) || ((pad ? slot_capacity : num_slots) && !dst_slot_mapping) ||
+      ((pad ? max_bsz : bsz) && (!dst_lens_q || !dst_lens_kv)))
+    return fail(PSK_E_ARG, "NULL metadata pointer");
+  GraphMeta m;
+  m.src_pt = src_page_table;
+  m.src_slots = src_slot_mapping;
+  m.src_lq = src_lens_q;
+  m.src_lkv = src_lens_kv;
+  m.src_cu = src_cu_seqlens_q;
+  m.dst_pt = dst_page_table;
+  m.dst_slots = dst_slot_mapping;
+  m.dst_lq = dst_lens_q;
+  m.dst_lkv = dst_lens_kv;
+  m.dst_cu = dst_cu_seqlens_q;
+  m.src_pt_stride = src_page_table_stride;
+  m.dst_pt_stride = dst_page_table_stride;
+  m.bsz = bsz;
+  m.width = width;
+  m.n_slots = num_slots;
+  m.pt_rows = pad ? max_bsz : bsz;
+  m.slot_end = pad ? slot_capacity : num_slots;
+  m.len_end = pad ? max_bsz : bsz;
+  m.pad_q_len = pad_q_len;
+  m.e_pt = m.pt_rows * width;
+  m.e_slot = m.e_pt + m.slot_end;
+  m.e_lq = m.e_slot + m.len_end;
+  m.e_lkv = m.e_lq + m.len_end;
+  m.e_cu = m.e_lkv + m.len_end + 1;
+  const int64_t blocks = ceil_div(m.e_cu, 256) < 1024 ? ceil_div(m.e_cu, 256) : 1024;
+  hipLaunchKernelGGL(graph_meta_refresh_kernel, dim3(unsigned(blocks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), m);
+  return check_launch("graph_meta_refresh_kernel launch");
+}
+
+int64_t psk_build_next_decode_metadata(int64_t num_seqs, const uint64_t* page_table_ptrs,
+                                       const int64_t* page_table_lens, const int64_t* positions,
+                                       const int32_t* lens_kv_prev, int64_t page_size, int64_t dcp_deg,
+                                       int64_t dcp_rank, int64_t dcp_interleave, int64_t* slot_mapping_out,
+                                       int32_t* lens_kv_out) {
+  g_err[0] = 0;
+  if (num_seqs < 0 || page_size <= 0 || dcp_deg <= 0 || dcp_rank < 0 || dcp_rank >= dcp_deg || dcp_interleave <= 0)
+    return fail(PSK_E_ARG, "bad decode metadata geometry (seqs=%lld page_size=%lld dcp=%lld/%lld interleave=%lld)",
+                (long long)num_seqs, (long long)page_size, (long long)dcp_rank, (long long)dcp_deg,
+                (long long)dcp_interleave);
+  if (dcp_deg > 1 && page_size % dcp_deg) return fail(PSK_E_ARG, "page_size must divide by the DCP degree");
+  if (num_seqs && (!page_table_ptrs || !page_table_lens || !positions || !lens_kv_prev || !slot_mapping_out ||
+                   !lens_kv_out))
+    return fail(PSK_E_ARG, "NULL array");
+  const int64_t phys = dcp_deg == 1 ? page_size : page_size / dcp_deg;
+  const int64_t stride = dcp_interleave * dcp_deg;
+  for (int64_t i = 0; i < num_seqs; ++i) {
+    const int64_t pos = positions[i];
+    if (pos < 0 || pos / page_size >= page_table_lens[i])
+      return fail(PSK_E_RANGE, "sequence %lld: position %lld needs page %lld of %lld", (long long)i, (long long)pos,
+                  (long long)(pos < 0 ? -1 : pos / page_size), (long long)page_table_lens[i]);
+    const int32_t* pt = reinterpret_cast<const int32_t*>(uintptr_t(page_table_ptrs[i]));
+    const int64_t page = pt[pos / page_size];
+    if (dcp_deg == 1) {
+      slot_mapping_out[i] = page * page_size + pos % page_size;
+      lens_kv_out[i] = lens_kv_prev[i] + 1;
+    } else if ((pos / dcp_interleave) % dcp_deg == dcp_rank) {
+      const int64_t local = pos % dcp_interleave + pos / stride * dcp_interleave;
+      slot_mapping_out[i] = page * phys + local % phys;
+      lens_kv_out[i] = lens_kv_prev[i] + 1;
+    } else {
+      slot_mapping_out[i] = -1;
+      lens_kv_out[i] = lens_kv_prev[i];
+    }
+  }
+  return num_seqs;
+}
+
 int64_t psk_kv_amax_workspace_len(void) { return kAmaxWsLen; }
 
 int psk_kv_amax_scale(const void* x0, const void* x1, int64_t rows, int64_t row_len, int64_t row_stride0,
                       int64_t row_stride1, int dtype, float qmax, float* scale_out, float* amax_out,
                       uint32_t* workspace, int64_t workspace_len, void* stream) {
-  g_err[0] = 0;
+  begin_device_call();
   if (rows < 0 || row_len < 0) return fail(PSK_E_ARG, "negative size");
   const int sz = dtype_size(dtype);
   if (!sz || dtype == PSK_DTYPE_FP8_E4M3FN) return fail(PSK_E_DTYPE, "amax input must be bf16, fp16 or fp32");

@@ -50,40 +50,6 @@ class KVCacheInfo:
     v_scale: Optional[torch.Tensor] = None
 
 
-def dcp_local_kv_len(prefix_len: int, dcp_deg: int, dcp_rank: int, dcp_interleave_size: int) -> int:
-    """Tokens of a prefix owned by one DCP rank (metadata.py:246-255)."""
-    stride = dcp_interleave_size * dcp_deg
-    n = prefix_len // stride * dcp_interleave_size
-    rem = prefix_len % stride
-    if rem >= (dcp_rank + 1) * dcp_interleave_size:
-        n += dcp_interleave_size
-    elif rem >= dcp_rank * dcp_interleave_size:
-        n += rem % dcp_interleave_size
-    return n
-
-
-def build_slot_mapping(page_table_row, start: int, end: int, page_size: int, dcp_deg: int = 1,
-                       dcp_rank: int = 0, dcp_interleave_size: int = 1) -> np.ndarray:
-    """int64 slots of positions [start, end) of one sequence (metadata.py:272-295).
-
-    dcp_deg == 1: slot = page_table[pos // ps] * ps + pos % ps.
-    DCP: a rank owns pos when (pos // interleave) % dcp == rank; its slot is
-    page_table[pos // ps] * (ps // dcp) + local_pos % (ps // dcp) with
-    local_pos = pos % interleave + pos // (interleave * dcp) * interleave;
-    positions of other ranks get -1.
-    """
-    pt = np.asarray(page_table_row, dtype=np.int64)
-    pos = np.arange(start, end, dtype=np.int64)
-    if dcp_deg == 1:
-        return pt[pos // page_size] * page_size + pos % page_size
-    phys = page_size // dcp_deg
-    stride = dcp_interleave_size * dcp_deg
-    owned = (pos // dcp_interleave_size) % dcp_deg == dcp_rank
-    local = pos % dcp_interleave_size + pos // stride * dcp_interleave_size
-    slots = pt[pos // page_size] * phys + local % phys
-    return np.where(owned, slots, -1).astype(np.int64)
-
-
 def coalesced_to_cuda(arr_list, device="cuda"):
     """One H2D copy for several small int arrays (impl_utils.py:340-358)."""
     arrs = []
@@ -249,25 +215,53 @@ def derive_kvcache_info_next_decode_step(
     device="cuda",
 ) -> KVCacheInfo:
     """Metadata for the next draft decode step (metadata.py:351-414): one new
-    token per sequence at position ``seq.offset``."""
-    assert len(seqs) != 0
-    lens_kv = prev.actual_lens_kv_cpu.numpy().astype(np.int32).copy()
-    slots = np.zeros(len(seqs), dtype=np.int64)
+    token per sequence at position ``seq.offset``; its slot, and lens_kv + 1
+    where this rank owns the token (always without DCP).
+
+    The per-sequence work runs natively (``psk_build_next_decode_metadata``)
+    into a pinned block that reaches the device in one asynchronous copy; the
+    page table, lens_q and cu_seqlens_q stay those of ``prev``."""
+    num_seqs = len(seqs)
+    assert num_seqs != 0
+    device = torch.device(device)
+    keep = []
+    ptrs = np.empty(num_seqs, dtype=np.uint64)
+    plen = np.empty(num_seqs, dtype=np.int64)
+    pos = np.empty(num_seqs, dtype=np.int64)
     for i, seq in enumerate(seqs):
-        s = build_slot_mapping(kv_page_table[seq.seq_id], seq.offset, seq.offset + 1, kv_page_size, dcp_deg,
-                               dcp_rank, dcp_interleave_size)[0]
-        slots[i] = s
-        if s >= 0:
-            lens_kv[i] += 1
-    slot_mapping = torch.from_numpy(slots).to(device, non_blocking=True)
-    lens_kv_cpu = torch.from_numpy(lens_kv)
+        ptrs[i], plen[i] = _page_ptr(kv_page_table[seq.seq_id], keep)
+        pos[i] = seq.offset
+    prev_kv = np.ascontiguousarray(prev.actual_lens_kv_cpu.numpy(), dtype=np.int32)
+    assert prev_kv.shape[0] >= num_seqs, "previous step has fewer sequences"
+    B = num_seqs
+    nbytes = 8 * B + 4 * B
+    on_gpu = device.type == "cuda"
+    stager = _stagers.setdefault(device if on_gpu else "cpu", _PinnedStager())
+    slot, blk = stager.acquire(nbytes)
+    base = blk.data_ptr()
+    got = lib().psk_build_next_decode_metadata(
+        B, ptrs.ctypes.data, plen.ctypes.data, pos.ctypes.data, prev_kv.ctypes.data, kv_page_size, dcp_deg,
+        dcp_rank, dcp_interleave_size, base, base + 8 * B,
+    )
+    if got < 0:
+        if got == -3:
+            raise IndexError(lib().psk_last_error().decode())
+        check(int(got), "derive_kvcache_info_next_decode_step")
+    host = blk[:nbytes]
+    if on_gpu:
+        dev = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        dev.copy_(host, non_blocking=True)
+        stager.release(slot, torch.cuda.current_stream(device))
+    else:
+        dev = host.clone()
+    lens_kv_cpu = host[8 * B:].clone().view(torch.int32)
     return KVCacheInfo(
         kv_cache=prev.kv_cache,
         mla_cache_tensor=prev.mla_cache_tensor,
         page_table=prev.page_table,
-        slot_mapping=slot_mapping,
+        slot_mapping=dev[: 8 * B].view(torch.int64),
         actual_lens_q=prev.actual_lens_q,
-        actual_lens_kv=lens_kv_cpu.to(device, non_blocking=True),
+        actual_lens_kv=dev[8 * B:].view(torch.int32),
         cu_seqlens_q=prev.cu_seqlens_q,
         actual_lens_q_cpu=prev.actual_lens_q_cpu,
         cu_seqlens_q_cpu=prev.cu_seqlens_q_cpu,

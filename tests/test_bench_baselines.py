@@ -7,7 +7,7 @@ import torch
 
 import bench
 from oracle import kv_oracle as O
-from pipeswift_amd import workloads
+import workloads
 
 
 def _u16(t):
@@ -42,3 +42,23 @@ def test_torch_gather_baseline_matches_oracle():
     bt, cu = cc.block_table.numpy(), cc.cu_seq_lens.numpy()
     assert np.array_equal(_u16(out[0]), O.gather_cache(_u16(cc.append.cache[:, 0]), bt, cu))
     assert np.array_equal(_u16(out[1]), O.gather_cache(_u16(cc.append.cache[:, 1]), bt, cu))
+
+
+def test_timed_launch_count_is_exactly_the_requested_steps():
+    """The bench captures exactly --steps launches (the driver runs --steps 20;
+    an earlier version replayed only whole 64-launch graphs and timed none)."""
+    for rotate in (1, 4, 8, 512):
+        for steps in (1, 5, 20, 63, 64, 65, 127, 2048):
+            sets = bench.launch_sets(steps, rotate)
+            assert len(sets) == steps
+            assert sets == [i % rotate for i in range(steps)]
+    assert bench.launch_sets(0, 8) == []
+
+
+def test_torch_mla_baseline_matches_oracle():
+    case = workloads.config4_mla(num_tokens=64, num_blocks=100, decode=True)
+    step, cache = bench.torch_cpu_mla_step(case, None)
+    step()
+    exp = np.zeros(tuple(case.cache.shape), np.uint16)
+    O.concat_and_cache_mla(_u16(case.kv_c), _u16(case.k_pe()), exp, case.slot_mapping.numpy())
+    assert np.array_equal(_u16(cache), exp)

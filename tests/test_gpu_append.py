@@ -9,7 +9,8 @@ import pytest
 import torch
 
 from oracle import kv_oracle as O
-from pipeswift_amd import cache_ops, impl_utils, metadata, workloads
+import workloads
+from pipeswift_amd import cache_ops, impl_utils, metadata
 from pipeswift_amd.reshape_and_cache import reshape_and_cache_flash, triton_reshape_and_cache_flash
 from tests.conftest import raw
 

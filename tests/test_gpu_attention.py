@@ -23,7 +23,8 @@ import pytest
 import torch
 
 from oracle import kv_oracle as O
-from pipeswift_amd import attention, cache_ops, workloads
+import workloads
+from pipeswift_amd import attention, cache_ops
 from pipeswift_amd.reshape_and_cache import reshape_and_cache_flash
 from tests.conftest import raw
 

@@ -5,7 +5,8 @@ import pytest
 import torch
 
 from oracle import kv_oracle as O
-from pipeswift_amd import cache_ops, copy_engine, workloads
+import workloads
+from pipeswift_amd import cache_ops, copy_engine
 from tests.conftest import raw
 
 pytestmark = pytest.mark.gpu

@@ -7,7 +7,8 @@ import numpy as np
 import pytest
 import torch
 
-from pipeswift_amd import attention, cache_ops, workloads
+import workloads
+from pipeswift_amd import attention, cache_ops
 from pipeswift_amd.reshape_and_cache import reshape_and_cache_flash_diffkv
 from tests.conftest import raw
 

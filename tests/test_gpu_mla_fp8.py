@@ -7,7 +7,8 @@ import pytest
 import torch
 
 from oracle import kv_oracle as O
-from pipeswift_amd import impl_utils, metadata, mla_fp8, workloads
+import workloads
+from pipeswift_amd import impl_utils, metadata, mla_fp8
 from tests.conftest import raw
 
 pytestmark = pytest.mark.gpu

@@ -5,7 +5,8 @@ import pytest
 import torch
 
 from oracle import kv_oracle as O
-from pipeswift_amd import cache_ops, impl_utils, metadata, workloads
+import workloads
+from pipeswift_amd import cache_ops, impl_utils, metadata
 from pipeswift_amd.reshape_and_cache import reshape_and_cache_flash, reshape_and_cache_flash_diffkv
 from tests.conftest import raw
 

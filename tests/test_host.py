@@ -2,12 +2,14 @@
 graph metadata refresh, the CopyEngine's coalescing and range check, and the
 shims' argument checks that fire before any device call."""
 
+from array import array
+
 import numpy as np
 import pytest
 import torch
 
 from oracle import kv_oracle as O
-from pipeswift_amd import cudagraph, metadata
+from pipeswift_amd import metadata
 from pipeswift_amd.copy_engine import CopyEngine, page_bytes
 
 
@@ -73,20 +75,69 @@ def test_next_decode_step_metadata():
     assert nxt.actual_lens_kv.tolist() == [41, 17]
 
 
-def test_graph_metadata_refresh_pads_with_minus_one():
-    static = cudagraph.initialize_graph_kvcacheinfo(8, 4, device="cpu")
-    assert (static.slot_mapping == -1).all()
-    info = metadata.KVCacheInfo(page_table=torch.ones(3, 2, dtype=torch.int32),
-                                slot_mapping=torch.tensor([5, 6, 7]), actual_lens_q=torch.ones(3, dtype=torch.int32),
-                                actual_lens_kv=torch.full((3,), 9, dtype=torch.int32),
-                                cu_seqlens_q=torch.arange(4, dtype=torch.int32))
-    static.slot_mapping.fill_(123)
-    cudagraph.set_graph_kvcacheinfo(static, info, 8)
-    assert static.slot_mapping.tolist() == [5, 6, 7, -1, -1, -1, -1, -1]
-    assert static.page_table[3:].abs().sum() == 0
-    assert static.cu_seqlens_q.tolist() == list(range(9))
-    sl = cudagraph.slice_kvcache_info(static, 3)
-    assert sl.slot_mapping.tolist() == [5, 6, 7] and sl.cg_bsz == 3
+def test_graph_refresh_oracle_hand_worked():
+    """The oracle of set_graph_kvcacheinfo (cudagraph.py:75-118) on a case
+    worked out by hand: 2 live sequences in a graph of 4, static buffers of 5
+    rows and 4 page columns, a 3-wide step page table, 2 tokens per sequence
+    (pad_q_len 2)."""
+    static = {"page_table": np.full((5, 4), 9, np.int32), "slot_mapping": np.full(10, 77, np.int64),
+              "lens_q": np.full(5, 7, np.int32), "lens_kv": np.full(5, 7, np.int32),
+              "cu_seqlens_q": np.full(6, 7, np.int32)}
+    step = {"page_table": np.array([[1, 2, 3], [4, 5, 0]], np.int32), "slot_mapping": np.array([16, 17, 64, 65]),
+            "lens_q": np.array([2, 2], np.int32), "lens_kv": np.array([40, 18], np.int32),
+            "cu_seqlens_q": np.array([0, 2, 4], np.int32)}
+    O.graph_refresh(static, step, cg_bsz=4, pad_q_len=2)
+    assert static["page_table"].tolist() == [[1, 2, 3, 9], [4, 5, 0, 9], [0, 0, 0, 9], [0, 0, 0, 9], [0, 0, 0, 9]]
+    assert static["slot_mapping"].tolist() == [16, 17, 64, 65, -1, -1, -1, -1, -1, -1]
+    assert static["lens_q"].tolist() == [2, 2, 2, 2, 2]
+    assert static["lens_kv"].tolist() == [40, 18, 0, 0, 0]
+    assert static["cu_seqlens_q"].tolist() == [0, 2, 4, 6, 8, 10]
+    # an unpadded refresh (bsz == cg_bsz) leaves everything past the batch alone
+    static2 = {k: v.copy() for k, v in static.items()}
+    step2 = {"page_table": np.array([[8, 8, 8]] * 4, np.int32), "slot_mapping": np.array([1, 2, 3, 4]),
+             "lens_q": np.ones(4, np.int32), "lens_kv": np.full(4, 3, np.int32),
+             "cu_seqlens_q": np.arange(5, dtype=np.int32)}
+    O.graph_refresh(static2, step2, cg_bsz=4, pad_q_len=1)
+    assert static2["page_table"][4].tolist() == [0, 0, 0, 9] and static2["slot_mapping"][4:].tolist() == [-1] * 6
+    assert static2["lens_q"].tolist() == [1, 1, 1, 1, 2] and static2["cu_seqlens_q"].tolist() == [0, 1, 2, 3, 4, 10]
+
+
+@pytest.mark.parametrize("dcp,il", [(1, 1), (2, 1), (2, 4), (4, 2)])
+def test_next_decode_step_native_matches_oracle(dcp, il):
+    rng = np.random.default_rng(dcp * 10 + il)
+    ps = 16
+    B = 37
+    for rank in range(dcp):
+        seqs, table, rows = [], {}, []
+        for b in range(B):
+            n = int(rng.integers(1, 300))
+            pages = (n + ps - 1) // ps
+            row = rng.permutation(5000)[:pages].astype(np.int32)
+            table[b] = array("i", row.tolist()) if b % 2 else row.tolist()
+            rows.append(row.tolist())
+            seqs.append(Seq(b, n, n - 1))
+        info = metadata.prepare_kv_info(seqs, table, ps, None, None, is_decode=True, dcp_deg=dcp, dcp_rank=rank,
+                                        dcp_interleave_size=il, device="cpu")
+        for s in seqs:
+            s.offset = len(s.token_ids) - 1
+        nxt = metadata.derive_kvcache_info_next_decode_step(info, seqs, table, ps, dcp_interleave_size=il,
+                                                            dcp_deg=dcp, dcp_rank=rank, device="cpu")
+        slots, lens = O.next_decode_step(rows, [s.offset for s in seqs], info.actual_lens_kv_cpu.tolist(), ps,
+                                         dcp, rank, il)
+        assert nxt.slot_mapping.tolist() == slots.tolist()
+        assert nxt.actual_lens_kv.tolist() == lens.tolist() == nxt.actual_lens_kv_cpu.tolist()
+        assert nxt.page_table is info.page_table and nxt.cu_seqlens_q is info.cu_seqlens_q
+
+
+def test_next_decode_step_position_without_page():
+    seqs = [Seq(0, 40, 39)]
+    table = {0: [5, 9, 2]}
+    info = metadata.prepare_kv_info(seqs, table, 16, None, None, is_decode=True, device="cpu")
+    seqs[0].offset = 48  # page 3 of a 3-page table
+    with pytest.raises(IndexError, match="needs page 3 of 3"):
+        metadata.derive_kvcache_info_next_decode_step(info, seqs, table, 16, device="cpu")
+    with pytest.raises(IndexError):
+        O.next_decode_step([[5, 9, 2]], [48], [40], 16)
 
 
 @pytest.mark.parametrize("seed", range(10))
