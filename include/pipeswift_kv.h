@@ -211,6 +211,23 @@ int psk_kv_amax_scale(const void* x0, const void* x1, int64_t rows, int64_t row_
 int64_t psk_kv_amax_workspace_len(void);
 
 /*
+ * psk_kv_amax_scale without a workspace argument: the partial maxima go to a
+ * scratch array inside the library (2 x 1024 uint32 words, 8 KiB per GPU, held
+ * until the process ends), so the call allocates nothing and needs no buffer
+ * beyond its inputs and outputs.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid allocation).  Results equal
+ * psk_kv_amax_scale's.  Every input size fits (the amax kernel writes at most
+ * 1024 partials per tensor).  The scratch needs no initial contents; each GPU
+ * has one, shared by every call on that GPU, so calls that overlap on one GPU
+ * (different streams, no ordering between them) race.  `stream` must belong
+ * to the current device; the first call on a device looks the scratch up.
+ */
+int psk_kv_amax_scale_noalloc(const void* x0, const void* x1, int64_t rows, int64_t row_len,
+                              int64_t row_stride0, int64_t row_stride1, int dtype, float qmax,
+                              float* scale_out, float* amax_out, void* stream);
+
+/*
  * Host-side step metadata (replaces the per-token Python loop of
  * prepare_kv_info, pipeswift/utils/metadata.py:206-348).  For sequence i with
  * page ids page_table_ptrs[i][0 .. page_table_lens[i]) (int32, host memory),

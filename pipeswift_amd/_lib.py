@@ -67,6 +67,10 @@ _SIGNATURES = {
         [_vp, _vp, _i64, _i64, _i64, _i64, _int, ctypes.c_float, _vp, _vp, _vp, _i64, _vp],
     ),
     "psk_kv_amax_workspace_len": (_i64, []),
+    "psk_kv_amax_scale_noalloc": (
+        _int,
+        [_vp, _vp, _i64, _i64, _i64, _i64, _int, ctypes.c_float, _vp, _vp, _vp],
+    ),
     "psk_build_kv_metadata": (
         _i64,
         [_i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _i64, _vp, _vp, _vp, _vp, _vp, _i64],

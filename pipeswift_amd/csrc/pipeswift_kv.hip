@@ -653,6 +653,37 @@ int64_t copy_blocks_lds(int64_t block_bytes, int waves) {
 constexpr int kAmaxMaxBlocks = 1024;
 constexpr int64_t kAmaxWsLen = 2 * int64_t(kAmaxMaxBlocks);
 
+}  // namespace
+
+// Scratch of psk_kv_amax_scale_noalloc: the partial maxima of two tensors,
+// kAmaxMaxBlocks each (8 KiB per GPU, held until the process ends).  Host code
+// never uses this name as an address: each device's copy is reached through
+// the pointer amax_scratch() obtains from hipGetSymbolAddress.
+static __device__ __align__(256) uint32_t scratch[kAmaxWsLen];
+
+namespace {
+
+// This device's address of `scratch`, looked up once per device (with that
+// device current) and kept; returns a status.
+int amax_scratch(uint32_t** out) {
+  static std::mutex mu;
+  static std::map<int, uint32_t*> ptrs;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = ptrs.find(dev);
+  if (it == ptrs.end()) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (!p) return fail(PSK_E_ARG, "hipGetSymbolAddress(scratch) returned NULL");
+    it = ptrs.emplace(dev, static_cast<uint32_t*>(p)).first;
+  }
+  *out = it->second;
+  return PSK_OK;
+}
+
 struct AmaxArgs {
   const char* x0;
   const char* x1;
@@ -1594,6 +1625,21 @@ int psk_kv_amax_scale(const void* x0, const void* x1, int64_t rows, int64_t row_
   if (st1 != PSK_OK) return st1;
   hipLaunchKernelGGL(amax_finalize_kernel, dim3(1), dim3(256), 0, st, a, int(blocks), x1 ? 2 : 1);
   return check_launch("amax_finalize_kernel launch");
+}
+
+int psk_kv_amax_scale_noalloc(const void* x0, const void* x1, int64_t rows, int64_t row_len, int64_t row_stride0,
+                              int64_t row_stride1, int dtype, float qmax, float* scale_out, float* amax_out,
+                              void* stream) {
+  begin_device_call();
+  uint32_t* ws = nullptr;
+  const int st = amax_scratch(&ws);
+  if (st != PSK_OK) return st;
+  // The amax kernel writes at most kAmaxMaxBlocks partial maxima per tensor
+  // whatever the input size (its grid is capped there and each thread strides
+  // over the rest), so every input fits the scratch; the workspace check of
+  // psk_kv_amax_scale rejects any change that would break that.
+  return psk_kv_amax_scale(x0, x1, rows, row_len, row_stride0, row_stride1, dtype, qmax, scale_out, amax_out, ws,
+                           kAmaxWsLen, stream);
 }
 
 int psk_host_alloc(int64_t bytes, void** ptr) {
