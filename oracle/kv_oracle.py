@@ -123,19 +123,35 @@ def e4m3fn_to_f32(q: np.ndarray) -> np.ndarray:
     return _e4m3_table()[np.asarray(q, dtype=np.uint8)]
 
 
-def quantize_e4m3(x: np.ndarray, scale: float = 1.0) -> np.ndarray:
-    """q = e4m3fn(clamp(float32(x) / scale, -448, 448)), NaN kept as NaN.
+NAN_TORCH = "torch"          # torch.clamp keeps a NaN: byte 0x7F | sign of the input
+NAN_CLAMP_MIN = "clamp_min"  # Triton's tl.minimum(tl.maximum(x, -448), 448): -448, byte 0xFE
 
-    At scale 1.0 this is the reference's FP8 append (reshape_and_cache.py:66-77)
-    and ``fp8_kv.quantize`` (fp8_kv.py:75-77); the division by a per-tensor
-    fp32 scale is the build's extension.  torch.clamp propagates NaN, so a NaN
-    input becomes 0x7F|sign.
+
+def quantize_e4m3(x: np.ndarray, scale: float = 1.0, nan: str = NAN_TORCH) -> np.ndarray:
+    """q = e4m3fn(clamp(float32(x) / scale, -448, 448)).
+
+    At scale 1.0 this is ``fp8_kv.quantize`` (fp8_kv.py:75-77) and the
+    reference's FP8 append (reshape_and_cache.py:66-77); the division by a
+    per-tensor fp32 scale is the build's extension.  A NaN quotient follows
+    ``nan``: NAN_TORCH, torch.clamp's propagation (fp8_kv.quantize), stores
+    0x7F with the input's sign; NAN_CLAMP_MIN, the append's Triton clamp,
+    stores -448 (0xFE): tl.minimum / tl.maximum default to PropagateNan.NONE,
+    i.e. LLVM minnum / maxnum, which return the non-NaN operand
+    (triton/language/core.py:2506,2528 and semantic.py:380-381, Triton 3.6).
     """
     x = np.asarray(x, dtype=np.float32)
     with np.errstate(invalid="ignore", divide="ignore", over="ignore"):
         y = (x / np.float32(scale)).astype(np.float32)
-    y = np.where(np.isnan(y), y, np.clip(y, -FP8_E4M3_MAX, FP8_E4M3_MAX)).astype(np.float32)
-    return e4m3fn_from_f32(y)
+    nanq = np.isnan(y)
+    y = np.where(nanq, np.float32(0.0), np.clip(y, -FP8_E4M3_MAX, FP8_E4M3_MAX)).astype(np.float32)
+    q = e4m3fn_from_f32(y)
+    if nan == NAN_CLAMP_MIN:
+        q[nanq] = 0xFE
+    elif nan == NAN_TORCH:
+        q[nanq] = 0x7F | (np.signbit(x[nanq]).astype(np.uint8) << 7)
+    else:
+        raise ValueError(f"unknown NaN policy {nan}")
+    return q
 
 
 def dequantize_e4m3(q: np.ndarray, scale: float, out_dtype: str) -> np.ndarray:
@@ -161,7 +177,7 @@ def _write_rows(cache, tok, blk, off, rows, in_dtype, cache_dtype, scale):
     if cache_dtype == in_dtype:
         vals = rows[tok]
     elif cache_dtype == "fp8":
-        vals = quantize_e4m3(to_f32(rows[tok], in_dtype), 1.0 if scale is None else scale)
+        vals = quantize_e4m3(to_f32(rows[tok], in_dtype), 1.0 if scale is None else scale, NAN_CLAMP_MIN)
     else:
         raise ValueError(f"cache dtype {cache_dtype} vs input {in_dtype}")
     cache[blk, off] = vals.reshape((len(tok),) + cache.shape[2:])
@@ -196,7 +212,7 @@ def concat_and_cache_mla(kv_c, k_pe, kv_cache, slot_mapping, in_dtype="bf16", ca
     if cache_dtype == in_dtype:
         kv_cache[blk, off] = row.reshape((len(tok),) + kv_cache.shape[2:])
     elif cache_dtype == "fp8":
-        q = quantize_e4m3(to_f32(row, in_dtype), 1.0 if scale is None else scale)
+        q = quantize_e4m3(to_f32(row, in_dtype), 1.0 if scale is None else scale, NAN_CLAMP_MIN)
         kv_cache[blk, off] = q.reshape((len(tok),) + kv_cache.shape[2:])
     else:
         raise ValueError(f"cache dtype {cache_dtype} vs input {in_dtype}")

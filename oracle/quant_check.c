@@ -1,40 +1,46 @@
 /*
  * quant_check.c -- TEST INFRASTRUCTURE (checker only, never shipped or timed).
  *
- * Host restatement of the division inside the FP8 quantizer of the append
- * kernels (pipeswift_amd/csrc/psk_common.h: make_qscale, div_fast, QuantConv)
- * and sweeps that compare it with the IEEE fp32 quotient, which is what the
- * reference's quantization computes: x.float() / scale, clamp to +-448, then
- * float8_e4m3fn (reference: pipeswift/utils/fp8_kv.py:75-77 at scale 1,
+ * Host restatement of the FP8 quantizer of the append kernels
+ * (pipeswift_amd/csrc/psk_common.h: make_qscale, QuantConv) and sweeps that
+ * compare its bytes with those of the IEEE fp32 quotient path, which is what
+ * the reference's quantization computes: x.float() / scale, clamp to +-448,
+ * then float8_e4m3fn (reference: pipeswift/utils/fp8_kv.py:75-77 at scale 1,
  * pipeswift/utils/triton_kernels/reshape_and_cache.py:66-77).
  *
  * The kernel sequence, for a per-tensor scale s (the same in every lane):
- *   r    = RN(1 / s)                           once per wave
+ *   r    = RN(1 / |s|)                         once per wave
  *   fast = 2^-80 <= |s| < 2^100
- *   fast:  y = RN(x * r);  e = fma(-y, s, x);  z = copysign(fma(e, r, y), y)
- *          quotient = |y| < inf ? z : y          (BOUNDED variant: z)
- *   else:  quotient = x / s                     (IEEE division)
- *   byte = e4m3fn_rne(med3(quotient, -448, 448)), NaN -> 0x7F | sign
+ *   fast:  a = |x|;  y = RN(a * r);  e = fma(-y, |s|, a);  m = fma(e, r, y)
+ *   else:  m = |x| / |s|                         (IEEE division)
+ *   byte = e4m3fn_rne(min(m, 448)) | (sign(x) ^ sign(s))
+ *          (min: the kernel's unsigned min on the bits of m >= +0 or NaN,
+ *           the same as IEEE minNum there: NaN and +inf -> 448)
+ *   NaN quotient (fast: x is NaN; else: m is NaN) -> policy byte:
+ *          0xFE (clamp_min, the reference's Triton clamp) or 0x7F | sign(x) (torch)
+ * The IEEE path: q = x / s; NaN -> the same policy byte; else
+ *   byte = e4m3fn_rne(clamp(q, -448, 448)).
  * The GPU code runs with f32 denormals preserved (IEEE mode); x86 SSE arithmetic
  * without FTZ/DAZ is the same IEEE binary32 arithmetic, and fmaf is the fused
  * multiply-add with one rounding, as v_fma_f32.  Build without -ffast-math.
  *
  * Exported for ctypes (tests/test_quant_division.py):
- *   qc_e4m3(x, n, out)                   E4M3FN RNE bytes of clamped fp32 values
- *   qc_quantize(x, n, s, bounded, out)   the kernel's bytes for one scale
+ *   qc_e4m3(x, n, out)                   E4M3FN RNE bytes of clamp(x), NaN -> 0x7F|sign
+ *   qc_quantize(x, n, s, policy, out)    the kernel's bytes for one scale
  *   qc_sweep_all(kind, amax_kind, variant, out, bad)  every 16-bit input
  *        pattern (bf16 or f16) x every scale RN(a / 448) for a over all finite
  *        positive 16-bit patterns of amax_kind
  *   qc_sweep_random(seed, n, mode, variant, out, bad)  sampled fp32 inputs and
  *        scales
- * Sweep counters out[0..5]: cases, fast-path cases, quotient mismatches (bit
- * patterns, NaN == NaN), byte mismatches, BOUNDED-variant quotient mismatches
- * (counted where |x| <= 448 * s, the only inputs that variant receives), and
- * quotient mismatches whose IEEE quotient is not below 2^-20 in magnitude.
- * Quotients below 2^-20 convert to a signed zero in E4M3 (its smallest
- * subnormal is 2^-9), so there only the sign has to agree; the kernel's
- * sequence may leave such a quotient inexact when |x| < 2^-100.
- * bad[0..2]: the first mismatching (x bits, s bits, kernel quotient bits).
+ * Sweep counters out[0..4]: cases, fast-path cases, clamped-magnitude
+ * mismatches (min(m, 448) against |clamp(x / s)| bit for bit, where the IEEE
+ * quotient is not NaN), byte mismatches (both NaN policies), and magnitude
+ * mismatches where |clamp(x / s)| is not below 2^-20.  Magnitudes below 2^-20
+ * convert to a signed zero in E4M3 (its smallest subnormal is 2^-9), so there
+ * only the sign has to agree; the kernel's sequence may leave such a quotient
+ * inexact when |x| < 2^-100.
+ * bad[0..2]: the first byte-mismatching (x bits, s bits, kernel magnitude bits),
+ * or the first magnitude mismatch when no byte differs.
  */
 #include <math.h>
 #include <stdint.h>
@@ -73,48 +79,77 @@ static inline uint8_t e4m3_of_clamped(float v) {
 
 static inline float med3_448(float q) { return q < -448.0f ? -448.0f : (q > 448.0f ? 448.0f : q); }
 
-static inline uint8_t byte_of_quotient(float q) { return isnan(q) ? e4m3_of_clamped(q) : e4m3_of_clamped(med3_448(q)); }
+static inline uint8_t sign_of(float x) { return (uint8_t)((fbits(x) >> 24) & 0x80u); }
+
+static inline uint8_t nan_byte(float x, int policy) { return policy == 0 ? (uint8_t)0xFE : (uint8_t)(0x7Fu | sign_of(x)); }
 
 typedef struct {
-  float s, r;
+  float s, r;   /* |scale| and RN(1 / |scale|) */
   int fast;
+  uint8_t neg;  /* 0x80 for a negative scale: flips every output sign */
+  float raw;    /* the scale as given */
 } qscale;
 
 static inline qscale make_qscale(float s) {
   qscale q;
-  q.s = s;
-  q.r = 1.0f / s;
-  const float a = fabsf(s);
-  q.fast = a >= 0x1p-80f && a < 0x1p100f;
+  q.raw = s;
+  q.s = fabsf(s);
+  q.r = 1.0f / q.s;
+  q.fast = q.s >= 0x1p-80f && q.s < 0x1p100f;
+  q.neg = signbit(s) ? 0x80 : 0;
   return q;
 }
 
 /* variant 0 is the kernel's sequence.  The others are planted mistakes for
  * the tests to show that the sweeps detect them: 1 drops the FMA correction
- * (the quotient is RN(x * RN(1/s))), 2 drops the range gate (every scale takes
- * the reciprocal path). */
+ * (the magnitude is RN(|x| * RN(1/s))), 2 drops the range gate (every scale
+ * takes the reciprocal path). */
 static int g_variant = 0;
 
-static inline float kernel_quotient(float x, const qscale* q, int bounded) {
-  if (!q->fast && g_variant != 2) return x / q->s;
-  const float y = x * q->r;
-  if (g_variant == 1) return y;
-  const float e = fmaf(-y, q->s, x);
-  const float z = copysignf(fmaf(e, q->r, y), y);
-  if (bounded) return z;
-  return fabsf(y) < INFINITY ? z : y;
+/* The kernel's byte; *mag = min(m, 448), the value the converter receives. */
+static inline uint8_t kernel_byte(float x, const qscale* q, int policy, float* mag) {
+  float m;
+  int nanq;
+  if (q->fast || g_variant == 2) {
+    const float a = fabsf(x);
+    const float y = a * q->r;
+    if (g_variant == 1) {
+      m = y;
+    } else {
+      const float e = fmaf(-y, q->s, a);
+      m = fmaf(e, q->r, y);
+    }
+    nanq = isnan(x);
+  } else {
+    m = fabsf(x) / q->s;
+    nanq = isnan(m);
+  }
+  *mag = fminf(m, 448.0f);
+  if (nanq) return nan_byte(x, policy);
+  return (uint8_t)(e4m3_of_clamped(*mag) | (sign_of(x) ^ q->neg));
 }
 
-static inline int same_float(float a, float b) { return (isnan(a) && isnan(b)) || fbits(a) == fbits(b); }
+/* The IEEE quotient path's byte; *mag = |clamp(x / s)| or NaN. */
+static inline uint8_t ieee_byte(float x, float s, int policy, float* mag) {
+  const float qv = x / s;
+  if (isnan(qv)) {
+    *mag = NAN;
+    return nan_byte(x, policy);
+  }
+  const float c = med3_448(qv);
+  *mag = fabsf(c);
+  return e4m3_of_clamped(c);
+}
 
 void qc_e4m3(const float* x, int64_t n, uint8_t* out) {
-  for (int64_t i = 0; i < n; ++i) out[i] = byte_of_quotient(x[i]);
+  for (int64_t i = 0; i < n; ++i) out[i] = isnan(x[i]) ? nan_byte(x[i], 1) : e4m3_of_clamped(med3_448(x[i]));
 }
 
-void qc_quantize(const float* x, int64_t n, float s, int bounded, uint8_t* out) {
+void qc_quantize(const float* x, int64_t n, float s, int policy, uint8_t* out) {
   g_variant = 0;
   const qscale q = make_qscale(s);
-  for (int64_t i = 0; i < n; ++i) out[i] = byte_of_quotient(kernel_quotient(x[i], &q, bounded));
+  float mag;
+  for (int64_t i = 0; i < n; ++i) out[i] = kernel_byte(x[i], &q, policy, &mag);
 }
 
 static float half_to_float(uint16_t h) {
@@ -133,53 +168,55 @@ static float pattern_to_float(int kind, uint32_t p) {
 }
 
 typedef struct {
-  int64_t cases, fast, quot_bad, byte_bad, bounded_bad, big_bad;
+  int64_t cases, fast, mag_bad, byte_bad, big_bad;
   uint32_t bad[3];
-  int have_bad;
+  int have_bad, have_byte_bad;
 } tally;
 
 static inline void check_one(float x, const qscale* q, tally* t) {
-  const float ref = x / q->s;
-  const float got = kernel_quotient(x, q, 0);
   t->cases++;
   t->fast += q->fast;
-  if (!same_float(got, ref)) {
-    t->quot_bad++;
-    if (byte_of_quotient(got) != byte_of_quotient(ref)) t->byte_bad++;
-    if (!(fabsf(ref) < 0x1p-20f)) t->big_bad++;
-    if (!t->have_bad) {
-      t->bad[0] = fbits(x);
-      t->bad[1] = fbits(q->s);
-      t->bad[2] = fbits(got);
-      t->have_bad = 1;
-    }
+  int byte_bad = 0, mag_bad = 0;
+  float km = 0.0f, rm = 0.0f;
+  for (int policy = 0; policy < 2; ++policy) {
+    const uint8_t kb = kernel_byte(x, q, policy, &km);
+    const uint8_t rb = ieee_byte(x, q->raw, policy, &rm);
+    byte_bad |= kb != rb;
   }
-  if (q->fast && fabsf(x) <= 448.0f * q->s) {
-    const float gb = kernel_quotient(x, q, 1);
-    if (!same_float(gb, ref)) t->bounded_bad++;
+  if (!isnan(rm) && fbits(km) != fbits(rm)) {
+    mag_bad = 1;
+    t->mag_bad++;
+    if (!(rm < 0x1p-20f)) t->big_bad++;
+  }
+  if (byte_bad) t->byte_bad++;
+  if ((byte_bad && !t->have_byte_bad) || (mag_bad && !t->have_bad)) {
+    t->bad[0] = fbits(x);
+    t->bad[1] = fbits(q->s);
+    t->bad[2] = fbits(km);
+    t->have_bad = 1;
+    t->have_byte_bad |= byte_bad;
   }
 }
 
 static void merge(tally* dst, const tally* src) {
   dst->cases += src->cases;
   dst->fast += src->fast;
-  dst->quot_bad += src->quot_bad;
+  dst->mag_bad += src->mag_bad;
   dst->byte_bad += src->byte_bad;
-  dst->bounded_bad += src->bounded_bad;
   dst->big_bad += src->big_bad;
-  if (!dst->have_bad && src->have_bad) {
+  if ((src->have_byte_bad && !dst->have_byte_bad) || (src->have_bad && !dst->have_bad)) {
     memcpy(dst->bad, src->bad, sizeof(dst->bad));
     dst->have_bad = 1;
+    dst->have_byte_bad |= src->have_byte_bad;
   }
 }
 
 static void emit(const tally* t, int64_t* out, uint32_t* bad) {
   out[0] = t->cases;
   out[1] = t->fast;
-  out[2] = t->quot_bad;
+  out[2] = t->mag_bad;
   out[3] = t->byte_bad;
-  out[4] = t->bounded_bad;
-  out[5] = t->big_bad;
+  out[4] = t->big_bad;
   if (bad) memcpy(bad, t->bad, sizeof(t->bad));
 }
 

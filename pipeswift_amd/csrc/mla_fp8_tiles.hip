@@ -83,6 +83,7 @@ __device__ __forceinline__ float tile_scale(float amax) {
   k.s = 448.0f;
   k.r = 1.0f / 448.0f;
   k.fast = true;
+  k.neg = 0u;
   const float q = amax >= 0x1p-90f ? div_fast(amax, k) : amax / 448.0f;
   return __builtin_fmaxf(q, kMinScale);
 }
@@ -151,10 +152,10 @@ __global__ void __launch_bounds__(kWaves * 64) tile_fp8_append_kernel(TileAppend
     // every lane takes part in the row max (inactive rows reduce zeros)
     const float s = tile_scale(__uint_as_float(row16_max_bits(amax8_bits(x))));
     if (active) {
-      // on the fast path s is finite and at least amax / 448, so no element is
-      // infinite and no quotient overflows: the bounded division applies
+      // NaN inputs store 0x7F with their sign (kNanTorch), as the tile's own
+      // rule has it
       const QScale qs = make_qscale(s);
-      u32x2 q = QuantConv<PSK_DTYPE_BF16, 8, true>::apply(x, qs);
+      u32x2 q = QuantConv<PSK_DTYPE_BF16, 8, kNanTorch>::apply(x, qs);
       if (__builtin_expect(__builtin_isinf(s), 0)) {
         // A tile holding an infinity has s = inf, and +-inf / inf is a NaN
         // whose sign the division does not define: store 0x7F with the sign
@@ -255,6 +256,7 @@ __global__ void __launch_bounds__(kWaves * 64) tile_fp8_gather_kernel(TileGather
     qs.s = 0.0f;
     qs.r = 0.0f;
     qs.fast = false;
+    qs.neg = 0u;
     if (rd) {
       if constexpr (NV == 8) {
         q = vload_nt<8>(entry + e);

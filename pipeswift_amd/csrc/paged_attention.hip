@@ -237,7 +237,7 @@ __device__ __forceinline__ void load_query_as(const char* src, float qd, int d0,
   } else {
     constexpr int kEsz = Elt<Q_DT>::kSize;
     constexpr int E = 16 / kEsz;  // elements per 16-byte load
-    using QC = QuantConv<Q_DT, E>;
+    using QC = QuantConv<Q_DT, E, kNanTorch>;  // the query is quantized as fp8_kv.quantize does
     const QScale qs = make_qscale(qd);
     uint8_t bytes[32];
 #pragma unroll

@@ -402,6 +402,7 @@ __global__ void __launch_bounds__(256) paged_gather_kernel(GatherGeom g) {
     qs.s = g.scale ? sv : 1.0f;
     qs.r = 0.0f;
     qs.fast = false;
+    qs.neg = 0u;
   }
 
   // Sequence lookup without a chain of dependent loads.  The lanes hold a

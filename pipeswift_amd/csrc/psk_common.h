@@ -199,18 +199,22 @@ __device__ __forceinline__ f32x2 e4m3_unpack2(uint32_t w, bool hi) {
 // Any other scale (|s| outside [2^-80, 2^100): 0, inf, NaN, tiny) takes the
 // plain IEEE division.  At s == 1.0 (the reference's fixed scale) r = 1, y = x
 // and e = 0, so the quotient is x.
+// QScale keeps |s| and 1 / |s|; the sign of a negative scale (which no caller
+// passes, but the C ABI accepts) is a byte mask that QuantConv puts onto the
+// signs of its outputs, so the quotients it divides are never negative.
 struct QScale {
-  float s;
-  float r;
+  float s;        // |scale|
+  float r;        // RN(1 / |scale|)
   bool fast;
+  uint32_t neg;   // 0x80808080 for a negative scale, else 0
 };
 
 __device__ __forceinline__ QScale make_qscale(float s) {
   QScale q;
-  q.s = s;
-  q.r = 1.0f / s;
-  const float a = __builtin_fabsf(s);
-  q.fast = a >= 0x1p-80f && a < 0x1p100f;
+  q.s = __builtin_fabsf(s);
+  q.r = 1.0f / q.s;
+  q.fast = q.s >= 0x1p-80f && q.s < 0x1p100f;
+  q.neg = __builtin_signbit(s) ? 0x80808080u : 0u;
   return q;
 }
 
@@ -249,11 +253,29 @@ struct CopyConv {
   __device__ static Out zero() { return Out(0); }
 };
 
-// E input elements of type IN_DT -> E E4M3FN bytes, q = e4m3(clamp(x / scale)).
-// The clamp is v_med3_f32 (exact for every non-NaN input, +-inf included);
-// the native convert turns NaN into 0xFF, so NaN lanes are patched to torch's
-// 0x7F|sign afterwards (rare path).
-template <int IN_DT, int E, bool BOUNDED = false>
+// What a NaN quotient stores.  kNanClampMin: the byte of -448 (0xFE), which
+// is what the reference's append stores: its clamp min(max(x, -448), 448) is
+// Triton's tl.minimum / tl.maximum, whose default PropagateNan.NONE lowers to
+// minnum / maxnum, and maxnum(NaN, -448) = -448 (reshape_and_cache.py:70-75;
+// triton/language/core.py:2506,2528, semantic.py:380-381 in Triton 3.6).
+// kNanTorch: 0x7F with the input's sign, torch's clamp-then-convert, which the
+// reference's query quantizer uses (fp8_kv.py:75-77).
+enum NanPolicy { kNanClampMin = 0, kNanTorch = 1 };
+
+// E input elements of type IN_DT -> E E4M3FN bytes, q = e4m3(clamp(x / scale)),
+// in sign-magnitude form (E4M3 is sign-magnitude and scales are positive):
+//   m = |x| / s    (div_fast's sequence on |x|; |x| is a free source
+//                   modifier, and a non-negative quotient needs no copysign)
+//   byte = e4m3(min(m, 448)) | sign(x)
+// One v_min_f32 both clamps and handles the infinite quotients: IEEE-mode min
+// returns the non-NaN operand, so the NaN that the correction step makes of an
+// infinite quotient (|x| infinite, or |x| / s overflowing) becomes 448, as the
+// clamp of an infinite quotient does.  A NaN quotient (a NaN input, or 0/0,
+// inf/inf and x/NaN for a scale outside the gate) is rewritten by the policy
+// afterwards (rare path).  Every element costs the multiply and two FMAs of
+// the division, one min, half a packed convert and the sign's move onto the
+// byte.  Scales outside [2^-80, 2^100) take the IEEE division of |x| by |s|.
+template <int IN_DT, int E, int NAN_POLICY = kNanClampMin>
 struct QuantConv {
   using EltT = Elt<IN_DT>;
   static constexpr int IN_B = E * EltT::kSize;
@@ -263,37 +285,85 @@ struct QuantConv {
   __device__ static Out apply(In v, const QScale& qs) {
     typename EltT::Bits e[E];
     __builtin_memcpy(e, &v, sizeof(v));
-    float f[E];
+    float m[E];
+    bool any_nan = false;
     if (__builtin_expect(qs.fast, 1)) {
 #pragma unroll
-      for (int i = 0; i < E; ++i) f[i] = div_fast<BOUNDED>(EltT::to_f32(e[i]), qs);
+      for (int i = 0; i < E; ++i) {
+        const float x = EltT::to_f32(e[i]);
+        any_nan |= __builtin_isnan(x);
+        const float a = __builtin_fabsf(x);
+        const float y = a * qs.r;
+        const float r = __builtin_fmaf(-y, qs.s, a);
+        m[i] = __builtin_fmaf(r, qs.r, y);
+      }
     } else {
       // scales outside [2^-80, 2^100) (0, inf, NaN, subnormal): IEEE division.
       // The empty volatile asm keeps this a branch: otherwise the compiler
       // computes both paths for every element and selects.
       asm volatile("");
 #pragma unroll
-      for (int i = 0; i < E; ++i) f[i] = EltT::to_f32(e[i]) / qs.s;
+      for (int i = 0; i < E; ++i) {
+        m[i] = __builtin_fabsf(EltT::to_f32(e[i])) / qs.s;
+        any_nan |= __builtin_isnan(m[i]);
+      }
     }
-    bool any_nan = false;
+    // Clamp: m is +0..+inf or a NaN, and for such bit patterns the unsigned
+    // order is the float order with every NaN above +inf, so one v_min_u32
+    // against 448's bits clamps and sends inf and NaN to 448 (a float min
+    // would first canonicalize its input, one more instruction).
+    uint32_t c[E];
 #pragma unroll
-    for (int i = 0; i < E; ++i) any_nan |= __builtin_isnan(f[i]);
-    uint8_t o[E];
-#pragma unroll
-    for (int i = 0; i < E; i += 2) {
-      const float a = __builtin_amdgcn_fmed3f(f[i], -448.0f, 448.0f);
-      const float b = i + 1 < E ? __builtin_amdgcn_fmed3f(f[i + 1], -448.0f, 448.0f) : 0.0f;
-      const uint32_t w = uint32_t(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false));
-      o[i] = uint8_t(w);
-      if (i + 1 < E) o[i + 1] = uint8_t(w >> 8);
+    for (int i = 0; i < E; ++i) {
+      const uint32_t b = __float_as_uint(m[i]);
+      c[i] = b < 0x43E00000u ? b : 0x43E00000u;
     }
-    if (__builtin_expect(any_nan, 0)) {
+    // Four elements per word: two packed converts into its halves, then the
+    // inputs' sign bits onto the four bytes.
+    constexpr int NW = (E + 3) / 4;
+    uint32_t q[NW];
+#pragma unroll
+    for (int g = 0; g < NW; ++g) {
+      const int i = 4 * g;
+      // the high half of `old` is overwritten below or not stored
+      uint32_t w = uint32_t(__builtin_amdgcn_cvt_pk_fp8_f32(__uint_as_float(c[i]),
+                                                             i + 1 < E ? __uint_as_float(c[i + 1]) : 0.0f,
+                                                             int(c[i]), false));
+      if (i + 2 < E)
+        w = uint32_t(__builtin_amdgcn_cvt_pk_fp8_f32(__uint_as_float(c[i + 2]),
+                                                      i + 3 < E ? __uint_as_float(c[i + 3]) : 0.0f, int(w), true));
+      q[g] = w;
+    }
+    if constexpr (EltT::kSize == 2 && E >= 2) {
+      // the high byte of every 16-bit input holds its sign bit
+      uint32_t in[E / 2];
+      __builtin_memcpy(in, &v, sizeof(in));
+#pragma unroll
+      for (int g = 0; g < NW; ++g) {
+        const uint32_t sg = E >= 4 ? __builtin_amdgcn_perm(in[2 * g + 1], in[2 * g], 0x07050301u)
+                                   : __builtin_amdgcn_perm(0u, in[0], 0x0C0C0301u);
+        q[g] |= (sg ^ qs.neg) & 0x80808080u;
+      }
+    } else {
 #pragma unroll
       for (int i = 0; i < E; ++i)
-        if (__builtin_isnan(f[i])) o[i] = uint8_t(e4m3_nan_byte(f[i]));
+        q[i / 4] |= (((uint32_t(e[i]) >> (8 * EltT::kSize - 8)) ^ qs.neg) & 0x80u) << (8 * (i % 4));
+    }
+    if (__builtin_expect(any_nan, 0)) {
+      // the NaN quotients: NaN inputs on the fast path (its NaN m of an
+      // infinite quotient is not one), NaN m on the IEEE path
+#pragma unroll
+      for (int i = 0; i < E; ++i) {
+        const float x = EltT::to_f32(e[i]);
+        if (qs.fast ? __builtin_isnan(x) : __builtin_isnan(m[i])) {
+          const uint32_t nb = NAN_POLICY == kNanClampMin ? 0xFEu : e4m3_nan_byte(x);
+          const int sh = 8 * (i % 4);
+          q[i / 4] = (q[i / 4] & ~(0xFFu << sh)) | (nb << sh);
+        }
+      }
     }
     Out r;
-    __builtin_memcpy(&r, o, sizeof(r));
+    __builtin_memcpy(&r, q, sizeof(r));
     return r;
   }
   __device__ static Out zero() { return Out(0); }

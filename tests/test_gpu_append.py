@@ -152,8 +152,12 @@ def test_fp8_every_bf16_pattern_matches_golden_table(dev):
     x = bits.to(dev)
     reshape_and_cache_flash(x, x, cache[:, 0], cache[:, 1], torch.arange(N, dtype=torch.int64, device=dev))
     got = raw(cache)
-    assert np.array_equal(got[:, 0].reshape(-1), golden)
-    assert np.array_equal(got[:, 1].reshape(-1), golden)
+    # the table is torch's clamp (NaN kept: 0x7F|sign); the append stores the
+    # reference's Triton clamp, which maps NaN to -448 (0xFE)
+    exp = golden.copy()
+    exp[np.isnan(O.bf16_to_f32(raw(bits).reshape(-1)))] = 0xFE
+    assert np.array_equal(got[:, 0].reshape(-1), exp)
+    assert np.array_equal(got[:, 1].reshape(-1), exp)
 
 
 @pytest.mark.parametrize("in_dtype", [torch.bfloat16, torch.float16, torch.float32])
@@ -176,7 +180,7 @@ def test_fp8_scaled_boundaries_match_golden(dev, in_dtype):
         sc = torch.tensor([float(s[a])], dtype=torch.float32, device=dev)
         reshape_and_cache_flash(xd, xd, cache[:, 0], cache[:, 1], torch.arange(n, dtype=torch.int64, device=dev),
                                 sc, sc)
-        exp = O.quantize_e4m3(O.to_f32(raw(xs), DT[in_dtype]), float(s[a]))
+        exp = O.quantize_e4m3(O.to_f32(raw(xs), DT[in_dtype]), float(s[a]), O.NAN_CLAMP_MIN)
         got = raw(cache)[:, 0].reshape(-1)
         assert np.array_equal(got, exp), f"scale {s[a]}"
         if in_dtype == torch.float32:
@@ -196,19 +200,28 @@ def test_fp8_every_bf16_pattern_at_scale(dev, scale):
     sc = torch.tensor([scale], dtype=torch.float32, device=dev)
     reshape_and_cache_flash(x, x, cache[:, 0], cache[:, 1], torch.arange(N, dtype=torch.int64, device=dev), sc, sc)
     s32 = float(np.float32(scale))
-    exp = O.quantize_e4m3(O.bf16_to_f32(raw(bits).reshape(-1)), s32)
+    xf = O.bf16_to_f32(raw(bits).reshape(-1))
+    exp = O.quantize_e4m3(xf, s32, O.NAN_CLAMP_MIN)
     assert np.array_equal(raw(cache)[:, 0].reshape(-1), exp)
-    ref = (bits.float().reshape(-1) / torch.tensor(s32)).clamp(-448, 448).to(torch.float8_e4m3fn)
-    assert np.array_equal(raw(cache)[:, 1].reshape(-1), raw(ref))
+    ref = raw((bits.float().reshape(-1) / torch.tensor(s32)).clamp(-448, 448).to(torch.float8_e4m3fn)).copy()
+    ref[np.isnan(xf)] = 0xFE  # torch keeps NaN; the append stores the Triton clamp's -448
+    assert np.array_equal(raw(cache)[:, 1].reshape(-1), ref)
 
 
 def test_fp8_nan_policy(dev):
+    """NaN inputs store -448 (0xFE) at every scale, as the reference's clamp
+    tl.minimum(tl.maximum(x, -448), 448) does (Triton's minnum / maxnum);
+    infinities saturate and -0 keeps its sign."""
     x = torch.tensor([float("nan"), -float("nan"), 1.0, float("inf"), -float("inf"), -0.0], dtype=torch.float32)
     n = x.shape[0]
-    cache = torch.zeros(n, 2, 1, 1, 1, dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
-    xd = x.view(n, 1, 1).to(dev)
-    reshape_and_cache_flash(xd, xd, cache[:, 0], cache[:, 1], torch.arange(n, dtype=torch.int64, device=dev))
-    assert raw(cache)[:, 0].reshape(-1).tolist() == [0x7F, 0xFF, 0x38, 0x7E, 0xFE, 0x80]
+    for scale in (None, 0.5, 1e-39):
+        cache = torch.zeros(n, 2, 1, 1, 1, dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
+        xd = x.view(n, 1, 1).to(dev)
+        sc = None if scale is None else torch.tensor([scale], dtype=torch.float32, device=dev)
+        reshape_and_cache_flash(xd, xd, cache[:, 0], cache[:, 1], torch.arange(n, dtype=torch.int64, device=dev),
+                                sc, sc)
+        want = [0xFE, 0xFE, 0x38 if scale is None else (0x40 if scale == 0.5 else 0x7E), 0x7E, 0xFE, 0x80]
+        assert raw(cache)[:, 0].reshape(-1).tolist() == want, scale
 
 
 def test_config2_fp8_decode_whole_cache(dev):

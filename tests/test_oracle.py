@@ -66,6 +66,32 @@ def test_e4m3_known_codes():
         assert O.quantize_e4m3(np.array([x], np.float32), 1.0)[0] == code, x
     assert O.quantize_e4m3(np.array([np.nan], np.float32), 1.0)[0] == 0x7F
     assert O.quantize_e4m3(np.array([-np.nan], np.float32), 1.0)[0] == 0xFF
+    for v in (np.nan, -np.nan):
+        assert O.quantize_e4m3(np.array([v], np.float32), 1.0, O.NAN_CLAMP_MIN)[0] == 0xFE
+
+
+def test_append_nan_policy_is_the_references_triton_clamp():
+    """The append's clamp is Triton's tl.minimum(tl.maximum(x, -448), 448)
+    (reshape_and_cache.py:70-75) with the default PropagateNan.NONE, i.e. LLVM
+    maxnum / minnum, which return the non-NaN operand (Triton 3.6:
+    language/core.py:2506,2528, semantic.py:380-381).  numpy's fmax / fmin have
+    those semantics: evaluating the reference's expression with them and
+    converting with torch gives the oracle's NAN_CLAMP_MIN bytes for every bf16
+    pattern, at scale 1 and at a scale != 1 (where x / s is clamped)."""
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    x = O.bf16_to_f32(bits)
+    for scale in (1.0, 0.37):
+        with np.errstate(invalid="ignore", over="ignore"):
+            y = (x / np.float32(scale)).astype(np.float32)
+        clamped = np.fmin(np.fmax(y, np.float32(-448.0)), np.float32(448.0))
+        assert not np.isnan(clamped).any()
+        ref = torch.from_numpy(clamped).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+        assert np.array_equal(O.quantize_e4m3(x, scale, O.NAN_CLAMP_MIN), ref)
+    # the append oracle uses it
+    cache = np.zeros((2, 2, 1, 3), np.uint8)
+    kv = np.array([[[0x7FC0, 0xFFC0, 0x3F80]]], np.uint16)
+    O.reshape_and_cache(kv, kv, cache[:, 0], cache[:, 1], np.array([1]), "bf16", "fp8")
+    assert cache[1, 0, 0].tolist() == [0xFE, 0xFE, 0x38]
 
 
 def test_e4m3_decode_matches_torch():
