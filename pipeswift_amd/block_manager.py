@@ -46,6 +46,8 @@ DEFAULT_L2_STEP_MS = 10.0  # block_manager.py:15
 # Decode headroom (tokens) every sequence holding pages must keep before the
 # pool is spent on a waiting one (block_manager.py:16-19).
 DECODE_RESERVE_TOKENS = 512
+# Pages per submitted piece of one L2 store batch (_schedule_l2_store_batch).
+L2_STORE_CHUNK = 1024
 
 
 # --------------------------------------------------------------------------- #
@@ -459,11 +461,21 @@ class BlockManager(_PagePool):
 
     def _schedule_l2_store_batch(self, stores):
         """One D2H transfer for every store not already resident or on its way;
-        stops at the first store no L2 page can take (:433-474)."""
+        stops at the first store no L2 page can take (:433-474).
+
+        The transfer is one logical copy, as in the reference, but it is
+        submitted in pieces of L2_STORE_CHUNK pages while this loop is still
+        walking the batch, so the link starts moving the first pages instead of
+        waiting for the host's per-page bookkeeping of the whole batch (about
+        12 ms for an 8192-page prompt).  Page ids, order and the deadline
+        priced from the whole batch's runs are those of a single submission."""
         if not self.enable_l2_cache:
             return 0
         gpu, l2, keys, toks = [], [], [], []
+        handles = []
+        sent = 0
         pool = self.l2_pool
+        engine = self.l2_copy_engine
         for page_idx, h, token_ids in stores:
             if pool.has_page_or_pending(h, token_ids):
                 continue
@@ -477,9 +489,17 @@ class BlockManager(_PagePool):
             l2.append(dst)
             keys.append(h)
             toks.append(token_ids)
+            if len(gpu) - sent >= L2_STORE_CHUNK:
+                handles.append(engine.store(gpu[sent:], l2[sent:]))
+                sent = len(gpu)
         if not gpu:
             return 0
-        copy = self.l2_copy_engine.store(gpu, l2)
+        if sent < len(gpu):
+            handles.append(engine.store(gpu[sent:], l2[sent:]))
+        if len(handles) == 1:
+            copy = handles[0]
+        else:
+            copy = copy_engine.JoinedCopyHandle(handles, engine.count_runs(gpu, l2), len(gpu))
         self.pending_l2_stores.append(
             {
                 "copy": copy,

@@ -22,11 +22,12 @@ What differs, by design for MI355X:
   * the mirror is allocated with hipHostMalloc (mapped, portable) through the
     library instead of torch's caching pinned allocator, which would round a
     multi-GiB mirror up to the next power of two;
-  * three transports: ``"blit"`` (default) moves every (view, page) unit in ONE
+  * two transports: ``"blit"`` (default) moves every (view, page) unit in ONE
     kernel that reads/writes the mapped host mirror directly, so the cost per
     descriptor that dominates the reference (copy_engine.py:15-36) disappears;
-    ``"batch"`` uses hipMemcpyBatchAsync and ``"memcpy"`` one hipMemcpyAsync per
-    (view, run) on the SDMA engines;
+    ``"memcpy"`` issues one hipMemcpyAsync per (view, run) on the SDMA engines
+    (the reference's batched-descriptor call, cuMemcpyBatchAsync, has a HIP
+    counterpart that this GPU's runtime does not export);
   * both streams keep the default priority.
 """
 
@@ -45,7 +46,7 @@ import torch
 from . import _lib
 from ._lib import check, lib
 
-TRANSPORTS = {"memcpy": _lib.SWAP_MEMCPY, "batch": _lib.SWAP_BATCH, "blit": _lib.SWAP_BLIT}
+TRANSPORTS = {"memcpy": _lib.SWAP_MEMCPY, "blit": _lib.SWAP_BLIT}
 DEFAULT_TRANSPORT = os.environ.get("PIPESWIFT_AMD_SWAP_TRANSPORT", "blit")
 _STAGING_SLOTS = 4
 
@@ -177,6 +178,33 @@ class CopyHandle:
         self.event.synchronize()
 
 
+class JoinedCopyHandle:
+    """One logical transfer submitted as several CopyHandles on one stream
+    (they complete in order).  ``num_runs`` / ``num_pages`` describe the whole
+    transfer as one submission would (the caller prices deadlines from them)."""
+
+    def __init__(self, handles, num_runs, num_pages):
+        self.handles = list(handles)
+        self.num_runs = num_runs
+        self.num_pages = num_pages
+
+    @property
+    def pending(self):
+        return any(h.pending for h in self.handles)
+
+    @property
+    def error(self):
+        return next((h.error for h in self.handles if h.error is not None), None)
+
+    @property
+    def event(self):
+        return self.handles[-1].event
+
+    def wait(self):
+        for h in self.handles:
+            h.wait()
+
+
 class CopyEngine:
     """Pinned host mirror of the KV cache plus the page mover between tiers.
 
@@ -238,6 +266,12 @@ class CopyEngine:
         compute_done = torch.cuda.Event()
         compute_done.record(torch.cuda.current_stream(self.device))
         return self._submit(gpu_page_idxs, l2_page_idxs, is_store=True, wait_event=compute_done)
+
+    def count_runs(self, src_ids, dst_ids):
+        """Runs one transfer of these page pairs would make (as CopyHandle.num_runs)."""
+        if not len(src_ids):
+            return 0
+        return len(self._coalesce(np.asarray(src_ids), np.asarray(dst_ids))[0])
 
     def load(self, l2_page_idxs, gpu_page_idxs):
         """H2D.  The caller must not read the GPU pages until the handle is waited on."""

@@ -71,6 +71,9 @@ class FakeEngine:
         self.calls.append(("load", list(l2_page_idxs), list(gpu_page_idxs)))
         return Handle(l2_page_idxs, gpu_page_idxs)
 
+    def count_runs(self, src, dst):
+        return O.coalesce_count(list(src), list(dst))
+
     def calibrate(self):
         return {d: dict(t) for d, t in MODEL.items()}
 
@@ -596,3 +599,13 @@ def test_random_traces_exercise_restores(monkeypatch):
     runs = [run_trace(monkeypatch, seed) for seed in range(16)]
     assert sum(c for c, _ in runs) > 6000
     assert sum(m.l2_load_cnt for _, m in runs) > 200 and sum(m.l2_hit_cnt for _, m in runs) > 200
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_trace_with_store_batches_submitted_in_pieces(seed, monkeypatch):
+    """A store batch goes to the copy engine in pieces of L2_STORE_CHUNK pages
+    while the ledger walks it; with pieces of 2 pages every ledger state,
+    deadline and page id still equals the reference order's (one submission)."""
+    monkeypatch.setattr(BM, "L2_STORE_CHUNK", 2)
+    compared, m = run_trace(monkeypatch, seed)
+    assert compared >= 60 and m.l2_store_cnt > 0
