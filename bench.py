@@ -28,6 +28,8 @@ torch CPU baseline:
   copy_blocks        config 5a: 2048 pairs over 61 layers of [8192, 2, 16, 8, 128]
   decode_attention   one decode step of FP8 paged attention over config 2's cache
   swap               config 5b: 8192 scattered blocks x 8 layers (4 GiB) D2H + H2D
+  metadata           host us of prepare_kv_info (configs 2 and 3) and of the
+                     graph static-metadata refresh, against the reference's way
 
 Each result carries:
   value            algorithmic HBM GB/s (bytes the kernel must move / time)
@@ -52,7 +54,6 @@ Other workloads (--workload NAME runs one alone): any name above, and
   attention_shapes   decode attention on several batch shapes, balanced vs split
   l2_cycle           BlockManager store -> evict -> restore of an 8192-page prompt
   swap_sweep         host-link GB/s vs bytes per page, per transport
-  metadata           host us per step of prepare_kv_info (native builder)
   hbm_copy           1 GiB device copy (achievable-bandwidth reference and the
                      PMC calibration run)
 """
@@ -618,6 +619,14 @@ def run_swap(args, device):
 
 
 def run_metadata(args, device):
+    res = measure_metadata(device)
+    line = dict({"metric": "host us per step for KV metadata (slot_mapping + page_table + H2D)", "n_gpus": 1,
+                 "higher_is_better": False, "vs_baseline": None, "dtype": "int64", "data": "synthetic (seeded)"},
+                **res)
+    print(json.dumps(line), flush=True)
+
+
+def measure_metadata(device):
     """Host time of one step's KV metadata (prepare_kv_info: slot_mapping,
     page_table, lengths, and their H2D) for config 2 (128 decode sequences,
     contexts up to 32k) and config 3 (6 sequences, 4096 new tokens), against a
@@ -677,13 +686,65 @@ def run_metadata(args, device):
         out[name] = {"tokens": int(info.slot_mapping.numel()), "pages_wide": int(info.page_table.shape[1]),
                      "ours_us": round(t_ours * 1e6, 1), "reference_style_python_us": round(t_ref * 1e6, 1)}
         print(json.dumps({name: out[name]}), file=sys.stderr, flush=True)
-    line = {"metric": "host us per step for KV metadata (slot_mapping + page_table + H2D)",
-            "value": out["config3_chunked"]["ours_us"], "unit": "us", "n_gpus": 1, "higher_is_better": False,
-            "vs_baseline": None, "dtype": "int64", "data": "synthetic (seeded)",
-            "config": {"workload": "metadata", "cases": out}, "roofline": None,
+    out["graph_refresh"] = measure_graph_refresh(device, cases["config2_decode"])
+    print(json.dumps({"graph_refresh": out["graph_refresh"]}), file=sys.stderr, flush=True)
+    return {"value": out["config3_chunked"]["ours_us"], "unit": "us per step (host)",
+            "config": {"workload": "metadata: prepare_kv_info and the graph static refresh", "cases": out},
+            "roofline": None,
             "cpu_baseline": {"value": out["config3_chunked"]["reference_style_python_us"], "unit": "us", "cores": 1,
                              "kind": "port", "sample": "per-token Python loop restating metadata.py:258-295"}}
-    print(json.dumps(line), flush=True)
+
+
+def reference_style_graph_refresh(static, info, cg_bsz, pad_q_len=1):
+    """The reference's set_graph_kvcacheinfo (cudagraph.py:75-118) as torch
+    device ops, for timing only: five copies, then with a padded batch three
+    fills, a zero and the arange chain of the cu_seqlens_q tail."""
+    import torch
+
+    bsz, max_pages = info.actual_lens_q.shape[0], info.page_table.shape[1]
+    static.page_table[:bsz, :max_pages].copy_(info.page_table, non_blocking=True)
+    static.slot_mapping[: info.slot_mapping.shape[0]].copy_(info.slot_mapping, non_blocking=True)
+    static.actual_lens_q[:bsz].copy_(info.actual_lens_q, non_blocking=True)
+    static.actual_lens_kv[:bsz].copy_(info.actual_lens_kv, non_blocking=True)
+    static.cu_seqlens_q[: bsz + 1].copy_(info.cu_seqlens_q, non_blocking=True)
+    if bsz != cg_bsz:
+        static.actual_lens_q[bsz:].fill_(pad_q_len)
+        static.slot_mapping[info.slot_mapping.shape[0]:].fill_(-1)
+        static.actual_lens_kv[bsz:].zero_()
+        static.page_table[bsz:, :max_pages].zero_()
+        tail = static.cu_seqlens_q.shape[0] - bsz
+        static.cu_seqlens_q[bsz + 1:].copy_(
+            static.cu_seqlens_q[bsz] + torch.arange(pad_q_len, tail * pad_q_len, pad_q_len, dtype=torch.int32,
+                                                    device=static.cu_seqlens_q.device), non_blocking=True)
+
+
+def measure_graph_refresh(device, case, reps=200):
+    """Graph static-metadata refresh for config 2's decode batch (128
+    sequences, a 1831-page table) into static buffers of a 256-sequence,
+    2048-page graph (a padded replay): the native one-launch refresh against
+    the reference's copy/fill sequence on the same buffers.  `host_us` is the
+    caller's time per call (enqueue only), `us` the time per call with the
+    device work included (reps calls, then one synchronize)."""
+    import torch
+
+    from pipeswift_amd import cudagraph, metadata
+
+    seqs, table, dec = case
+    info = metadata.prepare_kv_info(seqs, table, 16, None, None, is_decode=dec, device=device)
+    static = cudagraph.initialize_graph_kvcacheinfo(256, 2048, device=device)
+    res = {"batch": len(seqs), "graph_batch": 256, "page_table": list(info.page_table.shape), "static_pages": 2048}
+    for name, fn in (("native", cudagraph.set_graph_kvcacheinfo), ("reference_style", reference_style_graph_refresh)):
+        for _ in range(10):
+            fn(static, info, 256)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn(static, info, 256)
+        t1 = time.perf_counter()
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        res[name] = {"host_us": round((t1 - t0) / reps * 1e6, 2), "us": round((t2 - t0) / reps * 1e6, 2)}
+    return res
 
 
 def run_l2_cycle(args, device):
@@ -1387,6 +1448,7 @@ SECONDARY = (
     ("copy_blocks", 8, 2),
     ("decode_attention", 64, 8),
     ("swap", 2, 1),
+    ("metadata", 0, 0),
 )
 
 
@@ -1538,6 +1600,8 @@ def main():
             t0 = time.perf_counter()
             if sname == "swap":
                 r = measure_swap(device, ("blit",), reps=steps)
+            elif sname == "metadata":
+                r = measure_metadata(device)
             else:
                 r = measure_workload(args, device, sname, steps, warmup, achievable,
                                      cpu_budget=0 if nocpu else 1.0, port_budget=0)
