@@ -75,7 +75,11 @@ if ROOT not in sys.path:
 PEAK_HBM_GBS = 8000.0
 SPIN_CYCLES = 2_000_000  # shader clocks of the pre-timing spin (~1 ms at 2.4 GHz)
 STEADY_STEPS = 2048  # launches per graph for the steady per-launch figure of the us workloads
-QUEUED_MAX = 256  # longest run timed by the queued method (the rest: one graph replay)
+# Longest run timed by the queued method; longer runs replay one graph.  A
+# graph replay costs about 15 us once, while a dispatch from the queue costs
+# about 0.35 us (append) to 6 us (attention call) more than one replayed from a
+# graph: the queued method is the more faithful one below about 40 launches.
+QUEUED_MAX = 32
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
 
@@ -471,9 +475,8 @@ def measure_copy_floor(device, nbytes, steps=256):
     """Device microseconds of the HIP runtime's own contiguous copy (torch
     ``copy_``) moving the same bytes as one launch (nbytes / 2 each way), over
     rotated buffer pairs (a working set of at least 1 GiB, above the Infinity
-    Cache), timed as the kernels are (events inside one graph of `steps`
-    copies): the floor of a plain copy at this size, for the microsecond
-    workloads."""
+    Cache), `steps` copies timed as the workload's launches are: the floor of
+    a plain copy at this size, for the microsecond workloads."""
     import torch
 
     each = max(16, (nbytes // 2) // 16 * 16)
@@ -1331,9 +1334,11 @@ def time_launches(launch, rotate, steps, warmup, graph_len, device, eager_calls=
 
     Longer runs ("graph"): the K launches are captured into one graph, replayed
     once untimed (the first replay also uploads the graph), and stream events
-    bracket a second replay, which includes the replay's own dispatch cost
-    (about 15 us; torch refuses timing events inside a graph on ROCm, and
-    HIP's external event-record node fails under capture on this runtime).
+    bracket a second replay, which includes the replay's own fixed cost (about
+    15 us; torch refuses timing events inside a graph on ROCm, and HIP's
+    external event-record node fails under capture on this runtime).  Graph
+    replay is how the reference runs its decode step (llm.py:634-681), and a
+    replayed dispatch costs less than a queued one.
     graph_len == 0 forces eager launches between the events without a spin
     long enough for them ("eager").
 
@@ -1481,7 +1486,7 @@ def measure_workload(args, device, name, steps, warmup, achievable, cpu_budget, 
         steady = ts["ms"] * 1e3 / ts["launches"]
     floor = None
     if copy_floor and info["bytes"] < (64 << 20):
-        floor = measure_copy_floor(device, info["bytes"])
+        floor = measure_copy_floor(device, info["bytes"], steps)
     traffic = _load_traffic().get(name, {}).get("bytes_per_launch")
 
     cpu = None

@@ -67,7 +67,6 @@ extern "C" {
 
 /* swap transports */
 #define PSK_SWAP_MEMCPY 0 /* one hipMemcpyAsync per (view, run) on the stream */
-#define PSK_SWAP_BATCH 1  /* one hipMemcpyBatchAsync over every (view, run) */
 #define PSK_SWAP_BLIT 2   /* one copy kernel reading/writing mapped pinned memory */
 
 /* Message for the calling thread's most recent non-zero status. */
@@ -89,9 +88,10 @@ int psk_abi_version(void);
  * contiguously from its row start, as the reference does (:43-47, :63-64).
  * in_dtype == cache_dtype: q is the identity (bit copy, any dtype).
  * cache_dtype == FP8_E4M3FN, in_dtype in {BF16, F16, F32}:
- *   q(x, s) = e4m3fn_rne(clamp(float(x) / s, -448, 448)), NaN -> 0x7F|sign,
+ *   q(x, s) = e4m3fn_rne(clamp(float(x) / s, -448, 448)),
  *   s = *scale (device fp32) or 1.0 when the pointer is NULL.  At s == 1.0 this
- *   is the reference's IS_FP8 branch (:66-77) and fp8_kv.quantize (fp8_kv.py:75-77).
+ *   is the reference's IS_FP8 branch (:66-77).  A NaN quotient stores -448
+ *   (0xFE), as the reference's clamp with Triton's minnum/maxnum does (:70-75).
  */
 int psk_reshape_and_cache(const void* key, const void* value, void* key_cache, void* value_cache,
                           const int64_t* slot_mapping, int64_t num_tokens, int64_t num_heads,

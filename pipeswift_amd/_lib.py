@@ -27,7 +27,6 @@ DTYPE_CODES = {
 }
 
 SWAP_MEMCPY = 0
-SWAP_BATCH = 1
 SWAP_BLIT = 2
 
 _c_int64_p = ctypes.POINTER(ctypes.c_int64)

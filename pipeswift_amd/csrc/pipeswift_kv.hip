@@ -23,7 +23,6 @@
 
 #include <hip/hip_runtime.h>
 
-#include <dlfcn.h>
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -177,7 +176,8 @@ __global__ void __launch_bounds__(WPB * 64) paged_scatter_kernel(ScatterGeom g, 
 // Launch shape.  Decode-sized batches (< 1024 tokens) are latency bound: one
 // vector per lane (U = 1) and rows split over as many slices as they have
 // 64-vector stretches, so e.g. 128 tokens x (K, V) x 1024 bf16 -> 512 waves.
-// Larger batches give each wave 4 tokens and 2 vectors per lane.
+// Larger batches give each wave 4 tokens and 2 vectors per lane (2 tokens and
+// one vector when the append quantizes, see launch_scatter).
 struct ScatterShape {
   int ch;
   int u;
@@ -301,6 +301,11 @@ int launch_scatter(const ScatterGeom& g, const ScatterPart& p0, const ScatterPar
     return check_launch("paged_append_small_kernel launch");
   }
   if (sh.ch == 1) return launch_scatter_shape<C, 1, 1, true, 1>(g, p0, p1, sh.slice_shift, st);
+  // A quantizing append spends VALU time per element: twice the waves of
+  // two tokens each overlap it better (config 4's FP8 MLA prefill 3.71 us
+  // against 4.02 at four tokens and two vectors per lane, which stays best
+  // for the plain copies: bf16 MLA prefill 3.29 against 3.77).
+  if constexpr (C::OUT_B < C::IN_B) return launch_scatter_shape<C, 2, 1, true, 4>(g, p0, p1, 0, st);
   return launch_scatter_shape<C, 4, 2, true, 4>(g, p0, p1, sh.slice_shift, st);
 }
 
@@ -885,19 +890,6 @@ __global__ void __launch_bounds__(256) blit_pages_kernel(const SwapView* views, 
   }
 }
 
-// hipMemcpyBatchAsync is resolved at run time: the process uses whichever HIP
-// runtime PyTorch loaded, and older runtimes do not export it.
-using BatchMemcpyFn = hipError_t (*)(void**, void**, size_t*, size_t, hipMemcpyAttributes*, size_t*, size_t,
-                                     size_t*, hipStream_t);
-
-BatchMemcpyFn batch_memcpy_fn() {
-  static BatchMemcpyFn fn = [] {
-    void* p = dlvsym(RTLD_DEFAULT, "hipMemcpyBatchAsync", "hip_7.1");
-    return reinterpret_cast<BatchMemcpyFn>(p);
-  }();
-  return fn;
-}
-
 // Stable LSD radix sort of indices by non-negative key, 11-bit digits, only as
 // many passes as the largest key needs.  Keys below 2^32 travel packed with
 // their index in one uint64 (key << 32 | index), so every pass is a sequential
@@ -1321,32 +1313,6 @@ int psk_swap_blocks(int transport, const uint64_t* src_bases, const uint64_t* ds
                                       size_t(bpb * uint64_t(run_len[r])), hipMemcpyDefault, st);
         if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync");
       }
-    }
-    return PSK_OK;
-  }
-  if (transport == PSK_SWAP_BATCH) {
-    const size_t n = size_t(num_views * num_runs);
-    std::vector<void*> dsts(n), srcs(n);
-    std::vector<size_t> sizes(n);
-    size_t k = 0;
-    for (int64_t v = 0; v < num_views; ++v) {
-      const uint64_t bpb = bytes_per_page[v];
-      for (int64_t r = 0; r < num_runs; ++r, ++k) {
-        dsts[k] = reinterpret_cast<void*>(dst_bases[v] + uint64_t(dst_start[r]) * bpb);
-        srcs[k] = reinterpret_cast<void*>(src_bases[v] + uint64_t(src_start[r]) * bpb);
-        sizes[k] = size_t(bpb * uint64_t(run_len[r]));
-      }
-    }
-    hipMemcpyAttributes attr;
-    memset(&attr, 0, sizeof(attr));
-    attr.srcAccessOrder = hipMemcpySrcAccessOrderStream;
-    size_t attr_idx = 0, fail_idx = 0;
-    BatchMemcpyFn batch = batch_memcpy_fn();
-    if (!batch) return fail(PSK_E_ARG, "hipMemcpyBatchAsync is not exported by the loaded HIP runtime");
-    hipError_t e = batch(dsts.data(), srcs.data(), sizes.data(), n, &attr, &attr_idx, 1, &fail_idx, st);
-    if (e != hipSuccess) {
-      snprintf(g_err, sizeof(g_err), "hipMemcpyBatchAsync: %s (failIdx %zu)", hipGetErrorString(e), fail_idx);
-      return int(e);
     }
     return PSK_OK;
   }

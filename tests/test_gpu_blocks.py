@@ -73,26 +73,18 @@ def test_copy_blocks_config5a_full_size_pattern(dev):
 # --------------------------------------------------------------------------- #
 
 
-@pytest.mark.parametrize("transport", ["blit", "memcpy", "batch"])
+@pytest.mark.parametrize("transport", ["blit", "memcpy"])
 def test_copy_engine_round_trip(dev, transport):
     L, P, P2 = 3, 96, 64
     cache = workloads.sentinel((L, P, 2, 16, 2, 64), torch.bfloat16, 44)
     cd = cache.to(dev)
-    try:
-        eng = copy_engine.CopyEngine([cd], P, P2, transport=transport)
-    except AssertionError as e:  # hipMemcpyBatchAsync missing from the loaded runtime
-        pytest.skip(str(e))
+    eng = copy_engine.CopyEngine([cd], P, P2, transport=transport)
     try:
         rng = np.random.default_rng(45)
         gpu_ids = rng.permutation(P)[:40]
         l2_ids = np.concatenate([np.arange(10, 30), rng.permutation(np.arange(30, 64))[:20]])
         h = eng.store(gpu_ids.tolist(), l2_ids.tolist())
-        try:
-            h.wait()
-        except AssertionError as e:
-            if transport == "batch":
-                pytest.skip(str(e))
-            raise
+        h.wait()
         host = raw(eng.host_caches[0])
         src = raw(cache)
         assert np.array_equal(host[:, l2_ids], src[:, gpu_ids])
