@@ -111,7 +111,7 @@ class _PagePool:
 
     def __init__(self, num_pages: int, first_page: int = 0):
         self.num_pages = num_pages
-        self.ref_counts = np.zeros(num_pages, dtype=np.int32)
+        self.ref_counts = array("i", bytes(4 * num_pages))  # plain ints: no numpy scalar per access
         self.free_page_queue = deque(range(first_page, num_pages))
         self.cached_pages = OrderedDict()
         self.hash2page_idx_list: Dict[int, List[int]] = {}
@@ -159,6 +159,34 @@ class _PagePool:
                 self.free_page_queue.append(p)
             else:
                 self.cached_pages[p] = None
+
+    def _take_many(self, n):
+        """``n`` pages with one reference each, the pages and order of ``n``
+        calls of ``_take``; the caller has checked that the free and cached
+        queues together hold at least ``n``."""
+        free, rc = self.free_page_queue, self.ref_counts
+        k = min(n, len(free))
+        out = [free.popleft() for _ in range(k)]
+        if k < n:
+            # evict the cached queue's head n - k times, unkeying as _unkey_page does
+            cached, p2h, p2t, h2l = self.cached_pages, self.page_idx2hash, self.page_idx2token_ids, self.hash2page_idx_list
+            for _ in range(n - k):
+                p = cached.popitem(last=False)[0]
+                assert rc[p] == 0
+                h = p2h[p]
+                same = h2l.get(h) if h != -1 else None
+                if same is not None:
+                    if p in same:
+                        same.remove(p)
+                    if not same:
+                        del h2l[h]
+                p2h[p] = -1
+                p2t[p] = []
+                out.append(p)
+        for p in out:
+            assert rc[p] == 0
+            rc[p] = 1
+        return out
 
     def _take(self):
         """A page with one reference: the free queue's head, else the evicted
@@ -476,15 +504,22 @@ class BlockManager(_PagePool):
         sent = 0
         pool = self.l2_pool
         engine = self.l2_copy_engine
+        # pool.has_page_or_pending / acquire_pending_key and self._hold,
+        # inlined with the key tuple built once: this runs once per page
+        pending, find, take = pool._pending_store_keys, pool._find, pool.allocate_for_store
+        rc, cached = self.ref_counts, self.cached_pages
         for page_idx, h, token_ids in stores:
-            if pool.has_page_or_pending(h, token_ids):
+            key = (h, tuple(token_ids))
+            if h != -1 and (key in pending or find(h, token_ids) is not None):
                 continue
-            dst = pool.allocate_for_store()
+            dst = take()
             if dst is None:
                 break
             # Claimed now, so a duplicate later in this batch is caught above.
-            pool.acquire_pending_key((h, tuple(token_ids)))
-            self._hold(page_idx)
+            pending[key] = pending.get(key, 0) + 1
+            if rc[page_idx] == 0 and page_idx in cached:
+                del cached[page_idx]
+            rc[page_idx] += 1
             gpu.append(page_idx)
             l2.append(dst)
             keys.append(h)
@@ -529,9 +564,18 @@ class BlockManager(_PagePool):
     def _stage_l2_loads(self, seq, loads):
         """Queue a sequence's restore for the batched flush (:497-507).  Its
         pages are pinned here, so nothing recycles them before the flush."""
+        # _hold on both tiers, inlined: this runs once per restored page
+        rc, cached = self.ref_counts, self.cached_pages
+        l2 = self.l2_pool
+        rc2, cached2 = l2.ref_counts, l2.cached_pages
         for load in loads:
-            self._hold(load["gpu_page_idx"])
-            self.l2_pool.retain_for_load(load["l2_page_idx"])
+            g, q = load["gpu_page_idx"], load["l2_page_idx"]
+            if rc[g] == 0 and g in cached:
+                del cached[g]
+            rc[g] += 1
+            if rc2[q] == 0 and q in cached2:
+                del cached2[q]
+            rc2[q] += 1
         seq.l2_load_pending = True
         self._l2_pending_load_requests.append((seq, loads))
 
@@ -704,6 +748,49 @@ class BlockManager(_PagePool):
         self.hit_cnt += matched
         seq.offset += matched * ps
 
+        if len(self.free_page_queue) + len(self.cached_pages) >= page_num - matched:
+            loads = self._prefill_pages_batched(pages, matched, table)
+        else:
+            loads = self._prefill_pages_one_by_one(pages, matched, table)
+        self.kv_page_table[seq.seq_id] = table
+        if loads:
+            self._stage_l2_loads(seq, loads)
+
+    def _prefill_pages_batched(self, pages, matched, table):
+        """Pages past the L1 match when the free and cached queues serve every
+        allocation: no in-flight store is then reclaimed in between and what L2
+        holds stays fixed, so looking the restores up first and taking all
+        pages at once gives the pages, in the order, that one lookup and one
+        allocation per page give.  Returns the staged restores."""
+        page_num = len(pages)
+        rest = page_num - matched
+        srcs = []
+        if self.enable_l2_cache:
+            find = self.l2_pool._find
+            for i in range(matched, page_num - 1):
+                src = find(*pages[i])
+                if src is None:
+                    break
+                srcs.append(src)
+        self.l2_hit_cnt += len(srcs)
+        got = self._take_many(rest)
+        loads = []
+        for j, src in enumerate(srcs):
+            h, token_ids = pages[matched + j]
+            loads.append({"gpu_page_idx": got[j], "l2_page_idx": src, "hash": h, "token_ids": token_ids})
+        key, last = self._key_page, page_num - 1
+        for j in range(len(srcs), rest):
+            h, token_ids = pages[matched + j]
+            if h != -1 and matched + j != last:
+                key(got[j], h, token_ids)  # a fresh page: unkeyed, one reference
+        table.extend(got)
+        return loads
+
+    def _prefill_pages_one_by_one(self, pages, matched, table):
+        """Pages past the L1 match, one lookup and one allocation at a time
+        (:745-782): an allocation may retire an in-flight store, which keys L2
+        pages the next lookup can find."""
+        page_num = len(pages)
         loads = []
         if self.enable_l2_cache:
             for i in range(matched, page_num - 1):
@@ -723,9 +810,7 @@ class BlockManager(_PagePool):
             if h != -1 and i != page_num - 1:
                 self.update_page(p, h, token_ids)
             table.append(p)
-        self.kv_page_table[seq.seq_id] = table
-        if loads:
-            self._stage_l2_loads(seq, loads)
+        return loads
 
     def deallocate(self, seq):
         """Release every page of the sequence, suffix first, so its suffix is

@@ -653,7 +653,8 @@ int64_t copy_blocks_lds(int64_t block_bytes, int waves) {
 }
 
 // ----------------------------------------------------------------------------
-// amax -> scale (two-phase, last workgroup finishes; graph-safe, no memset)
+// amax -> scale (two launches: partial maxima, then one workgroup reduces them;
+// graph-safe, nothing to clear between calls)
 // ----------------------------------------------------------------------------
 
 constexpr int kAmaxMaxBlocks = 1024;

@@ -510,12 +510,53 @@ def test_allocate_drains_in_flight_stores_before_failing(monkeypatch):
     assert m.pending_l2_stores == [] and p == 2 and list(m.cached_pages) == [1]
 
 
+@pytest.mark.parametrize("kind", IMPLS)
+def test_restore_lookup_after_an_allocation_that_retires_a_store(kind, monkeypatch):
+    """With both queues empty the prompt's first restore target comes from
+    retiring the in-flight store, and that store keys the L2 page the next
+    lookup then finds: lookups and allocations must interleave page by page
+    (:741-767, :327-345).  Looking every page up before allocating would stage
+    one restore instead of two."""
+    m, _, st = build(kind, monkeypatch, 8, 2, l2_pages=8)
+    a = Seq(1, [1, 2, 3])  # page 1 = [1, 2] keyed, page 2 partial
+    m.allocate_prefill(a)
+    m.poll_l2_events(0)
+    m.schedule_l2_stores_for_confirmed_seq(a)  # page 1 -> L2 0
+    m.poll_l2_events(5)  # retired: L2 0 resident
+    m.deallocate(a)
+    assert st()["l1_free"] == [3, 4, 5, 6, 7, 2] and st()["l1_cached"] == [1]
+    b = Seq(2, [1, 2, 3, 4, 5, 6, 7, 8, 9])  # L1 hit on page 1, then 3, 4, 5 keyed, 6 partial
+    m.allocate_prefill(b)
+    assert st()["tables"][2] == [1, 3, 4, 5, 6]
+    m.schedule_l2_stores_for_confirmed_seq(b)  # [1, 2] already in L2; 3, 4, 5 -> L2 1, 2, 3 in flight
+    assert [(g, l) for g, l, _ in st()["stores"]] == [([3, 4, 5], [1, 2, 3])]
+    m.deallocate(b)  # 3, 4, 5 stay pinned by the store
+    assert st()["l1_free"] == [7, 2, 6] and st()["l1_cached"] == [1]
+    d = Seq(3, [50] * 7)  # 4 pages: the 3 free ones, then evicts 1
+    m.allocate_prefill(d)
+    s = st()
+    assert s["tables"][3] == [7, 2, 6, 1] and s["l1_free"] == [] and s["l1_cached"] == []
+    c = Seq(4, [1, 2, 3, 4, 0])
+    m.allocate_prefill(c)
+    # page 0: L2 hit on L2 0; its target retires the store (L1 cached [5, 4, 3])
+    # and takes 5; page 1: now an L2 hit on L2 1, target 4; partial page: 3
+    s = st()
+    assert s["stores"] == [] and s["tables"][4] == [5, 4, 3]
+    assert s["staged_loads"] == [(4, [(5, 0), (4, 1)])] and s["counts"][1] == 2
+    assert m.flush_l2_loads() == 2
+
+
 # --------------------------------------------------------------------------- #
 # random traces: product and reference-order oracle, call for call
 # --------------------------------------------------------------------------- #
 
 
-def run_trace(monkeypatch, seed, steps=600, num_pages=32, ps=4, l2_pages=64):
+def run_trace(monkeypatch, seed, steps=600, num_pages=32, ps=4, l2_pages=64, admit_past_free=0.0):
+    """Random calls on the product and the reference-order oracle, comparing
+    every state.  A fraction ``admit_past_free`` of the prompts is admitted
+    whatever the free count, so allocation may have to retire in-flight stores
+    part-way through a prompt; the trace ends at the first out-of-pages error,
+    which both must raise."""
     rng = random.Random(seed)
     m, _ = make_product(monkeypatch, num_pages, ps, l2_pages)
     r, _ = make_oracle(num_pages, ps, l2_pages)
@@ -529,12 +570,22 @@ def run_trace(monkeypatch, seed, steps=600, num_pages=32, ps=4, l2_pages=64):
             n = rng.randrange(1, 48)
             cut = rng.randrange(0, n + 1)
             toks = d[:cut] + [rng.randrange(40) for _ in range(n - cut)]
-            if m.free_pages() < (n + ps - 1) // ps:
+            need = (n + ps - 1) // ps
+            # past the free count only as far as in-flight stores pin pages
+            pinned = sum(len(x["gpu_page_idxs"]) for x in m.pending_l2_stores)
+            past_free = rng.random() < admit_past_free and m.free_pages() + pinned >= need
+            if not past_free and m.free_pages() < need:
                 continue
             pa, ra = Seq(next_id, toks), Seq(next_id, toks)
             next_id += 1
             assert m.probe_l2_prefetch(pa) == r.probe_l2_prefetch(ra)
-            m.allocate_prefill(pa)
+            try:
+                m.allocate_prefill(pa)
+            except RuntimeError as e:
+                assert past_free and "Out of KV Pages" in str(e)
+                with pytest.raises(RuntimeError, match="Out of KV Pages"):
+                    r.allocate_prefill(ra)
+                break
             r.allocate_prefill(ra)
             live[pa.seq_id] = (pa, ra)
             if rng.random() < 0.7:  # the scheduler flushes restores right after admitting them
@@ -609,3 +660,26 @@ def test_random_trace_with_store_batches_submitted_in_pieces(seed, monkeypatch):
     monkeypatch.setattr(BM, "L2_STORE_CHUNK", 2)
     compared, m = run_trace(monkeypatch, seed)
     assert compared >= 60 and m.l2_store_cnt > 0
+
+
+def test_random_trace_admitting_past_the_free_pages(monkeypatch):
+    """Prompts admitted past the free count take the page-by-page path of
+    allocate_prefill, where an allocation retires an in-flight store; the
+    short prompts of the other traces take the batched path.  Both match the
+    reference order state for state."""
+    paths = {"batched": 0, "one_by_one": 0, "one_by_one_reclaimed": 0}
+    for name in ("batched", "one_by_one"):
+        orig = getattr(BM.BlockManager, "_prefill_pages_" + name)
+
+        def counted(self, *a, _orig=orig, _name=name):
+            before = len(self.pending_l2_stores)
+            out = _orig(self, *a)  # counts only calls that returned
+            paths[_name] += 1
+            if _name == "one_by_one" and len(self.pending_l2_stores) < before:
+                paths["one_by_one_reclaimed"] += 1
+            return out
+
+        monkeypatch.setattr(BM.BlockManager, "_prefill_pages_" + name, counted)
+    compared = [run_trace(monkeypatch, seed, num_pages=24, admit_past_free=0.6)[0] for seed in range(24)]
+    assert sum(compared) > 2000
+    assert paths["one_by_one_reclaimed"] >= 5 and paths["batched"] >= 200, paths
