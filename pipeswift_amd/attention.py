@@ -11,8 +11,8 @@ same arguments for the decode case (one query token per sequence) and runs
 ``psk_paged_decode_attention``: Q K^T on the bf16 MFMA over exactly converted
 FP8 values (gfx950's FP8 MFMA truncates its sums), fp32 softmax, P V on the
 bf16 MFMA with P split into hi + lo bf16 parts (2^-17 relative per weight,
-fp32 sums; fp32 FMAs for block sizes that are not powers of two >= 16), and
-descales of any value per (sequence, kv head) -- for instance the per-tensor
+fp32 sums) for every block size, and descales of any value per (sequence,
+kv head) -- for instance the per-tensor
 scales ``cache_ops.compute_kv_scales`` gave the append.
 
 Prefill over the paged cache is not covered; ``max_seqlen_q`` must be 1.

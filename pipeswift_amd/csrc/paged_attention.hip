@@ -26,19 +26,21 @@
 //   * softmax runs in the exp2 domain with a lazily raised running maximum
 //     (raised only when a score exceeds it by 2^8), which keeps the rescaling of
 //     the accumulators off the per-tile path; normalisation is exact.
-//   * P V: for power-of-two block sizes >= 16 (every ring-based kernel) on the
-//     matrix cores, with S^T = K Q^T so that each lane holds one head's scores
-//     of four tokens (the P operand), V^T read from LDS by ds_read_b64_tr_b8,
-//     and P split into bf16 hi + lo (relative error 2^-17 per weight, fp32
-//     sums); see "P V on the matrix cores" below.  For other block sizes
-//     (decode_partial_kernel), on the VALU in fp32: lane l owns tokens (l / 8)
-//     and (l / 8 + 8) of the tile and d = 16 * (l % 8) .. +16, loaded as one
-//     16-byte vector per token; FP8 -> fp32 with the native pair convert.
-//   * flash-decoding split: a workgroup of 4 waves takes `split` tokens of one
-//     (sequence, kv head); its waves merge through LDS into one partial
-//     (max, sum, accumulator per query head) in the caller's workspace, and a
-//     second kernel merges the partials of a sequence and writes the output.
-//   * loads for tile i + 1 are issued before tile i is computed.
+//   * P V on the matrix cores, with S^T = K Q^T so that each lane holds one
+//     head's scores of four tokens (the P operand), V^T read from LDS by
+//     ds_read_b64_tr_b8, and P split into bf16 hi + lo (relative error 2^-17
+//     per weight, fp32 sums); see "P V on the matrix cores" below.
+//   * every tile goes through a per-wave ring of LDS slots filled by
+//     global_load_lds, R tiles in flight per wave.  For power-of-two block
+//     sizes >= 16 a tile lies in one page and is addressed wave-uniformly; for
+//     any other block size each lane addresses its own rows (ring_attend's GEN
+//     variant), so every block size takes the same kernels.
+//   * schedules: the balanced one (equal runs of (sequence, tile) units per
+//     workgroup across sequence boundaries, head-parallel from two sequences)
+//     by default, or an explicit split count; the waves of a workgroup merge
+//     through LDS into partial records (max, sum, accumulator per query head)
+//     in the caller's workspace, and a second kernel merges a sequence's
+//     records and writes the output.
 //
 // C ABI: include/pipeswift_kv.h.  Nothing here allocates or synchronizes.
 
@@ -71,7 +73,6 @@ constexpr int kMaxSplits = 128;
 constexpr int kMaxGroup = 8;   // query heads per kv head
 constexpr float kNegBig = -1.0e30f;  // finite "no token yet" maximum
 constexpr float kLazy = 8.0f;        // raise the running max past 2^8 headroom only
-constexpr int kPageCache = 512;      // page ids of a split staged in LDS
 constexpr int kRing = 2;             // LDS tile slots per wave (ring kernel)
 constexpr int kRingPages = 1024;     // page ids of a split in the ring kernel
 // Sequences of the balanced schedule: every workgroup scans their lengths
@@ -168,59 +169,10 @@ __device__ __forceinline__ int32_t checked_page(const DecodeArgs& a, const int32
   return (p >= 0 && p < a.num_blocks) ? p : -1;
 }
 
-// The page ids a workgroup's split touches, staged once in LDS (entry i holds
-// table entry first + i, -1 when missing); direct reads when they do not fit.
-struct PageIds {
-  const int32_t* lds;
-  const int32_t* bt_row;
-  int first;
-  bool staged;
-};
-
-__device__ __forceinline__ int64_t page_of(const DecodeArgs& a, const PageIds& ids, int t) {
-  const int pi = page_index(a, t);
-  return ids.staged ? int64_t(ids.lds[pi - ids.first]) : int64_t(checked_page(a, ids.bt_row, pi));
-}
-
-__device__ __forceinline__ int64_t row_of(const DecodeArgs& a, int t) {
-  return a.bs_shift >= 0 ? int64_t(t & (a.block_size - 1)) : int64_t(t % a.block_size);
-}
-
 // Tile loads of one lane: K (32 bytes of one token) and V (16 bytes of two tokens).
 struct TileLoads {
   u32x4 k0, k1, va, vb;
 };
-
-template <bool REPL>
-__device__ __forceinline__ TileLoads load_tile(const DecodeArgs& a, const PageIds& ids, int h, int t0, int t_end,
-                                               int lane) {
-  TileLoads r;
-  r.k0 = r.k1 = r.va = r.vb = u32x4(0);
-  const int tk = t0 + (lane & 15);
-  if (tk < t_end) {
-    const int64_t p = page_of(a, ids, tk);
-    if (p >= 0) {
-      const uint8_t* src = a.k + p * a.k_blk + row_of(a, tk) * a.k_row + h * a.k_head + 32 * (lane >> 4);
-      r.k0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
-      r.k1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + 16));
-    }
-  }
-  const int ta = t0 + token_slot<REPL>(lane), tb = ta + 8;
-  const int64_t dv = 16 * column_chunk<REPL>(lane);
-  if (ta < t_end) {
-    const int64_t p = page_of(a, ids, ta);
-    if (p >= 0)
-      r.va = __builtin_nontemporal_load(
-          reinterpret_cast<const u32x4*>(a.v + p * a.v_blk + row_of(a, ta) * a.v_row + h * a.v_head + dv));
-  }
-  if (tb < t_end) {
-    const int64_t p = page_of(a, ids, tb);
-    if (p >= 0)
-      r.vb = __builtin_nontemporal_load(
-          reinterpret_cast<const u32x4*>(a.v + p * a.v_blk + row_of(a, tb) * a.v_row + h * a.v_head + dv));
-  }
-  return r;
-}
 
 // 32 FP8 query bytes of this lane's MFMA row (query head h*G + lane%16, d from
 // 32 * (lane / 16)); zero rows beyond the group.
@@ -267,33 +219,6 @@ __device__ __forceinline__ void load_query(const DecodeArgs& a, int q_dtype, int
     case PSK_DTYPE_F16: load_query_as<PSK_DTYPE_F16>(src, qd, d0, qw); break;
     default: load_query_as<PSK_DTYPE_F32>(src, qd, d0, qw); break;
   }
-}
-
-// Tile addressing when the block size is a power of two >= 16: a 16-token tile
-// (tiles start at multiples of 16) lies in one page, so its page id and row
-// base are wave-uniform and every lane adds a fixed 32-bit offset.
-struct LaneOffsets {
-  uint32_t k, va, vb;
-};
-
-__device__ __forceinline__ TileLoads load_tile_uniform(const DecodeArgs& a, const PageIds& ids, int h, int t0,
-                                                       const LaneOffsets& off) {
-  TileLoads r;
-  const int pi = t0 >> a.bs_shift;
-  const int32_t pid =
-      __builtin_amdgcn_readfirstlane(ids.staged ? ids.lds[pi - ids.first] : checked_page(a, ids.bt_row, pi));
-  if (pid < 0) {
-    r.k0 = r.k1 = r.va = r.vb = u32x4(0);
-    return r;
-  }
-  const int64_t row0 = t0 & (a.block_size - 1);
-  const uint8_t* kb = a.k + int64_t(pid) * a.k_blk + row0 * a.k_row + int64_t(h) * a.k_head;
-  const uint8_t* vb = a.v + int64_t(pid) * a.v_blk + row0 * a.v_row + int64_t(h) * a.v_head;
-  r.k0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kb + off.k));
-  r.k1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kb + off.k + 16));
-  r.va = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vb + off.va));
-  r.vb = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vb + off.vb));
-  return r;
 }
 
 // Running softmax of one lane: per query head of the group the running
@@ -488,73 +413,6 @@ __device__ __forceinline__ void write_partial(const DecodeArgs& a, Softmax<NG>& 
     }
   }
   merge_write<NG>(a, rec_idx, s_acc, s_m, s_l);
-}
-
-template <int NG, bool UNIFORM>
-__global__ void __launch_bounds__(kWaves * 64) decode_partial_kernel(DecodeArgs a, int q_dtype) {
-  // split s of sequence b sits at blockIdx.x = (s + b) % max_splits: workgroups
-  // go round-robin to the 8 XCDs by blockIdx.x (max_splits is the fastest grid
-  // dimension), so the first splits of short sequences spread over all of them
-  const int h = blockIdx.y, b = blockIdx.z;
-  const int s = int((blockIdx.x + unsigned(a.max_splits) - unsigned(b % a.max_splits)) % unsigned(a.max_splits));
-  const int len = a.seq_lens[b];
-  const int t_begin = s * a.split;
-  if (t_begin >= len || s >= a.max_splits) return;  // uniform over the workgroup
-  const int t_end = min(len, t_begin + a.split);
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
-  const int G = a.group;
-
-  const float qd = descale(a.qd, a.qd_b, a.qd_h, b, h);
-  const float kd = descale(a.kd, a.kd_b, a.kd_h, b, h);
-  const float sl = a.scale_log2 * qd * kd;
-  uint32_t qw[8];
-  load_query<(NG <= 4)>(a, q_dtype, b, h, qd, lane, qw);
-  const bf16x8 qop[4] = {e4m3x8_to_bf16(qw[0], qw[1]), e4m3x8_to_bf16(qw[2], qw[3]), e4m3x8_to_bf16(qw[4], qw[5]),
-                         e4m3x8_to_bf16(qw[6], qw[7])};
-
-  __shared__ int32_t s_pages[kPageCache];
-  PageIds ids;
-  ids.lds = s_pages;
-  ids.bt_row = a.block_table + b * a.bt_stride;
-  ids.first = page_index(a, t_begin);
-  const int n_ids = page_index(a, t_end - 1) - ids.first + 1;
-  ids.staged = n_ids <= kPageCache;
-  if (ids.staged) {
-    for (int i = threadIdx.x; i < n_ids; i += kWaves * 64) s_pages[i] = checked_page(a, ids.bt_row, ids.first + i);
-    __syncthreads();
-  }
-
-  Softmax<NG> st;
-#pragma unroll
-  for (int g = 0; g < NG; ++g) {
-    st.m[g] = kNegBig;
-    st.mth[g] = kNegBig + kLazy;
-    st.l[g] = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 16; ++k) st.acc[g][k] = 0.0f;
-  }
-  LaneOffsets off;
-  off.k = uint32_t((lane & 15) * a.k_row + 32 * (lane >> 4));
-  off.va = uint32_t(token_slot<(NG <= 4)>(lane) * a.v_row + 16 * column_chunk<(NG <= 4)>(lane));
-  off.vb = uint32_t(off.va + 8 * a.v_row);
-
-  auto tile = [&](int t) -> TileLoads {
-    if constexpr (UNIFORM) return load_tile_uniform(a, ids, h, t, off);
-    else return load_tile<(NG <= 4)>(a, ids, h, t, t_end, lane);
-  };
-  // every tile of a wave but its last lies below t_end
-  const int stride = kTile * kWaves;
-  int t0 = t_begin + wave * kTile;
-  if (t0 < t_end) {
-    TileLoads c = tile(t0);
-    for (; t0 + stride < t_end; t0 += stride)
-      attend_step<NG, false>(st, c, qop, sl, t0, t_end, lane, [&] { c = tile(t0 + stride); });
-    attend_step<NG, true>(st, c, qop, sl, t0, t_end, lane, [] {});
-  }
-
-  __shared__ float s_acc[kWaves][NG][kHead];
-  write_partial<NG>(a, st, (int64_t(b) * a.num_kv_heads + h) * a.max_splits + s, lane, wave, s_acc);
 }
 
 // vmcnt <= n, expcnt and lgkmcnt untouched (gfx9 s_waitcnt encoding)
@@ -811,7 +669,17 @@ __device__ __forceinline__ void wait_vmcnt(int n) {
 // heads may differ): it stages the range's page ids behind a barrier.
 // `overlap` runs while the page-id loads are in flight (a new head's query
 // loads go there, so that both cost one memory latency).
-template <int NG, int W, int P, int R, class ST, class Overlap>
+//
+// GEN selects the addressing.  Without it the block size is a power of two >=
+// 16, so a tile lies in one page: the page id and row base are wave-uniform,
+// each lane adds a fixed 32-bit offset, and a missing page zeroes the slot.
+// With it (any other block size, or rows too far apart for 32-bit offsets)
+// the rows of a tile may come from different pages: each lane keeps the page
+// index and row of its two load rows, advanced by the tile stride, and
+// addresses them in 64 bits; a row on a missing page (or past t_end) loads row
+// 0 of page 0 instead, and a per-slot mask of the tile's 16 tokens (from two
+// ballots at issue) zeroes those tokens' K and V when the slot is read.
+template <int NG, int W, int P, int R, bool GEN, class ST, class Overlap>
 __device__ __forceinline__ void ring_attend(const DecodeArgs& a, ST& st, const bf16x8 (&qop)[4],
                                             const float& sl, int b, int h, int t_begin, int t_end, int lane,
                                             int wave, int phase, RingLdsT<W, R>& lds, const Overlap& overlap) {
@@ -819,8 +687,8 @@ __device__ __forceinline__ void ring_attend(const DecodeArgs& a, ST& st, const b
   constexpr int kIdsPerThread = kRingPages / (W * 64);
   static_assert(kRingPages % (W * 64) == 0, "page ids are staged a whole number per thread");
   const int32_t* bt_row = a.block_table + b * a.bt_stride;
-  const int first = t_begin >> a.bs_shift;
-  const int n_ids = ((t_end - 1) >> a.bs_shift) - first + 1;
+  const int first = GEN ? page_index(a, t_begin) : t_begin >> a.bs_shift;
+  const int n_ids = (GEN ? page_index(a, t_end - 1) : (t_end - 1) >> a.bs_shift) - first + 1;
   __syncthreads();  // the previous range's readers of pages and ring are done
   int32_t ids[kIdsPerThread];
 #pragma unroll
@@ -854,30 +722,89 @@ __device__ __forceinline__ void ring_attend(const DecodeArgs& a, ST& st, const b
   const int t_first = t_begin + phase * kTile;
   const int n_tiles = t_first < t_end ? (t_end - t_first + stride - 1) / stride : 0;
 
+  // GEN: page index and row of this lane's load rows (tokens t0 + drow and
+  // t0 + drow + 8 of the next tile to issue), and the tile stride in pages
+  // and rows
+  int pia = 0, ra = 0, pib = 0, rb = 0, sq = 0, sr = 0;
+  uint64_t tok_ok = 0;  // GEN: bits 16 s .. 16 s + 15: tokens of slot s on real pages
+  if constexpr (GEN) {
+    const int bs = a.block_size;
+    const int ta = t_first + drow;
+    pia = page_index(a, ta);
+    ra = ta - pia * bs;
+    pib = page_index(a, ta + 8);
+    rb = ta + 8 - pib * bs;
+    sq = page_index(a, stride);
+    sr = stride - sq * bs;
+  }
+
   // start the loads of tile j into its slot; a missing page reads page 0 (in
   // bounds) and is zeroed when consumed
   uint32_t valid = 0;  // bit j % R: slot holds a tile on a real page
   auto issue = [&](int j) {
     const int t0 = t_first + j * stride;
-    const int32_t raw = __builtin_amdgcn_readfirstlane(lds.pages[(t0 >> a.bs_shift) - first]);
     const int slot = j % R;
-    valid = raw >= 0 ? (valid | (1u << slot)) : (valid & ~(1u << slot));
-    const int64_t pid = raw >= 0 ? raw : 0;
-    const int64_t row0 = t0 & (a.block_size - 1);
-    const uint8_t* kb = a.k + pid * a.k_blk + row0 * a.k_row + int64_t(h) * a.k_head;
-    const uint8_t* vb = a.v + pid * a.v_blk + row0 * a.v_row + int64_t(h) * a.v_head;
-    __builtin_amdgcn_global_load_lds((gvoid*)(kb + off_k), (lvoid*)&ring[slot][0][0], 16, 0, kDmaNontemporal);
-    __builtin_amdgcn_global_load_lds((gvoid*)(kb + off_k8), (lvoid*)&ring[slot][1][0], 16, 0, kDmaNontemporal);
-    __builtin_amdgcn_global_load_lds((gvoid*)(vb + off_v), (lvoid*)&ring[slot][2][0], 16, 0, kDmaNontemporal);
-    __builtin_amdgcn_global_load_lds((gvoid*)(vb + off_v8), (lvoid*)&ring[slot][3][0], 16, 0, kDmaNontemporal);
+    if constexpr (GEN) {
+      const int ta = t0 + drow;
+      const int32_t ida = ta < t_end ? lds.pages[pia - first] : -1;
+      const int32_t idb = ta + 8 < t_end ? lds.pages[pib - first] : -1;
+      // every lane of a row agrees, so bit 8 r of a ballot is row r's
+      const uint64_t ba = __ballot(ida >= 0) & 0x0101010101010101ull;
+      const uint64_t bb = __ballot(idb >= 0) & 0x0101010101010101ull;
+      const uint64_t m16 = ((ba * 0x0102040810204080ull) >> 56) | (((bb * 0x0102040810204080ull) >> 56) << 8);
+      tok_ok = (tok_ok & ~(0xFFFFull << (16 * slot))) | (m16 << (16 * slot));
+      const int64_t pa = ida >= 0 ? ida : 0, rwa = ida >= 0 ? ra : 0;
+      const int64_t pb = idb >= 0 ? idb : 0, rwb = idb >= 0 ? rb : 0;
+      const uint8_t* ka = a.k + pa * a.k_blk + rwa * a.k_row + int64_t(h) * a.k_head;
+      const uint8_t* kb = a.k + pb * a.k_blk + rwb * a.k_row + int64_t(h) * a.k_head;
+      const uint8_t* va = a.v + pa * a.v_blk + rwa * a.v_row + int64_t(h) * a.v_head;
+      const uint8_t* vb = a.v + pb * a.v_blk + rwb * a.v_row + int64_t(h) * a.v_head;
+      __builtin_amdgcn_global_load_lds((gvoid*)(ka + 16 * dchunk), (lvoid*)&ring[slot][0][0], 16, 0, kDmaNontemporal);
+      __builtin_amdgcn_global_load_lds((gvoid*)(kb + 16 * (dchunk ^ 1)), (lvoid*)&ring[slot][1][0], 16, 0,
+                                       kDmaNontemporal);
+      __builtin_amdgcn_global_load_lds((gvoid*)(va + 16 * dchunk), (lvoid*)&ring[slot][2][0], 16, 0, kDmaNontemporal);
+      __builtin_amdgcn_global_load_lds((gvoid*)(vb + 16 * dchunk), (lvoid*)&ring[slot][3][0], 16, 0, kDmaNontemporal);
+      pia += sq;
+      ra += sr;
+      if (ra >= a.block_size) {
+        ra -= a.block_size;
+        ++pia;
+      }
+      pib += sq;
+      rb += sr;
+      if (rb >= a.block_size) {
+        rb -= a.block_size;
+        ++pib;
+      }
+    } else {
+      const int32_t raw = __builtin_amdgcn_readfirstlane(lds.pages[(t0 >> a.bs_shift) - first]);
+      valid = raw >= 0 ? (valid | (1u << slot)) : (valid & ~(1u << slot));
+      const int64_t pid = raw >= 0 ? raw : 0;
+      const int64_t row0 = t0 & (a.block_size - 1);
+      const uint8_t* kb = a.k + pid * a.k_blk + row0 * a.k_row + int64_t(h) * a.k_head;
+      const uint8_t* vb = a.v + pid * a.v_blk + row0 * a.v_row + int64_t(h) * a.v_head;
+      __builtin_amdgcn_global_load_lds((gvoid*)(kb + off_k), (lvoid*)&ring[slot][0][0], 16, 0, kDmaNontemporal);
+      __builtin_amdgcn_global_load_lds((gvoid*)(kb + off_k8), (lvoid*)&ring[slot][1][0], 16, 0, kDmaNontemporal);
+      __builtin_amdgcn_global_load_lds((gvoid*)(vb + off_v), (lvoid*)&ring[slot][2][0], 16, 0, kDmaNontemporal);
+      __builtin_amdgcn_global_load_lds((gvoid*)(vb + off_v8), (lvoid*)&ring[slot][3][0], 16, 0, kDmaNontemporal);
+    }
   };
+  // GEN: the 16-token mask of a slot
+  auto slot_tokens = [&](int slot) { return uint32_t(tok_ok >> (16 * slot)) & 0xFFFFu; };
   auto fetch = [&](int j) {
     // tiles issued after j: min(R - 1, n_tiles - 1 - j), four loads each
     if (j + R - 1 < n_tiles) __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 * (R - 1)));
     else wait_vmcnt(4 * (n_tiles - 1 - j));
     const int slot = j % R;
     TileLoads c = ring_read((uint32_t)(size_t)(lvoid*)&ring[slot][0][0], rk0, rk1, rv);
-    if (!((valid >> slot) & 1u)) c.k0 = c.k1 = c.va = c.vb = u32x4(0);
+    if constexpr (GEN) {
+      const uint32_t m = slot_tokens(slot);
+      if (!((m >> kt) & 1u)) c.k0 = c.k1 = u32x4(0);
+      if (!((m >> vt) & 1u)) c.va = u32x4(0);
+      if (!((m >> (vt + 8)) & 1u)) c.vb = u32x4(0);
+    } else {
+      if (!((valid >> slot) & 1u)) c.k0 = c.k1 = c.va = c.vb = u32x4(0);
+    }
     return c;
   };
   for (int j = 0; j < R && j < n_tiles; ++j) issue(j);
@@ -895,7 +822,15 @@ __device__ __forceinline__ void ring_attend(const DecodeArgs& a, ST& st, const b
       const int slot = j % R;
       PvTile c;
       ring_read_pv((uint32_t)(size_t)(lvoid*)&ring[slot][0][0], rk0, rk1, off, c.k0, c.k1, c.vw);
-      if (!((valid >> slot) & 1u)) {
+      if constexpr (GEN) {
+        // K: token lane & 15; V^T word byte i: token 4 (lane / 16) + i
+        const uint32_t m = slot_tokens(slot);
+        if (!((m >> kt) & 1u)) c.k0 = c.k1 = u32x4(0);
+        const uint32_t nib = (m >> (4 * (lane >> 4))) & 0xFu;
+        const uint32_t bytes = ((nib * 0x00204081u) & 0x01010101u) * 0xFFu;
+#pragma unroll
+        for (int b = 0; b < 8; ++b) c.vw[b] &= bytes;
+      } else if (!((valid >> slot) & 1u)) {
         c.k0 = c.k1 = u32x4(0);
 #pragma unroll
         for (int b = 0; b < 8; ++b) c.vw[b] = 0u;
@@ -928,6 +863,15 @@ __device__ __forceinline__ void ring_attend(const DecodeArgs& a, ST& st, const b
   }
 }
 
+// Tokens per page-id staging piece of a range: whole multiples of `align`
+// (the tile stride of every phase), spanning at most kRingPages pages from
+// any 16-aligned start.
+__device__ __forceinline__ int staging_piece(const DecodeArgs& a, int align) {
+  const int64_t tokens = a.bs_shift >= 0 ? int64_t(kRingPages - 1) << a.bs_shift
+                                         : int64_t(kRingPages - 1) * a.block_size;
+  return int(std::min<int64_t>(tokens, INT32_MAX / 2)) & ~(align - 1);
+}
+
 template <int NG>
 __device__ __forceinline__ void softmax_init(Softmax<NG>& st) {
 #pragma unroll
@@ -956,8 +900,8 @@ __device__ __forceinline__ float load_head(const DecodeArgs& a, int q_dtype, int
   return a.scale_log2 * qd * kd;
 }
 
-// P V on the matrix cores in the kernels built on ring_attend (the VALU path
-// stays for block sizes that are not powers of two, decode_partial_kernel).
+// P V on the matrix cores (PSK_PV_MFMA=0 builds the VALU P V of attend_step
+// instead, in fp32, for comparison).
 #ifndef PSK_PV_MFMA
 #define PSK_PV_MFMA 1
 #endif
@@ -966,7 +910,7 @@ template <int NG>
 using BalancedState = std::conditional_t<kPvMfma, SoftmaxM, Softmax<NG>>;
 
 // One workgroup per (split, kv head, sequence) (an explicit num_splits).
-template <int NG>
+template <int NG, bool GEN>
 __global__ void __launch_bounds__(kWaves * 64) decode_partial_ring_kernel(DecodeArgs a, int q_dtype) {
   // split s of sequence b sits at blockIdx.x = (s + b) % max_splits: workgroups
   // go round-robin to the 8 XCDs by blockIdx.x (max_splits is the fastest grid
@@ -985,9 +929,15 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_ring_kernel(Decode
   float sl = 0.0f;
   BalancedState<NG> st;
   softmax_init(st);
-  // the host keeps a split within kRingPages pages
-  ring_attend<NG, kWaves, kWaves, kRing>(a, st, qop, sl, b, h, t_begin, t_end, lane, wave, wave, lds,
-                                  [&] { sl = load_head<NG, !kPvMfma && (NG <= 4)>(a, q_dtype, b, h, lane, qop); });
+  // the split in pieces of at most kRingPages pages (one piece unless the pages are small)
+  const int piece = staging_piece(a, kTile * kWaves);
+  for (int t0 = t_begin; t0 < t_end; t0 += piece) {
+    const bool head = t0 == t_begin;
+    ring_attend<NG, kWaves, kWaves, kRing, GEN>(a, st, qop, sl, b, h, t0, min(t_end, t0 + piece), lane, wave, wave,
+                                                lds, [&] {
+      if (head) sl = load_head<NG, !kPvMfma && (NG <= 4)>(a, q_dtype, b, h, lane, qop);
+    });
+  }
   __syncthreads();  // every wave is done with the ring: it becomes the merge buffer
   write_partial<NG>(a, st, (int64_t(b) * a.num_kv_heads + h) * a.max_splits + s, lane, wave,
                     reinterpret_cast<float(*)[NG][kHead]>(&lds.ring[0][0][0][0]));
@@ -1073,7 +1023,7 @@ __device__ __forceinline__ void seek_unit(const int32_t* pref, int num_seqs, int
   t = int(u - pref[b]) - seq_units;
 }
 
-template <int NG>
+template <int NG, bool GEN>
 __global__ void __launch_bounds__(kWaves * 64) decode_partial_stream_kernel(DecodeArgs a, int q_dtype, int num_seqs) {
   const int w = blockIdx.x;
   const int lane = threadIdx.x & 63;
@@ -1098,8 +1048,7 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_stream_kernel(Deco
   seek_unit(pref, num_seqs, a.seq_units, u, b, t);
   // ring_attend's first barrier orders these prefix reads before the ring is refilled
 
-  // tokens per page staging: at most kRingPages pages from any 16-aligned start
-  const int piece = int(std::min<int64_t>(int64_t(kRingPages - 1) << a.bs_shift, INT32_MAX / 2)) & ~(kTile * kWaves - 1);
+  const int piece = staging_piece(a, kTile * kWaves);
   while (u < u_end && b < num_seqs) {
     if (t < 0) {  // leading units of b: no work
       const int skip = int(min<int64_t>(-t, u_end - u));
@@ -1117,7 +1066,8 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_stream_kernel(Deco
     const int t_end = min(len, (t + n) * kTile);
     for (int t0 = t * kTile; t0 < t_end; t0 += piece) {
       const bool head = t0 == t * kTile;
-      ring_attend<NG, kWaves, kWaves, kRing>(a, st, qop, sl, b, h, t0, min(t_end, t0 + piece), lane, wave, wave, lds, [&] {
+      ring_attend<NG, kWaves, kWaves, kRing, GEN>(a, st, qop, sl, b, h, t0, min(t_end, t0 + piece), lane, wave, wave,
+                                                  lds, [&] {
         if (head) sl = load_head<NG, !kPvMfma && (NG <= 4)>(a, q_dtype, b, h, lane, qop);
       });
     }
@@ -1261,7 +1211,7 @@ __device__ __forceinline__ void write_partial_heads(const DecodeArgs& a, Softmax
   }
 }
 
-template <int NG, int HG>
+template <int NG, int HG, bool GEN>
 __global__ void __launch_bounds__(kHeadWaves * 64) decode_partial_heads_kernel(DecodeArgs a, int q_dtype,
                                                                               int num_seqs) {
   constexpr int W = kHeadWaves;
@@ -1288,8 +1238,8 @@ __global__ void __launch_bounds__(kHeadWaves * 64) decode_partial_heads_kernel(D
   int b, t;
   seek_unit(s_pref, num_seqs, a.seq_units, u, b, t);
 
-  // page-id staging pieces: at most kRingPages pages, whole multiples of every phase stride
-  const int piece = int(std::min<int64_t>(int64_t(kRingPages - 1) << a.bs_shift, INT32_MAX / 2)) & ~(kTile * W - 1);
+  // page-id staging pieces: whole multiples of every phase stride
+  const int piece = staging_piece(a, kTile * W);
   while (u < u_end && b < num_seqs) {
     if (t < 0) {  // leading units of b: no work
       const int skip = int(min<int64_t>(-t, u_end - u));
@@ -1307,7 +1257,8 @@ __global__ void __launch_bounds__(kHeadWaves * 64) decode_partial_heads_kernel(D
     const int t_end = min(len, (t + n) * kTile);
     for (int t0 = t * kTile; t0 < t_end; t0 += piece) {
       const bool head = t0 == t * kTile;
-      ring_attend<NG, W, P, kHeadRing>(a, st, qop, sl, b, h, t0, min(t_end, t0 + piece), lane, wave, phase, lds, [&] {
+      ring_attend<NG, W, P, kHeadRing, GEN>(a, st, qop, sl, b, h, t0, min(t_end, t0 + piece), lane, wave, phase, lds,
+                                            [&] {
         if (head) sl = load_head<NG, !kPvMfma && (NG <= 4)>(a, q_dtype, b, h, lane, qop);
       });
     }
@@ -1482,7 +1433,9 @@ int decode_split(int64_t max_seq_len, int64_t num_splits, int64_t seq_heads) {
 }
 
 // Workgroups of the balanced schedule on the current device: one per slot that
-// can be resident at once (CUs x occupancy of the kernel instantiation).
+// can be resident at once (CUs x occupancy of the kernel instantiation).  The
+// general-page variants launch the same grid, so that the workspace size does
+// not depend on the block size.
 template <int NG>
 int64_t stream_wgs_for() {
   static std::mutex mu;
@@ -1494,7 +1447,7 @@ int64_t stream_wgs_for() {
   if (it != cache.end()) return it->second;
   int cus = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_partial_stream_kernel<NG>, kWaves * 64, 0) !=
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_partial_stream_kernel<NG, false>, kWaves * 64, 0) !=
           hipSuccess)
     return 0;
   const int64_t n = int64_t(cus) * std::max(per_cu, 1);
@@ -1529,7 +1482,7 @@ int64_t heads_wgs_for() {
   if (it != cache.end()) return it->second;
   int cus = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_partial_heads_kernel<NG, HG>, kHeadWaves * 64,
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_partial_heads_kernel<NG, HG, false>, kHeadWaves * 64,
                                                    0) != hipSuccess)
     return 0;
   const int64_t n = int64_t(cus) * std::max(per_cu, 1);
@@ -1560,14 +1513,48 @@ int64_t heads_runs(int ng, int64_t num_kv_heads) {
   return slots > 0 ? std::max<int64_t>(1, slots / (num_kv_heads / hg)) : 0;
 }
 
-template <int NG>
+template <int NG, bool GEN>
 void launch_heads_ng(const DecodeArgs& a, int q_dtype, int hg, dim3 grid, hipStream_t st, int ns) {
   const dim3 block(kHeadWaves * 64);
   switch (hg) {
-    case 1: hipLaunchKernelGGL((decode_partial_heads_kernel<NG, 1>), grid, block, 0, st, a, q_dtype, ns); break;
-    case 2: hipLaunchKernelGGL((decode_partial_heads_kernel<NG, 2>), grid, block, 0, st, a, q_dtype, ns); break;
-    case 4: hipLaunchKernelGGL((decode_partial_heads_kernel<NG, 4>), grid, block, 0, st, a, q_dtype, ns); break;
-    default: hipLaunchKernelGGL((decode_partial_heads_kernel<NG, 8>), grid, block, 0, st, a, q_dtype, ns); break;
+    case 1: hipLaunchKernelGGL((decode_partial_heads_kernel<NG, 1, GEN>), grid, block, 0, st, a, q_dtype, ns); break;
+    case 2: hipLaunchKernelGGL((decode_partial_heads_kernel<NG, 2, GEN>), grid, block, 0, st, a, q_dtype, ns); break;
+    case 4: hipLaunchKernelGGL((decode_partial_heads_kernel<NG, 4, GEN>), grid, block, 0, st, a, q_dtype, ns); break;
+    default: hipLaunchKernelGGL((decode_partial_heads_kernel<NG, 8, GEN>), grid, block, 0, st, a, q_dtype, ns); break;
+  }
+}
+
+// The partial kernels of one schedule for group slot ng: the balanced
+// schedule's head-parallel (heads) or per-head kernel with `runs` > 0, else
+// one workgroup per (split, kv head, sequence).
+template <bool GEN>
+void launch_partials(const DecodeArgs& a, int q_dtype, int ng, int64_t runs, bool heads, int64_t num_kv_heads,
+                     dim3 grid, hipStream_t st, int ns) {
+  const dim3 block(kWaves * 64);
+  if (runs > 0 && heads) {
+    const int hg = heads_hg(num_kv_heads);
+    const dim3 sgrid{unsigned(runs * (num_kv_heads / hg)), 1u, 1u};
+    switch (ng) {
+      case 1: launch_heads_ng<1, GEN>(a, q_dtype, hg, sgrid, st, ns); break;
+      case 2: launch_heads_ng<2, GEN>(a, q_dtype, hg, sgrid, st, ns); break;
+      case 4: launch_heads_ng<4, GEN>(a, q_dtype, hg, sgrid, st, ns); break;
+      default: launch_heads_ng<8, GEN>(a, q_dtype, hg, sgrid, st, ns); break;
+    }
+  } else if (runs > 0) {
+    const dim3 sgrid{unsigned(runs * num_kv_heads), 1u, 1u};
+    switch (ng) {
+      case 1: hipLaunchKernelGGL((decode_partial_stream_kernel<1, GEN>), sgrid, block, 0, st, a, q_dtype, ns); break;
+      case 2: hipLaunchKernelGGL((decode_partial_stream_kernel<2, GEN>), sgrid, block, 0, st, a, q_dtype, ns); break;
+      case 4: hipLaunchKernelGGL((decode_partial_stream_kernel<4, GEN>), sgrid, block, 0, st, a, q_dtype, ns); break;
+      default: hipLaunchKernelGGL((decode_partial_stream_kernel<8, GEN>), sgrid, block, 0, st, a, q_dtype, ns); break;
+    }
+  } else {
+    switch (ng) {
+      case 1: hipLaunchKernelGGL((decode_partial_ring_kernel<1, GEN>), grid, block, 0, st, a, q_dtype); break;
+      case 2: hipLaunchKernelGGL((decode_partial_ring_kernel<2, GEN>), grid, block, 0, st, a, q_dtype); break;
+      case 4: hipLaunchKernelGGL((decode_partial_ring_kernel<4, GEN>), grid, block, 0, st, a, q_dtype); break;
+      default: hipLaunchKernelGGL((decode_partial_ring_kernel<8, GEN>), grid, block, 0, st, a, q_dtype); break;
+    }
   }
 }
 
@@ -1600,17 +1587,6 @@ constexpr int kStreamSeqUnits = PSK_STREAM_SEQ_UNITS;
 // Runs per workgroup family of the balanced schedule for this batch.
 int64_t balanced_runs(int ng, int64_t num_seqs, int64_t num_kv_heads) {
   return num_seqs >= kHeadsMinSeqs ? heads_runs(ng, num_kv_heads) : stream_runs(ng, num_kv_heads);
-}
-
-template <bool UNIFORM>
-void launch_partial(const DecodeArgs& a, int q_dtype, dim3 grid, hipStream_t st, int ng) {
-  const dim3 block(kWaves * 64);
-  switch (ng) {
-    case 1: hipLaunchKernelGGL((decode_partial_kernel<1, UNIFORM>), grid, block, 0, st, a, q_dtype); break;
-    case 2: hipLaunchKernelGGL((decode_partial_kernel<2, UNIFORM>), grid, block, 0, st, a, q_dtype); break;
-    case 4: hipLaunchKernelGGL((decode_partial_kernel<4, UNIFORM>), grid, block, 0, st, a, q_dtype); break;
-    default: hipLaunchKernelGGL((decode_partial_kernel<8, UNIFORM>), grid, block, 0, st, a, q_dtype); break;
-  }
 }
 
 }  // namespace
@@ -1722,47 +1698,20 @@ int psk_paged_decode_attention(const void* q, int64_t q_tok_stride, int64_t q_he
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int ng = group_ng(G);
   const dim3 grid{unsigned(a.max_splits), unsigned(num_kv_heads), unsigned(num_seqs)};
-  // a 16-token tile stays in one page when the block size is a power of two >= 16
-  const bool ring = a.bs_shift >= 4 && 16 * std::max(a.k_row, a.v_row) < (int64_t(1) << 31);
+  // a 16-token tile stays in one page when the block size is a power of two >=
+  // 16 (and its rows are within 32-bit offsets): wave-uniform tile addressing;
+  // any other block size takes the general-page variants
+  const bool uniform = a.bs_shift >= 4 && 16 * std::max(a.k_row, a.v_row) < (int64_t(1) << 31);
   const bool heads = num_seqs >= kHeadsMinSeqs;
-  const int64_t runs =
-      ring && num_splits == 0 && num_seqs <= kStreamMaxSeqs ? balanced_runs(ng, num_seqs, num_kv_heads) : 0;
-  const bool uniform = ring && a.split / block_size + 1 <= kRingPages;
+  const int64_t runs = num_splits == 0 && num_seqs <= kStreamMaxSeqs ? balanced_runs(ng, num_seqs, num_kv_heads) : 0;
   if (runs > 0) {
     a.stream_wgs = int32_t(runs);
     a.seq_units = heads ? kHeadsSeqUnits : kStreamSeqUnits;
     a.prefix = reinterpret_cast<int32_t*>(workspace + (num_seqs + runs) * num_kv_heads * G * (kHead + 2));
-    const int ns = int(num_seqs);
-    if (heads) {
-      const int hg = heads_hg(num_kv_heads);
-      const dim3 sgrid{unsigned(runs * (num_kv_heads / hg)), 1u, 1u};
-      switch (ng) {
-        case 1: launch_heads_ng<1>(a, q_dtype, hg, sgrid, st, ns); break;
-        case 2: launch_heads_ng<2>(a, q_dtype, hg, sgrid, st, ns); break;
-        case 4: launch_heads_ng<4>(a, q_dtype, hg, sgrid, st, ns); break;
-        default: launch_heads_ng<8>(a, q_dtype, hg, sgrid, st, ns); break;
-      }
-    } else {
-      const dim3 sgrid{unsigned(runs * num_kv_heads), 1u, 1u}, block(kWaves * 64);
-      switch (ng) {
-        case 1: hipLaunchKernelGGL((decode_partial_stream_kernel<1>), sgrid, block, 0, st, a, q_dtype, ns); break;
-        case 2: hipLaunchKernelGGL((decode_partial_stream_kernel<2>), sgrid, block, 0, st, a, q_dtype, ns); break;
-        case 4: hipLaunchKernelGGL((decode_partial_stream_kernel<4>), sgrid, block, 0, st, a, q_dtype, ns); break;
-        default: hipLaunchKernelGGL((decode_partial_stream_kernel<8>), sgrid, block, 0, st, a, q_dtype, ns); break;
-      }
-    }
-  } else if (uniform) {
-    const dim3 block(kWaves * 64);
-    switch (ng) {
-      case 1: hipLaunchKernelGGL((decode_partial_ring_kernel<1>), grid, block, 0, st, a, q_dtype); break;
-      case 2: hipLaunchKernelGGL((decode_partial_ring_kernel<2>), grid, block, 0, st, a, q_dtype); break;
-      case 4: hipLaunchKernelGGL((decode_partial_ring_kernel<4>), grid, block, 0, st, a, q_dtype); break;
-      default: hipLaunchKernelGGL((decode_partial_ring_kernel<8>), grid, block, 0, st, a, q_dtype); break;
-    }
-  } else {
-    launch_partial<false>(a, q_dtype, grid, st, ng);
   }
-  const int st1 = check_launch("decode_partial_kernel launch");
+  if (uniform) launch_partials<false>(a, q_dtype, ng, runs, heads, num_kv_heads, grid, st, int(num_seqs));
+  else launch_partials<true>(a, q_dtype, ng, runs, heads, num_kv_heads, grid, st, int(num_seqs));
+  const int st1 = check_launch("decode partial kernel launch");
   if (st1 != PSK_OK) return st1;
   const dim3 grid2{unsigned(num_q_heads), unsigned(num_seqs), 1u};
   // waves per query head in the combine: one per kCombineChunk records a

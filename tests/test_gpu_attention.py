@@ -104,12 +104,22 @@ def test_decode_attention_matches_oracle(dev, Hq, Hkv, ps, q_dtype, out_dtype, d
     _case(dev, 11 + Hq + ps, len(LENS), Hq, Hkv, ps, 700, LENS, q_dtype, out_dtype, descales)
 
 
+@pytest.mark.parametrize("ps", [16, 24])
 @pytest.mark.parametrize("num_splits", [0, 1, 3, 40])
-def test_balanced_and_split_schedules(dev, num_splits):
+def test_balanced_and_split_schedules(dev, num_splits, ps):
     """num_splits 0 is the balanced schedule (every workgroup an equal run of
     (sequence, kv head, tile) units across sequence boundaries); an explicit
-    count splits each sequence, as FA's num_splits."""
-    _case(dev, 21, len(LENS), 8, 2, 16, 700, LENS, "bf16", torch.float32, "per_seq_head", num_splits=num_splits)
+    count splits each sequence, as FA's num_splits.  Pages of 24 tokens take
+    the general-page variants of the same kernels."""
+    _case(dev, 21, len(LENS), 8, 2, ps, 700, LENS, "bf16", torch.float32, "per_seq_head", num_splits=num_splits)
+
+
+@pytest.mark.parametrize("ps,G", [(5, 1), (12, 8), (48, 4), (100, 2)])
+def test_single_sequence_general_pages(dev, ps, G):
+    """One sequence (the per-head balanced kernel) on pages that are not a
+    power of two >= 16: tiles straddle pages, each lane addresses its own rows."""
+    print(f"single sequence: ps={ps} G={G}", flush=True)
+    _case(dev, 41 + ps, 1, 2 * G, 2, ps, 2000, [6001], "fp8", torch.float32, "per_seq_head")
 
 
 @pytest.mark.parametrize("B,Hkv,long_len", [(300, 1, 40000), (2, 4, 0), (1025, 2, 3000)])
@@ -128,13 +138,16 @@ def test_balanced_schedule_skewed_batches(dev, B, Hkv, long_len):
     _case(dev, 31 + B, B, 4 * Hkv, Hkv, 16, P, lens, "bf16", torch.float32, None)
 
 
-def test_decode_attention_bad_page_ids_read_as_zero_rows(dev):
-    _case(dev, 5, 3, 8, 2, 16, 300, [40, 70, 33], "bf16", torch.float32, None, bad_ids=True)
+@pytest.mark.parametrize("ps", [16, 24, 5])
+def test_decode_attention_bad_page_ids_read_as_zero_rows(dev, ps):
+    """A -1 and an out-of-range page id: their tokens read as zero K and V rows
+    (a whole tile with pages of 16; single tokens of a tile with 24 or 5)."""
+    _case(dev, 5, 3, 8, 2, ps, 300, [40, 70, 33], "bf16", torch.float32, None, bad_ids=True)
 
 
 def test_decode_attention_page_ids_beyond_lds_staging(dev):
-    """block_size 1 and a 70000-wide table: a split spans 1024 pages, more than
-    the LDS staging holds, so page ids are read from the table directly."""
+    """block_size 1 and a 70000-wide table: a range spans more pages than one
+    LDS staging of page ids holds (1024), so it is staged in pieces."""
     _case(dev, 6, 2, 4, 1, 1, 80000, [3000, 1100], "bf16", torch.float32, "per_seq_head", W=70000)
 
 
@@ -313,3 +326,24 @@ def test_decode_attention_random_shapes(dev, seed):
     num_splits = 0 if seed % 3 else int(rng.integers(1, 24))
     print(f"random {seed}: G={G} Hkv={Hkv} ps={ps} B={B} splits={num_splits} {q_dtype}", flush=True)
     _case(dev, 2000 + seed, B, G * Hkv, Hkv, ps, P, lens, q_dtype, out_dtype, descales, num_splits=num_splits)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_decode_attention_random_general_pages(dev, seed):
+    """Seeded random batches on pages that are not a power of two >= 16 (1 to
+    100 tokens): the general-page variants of every schedule, with the same
+    groups, lengths, dtypes and descales as the power-of-two cases."""
+    rng = np.random.default_rng(3000 + seed)
+    G = int(rng.integers(1, 9))
+    Hkv = int(rng.choice([1, 2, 4, 8]))
+    ps = int(rng.choice([1, 3, 8, 12, 24, 40, 100]))
+    B = int(rng.choice([1, 2, 3, 7, 8, 13, 40]))
+    lens = rng.integers(0, 3000, B).tolist()
+    lens[int(rng.integers(0, B))] = int(rng.integers(1, 3000))
+    P = max(64, sum(-(-x // ps) for x in lens) + 8)
+    q_dtype = "fp8" if seed % 2 else "bf16"
+    out_dtype = torch.float32 if seed % 4 < 2 else torch.bfloat16
+    descales = [None, "scalar", "per_seq_head"][seed % 3]
+    num_splits = 0 if seed % 3 else int(rng.integers(1, 24))
+    print(f"random general {seed}: G={G} Hkv={Hkv} ps={ps} B={B} splits={num_splits} {q_dtype}", flush=True)
+    _case(dev, 4000 + seed, B, G * Hkv, Hkv, ps, P, lens, q_dtype, out_dtype, descales, num_splits=num_splits)
