@@ -848,9 +848,10 @@ def run_l2_cycle(args, device):
 
     # host cost of keying the prompt: native chain against the reference's loop
     reps = 20
+    seqs = [Seq(9, prompt) for _ in range(reps)]  # fresh sequences: the keys are memoized per sequence
     t0 = time.perf_counter()
-    for _ in range(reps):
-        m._prompt_page_hashes(Seq(9, prompt))
+    for sq in seqs:
+        m._prompt_page_hashes(sq)
     t_native = (time.perf_counter() - t0) / reps
     oracle_ledger = OB.RefLedger(4, ps)
     t0 = time.perf_counter()
@@ -877,9 +878,10 @@ def run_l2_cycle(args, device):
 
 
 def run_attention_shapes(args, device):
-    """Decode attention over several batch shapes, under the balanced schedule
-    (num_splits 0, the default) and under the split schedule at the count the
-    split heuristic would pick; random FP8 pages, shuffled block tables.  `us`
+    """Decode attention over several batch shapes and block sizes, under the
+    balanced schedule (num_splits 0, the default) and under the split schedule
+    at the count the split heuristic would pick; random FP8 pages, shuffled
+    block tables.  `us`
     is the device time per call, from HIP events around graph replays of 10
     calls; `eager_us` is the same around eager calls, which includes the host
     time of the Python call where that exceeds the device time."""
@@ -901,10 +903,15 @@ def run_attention_shapes(args, device):
     ]
     # group 8 (64 query heads over 8 kv heads, Llama-3-70B class) on two of them
     shapes += [("128 log-uniform 128-32768, group 8", 8, 8, shapes[4][3]), ("32 x 8192, group 8", 8, 8, [8192] * 32)]
+    shapes = [(*x, 16) for x in shapes]
+    # pages that are not a power of two >= 16: the general-page kernel variants
+    shapes += [("128 log-uniform 128-32768, pages of 24", 8, 4, shapes[4][3], 24),
+               ("32 x 8192, pages of 48", 8, 4, [8192] * 32, 48), ("32 x 8192, pages of 5", 8, 4, [8192] * 32, 5),
+               ("32 x 8192, group 8, pages of 24", 8, 8, [8192] * 32, 24), ("1 x 32768, pages of 24", 8, 4, [32768], 24)]
     reps = max(10, min(args.steps, 50))
     results = []
-    for name, Hkv, G, lens in shapes:
-        B, ps = len(lens), 16
+    for name, Hkv, G, lens, ps in shapes:
+        B = len(lens)
         g = torch.Generator(device=device).manual_seed(1)
         pages = [math.ceil(x / ps) for x in lens]
         P = sum(pages) + 8
@@ -923,7 +930,7 @@ def run_attention_shapes(args, device):
         out = torch.empty(B, Hkv * G, 128, dtype=torch.bfloat16, device=device)
         kv_bytes = sum(lens) * Hkv * 128 * 2
         split = min(128, max(20, math.ceil(1536 / (B * Hkv))))
-        row = {"shape": name, "tokens": sum(lens), "kv_bytes": kv_bytes}
+        row = {"shape": name, "block_size": ps, "tokens": sum(lens), "kv_bytes": kv_bytes}
         for label, ns in (("balanced", 0), (f"split_{split}", split)):
             ws = torch.empty(attention.workspace_floats(B, Hkv * G, Hkv, W * ps, ns), dtype=torch.float32, device=device)
 
@@ -1451,7 +1458,7 @@ SECONDARY = (
     ("mla_prefill_fp8", 1024, 64),
     ("mla_decode_fp8", 1024, 64),
     ("copy_blocks", 8, 2),
-    ("decode_attention", 64, 8),
+    ("decode_attention", 256, 8),
     ("swap", 2, 1),
     ("metadata", 0, 0),
 )
