@@ -1023,8 +1023,12 @@ __device__ __forceinline__ void seek_unit(const int32_t* pref, int num_seqs, int
   t = int(u - pref[b]) - seq_units;
 }
 
+// Three waves per SIMD: left to itself the compiler keeps the MFMA accumulators in
+// AGPRs, which puts the general-page variant at 141 VGPRs + 36 AGPRs and two waves
+// per SIMD; asked for three it fits every variant in 143 VGPRs without spilling.
 template <int NG, bool GEN>
-__global__ void __launch_bounds__(kWaves * 64) decode_partial_stream_kernel(DecodeArgs a, int q_dtype, int num_seqs) {
+__global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(3)))
+decode_partial_stream_kernel(DecodeArgs a, int q_dtype, int num_seqs) {
   const int w = blockIdx.x;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
