@@ -847,16 +847,25 @@ def run_l2_cycle(args, device):
     res["bytes_checked"] = True
 
     # host cost of keying the prompt: native chain against the reference's loop
+    # both timed with the cyclic collector off (after one collection), so that a
+    # collection pass over the process's objects lands in neither
+    import gc
+
     reps = 20
-    seqs = [Seq(9, prompt) for _ in range(reps)]  # fresh sequences: the keys are memoized per sequence
-    t0 = time.perf_counter()
-    for sq in seqs:
-        m._prompt_page_hashes(sq)
-    t_native = (time.perf_counter() - t0) / reps
+    seqs = [Seq(9, prompt) for _ in range(reps + 1)]  # fresh sequences: the keys are memoized per sequence
     oracle_ledger = OB.RefLedger(4, ps)
-    t0 = time.perf_counter()
-    ref_keys = oracle_ledger.prompt_pages(Seq(9, prompt))
-    t_ref = time.perf_counter() - t0
+    gc.collect()
+    gc.disable()
+    try:
+        t0 = time.perf_counter()
+        for sq in seqs[:reps]:
+            m._prompt_page_hashes(sq)
+        t_native = (time.perf_counter() - t0) / reps
+        t0 = time.perf_counter()
+        ref_keys = oracle_ledger.prompt_pages(seqs[reps])
+        t_ref = time.perf_counter() - t0
+    finally:
+        gc.enable()
     assert [h for h, _ in ref_keys] == [h for h, _ in m._prompt_page_hashes(Seq(9, prompt))]
     res["prompt_keys_ms"] = {"native": 1e3 * t_native, "reference_loop": 1e3 * t_ref, "first_prefill_ms": 1e3 * t_alloc}
     print(json.dumps(res), file=sys.stderr, flush=True)

@@ -48,6 +48,21 @@ DEFAULT_L2_STEP_MS = 10.0  # block_manager.py:15
 DECODE_RESERVE_TOKENS = 512
 # Pages per submitted piece of one L2 store batch (_schedule_l2_store_batch).
 L2_STORE_CHUNK = 1024
+# Pages per restore piece submitted while allocate_prefill walks a prompt.
+L2_LOAD_CHUNK = 1024
+
+
+class _StagedLoads(list):
+    """A sequence's staged restores (one dict per page, as the reference stages
+    them), plus the copies already submitted for them and whether their pages
+    are pinned; the flush joins those copies into its transfers."""
+
+    __slots__ = ("handles", "pinned")
+
+    def __init__(self):
+        super().__init__()
+        self.handles = []
+        self.pinned = False
 
 
 # --------------------------------------------------------------------------- #
@@ -561,10 +576,9 @@ class BlockManager(_PagePool):
 
     # -- L2 loads (host -> GPU) -------------------------------------------- #
 
-    def _stage_l2_loads(self, seq, loads):
-        """Queue a sequence's restore for the batched flush (:497-507).  Its
-        pages are pinned here, so nothing recycles them before the flush."""
-        # _hold on both tiers, inlined: this runs once per restored page
+    def _pin_loads(self, loads):
+        """Pin both pages of each restore (_hold on both tiers, inlined: this
+        runs once per restored page)."""
         rc, cached = self.ref_counts, self.cached_pages
         l2 = self.l2_pool
         rc2, cached2 = l2.ref_counts, l2.cached_pages
@@ -576,6 +590,13 @@ class BlockManager(_PagePool):
             if rc2[q] == 0 and q in cached2:
                 del cached2[q]
             rc2[q] += 1
+
+    def _stage_l2_loads(self, seq, loads):
+        """Queue a sequence's restore for the batched flush (:497-507).  Its
+        pages are pinned here (or already, where its copies went out early), so
+        nothing recycles them before the flush."""
+        if not getattr(loads, "pinned", False):
+            self._pin_loads(loads)
         seq.l2_load_pending = True
         self._l2_pending_load_requests.append((seq, loads))
 
@@ -586,13 +607,26 @@ class BlockManager(_PagePool):
             return 0
         staged, self._l2_pending_load_requests = self._l2_pending_load_requests, []
         total = 0
+        engine = self.l2_copy_engine
         for group in self._split_l2_loads(staged):
-            src, dst = [], []
+            # pages whose copies already went out (submitted while their prompt
+            # was allocated) join the transfer as they are; the rest go now
+            src, dst, handles, late_src, late_dst = [], [], [], [], []
             for _, loads in group:
+                early = getattr(loads, "handles", None)
+                if early:
+                    handles.extend(early)
                 for load in loads:
                     src.append(load["l2_page_idx"])
                     dst.append(load["gpu_page_idx"])
-            copy = self.l2_copy_engine.load(src, dst)
+                    if not early:
+                        late_src.append(load["l2_page_idx"])
+                        late_dst.append(load["gpu_page_idx"])
+            if late_src:
+                handles.append(engine.load(late_src, late_dst))
+            # one transfer, priced from the whole group's runs as one submission
+            copy = handles[0] if len(handles) == 1 else copy_engine.JoinedCopyHandle(
+                handles, engine.count_runs(src, dst), len(dst))
             self.pending_l2_loads.append(
                 {"copy": copy, "due_step": self._l2_retire_step(copy, "load"), "seq_loads": group}
             )
@@ -759,30 +793,47 @@ class BlockManager(_PagePool):
     def _prefill_pages_batched(self, pages, matched, table):
         """Pages past the L1 match when the free and cached queues serve every
         allocation: no in-flight store is then reclaimed in between and what L2
-        holds stays fixed, so looking the restores up first and taking all
-        pages at once gives the pages, in the order, that one lookup and one
-        allocation per page give.  Returns the staged restores."""
+        holds stays fixed, so taking the pages in pieces after the lookups of
+        each piece gives the pages, in the order, that one lookup and one
+        allocation per page give.  The restores go to the copy engine in pieces
+        of L2_LOAD_CHUNK pages as they are found (their pages pinned first), so
+        the link starts while the rest of the prompt is still being walked; the
+        flush joins them into its transfers.  Returns the staged restores."""
         page_num = len(pages)
-        rest = page_num - matched
-        srcs = []
+        loads = _StagedLoads()
+        i = matched
         if self.enable_l2_cache:
             find = self.l2_pool._find
-            for i in range(matched, page_num - 1):
-                src = find(*pages[i])
-                if src is None:
+            engine = self.l2_copy_engine
+            hit = True
+            while hit and i < page_num - 1:
+                srcs = []
+                while i + len(srcs) < page_num - 1 and len(srcs) < L2_LOAD_CHUNK:
+                    src = find(*pages[i + len(srcs)])
+                    if src is None:
+                        hit = False
+                        break
+                    srcs.append(src)
+                if not srcs:
                     break
-                srcs.append(src)
-        self.l2_hit_cnt += len(srcs)
-        got = self._take_many(rest)
-        loads = []
-        for j, src in enumerate(srcs):
-            h, token_ids = pages[matched + j]
-            loads.append({"gpu_page_idx": got[j], "l2_page_idx": src, "hash": h, "token_ids": token_ids})
+                got = self._take_many(len(srcs))
+                piece = []
+                for j, src in enumerate(srcs):
+                    h, token_ids = pages[i + j]
+                    piece.append({"gpu_page_idx": got[j], "l2_page_idx": src, "hash": h, "token_ids": token_ids})
+                self._pin_loads(piece)
+                loads.extend(piece)
+                loads.handles.append(engine.load(srcs, got))
+                table.extend(got)
+                i += len(srcs)
+            loads.pinned = True
+        self.l2_hit_cnt += len(loads)
+        got = self._take_many(page_num - i)
         key, last = self._key_page, page_num - 1
-        for j in range(len(srcs), rest):
-            h, token_ids = pages[matched + j]
-            if h != -1 and matched + j != last:
-                key(got[j], h, token_ids)  # a fresh page: unkeyed, one reference
+        for j, p in enumerate(got):
+            h, token_ids = pages[i + j]
+            if h != -1 and i + j != last:
+                key(p, h, token_ids)  # a fresh page: unkeyed, one reference
         table.extend(got)
         return loads
 

@@ -49,6 +49,9 @@ from ._lib import check, lib
 TRANSPORTS = {"memcpy": _lib.SWAP_MEMCPY, "blit": _lib.SWAP_BLIT}
 DEFAULT_TRANSPORT = os.environ.get("PIPESWIFT_AMD_SWAP_TRANSPORT", "blit")
 _STAGING_SLOTS = 4
+# How long a submitter sleeps after queuing a transfer, so that the copy thread
+# takes the GIL and enqueues it (CopyEngine._submit).
+GIL_HANDOFF_S = 1e-4
 
 _i64p = ctypes.POINTER(ctypes.c_int64)
 _u64p = ctypes.POINTER(ctypes.c_uint64)
@@ -168,13 +171,16 @@ class CopyHandle:
         self.num_pages = 0
 
     def wait(self):
-        """Block until the transfer has landed (copy_engine.py:164-177)."""
+        """Block until the transfer has landed (copy_engine.py:164-177).  Until
+        the copy thread has enqueued the transfer there is no event to wait on;
+        the loop sleeps rather than spins, because the copy thread needs the GIL
+        to get there and a spin with os.sched_yield keeps holding it."""
         if not self.pending:
             return
         while self.event is None:
             if self.error is not None:
                 raise self.error
-            os.sched_yield()
+            time.sleep(GIL_HANDOFF_S)
         self.event.synchronize()
 
 
@@ -341,6 +347,11 @@ class CopyEngine:
         handle.num_runs = len(runs[0])
         handle.num_pages = len(src_ids)
         self.queue.put((runs, wait_event, handle, params))
+        # Hand the GIL to the copy thread so that it enqueues the transfer now: a
+        # caller that goes on with a long Python loop (the ledger walking a
+        # prompt) would otherwise hold it for up to the interpreter's 5 ms switch
+        # interval per piece.  sleep(0) returns before the thread has woken.
+        time.sleep(GIL_HANDOFF_S)
         return handle
 
     # -- copy thread --------------------------------------------------------- #

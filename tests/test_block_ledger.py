@@ -683,3 +683,20 @@ def test_random_trace_admitting_past_the_free_pages(monkeypatch):
     compared = [run_trace(monkeypatch, seed, num_pages=24, admit_past_free=0.6)[0] for seed in range(24)]
     assert sum(compared) > 2000
     assert paths["one_by_one_reclaimed"] >= 5 and paths["batched"] >= 200, paths
+
+
+def test_random_traces_with_restores_submitted_while_allocating(monkeypatch):
+    """Restores go to the copy engine in pieces of L2_LOAD_CHUNK pages while
+    allocate_prefill walks the prompt, and the flush joins them into its
+    transfers; with pieces of 2 pages every ledger state, deadline and page id
+    still equals the reference order's (one submission per transfer, at the
+    flush), and the restored tags land where the reference's do."""
+    monkeypatch.setattr(BM, "L2_LOAD_CHUNK", 2)
+    runs = [run_trace(monkeypatch, seed) for seed in range(12)]
+    assert sum(c for c, _ in runs) > 4000
+    assert sum(m.l2_load_cnt for _, m in runs) > 150
+    loads = [c for _, m in runs for c in m.l2_copy_engine.calls if c[0] == "load"]
+    # every restored page went out exactly once, in pieces of at most 2 pages
+    assert loads and all(len(c[1]) <= 2 for c in loads)
+    staged = sum(len(lds) for _, m in runs for _, lds in m._l2_pending_load_requests)
+    assert sum(len(c[1]) for c in loads) == sum(m.l2_load_cnt for _, m in runs) + staged
