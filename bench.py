@@ -1,17 +1,18 @@
 """Benchmark of the MI355X paged KV-cache path (one GPU).
 
-    python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline]
+    python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline] [--eager]
 
 A step is one launch of the hot-path kernel over one batch of synthetic input
 (one decode step's K/V append for one layer, by default).  Exactly K launches
-are timed after W untimed ones: they are replayed from HIP graphs of G
-launches (G = min(--graph, K, rotation sets)) plus one tail graph of K mod G
-launches, each launch over a different rotation set of inputs and slot
-mappings, as the reference replays its decode step from a CUDA graph
-(llm.py:634-681); the rotation keeps the working set far above the 256 MB
-Infinity Cache.  Inputs are resident in HBM before timing.  HIP events on the
-launch stream bracket the K launches, behind a bounded spin kernel so that
-host submission stays outside the timed region.
+are timed after W untimed ones, each over a different rotation set of inputs
+and slot mappings (the rotation keeps the working set far above the 256 MB
+Infinity Cache); inputs are resident in HBM before timing.  HIP events on the
+launch stream bracket the K launches (time_launches): up to 32 launches are
+queued behind a spin kernel, so that they run back to back with host
+submission outside the timed region; longer runs are one HIP graph of the K
+launches, replayed as the reference replays its decode step from a CUDA graph
+(llm.py:634-681).  --eager times plain launches instead (the PMC profiling
+runs use it).
 
 The default run reports config 2 (the FP8 decode append) as the headline and
 every other benchmark configuration under `secondary`, each a bounded run of
@@ -483,7 +484,7 @@ def measure_copy_floor(device, nbytes, steps=256):
     n = int(min(512, max(16, math.ceil((1 << 30) / (2 * each)))))
     src = torch.zeros(n, each, dtype=torch.uint8, device=device)
     dst = torch.empty_like(src)
-    t = time_launches(lambda i: dst[i].copy_(src[i]), n, steps, 16, 64, device, eager_calls=1)
+    t = time_launches(lambda i: dst[i].copy_(src[i]), n, steps, 16, device, eager_calls=1)
     del src, dst
     torch.cuda.empty_cache()
     return t["ms"] * 1e3 / t["launches"]
@@ -1334,7 +1335,7 @@ def _spin_us_per_cycle(device):
     return _SPIN_US_PER_CYCLE
 
 
-def time_launches(launch, rotate, steps, warmup, graph_len, device, eager_calls=200):
+def time_launches(launch, rotate, steps, warmup, device, eager_calls=200, eager=False):
     """HIP-event time of exactly `steps` launches on one stream, after `warmup`
     untimed ones.  Launch i uses rotation set i % rotate.
 
@@ -1355,8 +1356,8 @@ def time_launches(launch, rotate, steps, warmup, graph_len, device, eager_calls=
     external event-record node fails under capture on this runtime).  Graph
     replay is how the reference runs its decode step (llm.py:634-681), and a
     replayed dispatch costs less than a queued one.
-    graph_len == 0 forces eager launches between the events without a spin
-    long enough for them ("eager").
+    `eager` times plain launches between the events, without a spin
+    ("eager": the host's launch rate included).
 
     Returns a dict with the elapsed ms, the launch count, the method and the
     host wall time of one eager call (Python shim, argument checks, launch)."""
@@ -1385,7 +1386,7 @@ def time_launches(launch, rotate, steps, warmup, graph_len, device, eager_calls=
 
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
     method, ms = None, None
-    if int(graph_len) > 0 and 0 < steps <= QUEUED_MAX:
+    if not eager and 0 < steps <= QUEUED_MAX:
         us_per_cycle = _spin_us_per_cycle(device)
         spin_us = 2.0 * steps * eager_us + 200.0
         for _ in range(3):
@@ -1404,7 +1405,7 @@ def time_launches(launch, rotate, steps, warmup, graph_len, device, eager_calls=
                 method, ms = "queued", ev[1].elapsed_time(ev[2])
                 break
             spin_us *= 2.0
-    if method is None and int(graph_len) > 0 and steps > 0:
+    if method is None and not eager and steps > 0:
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.stream(stream):
             with torch.cuda.graph(graph, stream=stream):
@@ -1489,16 +1490,15 @@ def measure_workload(args, device, name, steps, warmup, achievable, cpu_budget, 
 
     launch, info = SETUPS[name](args, device)
     R = info.get("rotate", args.rotate)
-    graph_len = args.graph
-    t = time_launches(launch, R, steps, warmup, graph_len, device)
+    t = time_launches(launch, R, steps, warmup, device, eager=args.eager)
     per_launch_s = t["ms"] / 1e3 / t["launches"]
     achieved = info["bytes"] / per_launch_s / 1e9
     # For the microsecond workloads the same kernel is also timed over 2048
     # launches in one graph: the per-launch time inside a long graph, such as
     # a decode step, a cross-check of the short run's method.
     steady = None
-    if graph_len > 0 and steps < STEADY_STEPS and info["bytes"] < (64 << 20):
-        ts = time_launches(launch, R, STEADY_STEPS, warmup, graph_len, device, eager_calls=1)
+    if not args.eager and steps < STEADY_STEPS and info["bytes"] < (64 << 20):
+        ts = time_launches(launch, R, STEADY_STEPS, warmup, device, eager_calls=1)
         steady = ts["ms"] * 1e3 / ts["launches"]
     floor = None
     if copy_floor and info["bytes"] < (64 << 20):
@@ -1579,7 +1579,7 @@ def main():
                    help="default: config 2 as the headline plus every other configuration under `secondary`")
     p.add_argument("--no-secondary", action="store_true", help="default workload: the headline only")
     p.add_argument("--rotate", type=int, default=512, help="rotation sets of inputs/slots")
-    p.add_argument("--graph", type=int, default=64, help="launches captured per HIP graph (0: eager)")
+    p.add_argument("--eager", action="store_true", help="time plain eager launches (host launch rate included)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--transports", default="blit,memcpy", help="swap workload: transports to compare")
     p.add_argument("--swap-reps", type=int, default=3)
