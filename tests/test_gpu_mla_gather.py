@@ -196,6 +196,59 @@ def test_gather_many_sequences_kv_variants(dev, ps, H, D, with_starts):
         assert np.array_equal(raw(out), exp)
 
 
+@pytest.mark.parametrize("ps,H,D,dequant,pad", [(16, 4, 128, False, 0), (16, 8, 128, False, 64),
+                                                (16, 16, 128, False, 0), (24, 4, 128, False, 0),
+                                                (16, 4, 128, True, 0), (32, 8, 128, True, 128)])
+def test_gather_large_mixed_sequences(dev, ps, H, D, dequant, pad):
+    """Gathers of 4096+ tokens (the multi-token-per-wave launches) with rows of
+    64, 128 or 256 16-byte vectors: long and short sequences so a wave's
+    tokens start inside sequences and straddle their ends, more than 64
+    sequences, seq_starts, bad block ids, padded output rows, fp8
+    dequantization, output rows past the batch untouched."""
+    g = torch.Generator().manual_seed(50 + ps + H + int(dequant))
+    P, B = 4096, 90
+    row = H * D
+    lens = torch.randint(0, 40, (B,), generator=g)
+    lens[::11] = torch.randint(300, 1500, (len(lens[::11]),), generator=g)
+    lens[5] = 0
+    cu = torch.zeros(B + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(lens, 0)
+    starts = torch.randint(0, 2 * ps, (B,), generator=g).to(torch.int32)
+    W = (int(lens.max()) + 2 * ps) // ps + 1
+    bt = torch.randint(0, P, (B, W), generator=g, dtype=torch.int32)
+    bt[0, 1] = P + 3  # out of range -> zero rows
+    bt[11, 0] = -2
+    T = int(cu[-1]) + 21
+    assert T >= 4096
+    if dequant:
+        caches = [torch.randint(0, 256, (P, ps, H, D), generator=g, dtype=torch.uint8) for _ in range(2)]
+        for c in caches:
+            c[(c & 0x7F) == 0x7F] = 0x21  # no NaN codes: NaN payloads are not pinned
+        src = [c.to(dev).view(torch.float8_e4m3fn) for c in caches]
+        out_dt, scale = torch.bfloat16, 0.375
+    else:
+        caches = [workloads.sentinel((P, ps, H, D), torch.bfloat16, 51 + i) for i in range(2)]
+        src = [c.to(dev) for c in caches]
+        out_dt, scale = torch.bfloat16, None
+    print(f"large gather: ps={ps} H={H} D={D} dequant={dequant} pad={pad} T={T}", flush=True)
+    full = [torch.full((T, row + pad), 3, dtype=out_dt, device=dev) for _ in range(2)]
+    outs = [f[:, :row].view(T, H, D) for f in full]
+    cache_ops.gather_cache(src[0], outs[0], bt.to(dev), cu.to(dev), seq_starts=starts.to(dev),
+                           scale=None if scale is None else torch.tensor([scale], dtype=torch.float32, device=dev),
+                           src_cache_v=src[1], dst_v=outs[1])
+    fill = raw(torch.full((1,), 3, dtype=out_dt))[0]
+    for cache, f in zip(caches, full):
+        exp = np.full((T, row + pad), fill, np.uint16)
+        body = exp[:, :row].reshape(T, H, D)
+        if dequant:
+            got = O.gather_cache(cache.numpy(), bt.numpy(), cu.numpy(), seq_starts=starts.numpy(),
+                                 cache_dtype="fp8", out_dtype="bf16", scale=scale, out=body.copy())
+        else:
+            got = O.gather_cache(raw(cache), bt.numpy(), cu.numpy(), seq_starts=starts.numpy(), out=body.copy())
+        exp[:, :row] = got.reshape(T, row)
+        assert np.array_equal(raw(f), exp)
+
+
 def test_config3_block_size_128_append_then_gather(dev):
     """Config 3's sensitivity run: the same chunked prefill at 128-token pages
     (4096 blocks, the same slot capacity), append then gather, against the
