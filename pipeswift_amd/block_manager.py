@@ -50,6 +50,10 @@ DECODE_RESERVE_TOKENS = 512
 L2_STORE_CHUNK = 1024
 # Pages per restore piece submitted while allocate_prefill walks a prompt.
 L2_LOAD_CHUNK = 1024
+# The first piece of a batch or prompt is this many pages (at most the chunk)
+# and each later one twice the one before, up to the chunk: the link starts
+# after the host has walked 128 pages (~0.2 ms) instead of 1024 (~1.4 ms).
+L2_FIRST_PIECE = 128
 
 
 class _StagedLoads(list):
@@ -507,10 +511,10 @@ class BlockManager(_PagePool):
         stops at the first store no L2 page can take (:433-474).
 
         The transfer is one logical copy, as in the reference, but it is
-        submitted in pieces of L2_STORE_CHUNK pages while this loop is still
-        walking the batch, so the link starts moving the first pages instead of
-        waiting for the host's per-page bookkeeping of the whole batch (about
-        12 ms for an 8192-page prompt).  Page ids, order and the deadline
+        submitted in pieces (L2_FIRST_PIECE pages, doubling up to
+        L2_STORE_CHUNK) while this loop is still walking the batch, so the link
+        starts moving the first pages instead of waiting for the host's per-page
+        bookkeeping of the whole batch (about 12 ms for an 8192-page prompt).  Page ids, order and the deadline
         priced from the whole batch's runs are those of a single submission."""
         if not self.enable_l2_cache:
             return 0
@@ -523,6 +527,7 @@ class BlockManager(_PagePool):
         # inlined with the key tuple built once: this runs once per page
         pending, find, take = pool._pending_store_keys, pool._find, pool.allocate_for_store
         rc, cached = self.ref_counts, self.cached_pages
+        piece = min(L2_FIRST_PIECE, L2_STORE_CHUNK)
         for page_idx, h, token_ids in stores:
             key = (h, tuple(token_ids))
             if h != -1 and (key in pending or find(h, token_ids) is not None):
@@ -539,9 +544,10 @@ class BlockManager(_PagePool):
             l2.append(dst)
             keys.append(h)
             toks.append(token_ids)
-            if len(gpu) - sent >= L2_STORE_CHUNK:
+            if len(gpu) - sent >= piece:
                 handles.append(engine.store(gpu[sent:], l2[sent:]))
                 sent = len(gpu)
+                piece = min(2 * piece, L2_STORE_CHUNK)
         if not gpu:
             return 0
         if sent < len(gpu):
@@ -796,9 +802,10 @@ class BlockManager(_PagePool):
         holds stays fixed, so taking the pages in pieces after the lookups of
         each piece gives the pages, in the order, that one lookup and one
         allocation per page give.  The restores go to the copy engine in pieces
-        of L2_LOAD_CHUNK pages as they are found (their pages pinned first), so
-        the link starts while the rest of the prompt is still being walked; the
-        flush joins them into its transfers.  Returns the staged restores."""
+        (L2_FIRST_PIECE pages, doubling up to L2_LOAD_CHUNK) as they are found
+        (their pages pinned first), so the link starts while the rest of the
+        prompt is still being walked; the flush joins them into its transfers.
+        Returns the staged restores."""
         page_num = len(pages)
         loads = _StagedLoads()
         i = matched
@@ -806,9 +813,10 @@ class BlockManager(_PagePool):
             find = self.l2_pool._find
             engine = self.l2_copy_engine
             hit = True
+            limit = min(L2_FIRST_PIECE, L2_LOAD_CHUNK)
             while hit and i < page_num - 1:
                 srcs = []
-                while i + len(srcs) < page_num - 1 and len(srcs) < L2_LOAD_CHUNK:
+                while i + len(srcs) < page_num - 1 and len(srcs) < limit:
                     src = find(*pages[i + len(srcs)])
                     if src is None:
                         hit = False
@@ -826,6 +834,7 @@ class BlockManager(_PagePool):
                 loads.handles.append(engine.load(srcs, got))
                 table.extend(got)
                 i += len(srcs)
+                limit = min(2 * limit, L2_LOAD_CHUNK)
             loads.pinned = True
         self.l2_hit_cnt += len(loads)
         got = self._take_many(page_num - i)
