@@ -392,10 +392,15 @@ struct GatherGeom {
 template <class C, int CH, int U, bool POW2>
 __global__ void __launch_bounds__(256) paged_gather_kernel(GatherGeom g) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t wave = int64_t(blockIdx.x) * (blockDim.x / kWave) +
-                       __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
-  const int part = g.nparts == 2 ? int(wave & 1) : 0;
-  const int64_t t0 = (g.nparts == 2 ? (wave >> 1) : wave) * CH;
+  // Part 0 (K) fills the first half of the grid and part 1 (V) the second, so
+  // the waves in flight at any time stream one part's pages into one
+  // contiguous output (config 3: 116.5 us against 118.5 with the parts
+  // interleaved wave by wave).  The launch gives each part the same number of
+  // workgroups.
+  const int64_t half = gridDim.x >> 1;
+  const int part = g.nparts == 2 && int64_t(blockIdx.x) >= half ? 1 : 0;
+  const int64_t t0 = ((int64_t(blockIdx.x) - part * half) * (blockDim.x / kWave) +
+                      __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave)) * CH;
   const char* src = part ? g.src1 : g.src0;
   char* dst = part ? g.dst1 : g.dst0;
   // Branch-free up to the row loads (a wave past the last token runs with
@@ -512,29 +517,31 @@ __global__ void __launch_bounds__(256) paged_gather_kernel(GatherGeom g) {
   }
 }
 
+// Workgroups of `wpb` waves for chunks of `ch` tokens: the same number per
+// part (paged_gather_kernel splits the grid in halves between K and V).
+inline int64_t gather_grid(const GatherGeom& g, int ch, int wpb) {
+  return ceil_div(ceil_div(g.num_tokens, ch), wpb) * g.nparts;
+}
+
 template <class C, bool POW2>
 void launch_gather_pow2(const GatherGeom& g, hipStream_t st) {
   if (g.num_tokens < 4096) {
-    const int64_t waves = g.num_tokens * g.nparts;
     const int threads = g.num_tokens <= 1024 ? 64 : 256;
-    hipLaunchKernelGGL((paged_gather_kernel<C, 1, 2, POW2>), dim3(ceil_div(waves, threads / kWave)), dim3(threads),
-                       0, st, g);
+    hipLaunchKernelGGL((paged_gather_kernel<C, 1, 2, POW2>), dim3(gather_grid(g, 1, threads / kWave)),
+                       dim3(threads), 0, st, g);
   } else {
     // About 2 KiB of cache per wave: one token of a row over 64 vectors (two
     // vectors per lane, looping beyond), two tokens of a 1 KiB row, four of a
     // smaller one.  Measured on config 3's 1 KiB rows: 118.5 us at two tokens
-    // per wave, 123 at four, 133 at sixteen, 135 at one.
+    // per wave, 123 at four, 133 at sixteen, 135 at one (parts interleaved);
+    // with the parts in grid halves 116.5 at two, 121.7 at four, 135 at one.
     const int64_t in_row = int64_t(g.row_vecs) * C::IN_B;
-    if (g.row_vecs > kWave) {
-      const int64_t waves = g.num_tokens * g.nparts;
-      hipLaunchKernelGGL((paged_gather_kernel<C, 1, 2, POW2>), dim3(ceil_div(waves, 4)), dim3(256), 0, st, g);
-    } else if (in_row >= 1024) {
-      const int64_t waves = ceil_div(g.num_tokens, 2) * g.nparts;
-      hipLaunchKernelGGL((paged_gather_kernel<C, 2, 1, POW2>), dim3(ceil_div(waves, 4)), dim3(256), 0, st, g);
-    } else {
-      const int64_t waves = ceil_div(g.num_tokens, 4) * g.nparts;
-      hipLaunchKernelGGL((paged_gather_kernel<C, 4, 1, POW2>), dim3(ceil_div(waves, 4)), dim3(256), 0, st, g);
-    }
+    if (g.row_vecs > kWave)
+      hipLaunchKernelGGL((paged_gather_kernel<C, 1, 2, POW2>), dim3(gather_grid(g, 1, 4)), dim3(256), 0, st, g);
+    else if (in_row >= 1024)
+      hipLaunchKernelGGL((paged_gather_kernel<C, 2, 1, POW2>), dim3(gather_grid(g, 2, 4)), dim3(256), 0, st, g);
+    else
+      hipLaunchKernelGGL((paged_gather_kernel<C, 4, 1, POW2>), dim3(gather_grid(g, 4, 4)), dim3(256), 0, st, g);
   }
 }
 
