@@ -107,8 +107,14 @@ struct TileAppendArgs {
 };
 
 // RV: bytes per rope vector; NV: bytes per E4M3 store (8, or 4 when entries
-// are only 4-byte aligned).
-template <int RV, int NV>
+// are only 4-byte aligned).  WHOLE: the DeepSeek-V3 entry (4 tiles, 16 scale
+// bytes, 128 rope bytes: 656 bytes on 16-byte boundaries), written by one
+// store instruction of 16 bytes per lane over the whole entry.  An entry then
+// leaves the L1 as one write request per 64-byte line it touches (11), so only
+// the two lines it shares with its neighbours are partial; written as three
+// parts (E4M3, scales, rope), the lines where the parts meet are split into
+// separate partial requests too (12.5 per entry).
+template <int RV, int NV, bool WHOLE = false>
 __global__ void __launch_bounds__(kWaves * 64) tile_fp8_append_kernel(TileAppendArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t t_wave = int64_t(blockIdx.x) * kWaves + __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
@@ -138,7 +144,9 @@ __global__ void __launch_bounds__(kWaves * 64) tile_fp8_append_kernel(TileAppend
   char* entry = a.cache + blk * a.blk_stride + off * a.page_stride;
   const int nope_bytes = a.tiles * kTileElems;
 
-  if (lane < a.rope_vecs) vstore_nt<RV>(entry + a.rope_off + lane * RV, r0);
+  if constexpr (!WHOLE) {
+    if (lane < a.rope_vecs) vstore_nt<RV>(entry + a.rope_off + lane * RV, r0);
+  }
   for (int i = lane + 64; i < a.rope_vecs; i += 64) vstore_nt<RV>(entry + a.rope_off + i * RV, vload_nt<RV>(pe + i * RV));
   for (int p = 0; p * kTilesPerPass < a.tiles; ++p) {
     const int tile = p * kTilesPerPass + (lane >> 4);
@@ -169,13 +177,30 @@ __global__ void __launch_bounds__(kWaves * 64) tile_fp8_append_kernel(TileAppend
           }
         }
       }
-      if constexpr (NV == 8) {
-        vstore_nt<8>(entry + e, q);
+      if constexpr (WHOLE) {
+        // one pass, every lane active: lane j < 32 takes the E4M3 bytes of
+        // lanes 2j and 2j + 1, lane 32 the four scales (rows 0..3), lanes
+        // 33..40 the rope vectors of lanes 0..7
+        const uint32_t n0 = uint32_t(__shfl(int(q[0]), 2 * lane)), n1 = uint32_t(__shfl(int(q[1]), 2 * lane));
+        const uint32_t n2 = uint32_t(__shfl(int(q[0]), 2 * lane + 1)), n3 = uint32_t(__shfl(int(q[1]), 2 * lane + 1));
+        const int rl = lane - 33;
+        const u32x4 rope = __builtin_bit_cast(u32x4, r0);
+        const uint32_t r0w = uint32_t(__shfl(int(rope[0]), rl)), r1w = uint32_t(__shfl(int(rope[1]), rl));
+        const uint32_t r2w = uint32_t(__shfl(int(rope[2]), rl)), r3w = uint32_t(__shfl(int(rope[3]), rl));
+        const uint32_t sb = __float_as_uint(s);
+        const u32x4 sc = {uint32_t(__builtin_amdgcn_readlane(int(sb), 0)), uint32_t(__builtin_amdgcn_readlane(int(sb), 16)),
+                          uint32_t(__builtin_amdgcn_readlane(int(sb), 32)), uint32_t(__builtin_amdgcn_readlane(int(sb), 48))};
+        const u32x4 w = lane < 32 ? u32x4{n0, n1, n2, n3} : lane == 32 ? sc : u32x4{r0w, r1w, r2w, r3w};
+        if (lane <= 40) vstore_nt<16>(entry + 16 * lane, w);
       } else {
-        vstore_nt<4>(entry + e, q[0]);
-        vstore_nt<4>(entry + e + 4, q[1]);
+        if constexpr (NV == 8) {
+          vstore_nt<8>(entry + e, q);
+        } else {
+          vstore_nt<4>(entry + e, q[0]);
+          vstore_nt<4>(entry + e + 4, q[1]);
+        }
+        if ((lane & 15) == 0) vstore_nt<4>(entry + nope_bytes + 4 * tile, __float_as_uint(s));
       }
-      if ((lane & 15) == 0) vstore_nt<4>(entry + nope_bytes + 4 * tile, __float_as_uint(s));
     }
   }
 }
@@ -354,6 +379,17 @@ int psk_concat_and_cache_mla_fp8_tiles(const void* kv_c, const void* k_pe, void*
 #define PSK_TILE_APPEND(RV)                                                       \
   if (nv == 8) hipLaunchKernelGGL((tile_fp8_append_kernel<RV, 8>), grid, block, 0, s, a); \
   else hipLaunchKernelGGL((tile_fp8_append_kernel<RV, 4>), grid, block, 0, s, a)
+  // the DeepSeek-V3 entry on 16-byte boundaries, prefill-sized batches: one
+  // store over the entry (config 4 prefill 4.33 -> 4.20 us, HBM bytes 1.059x
+  // -> 1.032x the algorithmic).  A decode-sized batch is latency bound, and the
+  // lane exchange that assembles the entry lengthens its critical path (128
+  // tokens: 2.68 -> 2.74 us), so it keeps the three-part stores.
+  const bool whole = num_tokens >= 1024 && tiles == kTilesPerPass && rope_off == kPassElems + 4 * kTilesPerPass &&
+                     2 * rope_len == 128 && rv == 16 && common_align(ent_v, 3, 16) == 16;
+  if (whole) {
+    hipLaunchKernelGGL((tile_fp8_append_kernel<16, 8, true>), grid, block, 0, s, a);
+    return check_launch("tile_fp8_append_kernel launch");
+  }
   switch (rv) {
     case 16: PSK_TILE_APPEND(16); break;
     case 8: PSK_TILE_APPEND(8); break;

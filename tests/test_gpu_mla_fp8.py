@@ -39,9 +39,13 @@ def test_config4_append_whole_cache(dev, decode):
     assert len(np.unique(s)) > 100
 
 
-def test_slots_and_special_values(dev):
+@pytest.mark.parametrize("n,P", [(300, 40), (1500, 120)])
+def test_slots_and_special_values(dev, n, P):
+    """Zero, NaN, infinite, tiny and overflowing tiles, skipped and
+    out-of-range slots; 1500 tokens take the prefill launch, which writes
+    each entry with one store."""
     g = torch.Generator().manual_seed(41)
-    n, P, ps = 300, 40, 16
+    ps = 16
     x = torch.randn(n, 512, generator=g) * torch.exp2(torch.randint(-20, 20, (n, 1), generator=g).float())
     x[0, :128] = 0.0                      # zero tile
     x[1, 200] = float("nan")
