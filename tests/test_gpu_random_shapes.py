@@ -1,5 +1,5 @@
-"""Seeded random-shape parity sweeps of the append, MLA concat, gather and
-copy_blocks entry points against the CPU oracle.
+"""Seeded random-shape parity sweeps of the append, MLA concat, gather,
+copy_blocks and L2 page transport entry points against the CPU oracle.
 
 Each case draws its geometry (heads, head size, block size, pool size, token
 count across the decode-sized and prefill-sized launches), dtypes, strides and
@@ -175,3 +175,53 @@ def test_random_copy_blocks(dev, seed):
     exp = raw(stack).copy()
     O.copy_blocks(exp, pairs.numpy())
     assert np.array_equal(raw(sd), exp)
+
+
+def _page_ids(rng, n, limit):
+    """n unique page ids of [0, limit): runs of consecutive ids mixed with
+    scattered ones, so the transfer coalesces some pages and not others."""
+    out, used = [], set()
+    while len(out) < n:
+        start = int(rng.integers(0, limit))
+        run = int(rng.choice([1, 1, 2, 5, 17]))
+        for p in range(start, min(limit, start + run)):
+            if p not in used and len(out) < n:
+                used.add(p)
+                out.append(p)
+    return np.array(out, np.int64)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_swaps(dev, seed):
+    """CopyEngine store (device -> pinned host) then load (host -> other device
+    pages) over one or two layered caches of different page sizes."""
+    from pipeswift_amd import copy_engine
+
+    rng = np.random.default_rng(9000 + seed)
+    L = int(rng.choice([1, 2, 5]))
+    P, P2 = int(rng.integers(20, 300)), int(rng.integers(20, 300))
+    shapes = [[(2, 16, 2, 64), (16, 576), (2, 5, 3, 40)][seed % 3]]
+    if seed % 2:
+        shapes.append((8, 72))
+    transport = "blit" if seed % 4 < 3 else "memcpy"
+    n = int(rng.integers(1, min(P, P2) + 1))
+    print(f"swap seed={seed}: L={L} P={P} P2={P2} shapes={shapes} n={n} {transport}", flush=True)
+    caches = [workloads.sentinel((L, P) + sh, torch.bfloat16, 9100 + seed + i) for i, sh in enumerate(shapes)]
+    cds = [c.to(dev) for c in caches]
+    eng = copy_engine.CopyEngine(cds, P, P2, transport=transport)
+    try:
+        gpu_ids, l2_ids = _page_ids(rng, n, P), _page_ids(rng, n, P2)
+        eng.store(gpu_ids.tolist(), l2_ids.tolist()).wait()
+        for c, hc in zip(caches, eng.host_caches):
+            assert np.array_equal(raw(hc)[:, l2_ids], raw(c)[:, gpu_ids])
+        back = _page_ids(rng, n, P)
+        for cd in cds:
+            cd.zero_()
+        eng.load(l2_ids.tolist(), back.tolist()).wait()
+        untouched = np.setdiff1d(np.arange(P), back)
+        for c, cd in zip(caches, cds):
+            got = raw(cd)
+            assert np.array_equal(got[:, back], raw(c)[:, gpu_ids])
+            assert not got[:, untouched].any()
+    finally:
+        eng.close()
