@@ -300,14 +300,20 @@ int64_t psk_build_next_decode_metadata(int64_t num_seqs, const uint64_t* page_ta
  * Paged decode attention over an FP8 E4M3FN KV cache (replaces the reader the
  * reference calls through vLLM's FA3 fork, pipeswift/llms/layers/attention.py:
  * 148-187, which takes an FP8 query and per-(sequence, kv head) descales).
- * One query token per sequence.  For sequence b, query head hq = h*G + g
- * (G = num_q_heads / num_kv_heads <= 8) and tokens j < seq_lens[b]:
- *   q~  = e4m3(q[b,hq] / qd)   (q_dtype FP8: q as is)
+ * Decode and speculative decode: sequence b has n_b query tokens, the last n_b
+ * positions of the sequence, at rows [c_b, c_b + n_b) of q and out, with
+ * c_b = cu_seqlens_q[b] and n_b = cu_seqlens_q[b+1] - c_b (cu_seqlens_q NULL:
+ * c_b = b * q_len, n_b = q_len); q_len bounds every n_b and
+ * q_len * num_q_heads / num_kv_heads must be at most 16.  For query token
+ * r = c_b + i, query head hq = h*G + g (G = num_q_heads / num_kv_heads) and
+ * keys j < L_i, where L_i = seq_lens[b] - n_b + 1 + i when causal (FA's
+ * bottom-right alignment) and seq_lens[b] otherwise:
+ *   q~  = e4m3(q[r,hq] / qd)   (q_dtype FP8: q as is)
  *   s_j = softmax_scale * qd * kd * (q~ . K[j,h])
- *   out[b,hq] = vd * sum_j softmax(s)_j V[j,h],   lse[hq,b] = log sum_j exp(s_j)
+ *   out[r,hq] = vd * sum_j softmax(s)_j V[j,h],   lse[hq,r] = log sum_j exp(s_j)
  * qd/kd/vd = descale[b * stride_b + h * stride_h] (descale_strides holds the
  * (b, h) strides of q, k, v in that order; a NULL descale is 1.0).
- * q: [B, Hq, 128] at element strides (q_tok_stride, q_head_stride).
+ * q: [total_q, Hq, 128] at element strides (q_tok_stride, q_head_stride).
  * k_cache, v_cache: FP8 [num_blocks, block_size, Hkv, 128]; *_strides are the
  * (block, row, head) strides in bytes, every one and both bases 16-byte aligned.
  * Token j of sequence b is row j % block_size of page
@@ -321,8 +327,9 @@ int64_t psk_build_next_decode_metadata(int64_t num_seqs, const uint64_t* page_ta
  * 16-token tiles across sequence boundaries, a sequence start priced as
  * extra tiles), otherwise an automatic split count.
  * out: bf16 or f32 at element strides (out_tok_stride, out_head_stride); lse
- * (fp32, optional) at lse[hq * lse_head_stride + b]; a sequence of length 0
- * writes zeros and lse = -inf.  workspace: device floats, at least
+ * (fp32, optional) at lse[hq * lse_head_stride + r]; a query token that sees
+ * no key (a sequence of length 0) writes zeros and lse = -inf.  Rows of q and
+ * out outside every [c_b, c_b + n_b) are not touched.  workspace: device floats, at least
  * psk_paged_decode_workspace_len(); no initial contents needed.  Two launches.
  */
 int psk_paged_decode_attention(const void* q, int64_t q_tok_stride, int64_t q_head_stride, int q_dtype,
@@ -332,6 +339,7 @@ int psk_paged_decode_attention(const void* q, int64_t q_tok_stride, int64_t q_he
                                const int32_t* seq_lens, int64_t num_seqs, int64_t num_q_heads,
                                int64_t num_kv_heads, int64_t head_size, int64_t block_size,
                                int64_t num_blocks, int64_t max_seq_len, int64_t num_splits,
+                               int64_t q_len, const int32_t* cu_seqlens_q, int causal,
                                float softmax_scale,
                                const float* q_descale, const float* k_descale,
                                const float* v_descale, const int64_t* descale_strides, void* out,
@@ -339,8 +347,8 @@ int psk_paged_decode_attention(const void* q, int64_t q_tok_stride, int64_t q_he
                                float* lse, int64_t lse_head_stride, float* workspace,
                                int64_t workspace_len, void* stream);
 
-int64_t psk_paged_decode_workspace_len(int64_t num_seqs, int64_t num_q_heads, int64_t num_kv_heads,
-                                       int64_t max_seq_len, int64_t num_splits);
+int64_t psk_paged_decode_workspace_len(int64_t num_seqs, int64_t q_len, int64_t num_q_heads,
+                                       int64_t num_kv_heads, int64_t max_seq_len, int64_t num_splits);
 
 /*
  * FP8 MLA latent entries with one scale per 128-element tile (build-defined;

@@ -508,52 +508,70 @@ def graph_refresh(static, step, cg_bsz, pad_q_len=1):
 
 
 def paged_decode_attention(q, q_dtype, k_cache, v_cache, block_table, seq_lens, softmax_scale, q_descale=None,
-                           k_descale=None, v_descale=None):
-    """Decode attention of one query token per sequence over an FP8 E4M3FN
-    paged cache, in float64 (the semantics the reference gets from vLLM's FA3
-    fork, pipeswift/llms/layers/attention.py:148-187: FP8 query, descales per
+                           k_descale=None, v_descale=None, cu_seqlens_q=None, causal=False):
+    """Decode attention over an FP8 E4M3FN paged cache, in float64 (the
+    semantics the reference gets from vLLM's FA3 fork,
+    pipeswift/llms/layers/attention.py:148-187: FP8 query, descales per
     (sequence, kv head), here any values instead of the fixed 1.0 of
-    fp8_kv.py:94-103).
+    fp8_kv.py:94-103; ``max_seqlen_q`` = attention.py:175, ``causal`` =
+    attention.py:181).
 
-    q: raw bits [B, Hq, D] of ``q_dtype`` ("fp8" is used as is, others are
+    q: raw bits [TQ, Hq, D] of ``q_dtype`` ("fp8" is used as is, others are
     quantized as e4m3(q / q_descale)); k_cache, v_cache: uint8 [P, ps, Hkv, D];
     block_table: int [B, W]; seq_lens: int [B]; descales: float [B, Hkv] or None.
-    Returns (out [B, Hq, D], lse [B, Hq]) as float64; a sequence of length 0
-    gives zeros and lse = -inf.  Table entries outside [0, P) read as zero rows.
+    cu_seqlens_q: int [B + 1], sequence b's query tokens at rows
+    [cu[b], cu[b+1]) of q, its last positions; None: one token per sequence
+    (TQ = B).  With ``causal`` query token i of n sees keys
+    [0, seq_len - n + 1 + i) (FA's bottom-right alignment), else all of them.
+    Returns (out [TQ, Hq, D], lse [TQ, Hq]) as float64; a query token that
+    sees no key, and a row no sequence owns, gives zeros and lse = -inf.  Table
+    entries outside [0, P) read as zero rows.
     """
     q = np.asarray(q)
-    B, Hq, D = q.shape
+    TQ, Hq, D = q.shape
     P, ps, Hkv, _ = k_cache.shape
     G = Hq // Hkv
-    out = np.zeros((B, Hq, D), dtype=np.float64)
-    lse = np.full((B, Hq), -np.inf, dtype=np.float64)
+    if cu_seqlens_q is None:
+        cu = np.arange(TQ + 1)
+    else:
+        cu = np.asarray(cu_seqlens_q, dtype=np.int64)
+    B = len(cu) - 1
+    out = np.zeros((TQ, Hq, D), dtype=np.float64)
+    lse = np.full((TQ, Hq), -np.inf, dtype=np.float64)
     ones = np.ones((B, Hkv), dtype=np.float32)
     qd_all = ones if q_descale is None else np.asarray(q_descale, dtype=np.float32)
     kd_all = ones if k_descale is None else np.asarray(k_descale, dtype=np.float32)
     vd_all = ones if v_descale is None else np.asarray(v_descale, dtype=np.float32)
     for b in range(B):
         n = int(seq_lens[b])
-        if n == 0:
+        c0, nq = int(cu[b]), int(cu[b + 1] - cu[b])
+        if n == 0 or nq <= 0:
             continue
+        # keys each query token sees
+        lim = np.array([min(n, max(0, n - nq + 1 + i)) if causal else n for i in range(nq)])
         j = np.arange(n)
         pages = np.asarray(block_table[b], dtype=np.int64)[j // ps]
         ok = (pages >= 0) & (pages < P)
         rows = j % ps
         for h in range(Hkv):
             qd, kd, vd = float(qd_all[b, h]), float(kd_all[b, h]), float(vd_all[b, h])
-            qs = q[b, h * G:(h + 1) * G]
-            if q_dtype == "fp8":
-                qq = e4m3fn_to_f32(qs).astype(np.float64)
-            else:
-                qq = e4m3fn_to_f32(quantize_e4m3(to_f32(qs, q_dtype), qd)).astype(np.float64)
             K = np.zeros((n, D), dtype=np.float64)
             V = np.zeros((n, D), dtype=np.float64)
             K[ok] = e4m3fn_to_f32(k_cache[pages[ok], rows[ok], h]).astype(np.float64)
             V[ok] = e4m3fn_to_f32(v_cache[pages[ok], rows[ok], h]).astype(np.float64)
-            s = (qq @ K.T) * (float(np.float32(softmax_scale)) * qd * kd)
-            m = s.max(axis=1, keepdims=True)
-            p = np.exp(s - m)
-            den = p.sum(axis=1, keepdims=True)
-            out[b, h * G:(h + 1) * G] = (p @ V) / den * vd
-            lse[b, h * G:(h + 1) * G] = (m + np.log(den))[:, 0]
+            for i in range(nq):
+                L = int(lim[i])
+                if L == 0:
+                    continue
+                qs = q[c0 + i, h * G:(h + 1) * G]
+                if q_dtype == "fp8":
+                    qq = e4m3fn_to_f32(qs).astype(np.float64)
+                else:
+                    qq = e4m3fn_to_f32(quantize_e4m3(to_f32(qs, q_dtype), qd)).astype(np.float64)
+                s = (qq @ K[:L].T) * (float(np.float32(softmax_scale)) * qd * kd)
+                m = s.max(axis=1, keepdims=True)
+                p = np.exp(s - m)
+                den = p.sum(axis=1, keepdims=True)
+                out[c0 + i, h * G:(h + 1) * G] = (p @ V[:L]) / den * vd
+                lse[c0 + i, h * G:(h + 1) * G] = (m + np.log(den))[:, 0]
     return out, lse

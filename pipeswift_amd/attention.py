@@ -7,7 +7,8 @@ cu_seqlens_q, max_seqlen_k=None, seqused_k, block_table, softmax_scale,
 causal, fa_version=3, q_descale, k_descale, v_descale)``
 (pipeswift/llms/layers/attention.py:148-187), with every descale 1.0
 (pipeswift/utils/fp8_kv.py:94-103).  ``flash_attn_varlen_func`` here takes the
-same arguments for the decode case (one query token per sequence) and runs
+same arguments for decode and speculative decode (a few query tokens per
+sequence, causal with FA's bottom-right alignment) and runs
 ``psk_paged_decode_attention``: Q K^T on the bf16 MFMA over exactly converted
 FP8 values (gfx950's FP8 MFMA truncates its sums), fp32 softmax, P V on the
 bf16 MFMA with P split into hi + lo bf16 parts (2^-17 relative per weight,
@@ -15,7 +16,10 @@ fp32 sums) for every block size, and descales of any value per (sequence,
 kv head) -- for instance the per-tensor
 scales ``cache_ops.compute_kv_scales`` gave the append.
 
-Prefill over the paged cache is not covered; ``max_seqlen_q`` must be 1.
+The query tokens of a sequence and the query heads of a kv head share the
+16 rows of one MFMA tile: ``max_seqlen_q * Hq / Hkv`` must be at most 16
+(e.g. 4 draft positions at 4 heads per kv head).  Prefill over the paged
+cache is not covered.
 """
 
 from __future__ import annotations
@@ -27,13 +31,15 @@ import torch
 from ._lib import check, dtype_code, i64_array, lib, ptr, stream_handle
 
 HEAD_DIM = 128
-MAX_GROUP = 8
+MAX_ROWS = 16  # query tokens x query heads per kv head
 
 _OUT_CODES = {torch.bfloat16: 2, torch.float32: 0}
 
 
-def workspace_floats(num_seqs: int, num_q_heads: int, num_kv_heads: int, max_seq_len: int, num_splits: int = 0) -> int:
-    n = int(lib().psk_paged_decode_workspace_len(num_seqs, num_q_heads, num_kv_heads, max_seq_len, num_splits))
+def workspace_floats(num_seqs: int, num_q_heads: int, num_kv_heads: int, max_seq_len: int, num_splits: int = 0,
+                     q_len: int = 1) -> int:
+    n = int(lib().psk_paged_decode_workspace_len(num_seqs, q_len, num_q_heads, num_kv_heads, max_seq_len,
+                                                  num_splits))
     if n < 0:
         check(n, "paged decode workspace")
     return n
@@ -68,15 +74,23 @@ def paged_decode_attention(
     max_seq_len: Optional[int] = None,
     workspace: Optional[torch.Tensor] = None,
     num_splits: int = 0,
+    q_len: int = 1,
+    cu_seqlens_q: Optional[torch.Tensor] = None,
+    causal: bool = True,
 ):
     """One decode step of attention for every sequence.
 
-    q: [B, Hq, 128] (fp8 e4m3fn used as is; bf16/fp16/fp32 quantized as
-    e4m3(q / q_descale), as the reference quantizes its query).
+    q: [total_q, Hq, 128] (fp8 e4m3fn used as is; bf16/fp16/fp32 quantized as
+    e4m3(q / q_descale), as the reference quantizes its query).  Sequence b
+    owns query rows [cu_seqlens_q[b], cu_seqlens_q[b+1]) (int32 [B+1]; None:
+    q_len rows each, total_q = B * q_len), at most ``q_len`` of them: its last
+    positions.  With ``causal`` query token i of n sees the first
+    seq_lens[b] - n + 1 + i keys (FA's bottom-right alignment), else all.
     k_cache, v_cache: fp8 [num_blocks, block_size, Hkv, 128] (views of the fused
     [P, 2, ps, H, D] layer are fine).  block_table: int32 [B, W];
-    seq_lens: int32 [B] (``seqused_k``).  Returns out [B, Hq, 128] (bf16 unless
-    ``out`` is given as float32) and, when asked, lse [Hq, B] float32.
+    seq_lens: int32 [B] (``seqused_k``).  Returns out [total_q, Hq, 128] (bf16
+    unless ``out`` is given as float32) and, when asked, lse [Hq, total_q]
+    float32; rows no sequence owns are left as they were.
     ``num_splits``: workgroups per longest sequence, as FA's; 0 (default)
     balances the work instead: one workgroup per resident slot, each streaming
     an equal run of the batch's 16-token tiles of one kv head across sequence
@@ -87,9 +101,19 @@ def paged_decode_attention(
     assert k_cache.dtype == torch.float8_e4m3fn and v_cache.dtype == torch.float8_e4m3fn, "the cache must be fp8 e4m3fn"
     assert k_cache.dim() == 4 and k_cache.shape == v_cache.shape and k_cache.shape[3] == HEAD_DIM
     assert k_cache.stride(3) == 1 and v_cache.stride(3) == 1
-    B, Hq, _ = q.shape
+    TQ, Hq, _ = q.shape
     P, ps, Hkv, _ = k_cache.shape
-    assert Hq % Hkv == 0 and Hq // Hkv <= MAX_GROUP, f"{Hq} query heads over {Hkv} kv heads (at most {MAX_GROUP} per)"
+    q_len = int(q_len)
+    assert q_len >= 1
+    if cu_seqlens_q is None:
+        assert TQ % q_len == 0, f"{TQ} query rows are not {q_len} per sequence"
+        B = TQ // q_len
+    else:
+        assert cu_seqlens_q.dtype == torch.int32 and cu_seqlens_q.is_contiguous() and cu_seqlens_q.dim() == 1
+        assert cu_seqlens_q.device == q.device
+        B = cu_seqlens_q.shape[0] - 1
+    assert Hq % Hkv == 0 and q_len * (Hq // Hkv) <= MAX_ROWS, \
+        f"{q_len} query tokens x {Hq // Hkv} heads per kv head (at most {MAX_ROWS} rows)"
     assert block_table.dtype == torch.int32 and block_table.dim() == 2 and block_table.stride(1) == 1
     assert block_table.shape[0] >= B
     assert seq_lens.dtype == torch.int32 and seq_lens.is_contiguous() and seq_lens.numel() >= B
@@ -99,10 +123,10 @@ def paged_decode_attention(
     if max_seq_len is None:
         max_seq_len = block_table.shape[1] * ps  # bounds every sequence, no host sync
     if out is None:
-        out = torch.empty(B, Hq, HEAD_DIM, dtype=torch.bfloat16, device=device)
-    assert out.dtype in _OUT_CODES and out.shape == (B, Hq, HEAD_DIM) and out.stride(2) == 1
-    lse = torch.empty(Hq, B, dtype=torch.float32, device=device) if return_softmax_lse else None
-    need = workspace_floats(B, Hq, Hkv, max_seq_len, num_splits)
+        out = torch.empty(TQ, Hq, HEAD_DIM, dtype=torch.bfloat16, device=device)
+    assert out.dtype in _OUT_CODES and out.shape == (TQ, Hq, HEAD_DIM) and out.stride(2) == 1
+    lse = torch.empty(Hq, TQ, dtype=torch.float32, device=device) if return_softmax_lse else None
+    need = workspace_floats(B, Hq, Hkv, max_seq_len, num_splits, q_len)
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(max(need, 1), dtype=torch.float32, device=device)
     qd, qsb, qsh = _descale(q_descale, B, Hkv, device)
@@ -112,9 +136,10 @@ def paged_decode_attention(
         q.data_ptr(), q.stride(0), q.stride(1), dtype_code(q.dtype),
         k_cache.data_ptr(), v_cache.data_ptr(), i64_array(k_cache.stride()[:3]), i64_array(v_cache.stride()[:3]),
         block_table.data_ptr(), block_table.stride(0), block_table.shape[1], seq_lens.data_ptr(), B, Hq, Hkv,
-        HEAD_DIM, ps, P, int(max_seq_len), int(num_splits), float(softmax_scale), ptr(qd), ptr(kd), ptr(vd),
+        HEAD_DIM, ps, P, int(max_seq_len), int(num_splits), q_len, ptr(cu_seqlens_q), 1 if causal else 0,
+        float(softmax_scale), ptr(qd), ptr(kd), ptr(vd),
         i64_array([qsb, qsh, ksb, ksh, vsb, vsh]), out.data_ptr(), out.stride(0), out.stride(1),
-        _OUT_CODES[out.dtype], ptr(lse), B if lse is not None else 0, workspace.data_ptr(), workspace.numel(),
+        _OUT_CODES[out.dtype], ptr(lse), TQ if lse is not None else 0, workspace.data_ptr(), workspace.numel(),
         stream_handle(device),
     )
     check(st, "paged_decode_attention")
@@ -141,18 +166,23 @@ def flash_attn_varlen_func(
     num_splits=0,
 ):
     """The FA3 entry the reference's ``_fp8_paged_attn`` calls
-    (attention.py:166-184), for decode: q is [total_q, Hq, D] with one token per
-    sequence (``max_seqlen_q == 1``; ``cu_seqlens_q`` then is 0..B and
-    ``causal`` has nothing to mask).  ``max_seqlen_k`` bounds the lengths when
-    given, else the block table's width does.  ``num_splits`` is the
-    flash-decoding split count (0: the balanced schedule); ``fa_version`` is
-    accepted for signature compatibility."""
-    assert max_seqlen_q == 1, "decode only: one query token per sequence"
+    (attention.py:166-184), for decode and speculative decode: q is
+    [total_q, Hq, D], sequence b's query tokens at rows
+    [cu_seqlens_q[b], cu_seqlens_q[b+1]), at most ``max_seqlen_q`` of them
+    (``max_seqlen_q * Hq / Hkv <= 16``), the sequence's last positions; with
+    ``causal`` each sees the keys up to its own position.  ``max_seqlen_k``
+    bounds the lengths when given, else the block table's width does.
+    ``num_splits`` is the flash-decoding split count (0: the balanced
+    schedule); ``fa_version`` is accepted for signature compatibility."""
     assert seqused_k is not None and block_table is not None, "paged decode needs seqused_k and block_table"
     B = seqused_k.shape[0]
-    assert q.shape[0] == B and cu_seqlens_q.shape[0] == B + 1
+    assert cu_seqlens_q is not None and cu_seqlens_q.shape[0] == B + 1
+    q_len = int(max_seqlen_q)
+    # one token per sequence: rows 0..B-1 whatever cu_seqlens_q holds (it is 0..B)
+    cu = None if q_len == 1 else cu_seqlens_q
+    assert q_len > 1 or q.shape[0] == B
     ps = k.shape[1]
     bound = block_table.shape[1] * ps if max_seqlen_k is None else min(int(max_seqlen_k), block_table.shape[1] * ps)
     return paged_decode_attention(q, k, v, block_table, seqused_k, softmax_scale, q_descale, k_descale, v_descale,
                                   out=out, return_softmax_lse=return_softmax_lse, max_seq_len=bound,
-                                  num_splits=num_splits)
+                                  num_splits=num_splits, q_len=q_len, cu_seqlens_q=cu, causal=causal)

@@ -70,7 +70,9 @@ constexpr int kTile = 16;     // tokens per tile (N of the 16x16x32 MFMA)
 constexpr int kWaves = 4;     // waves per workgroup
 constexpr int kMinSplit = 256;
 constexpr int kMaxSplits = 128;
-constexpr int kMaxGroup = 8;   // query heads per kv head
+// MFMA rows per (sequence, kv head): query tokens x query heads per kv head,
+// padded to 1, 2, 4, 8 or 16 (16 with P V on the matrix cores)
+constexpr int kMaxRows = 16;
 constexpr float kNegBig = -1.0e30f;  // finite "no token yet" maximum
 constexpr float kLazy = 8.0f;        // raise the running max past 2^8 headroom only
 constexpr int kRing = 2;             // LDS tile slots per wave (ring kernel)
@@ -99,7 +101,11 @@ struct DecodeArgs {
   int32_t block_size;
   int32_t bs_shift;  // log2(block_size) or -1
   int32_t num_kv_heads;
-  int32_t group;     // query heads per kv head
+  int32_t group;     // MFMA rows per (sequence, kv head): q_len query tokens x heads
+  int32_t heads;     // query heads per kv head
+  int32_t q_len;     // query token slots per sequence (the most query tokens any sequence has)
+  const int32_t* cu_q;  // query tokens of sequence b: [cu_q[b], cu_q[b+1]); NULL: [b q_len, (b+1) q_len)
+  int32_t causal;    // query token i of n of a sequence of length L sees keys [0, L - n + 1 + i)
   int32_t split;     // tokens per workgroup
   int32_t max_splits;
   float scale_log2;  // softmax_scale * log2(e)
@@ -120,6 +126,14 @@ struct DecodeArgs {
   float* lse;               // [Hq][lse_head_stride] (entry [hq][b]) or nullptr
   int64_t lse_head_stride;
 };
+
+// First query token of sequence b and how many it has (at most q_len).
+__device__ __forceinline__ int64_t q_first(const DecodeArgs& a, int b) {
+  return a.cu_q ? int64_t(a.cu_q[b]) : int64_t(b) * a.q_len;
+}
+__device__ __forceinline__ int q_count(const DecodeArgs& a, int b) {
+  return a.cu_q ? max(0, min(a.q_len, a.cu_q[b + 1] - a.cu_q[b])) : a.q_len;
+}
 
 __device__ __forceinline__ float descale(const float* p, int64_t sb, int64_t sh, int b, int h) {
   return p ? p[b * sb + h * sh] : 1.0f;
@@ -211,7 +225,10 @@ __device__ __forceinline__ void load_query(const DecodeArgs& a, int q_dtype, int
   for (int i = 0; i < 8; ++i) qw[i] = 0;
   const int row = REPL ? (lane & 3) : (lane & 15);
   if (row >= a.group) return;
-  const char* src = a.q + b * a.q_tok_stride + int64_t(h * a.group + row) * a.q_head_stride;
+  // row = i * heads + g: query token i of the sequence, head g of the group
+  const int i = row / a.heads, g = row - i * a.heads;
+  if (i >= q_count(a, b)) return;
+  const char* src = a.q + (q_first(a, b) + i) * a.q_tok_stride + int64_t(h * a.heads + g) * a.q_head_stride;
   const int d0 = 32 * (lane >> 4);
   switch (q_dtype) {
     case PSK_DTYPE_FP8_E4M3FN: load_query_as<PSK_DTYPE_FP8_E4M3FN>(src, qd, d0, qw); break;
@@ -539,11 +556,15 @@ __device__ __forceinline__ void ring_read_pv(uint32_t slot, uint32_t rk0, uint32
 
 // One 16-token tile of one wave on the matrix cores.  vw: V^T words (byte j =
 // token 4 (lane / 16) + j of column 16 b + lane % 16), zero for a missing page;
-// G query heads of the group are rows 0 .. G-1.
-template <bool PARTIAL, class Consumed>
+// rows 0 .. G-1 are the group's (query token, query head) pairs.
+//
+// MASKED: a tile that reaches t_end or the causal band; this lane's row then
+// sees keys below min(t_end, row_lim).  Every other tile is whole and visible
+// to every row.
+template <bool MASKED, class Consumed>
 __device__ __forceinline__ void attend_step_pv(SoftmaxM& st, const u32x4& k0, const u32x4& k1,
                                                const uint32_t (&vw)[8], const bf16x8 qop[4], float sl, int t0,
-                                               int t_end, int G, int lane, const Consumed& consumed) {
+                                               int t_end, int G, int lane, int row_lim, const Consumed& consumed) {
   f32x4 sc = {0.0f, 0.0f, 0.0f, 0.0f};
   sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(e4m3x8_to_bf16(k0[0], k0[1]), qop[0], sc, 0, 0, 0);
   sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(e4m3x8_to_bf16(k0[2], k0[3]), qop[1], sc, 0, 0, 0);
@@ -553,9 +574,10 @@ __device__ __forceinline__ void attend_step_pv(SoftmaxM& st, const u32x4& k0, co
 
   const int g = lane & 15, tq = 4 * (lane >> 4);
   float s4[4];
+  const int lim = MASKED ? min(t_end, row_lim) : 0;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const bool ok = g < G && (!PARTIAL || t0 + tq + r < t_end);
+    const bool ok = g < G && (!MASKED || t0 + tq + r < lim);
     s4[r] = ok ? sc[r] * sl : -__builtin_inff();
   }
   float mx = __builtin_fmaxf(__builtin_fmaxf(s4[0], s4[1]), __builtin_fmaxf(s4[2], s4[3]));
@@ -583,7 +605,7 @@ __device__ __forceinline__ void attend_step_pv(SoftmaxM& st, const u32x4& k0, co
   const bf16x4 lo = {(__bf16)(p[0] - (float)hi[0]), (__bf16)(p[1] - (float)hi[1]), (__bf16)(p[2] - (float)hi[2]),
                      (__bf16)(p[3] - (float)hi[3])};
   uint32_t vmask = 0xFFFFFFFFu;
-  if constexpr (PARTIAL) {
+  if constexpr (MASKED) {
     // tokens at or past t_end may hold anything (a NaN would survive p = 0)
     const int n_ok = t_end - (t0 + tq);
     vmask = n_ok >= 4 ? 0xFFFFFFFFu : n_ok <= 0 ? 0u : (0xFFFFFFFFu >> (32 - 8 * n_ok));
@@ -681,7 +703,7 @@ __device__ __forceinline__ void wait_vmcnt(int n) {
 // ballots at issue) zeroes those tokens' K and V when the slot is read.
 template <int NG, int W, int P, int R, bool GEN, class ST, class Overlap>
 __device__ __forceinline__ void ring_attend(const DecodeArgs& a, ST& st, const bf16x8 (&qop)[4],
-                                            const float& sl, int b, int h, int t_begin, int t_end, int lane,
+                                            const float& sl, int b, int h, int t_begin, int t_end, int len, int lane,
                                             int wave, int phase, RingLdsT<W, R>& lds, const Overlap& overlap) {
   static_assert(R >= 2 && R <= 4, "ring of 2 to 4 tiles per wave");
   constexpr int kIdsPerThread = kRingPages / (W * 64);
@@ -739,11 +761,16 @@ __device__ __forceinline__ void ring_attend(const DecodeArgs& a, ST& st, const b
   }
 
   // start the loads of tile j into its slot; a missing page reads page 0 (in
-  // bounds) and is zeroed when consumed
+  // bounds) and is zeroed when consumed.  Before a new tile goes out, the
+  // loads still in flight land: the waves of a workgroup, which read the same
+  // token rows, then stay in step.  Config 2's decode: 225 us; two tiles in
+  // flight per wave 230; a three-slot ring with one or two in flight 227 and
+  // 235
   uint32_t valid = 0;  // bit j % R: slot holds a tile on a real page
   auto issue = [&](int j) {
     const int t0 = t_first + j * stride;
     const int slot = j % R;
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     if constexpr (GEN) {
       const int ta = t0 + drow;
       const int32_t ida = ta < t_end ? lds.pages[pia - first] : -1;
@@ -837,16 +864,30 @@ __device__ __forceinline__ void ring_attend(const DecodeArgs& a, ST& st, const b
       }
       return c;
     };
+    // query token i of n sees keys below causal_lo + i, causal_lo = len - n + 1
+    // when causal (FA's bottom-right alignment), else every key: row_lim
+    const int causal_lo = __builtin_amdgcn_readfirstlane(a.causal ? len - max(q_count(a, b), 1) + 1 : len);
+    const int qrow = lane & 15;
+    const int row_lim = causal_lo + (a.causal && qrow < G ? qrow / a.heads : 0);
     if (n_tiles > 0) {
+      // tiles j >= j_mask reach t_end or causal_lo and mask per row: the last
+      // one, and with several query tokens and a one-tile stride possibly the
+      // one before (causal_lo > len - 16); the loop over the others has no test
+      const int lo = causal_lo - kTile - t_first;
+      const int j_mask = min(n_tiles - 1, lo < 0 ? 0 : lo / stride + 1);
       int j = 0;
-      for (; j + 1 < n_tiles; ++j) {
+      for (; j < j_mask; ++j) {
         PvTile c = fetch_pv(j);
-        attend_step_pv<false>(st, c.k0, c.k1, c.vw, qop, sl, t_first + j * stride, t_end, G, lane, [&] {
+        attend_step_pv<false>(st, c.k0, c.k1, c.vw, qop, sl, t_first + j * stride, t_end, G, lane, row_lim, [&] {
           if (j + R < n_tiles) issue(j + R);
         });
       }
-      PvTile c = fetch_pv(j);
-      attend_step_pv<true>(st, c.k0, c.k1, c.vw, qop, sl, t_first + j * stride, t_end, G, lane, [] {});
+      for (; j < n_tiles; ++j) {
+        PvTile c = fetch_pv(j);
+        attend_step_pv<true>(st, c.k0, c.k1, c.vw, qop, sl, t_first + j * stride, t_end, G, lane, row_lim, [&] {
+          if (j + R < n_tiles) issue(j + R);
+        });
+      }
     }
   } else {
     if (n_tiles > 0) {
@@ -933,8 +974,8 @@ __global__ void __launch_bounds__(kWaves * 64) decode_partial_ring_kernel(Decode
   const int piece = staging_piece(a, kTile * kWaves);
   for (int t0 = t_begin; t0 < t_end; t0 += piece) {
     const bool head = t0 == t_begin;
-    ring_attend<NG, kWaves, kWaves, kRing, GEN>(a, st, qop, sl, b, h, t0, min(t_end, t0 + piece), lane, wave, wave,
-                                                lds, [&] {
+    ring_attend<NG, kWaves, kWaves, kRing, GEN>(a, st, qop, sl, b, h, t0, min(t_end, t0 + piece), len, lane, wave,
+                                                wave, lds, [&] {
       if (head) sl = load_head<NG, !kPvMfma && (NG <= 4)>(a, q_dtype, b, h, lane, qop);
     });
   }
@@ -1070,8 +1111,8 @@ decode_partial_stream_kernel(DecodeArgs a, int q_dtype, int num_seqs) {
     const int t_end = min(len, (t + n) * kTile);
     for (int t0 = t * kTile; t0 < t_end; t0 += piece) {
       const bool head = t0 == t * kTile;
-      ring_attend<NG, kWaves, kWaves, kRing, GEN>(a, st, qop, sl, b, h, t0, min(t_end, t0 + piece), lane, wave, wave,
-                                                  lds, [&] {
+      ring_attend<NG, kWaves, kWaves, kRing, GEN>(a, st, qop, sl, b, h, t0, min(t_end, t0 + piece), len, lane, wave,
+                                                  wave, lds, [&] {
         if (head) sl = load_head<NG, !kPvMfma && (NG <= 4)>(a, q_dtype, b, h, lane, qop);
       });
     }
@@ -1100,7 +1141,7 @@ decode_partial_stream_kernel(DecodeArgs a, int q_dtype, int num_seqs) {
 // per-head balanced schedule, so the same combine reads them.
 constexpr int kHeadWaves = 8;
 // LDS tile slots per wave.  At one workgroup per CU deeper rings cost no
-// occupancy, but measured slower on config 2: 250 us at three, 252 at four.
+// occupancy, but measured slower on config 2: 227 us at three against 225.
 constexpr int kHeadRing = 2;
 
 
@@ -1261,8 +1302,8 @@ __global__ void __launch_bounds__(kHeadWaves * 64) decode_partial_heads_kernel(D
     const int t_end = min(len, (t + n) * kTile);
     for (int t0 = t * kTile; t0 < t_end; t0 += piece) {
       const bool head = t0 == t * kTile;
-      ring_attend<NG, W, P, kHeadRing, GEN>(a, st, qop, sl, b, h, t0, min(t_end, t0 + piece), lane, wave, phase, lds,
-                                            [&] {
+      ring_attend<NG, W, P, kHeadRing, GEN>(a, st, qop, sl, b, h, t0, min(t_end, t0 + piece), len, lane, wave, phase,
+                                            lds, [&] {
         if (head) sl = load_head<NG, !kPvMfma && (NG <= 4)>(a, q_dtype, b, h, lane, qop);
       });
     }
@@ -1297,7 +1338,8 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v + __shfl_xor(v, 32);
 }
 
-// One workgroup per (query head h G + g, sequence), S waves (S = blockDim /
+// One workgroup per (row h G + g, sequence) -- row g of kv head h is query
+// token g / heads of the sequence and query head h heads + g % heads -- with S waves (S = blockDim /
 // 64, chosen by the host from the records a sequence is expected to have, one
 // wave per kCombineChunk of them): wave s takes the s-th of S equal stretches
 // of the records.  The records are taken 64 at a time: lane r holds record r's
@@ -1314,8 +1356,12 @@ constexpr int kCombineMaxWaves = 16;
 
 template <int OUT_DT>
 __global__ void __launch_bounds__(64 * kCombineMaxWaves) decode_combine_kernel(DecodeArgs a) {
+  // G rows per (sequence, kv head); row g is query token qi, head gh of the group
   const int G = a.group;
   const int h = int(blockIdx.x) / G, g = int(blockIdx.x) - h * G, b = blockIdx.y;
+  const int qi = g / a.heads, gh = g - qi * a.heads;
+  if (qi >= q_count(a, b)) return;  // uniform over the workgroup: a query token slot b does not use
+  const int64_t tok = q_first(a, b) + qi;
   const int w = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
   const int S = int(blockDim.x) / 64;
   const int sidx = w;
@@ -1347,7 +1393,7 @@ __global__ void __launch_bounds__(64 * kCombineMaxWaves) decode_combine_kernel(D
   const float* part = a.part + first * rec;
   const float* col = part + 2 * G + g * kHead + 2 * lane;
   using Bits = typename Elt<OUT_DT>::Bits;
-  Bits* dst = reinterpret_cast<Bits*>(a.out + b * a.out_tok_stride + int64_t(h * G + g) * a.out_head_stride);
+  Bits* dst = reinterpret_cast<Bits*>(a.out + tok * a.out_tok_stride + int64_t(h * a.heads + gh) * a.out_head_stride);
   float mx = kNegBig, den = 0.0f, o0 = 0.0f, o1 = 0.0f;
   const int r_end = int(int64_t(n) * (sidx + 1) / S);
   for (int c0 = int(int64_t(n) * sidx / S); c0 < r_end; c0 += 64) {
@@ -1415,7 +1461,7 @@ __global__ void __launch_bounds__(64 * kCombineMaxWaves) decode_combine_kernel(D
   dst[2 * lane + 1] = Elt<OUT_DT>::from_f32(o1 * inv);
   // natural-log sum of exp(s): 2^mx * den in the exp2 domain
   if (lane == 0 && a.lse)
-    a.lse[int64_t(h * G + g) * a.lse_head_stride + b] =
+    a.lse[int64_t(h * a.heads + gh) * a.lse_head_stride + tok] =
         den > 0.0f ? (mx + __builtin_log2f(den)) * 0.6931471805599453f : -__builtin_inff();
 }
 
@@ -1464,11 +1510,14 @@ int64_t stream_wgs(int ng) {
     case 1: return stream_wgs_for<1>();
     case 2: return stream_wgs_for<2>();
     case 4: return stream_wgs_for<4>();
-    default: return stream_wgs_for<8>();
+    case 8: return stream_wgs_for<8>();
+    default:
+      if constexpr (kPvMfma) return stream_wgs_for<16>();
+      return 0;
   }
 }
 
-int group_ng(int64_t G) { return G == 1 ? 1 : G == 2 ? 2 : G <= 4 ? 4 : 8; }
+int group_ng(int64_t G) { return G == 1 ? 1 : G == 2 ? 2 : G <= 4 ? 4 : G <= 8 ? 8 : 16; }
 
 // kv heads per workgroup of the head-parallel schedule: the largest of 8, 4,
 // 2, 1 that divides Hkv.
@@ -1512,7 +1561,10 @@ int64_t heads_runs(int ng, int64_t num_kv_heads) {
     case 1: slots = heads_wgs_ng<1>(hg); break;
     case 2: slots = heads_wgs_ng<2>(hg); break;
     case 4: slots = heads_wgs_ng<4>(hg); break;
-    default: slots = heads_wgs_ng<8>(hg); break;
+    case 8: slots = heads_wgs_ng<8>(hg); break;
+    default:
+      if constexpr (kPvMfma) slots = heads_wgs_ng<16>(hg);
+      break;
   }
   return slots > 0 ? std::max<int64_t>(1, slots / (num_kv_heads / hg)) : 0;
 }
@@ -1542,7 +1594,10 @@ void launch_partials(const DecodeArgs& a, int q_dtype, int ng, int64_t runs, boo
       case 1: launch_heads_ng<1, GEN>(a, q_dtype, hg, sgrid, st, ns); break;
       case 2: launch_heads_ng<2, GEN>(a, q_dtype, hg, sgrid, st, ns); break;
       case 4: launch_heads_ng<4, GEN>(a, q_dtype, hg, sgrid, st, ns); break;
-      default: launch_heads_ng<8, GEN>(a, q_dtype, hg, sgrid, st, ns); break;
+      case 8: launch_heads_ng<8, GEN>(a, q_dtype, hg, sgrid, st, ns); break;
+      default:
+        if constexpr (kPvMfma) launch_heads_ng<16, GEN>(a, q_dtype, hg, sgrid, st, ns);
+        break;
     }
   } else if (runs > 0) {
     const dim3 sgrid{unsigned(runs * num_kv_heads), 1u, 1u};
@@ -1550,14 +1605,21 @@ void launch_partials(const DecodeArgs& a, int q_dtype, int ng, int64_t runs, boo
       case 1: hipLaunchKernelGGL((decode_partial_stream_kernel<1, GEN>), sgrid, block, 0, st, a, q_dtype, ns); break;
       case 2: hipLaunchKernelGGL((decode_partial_stream_kernel<2, GEN>), sgrid, block, 0, st, a, q_dtype, ns); break;
       case 4: hipLaunchKernelGGL((decode_partial_stream_kernel<4, GEN>), sgrid, block, 0, st, a, q_dtype, ns); break;
-      default: hipLaunchKernelGGL((decode_partial_stream_kernel<8, GEN>), sgrid, block, 0, st, a, q_dtype, ns); break;
+      case 8: hipLaunchKernelGGL((decode_partial_stream_kernel<8, GEN>), sgrid, block, 0, st, a, q_dtype, ns); break;
+      default:
+        if constexpr (kPvMfma)
+          hipLaunchKernelGGL((decode_partial_stream_kernel<16, GEN>), sgrid, block, 0, st, a, q_dtype, ns);
+        break;
     }
   } else {
     switch (ng) {
       case 1: hipLaunchKernelGGL((decode_partial_ring_kernel<1, GEN>), grid, block, 0, st, a, q_dtype); break;
       case 2: hipLaunchKernelGGL((decode_partial_ring_kernel<2, GEN>), grid, block, 0, st, a, q_dtype); break;
       case 4: hipLaunchKernelGGL((decode_partial_ring_kernel<4, GEN>), grid, block, 0, st, a, q_dtype); break;
-      default: hipLaunchKernelGGL((decode_partial_ring_kernel<8, GEN>), grid, block, 0, st, a, q_dtype); break;
+      case 8: hipLaunchKernelGGL((decode_partial_ring_kernel<8, GEN>), grid, block, 0, st, a, q_dtype); break;
+      default:
+        if constexpr (kPvMfma) hipLaunchKernelGGL((decode_partial_ring_kernel<16, GEN>), grid, block, 0, st, a, q_dtype);
+        break;
     }
   }
 }
@@ -1597,17 +1659,17 @@ int64_t balanced_runs(int ng, int64_t num_seqs, int64_t num_kv_heads) {
 
 extern "C" {
 
-int64_t psk_paged_decode_workspace_len(int64_t num_seqs, int64_t num_q_heads, int64_t num_kv_heads,
+int64_t psk_paged_decode_workspace_len(int64_t num_seqs, int64_t q_len, int64_t num_q_heads, int64_t num_kv_heads,
                                        int64_t max_seq_len, int64_t num_splits) {
-  if (num_seqs < 0 || num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads || max_seq_len < 0 ||
-      num_splits < 0)
+  if (num_seqs < 0 || q_len <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads ||
+      max_seq_len < 0 || num_splits < 0)
     return PSK_E_ARG;
-  const int64_t G = num_q_heads / num_kv_heads;
+  const int64_t G = q_len * (num_q_heads / num_kv_heads);  // MFMA rows per (sequence, kv head)
   const int64_t rec = G * (kHead + 2);
   const int64_t splits =
       std::max<int64_t>(1, ceil_div(max_seq_len, decode_split(max_seq_len, num_splits, num_seqs * num_kv_heads)));
   int64_t need = num_seqs * num_kv_heads * splits * rec;
-  if (num_splits == 0 && num_seqs <= kStreamMaxSeqs && G <= kMaxGroup) {
+  if (num_splits == 0 && num_seqs <= kStreamMaxSeqs && G <= kMaxRows) {
     // the balanced schedule: a record per (sequence, kv head) and per workgroup, then the units prefix
     need = std::max(need,
                     (num_seqs + balanced_runs(group_ng(G), num_seqs, num_kv_heads)) * num_kv_heads * rec + num_seqs + 1);
@@ -1620,16 +1682,22 @@ int psk_paged_decode_attention(const void* q, int64_t q_tok_stride, int64_t q_he
                                const int64_t* v_strides, const int32_t* block_table, int64_t block_table_stride,
                                int64_t block_table_width, const int32_t* seq_lens, int64_t num_seqs,
                                int64_t num_q_heads, int64_t num_kv_heads, int64_t head_size, int64_t block_size,
-                               int64_t num_blocks, int64_t max_seq_len, int64_t num_splits, float softmax_scale,
-                               const float* q_descale,
+                               int64_t num_blocks, int64_t max_seq_len, int64_t num_splits, int64_t q_len,
+                               const int32_t* cu_seqlens_q, int causal, float softmax_scale, const float* q_descale,
                                const float* k_descale, const float* v_descale, const int64_t* descale_strides,
                                void* out, int64_t out_tok_stride, int64_t out_head_stride, int out_dtype, float* lse,
                                int64_t lse_head_stride, float* workspace, int64_t workspace_len, void* stream) {
   begin_device_call();
   if (num_seqs < 0 || num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads)
     return fail(PSK_E_ARG, "bad head counts (q %lld, kv %lld)", (long long)num_q_heads, (long long)num_kv_heads);
-  const int64_t G = num_q_heads / num_kv_heads;
-  if (G > kMaxGroup) return fail(PSK_E_ARG, "at most %d query heads per kv head (got %lld)", kMaxGroup, (long long)G);
+  const int64_t group = num_q_heads / num_kv_heads;
+  if (q_len <= 0) return fail(PSK_E_ARG, "q_len %lld", (long long)q_len);
+  const int64_t G = group * q_len;  // MFMA rows per (sequence, kv head)
+  if (G > kMaxRows)
+    return fail(PSK_E_ARG, "query tokens x query heads per kv head must be at most %d (got %lld x %lld)", kMaxRows,
+                (long long)q_len, (long long)group);
+  if (!kPvMfma && (G > 8 || q_len > 1))
+    return fail(PSK_E_ARG, "this build (P V on the VALU) takes one query token and at most 8 heads per kv head");
   if (head_size != kHead) return fail(PSK_E_ARG, "head_size must be %d (got %lld)", kHead, (long long)head_size);
   if (block_size <= 0 || num_blocks <= 0 || num_blocks > INT32_MAX || block_table_width <= 0 || max_seq_len < 0 ||
       max_seq_len > INT32_MAX)
@@ -1652,7 +1720,8 @@ int psk_paged_decode_attention(const void* q, int64_t q_tok_stride, int64_t q_he
   const uint64_t q_align[3] = {uint64_t(uintptr_t(q)), uint64_t(q_tok_stride * qsz), uint64_t(q_head_stride * qsz)};
   if (common_align(q_align, 3, 16) < 16) return fail(PSK_E_ARG, "query rows need 16-byte alignment");
   if (num_splits < 0) return fail(PSK_E_ARG, "num_splits %lld", (long long)num_splits);
-  const int64_t need = psk_paged_decode_workspace_len(num_seqs, num_q_heads, num_kv_heads, max_seq_len, num_splits);
+  const int64_t need =
+      psk_paged_decode_workspace_len(num_seqs, q_len, num_q_heads, num_kv_heads, max_seq_len, num_splits);
   if (workspace_len < need)
     return fail(PSK_E_WORKSPACE, "workspace of %lld floats, need %lld", (long long)workspace_len, (long long)need);
 
@@ -1677,6 +1746,10 @@ int psk_paged_decode_attention(const void* q, int64_t q_tok_stride, int64_t q_he
   a.bs_shift = log2_exact(block_size);
   a.num_kv_heads = int32_t(num_kv_heads);
   a.group = int32_t(G);
+  a.heads = int32_t(group);
+  a.q_len = int32_t(q_len);
+  a.cu_q = cu_seqlens_q;
+  a.causal = causal ? 1 : 0;
   a.split = decode_split(max_seq_len, num_splits, num_seqs * num_kv_heads);
   a.max_splits = int32_t(std::max<int64_t>(1, ceil_div(max_seq_len, a.split)));
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
@@ -1717,7 +1790,7 @@ int psk_paged_decode_attention(const void* q, int64_t q_tok_stride, int64_t q_he
   else launch_partials<true>(a, q_dtype, ng, runs, heads, num_kv_heads, grid, st, int(num_seqs));
   const int st1 = check_launch("decode partial kernel launch");
   if (st1 != PSK_OK) return st1;
-  const dim3 grid2{unsigned(num_q_heads), unsigned(num_seqs), 1u};
+  const dim3 grid2{unsigned(num_kv_heads * G), unsigned(num_seqs), 1u};
   // waves per query head in the combine: one per kCombineChunk records a
   // sequence is expected to have (the balanced schedule spreads runs /
   // sequences + 1 on average; the split schedule at most max_splits), at most

@@ -2,7 +2,9 @@
 torch's own scaled_dot_product_attention over a dense gather of the same pages
 (float64, K/V heads repeated per query group), the reference's accuracy gate as a
 closed form (a constant V comes back exactly; scripts/check_fp8_kv_backend.py),
-a one-token sequence, the log-sum-exp, and page-permutation invariance."""
+a one-token sequence, the log-sum-exp, and page-permutation invariance; with
+several query tokens per sequence, torch SDPA under torch's bottom-right causal
+mask, and the reduction of each causal token to one-token decode."""
 
 import numpy as np
 import pytest
@@ -103,3 +105,67 @@ def test_page_permutation_invariance():
     a, _ = O.paged_decode_attention(q, "bf16", kc, vc, bt, lens, 0.1)
     b, _ = O.paged_decode_attention(q, "bf16", kc[inv], vc[inv], perm[bt].astype(np.int32), lens, 0.1)
     np.testing.assert_array_equal(a, b)
+
+
+def test_multi_token_causal_matches_torch_lower_right_sdpa():
+    """Several query tokens per sequence (speculative decode), ragged counts:
+    the oracle against torch SDPA under torch's own bottom-right causal mask
+    (torch.nn.attention.bias.causal_lower_right), float64 over a dense gather;
+    and without causal, against SDPA with no mask."""
+    from torch.nn.attention.bias import causal_lower_right
+
+    rng = np.random.default_rng(31)
+    Hq, Hkv, P, ps = 8, 2, 60, 16
+    G = Hq // Hkv
+    counts = np.array([1, 3, 2, 4, 4])
+    lens = np.array([5, 3, 40, 200, 1])  # a sequence shorter than its query count
+    cu = np.concatenate([[0], np.cumsum(counts)])
+    TQ = int(cu[-1])
+    k = torch.from_numpy((rng.standard_normal((P, ps, Hkv, 128)) * 2).astype(np.float32)).to(torch.float8_e4m3fn)
+    v = torch.from_numpy((rng.standard_normal((P, ps, Hkv, 128)) * 2).astype(np.float32)).to(torch.float8_e4m3fn)
+    W = int(-(-lens.max() // ps))
+    bt = np.stack([rng.permutation(P)[:W] for _ in range(len(lens))]).astype(np.int32)
+    q8 = torch.from_numpy((rng.standard_normal((TQ, Hq, 128)) * 3).astype(np.float32)).to(torch.float8_e4m3fn)
+    scale = float(np.float32(0.1))  # the kernel takes the scale as a float
+    for causal in (True, False):
+        got, lse = O.paged_decode_attention(q8.view(torch.uint8).numpy(), "fp8", k.view(torch.uint8).numpy(),
+                                            v.view(torch.uint8).numpy(), bt, lens, scale, cu_seqlens_q=cu,
+                                            causal=causal)
+        for b in range(len(lens)):
+            n, nq, c0 = int(lens[b]), int(counts[b]), int(cu[b])
+            idx = torch.arange(n)
+            pages = torch.from_numpy(bt[b].astype(np.int64))[idx // ps]
+            K = k.double()[pages, idx % ps].repeat_interleave(G, dim=1).permute(1, 0, 2)[None]  # [1, Hq, n, D]
+            V = v.double()[pages, idx % ps].repeat_interleave(G, dim=1).permute(1, 0, 2)[None]
+            Q = q8.double()[c0:c0 + nq].permute(1, 0, 2)[None]  # [1, Hq, nq, D]
+            if causal:
+                mask = causal_lower_right(nq, n)._materialize()
+                seen = mask.any(dim=1)  # tokens that see at least one key
+                ref = torch.nn.functional.scaled_dot_product_attention(Q, K, V, attn_mask=mask, scale=scale)
+                ref = torch.where(seen[None, None, :, None], ref, torch.zeros_like(ref))
+                s = (Q @ K.transpose(-1, -2)) * scale
+                ref_lse = torch.logsumexp(s.masked_fill(~mask, -float("inf")), dim=-1)
+            else:
+                ref = torch.nn.functional.scaled_dot_product_attention(Q, K, V, scale=scale)
+                ref_lse = torch.logsumexp((Q @ K.transpose(-1, -2)) * scale, dim=-1)
+            np.testing.assert_allclose(got[c0:c0 + nq], ref[0].permute(1, 0, 2).numpy(), rtol=1e-10, atol=1e-10)
+            exp_lse = ref_lse[0].T.numpy()
+            np.testing.assert_allclose(lse[c0:c0 + nq], exp_lse, rtol=1e-12)
+
+
+def test_multi_token_reduces_to_single_token_decode():
+    """Causal query token i of n over a sequence of length L is the one-token
+    decode of the same query over the first L - n + 1 + i keys: the last token
+    is plain decode, earlier ones see a shorter sequence."""
+    q, kc, vc, bt, _ = make_case(12, B=1, Hq=8, Hkv=2, max_len=300)
+    rng = np.random.default_rng(3)
+    nq, L = 4, bt.shape[1] * kc.shape[1] - 5
+    qm = (rng.standard_normal((nq, 8, 128)) * 3).astype(np.float32)
+    qm = torch.from_numpy(qm).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    qd, kd, vd = [rng.uniform(0.5, 2.0, (1, 2)).astype(np.float32) for _ in range(3)]
+    got, lse = O.paged_decode_attention(qm, "bf16", kc, vc, bt, [L], 0.09, qd, kd, vd,
+                                        cu_seqlens_q=[0, nq], causal=True)
+    for i in range(nq):
+        one, one_lse = O.paged_decode_attention(qm[i:i + 1], "bf16", kc, vc, bt, [L - nq + 1 + i], 0.09, qd, kd, vd)
+        np.testing.assert_array_equal(got[i], one[0])
+        np.testing.assert_array_equal(lse[i], one_lse[0])

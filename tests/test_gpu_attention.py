@@ -293,8 +293,11 @@ def test_flash_attn_varlen_func_matches_direct_call(dev):
         q_descale=descale, k_descale=descale, v_descale=descale)
     b = attention.paged_decode_attention(q, fd[:, 0], fd[:, 1], bt, lens, 0.1)
     assert torch.equal(a, b)
-    with pytest.raises(AssertionError):
+    with pytest.raises(AssertionError):  # no cu_seqlens_q
         attention.flash_attn_varlen_func(q, fd[:, 0], fd[:, 1], 2, None, seqused_k=lens, block_table=bt)
+    with pytest.raises(AssertionError):  # 5 query tokens x 4 heads: more than 16 rows per kv head
+        attention.flash_attn_varlen_func(q, fd[:, 0], fd[:, 1], 5, torch.arange(B + 1, dtype=torch.int32, device=dev),
+                                         seqused_k=lens, block_table=bt)
 
 
 @pytest.mark.parametrize("Hq,Hkv,length", [(8, 2, 20000), (64, 8, 9000), (3, 1, 33000)])
