@@ -28,6 +28,8 @@ torch CPU baseline:
                      or per-tensor FP8
   copy_blocks        config 5a: 2048 pairs over 61 layers of [8192, 2, 16, 8, 128]
   decode_attention   one decode step of FP8 paged attention over config 2's cache
+  decode_attention_q4  the same with 4 causal query tokens per sequence
+                     (speculative decode: 16 MFMA rows per kv head)
   swap               config 5b: 8192 scattered blocks x 8 layers (4 GiB) D2H + H2D
   metadata           host us of prepare_kv_info (configs 2 and 3) and of the
                      graph static-metadata refresh, against the reference's way
@@ -183,12 +185,13 @@ def setup_append(args, device, fp8, rescale=False):
     return launch, info
 
 
-def setup_decode_attention(args, device):
+def setup_decode_attention(args, device, q_len=1):
     """One decode step of paged attention over config 2's FP8 cache: 128
     sequences with log-uniform 128-32768 token contexts in the
     [65536, 16, 8, 128] E4M3FN cache, 32 query heads (4 per kv head), per-tensor
-    K/V descales.  Algorithmic bytes: every context token's K and V rows of
-    every kv head, the page ids, the bf16 query and the bf16 output."""
+    K/V descales.  q_len > 1: that many query tokens per sequence (speculative
+    decode), causal.  Algorithmic bytes: every context token's K and V rows of
+    every kv head, the page ids, the bf16 queries and the bf16 outputs."""
     import torch
 
     import workloads
@@ -209,31 +212,35 @@ def setup_decode_attention(args, device):
     bt = bt.to(device)
     lens = ctx.to(torch.int32).to(device)
     R = min(args.rotate, 64)
-    q = (torch.randn(R, B, Hq, D, device=device, generator=dgen) * 2.0).to(torch.bfloat16)
+    q = (torch.randn(R, B * q_len, Hq, D, device=device, generator=dgen) * 2.0).to(torch.bfloat16)
     scales = torch.tensor([0.01, 0.02], dtype=torch.float32, device=device)
-    out = torch.empty(B, Hq, D, dtype=torch.bfloat16, device=device)
-    ws = torch.empty(attention.workspace_floats(B, Hq, H, W * ps, args.num_splits), dtype=torch.float32,
+    out = torch.empty(B * q_len, Hq, D, dtype=torch.bfloat16, device=device)
+    ws = torch.empty(attention.workspace_floats(B, Hq, H, W * ps, args.num_splits, q_len), dtype=torch.float32,
                      device=device)
     kc, vc = cache[:, 0], cache[:, 1]
 
     def launch(i):
         attention.paged_decode_attention(q[i], kc, vc, bt, lens, D ** -0.5, None, scales[0:1], scales[1:2], out=out,
-                                         workspace=ws, num_splits=args.num_splits)
+                                         workspace=ws, num_splits=args.num_splits, q_len=q_len, causal=True)
 
     total = int(ctx.sum())
     pages = int(sum(len(t) for t in tables))
-    nbytes = total * H * D * 2 + pages * 4 + 2 * B * Hq * D * 2
+    nbytes = total * H * D * 2 + pages * 4 + 2 * B * q_len * Hq * D * 2
+    config = {"workload": "FP8 paged decode attention (config 2 cache)", "sequences": B, "context_tokens": total,
+              "kv_heads": H, "q_heads": Hq, "head_dim": D, "block_size": ps, "num_blocks": cache.shape[0],
+              "num_splits": args.num_splits or "auto", "descales": "per-tensor K/V"}
+    if q_len > 1:
+        config["workload"] = f"FP8 paged attention, {q_len} causal query tokens per sequence (config 2 cache)"
+        config["query_tokens_per_sequence"] = q_len
     info = {
-        "name": "decode_attention",
+        "name": "decode_attention" if q_len == 1 else f"decode_attention_q{q_len}",
         # the head-parallel balanced schedule from 2 sequences up, the split schedule for an explicit count
         "kernel": "decode_partial_heads_kernel" if args.num_splits == 0 else "decode_partial_ring_kernel",
         "bytes": nbytes, "tokens": B,
         "dtype": "fp8_e4m3fn",
         "rotate": R,
-        "config": {"workload": "FP8 paged decode attention (config 2 cache)", "sequences": B, "context_tokens": total,
-                   "kv_heads": H, "q_heads": Hq, "head_dim": D, "block_size": ps, "num_blocks": cache.shape[0],
-                   "num_splits": args.num_splits or "auto", "descales": "per-tensor K/V"},
-        "cpu": lambda b: cpu_decode_attention(kc, vc, bt, ctx, q[0], scales, total * H * D * 2, b),
+        "config": config,
+        "cpu": lambda b: cpu_decode_attention(kc, vc, bt, ctx, q[0], scales, total * H * D * 2, b, q_len),
     }
     return launch, info
 
@@ -1061,10 +1068,10 @@ def _raw(t):
     return t.numpy()
 
 
-def cpu_decode_attention(kc, vc, bt, ctx, q, scales, kv_bytes, budget_s=10.0):
-    """The float64 numpy oracle over the first sequences of the batch until the
-    budget is spent; returns (fraction of one launch's K/V bytes processed,
-    seconds, sample)."""
+def cpu_decode_attention(kc, vc, bt, ctx, q, scales, kv_bytes, budget_s=10.0, q_len=1):
+    """The float64 numpy oracle over the first sequences of the batch (q_len
+    causal query tokens each) until the budget is spent; returns (fraction of
+    one launch's K/V bytes processed, seconds, sample)."""
     import numpy as np
 
     from oracle import kv_oracle as O
@@ -1080,9 +1087,10 @@ def cpu_decode_attention(kc, vc, bt, ctx, q, scales, kv_bytes, budget_s=10.0):
         pages = bt[done, :w].long()
         k = _raw(kc[pages].cpu())
         v = _raw(vc[pages].cpu())
-        O.paged_decode_attention(_raw(q[done: done + 1].cpu()), "bf16", k, v,
+        O.paged_decode_attention(_raw(q[done * q_len: (done + 1) * q_len].cpu()), "bf16", k, v,
                                  np.arange(w, dtype=np.int32)[None], [n], D ** -0.5, None,
-                                 np.full((1, H), ks, np.float32), np.full((1, H), vs, np.float32))
+                                 np.full((1, H), ks, np.float32), np.full((1, H), vs, np.float32),
+                                 cu_seqlens_q=[0, q_len], causal=True)
         nbytes += n * H * D * 2
         done += 1
     el = time.perf_counter() - t0
@@ -1451,6 +1459,7 @@ SETUPS = {
     "bf16_append": lambda a, d: setup_append(a, d, fp8=False),
     "kv_scales": setup_kv_scales,
     "decode_attention": setup_decode_attention,
+    "decode_attention_q4": lambda a, d: setup_decode_attention(a, d, q_len=4),
     "chunked_append": lambda a, d: setup_chunked(a, d, gather=False),
     "gather": lambda a, d: setup_chunked(a, d, gather=True),
     "mla_prefill": lambda a, d: setup_mla(a, d, decode=False),
@@ -1468,6 +1477,7 @@ SETUPS = {
 # on a short budget.  (name, steps, warmup)
 SECONDARY = (
     ("decode_attention", 256, 8),
+    ("decode_attention_q4", 256, 8),
     ("fp8_decode_write", 1024, 64),
     ("kv_scales", 1024, 64),
     ("bf16_append", 1024, 64),
