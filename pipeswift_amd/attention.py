@@ -178,9 +178,8 @@ def flash_attn_varlen_func(
     B = seqused_k.shape[0]
     assert cu_seqlens_q is not None and cu_seqlens_q.shape[0] == B + 1
     q_len = int(max_seqlen_q)
-    # one token per sequence: rows 0..B-1 whatever cu_seqlens_q holds (it is 0..B)
-    cu = None if q_len == 1 else cu_seqlens_q
-    assert q_len > 1 or q.shape[0] == B
+    # B rows of at most one token each: one per sequence, cu_seqlens_q is 0..B
+    cu = None if q_len == 1 and q.shape[0] == B else cu_seqlens_q
     ps = k.shape[1]
     bound = block_table.shape[1] * ps if max_seqlen_k is None else min(int(max_seqlen_k), block_table.shape[1] * ps)
     return paged_decode_attention(q, k, v, block_table, seqused_k, softmax_scale, q_descale, k_descale, v_descale,

@@ -170,3 +170,54 @@ def test_flash_attn_varlen_func_spec_decode(dev):
                                       lens.cpu().numpy(), 0.1, cu_seqlens_q=cu.cpu().numpy(), causal=True)
     vmax = float(np.abs(O.e4m3fn_to_f32(raw(fused[:, 1]))).max())
     _check(a, exp, vmax, True)
+
+
+def test_flash_attn_varlen_func_sequences_without_query_tokens(dev):
+    """max_seqlen_q == 1 with sequences that have no query token this step
+    (cu_seqlens_q repeats a value): their rows do not exist in q, and the
+    other sequences' rows are read and written where cu_seqlens_q puts them."""
+    g = torch.Generator().manual_seed(9)
+    P, ps, H, Hq = 200, 16, 2, 8
+    fused = torch.zeros(P, 2, ps, H, 128, dtype=torch.float8_e4m3fn)
+    fused[:, 0] = _fp8((P, ps, H, 128), 1.0, g)
+    fused[:, 1] = _fp8((P, ps, H, 128), 1.0, g)
+    fd = fused.to(dev)
+    B = 5
+    bt = torch.stack([torch.randperm(P, generator=g)[:30] for _ in range(B)]).to(torch.int32).to(dev)
+    lens = torch.tensor([40, 300, 7, 480, 33], dtype=torch.int32, device=dev)
+    cu = torch.tensor([0, 1, 1, 2, 2, 3], dtype=torch.int32, device=dev)
+    q = (torch.randn(3, Hq, 128, generator=g)).to(torch.bfloat16).to(dev)
+    print("varlen decode with empty query rows", flush=True)
+    a = attention.flash_attn_varlen_func(q=q, k=fd[:, 0], v=fd[:, 1], max_seqlen_q=1, cu_seqlens_q=cu,
+                                         seqused_k=lens, block_table=bt, softmax_scale=0.1, causal=True)
+    assert a.shape == (3, Hq, 128)
+    exp, _ = O.paged_decode_attention(raw(q), "bf16", raw(fused[:, 0]), raw(fused[:, 1]), bt.cpu().numpy(),
+                                      lens.cpu().numpy(), 0.1, cu_seqlens_q=cu.cpu().numpy(), causal=True)
+    vmax = float(np.abs(O.e4m3fn_to_f32(raw(fused[:, 1]))).max())
+    _check(a, exp, vmax, True)
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_spec_decode_random_shapes(dev, seed):
+    """Seeded random batches: 1-16 query tokens per sequence times 1-8 heads
+    per kv head within 16 rows, ragged or uniform, causal or not, power-of-two
+    and other page sizes, 1-40 sequences of 0-3000 tokens, the balanced and
+    split schedules, fp8 and bf16 queries and outputs."""
+    rng = np.random.default_rng(3000 + seed)
+    G = int(rng.choice([1, 2, 3, 4, 5, 8]))
+    q_len = int(rng.integers(1, 16 // G + 1))
+    Hkv = int(rng.choice([1, 2, 4, 8]))
+    ps = int(rng.choice([16, 32, 64, 24, 5]))
+    B = int(rng.choice([1, 2, 3, 7, 13, 40]))
+    lens = rng.integers(0, 3000, B).tolist()
+    lens[int(rng.integers(0, B))] = int(rng.integers(1, 3000))
+    ragged = bool(seed % 2)
+    counts = rng.integers(0 if ragged else 1, q_len + 1, B).tolist()
+    causal = seed % 3 != 2
+    num_splits = 0 if seed % 4 else int(rng.integers(1, 24))
+    q_dtype = "fp8" if seed % 5 < 2 else "bf16"
+    out_dtype = torch.float32 if seed % 2 else torch.bfloat16
+    print(f"spec random {seed}: G={G} q_len={q_len} Hkv={Hkv} ps={ps} B={B} ragged={ragged} causal={causal} "
+          f"splits={num_splits}", flush=True)
+    _spec_case(dev, 4000 + seed, lens, counts, G * Hkv, Hkv, ps, q_len, causal, q_dtype, out_dtype,
+               num_splits=num_splits, ragged=ragged)
