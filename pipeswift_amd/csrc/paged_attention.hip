@@ -1338,38 +1338,70 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v + __shfl_xor(v, 32);
 }
 
-// One workgroup per (row h G + g, sequence) -- row g of kv head h is query
-// token g / heads of the sequence and query head h heads + g % heads -- with S waves (S = blockDim /
-// 64, chosen by the host from the records a sequence is expected to have, one
-// wave per kCombineChunk of them): wave s takes the s-th of S equal stretches
-// of the records.  The records are taken 64 at a time: lane r holds record r's
-// maximum and sum, two wave reductions (with an online rescale across chunks)
-// give the weights, and readlane hands each weight to every lane.  Each lane
-// sums two output columns over the records; the columns of the first
-// kCombineChunk records of a chunk are loaded together with its maxima, so a
-// stretch of up to kCombineChunk records costs one round of loads.  With
-// S > 1 the S partial states merge through LDS and wave 0 writes the output.
-// A workgroup per query head rather than per kv head spreads a single long
-// sequence's records over G times the CUs.
-constexpr int kCombineChunk = 16;
+// Per sequence, one workgroup per ROWS output rows (row h G + g: query token
+// g / heads of the sequence, query head h heads + g % heads), with S waves
+// (S = blockDim / 64, chosen by the host from the records a sequence is
+// expected to have): wave s takes the s-th of S equal stretches of the
+// records.  In a wave, 64 / ROWS lanes serve one output row, lane c of them
+// 2 ROWS consecutive columns.  ROWS = 4 (a few records per sequence, batched
+// decode) merges four rows per wave, and the combine's time follows its
+// number of waves; ROWS = 1 (many records: a long sequence spread over many
+// runs) gives each row its own workgroup, so that its records spread over
+// more CUs.  The records are taken 64 / ROWS at a time: lane c of the row
+// holds record c's maximum and sum, reductions over the row's lanes (with an
+// online rescale across chunks) give the weights, and a permute hands each
+// weight to the row's lanes; the column loads of a batch of records go out
+// together.  With S > 1 the S partial states merge through LDS and wave 0
+// writes the output.
 constexpr int kCombineMaxWaves = 16;
+// Records per round of column loads, per lane: 2 ROWS floats each.
+template <int ROWS> constexpr int combine_batch() { return ROWS == 1 ? 16 : 8; }
+// Dynamic LDS of a combine workgroup of S waves (nothing for one wave).
+template <int ROWS>
+constexpr size_t combine_lds_bytes(int64_t S) {
+  return S > 1 ? size_t(S) * (2 * ROWS + 64 * 2 * ROWS) * sizeof(float) : 0;
+}
 
-template <int OUT_DT>
+// max and sum over the L lanes of each row group of a wave (L = 16 or 64)
+template <int L>
+__device__ __forceinline__ float group_max(float v) {
+  if constexpr (L == 64) return wave_max(v);
+  v = __builtin_fmaxf(v, dpp<kDppXor1>(v));
+  v = __builtin_fmaxf(v, dpp<kDppXor2>(v));
+  v = __builtin_fmaxf(v, dpp<kDppHalfMirror>(v));
+  return __builtin_fmaxf(v, dpp<kDppRowMirror>(v));
+}
+template <int L>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (L == 64) return wave_sum(v);
+  v += dpp<kDppXor1>(v);
+  v += dpp<kDppXor2>(v);
+  v += dpp<kDppHalfMirror>(v);
+  return v + dpp<kDppRowMirror>(v);
+}
+
+template <int OUT_DT, int ROWS>
 __global__ void __launch_bounds__(64 * kCombineMaxWaves) decode_combine_kernel(DecodeArgs a) {
-  // G rows per (sequence, kv head); row g is query token qi, head gh of the group
+  constexpr int L = 64 / ROWS;    // lanes per output row, and records per chunk
+  constexpr int CPL = 2 * ROWS;   // columns per lane
+  constexpr int NB = combine_batch<ROWS>();
   const int G = a.group;
-  const int h = int(blockIdx.x) / G, g = int(blockIdx.x) - h * G, b = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int rr = lane / L, c = lane % L;
+  const int fr = int(blockIdx.x) * ROWS + rr;  // this lane's output row
+  const bool row_ok = fr < a.num_kv_heads * G;
+  const int h = row_ok ? fr / G : 0, g = row_ok ? fr - h * G : 0, b = blockIdx.y;
   const int qi = g / a.heads, gh = g - qi * a.heads;
-  if (qi >= q_count(a, b)) return;  // uniform over the workgroup: a query token slot b does not use
+  // a row past the last, or a query token slot b does not use, merges nothing
+  // and writes nothing
+  const bool live = row_ok && qi < q_count(a, b);
   const int64_t tok = q_first(a, b) + qi;
   const int w = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
   const int S = int(blockDim.x) / 64;
-  const int sidx = w;
-  const int lane = threadIdx.x & 63;
   const int rec = G * (kHead + 2);
   int64_t first = 0;  // index of the first record of (b, h)
   int64_t rs = rec;   // floats between consecutive records of (b, h)
-  int n = 0;          // records of (b, h)
+  int n = 0;          // records of (b, h): the same for every kv head of b
   if (a.stream_wgs > 0) {
     // run j of head h took units [T j / M, T (j+1) / M); unit u belongs to run
     // j(u) = ((u + 1) M - 1) / T, and b owns units [p0, p0 + units), of which
@@ -1391,76 +1423,93 @@ __global__ void __launch_bounds__(64 * kCombineMaxWaves) decode_combine_kernel(D
   }
   const float vd = descale(a.vd, a.vd_b, a.vd_h, b, h);
   const float* part = a.part + first * rec;
-  const float* col = part + 2 * G + g * kHead + 2 * lane;
-  using Bits = typename Elt<OUT_DT>::Bits;
-  Bits* dst = reinterpret_cast<Bits*>(a.out + tok * a.out_tok_stride + int64_t(h * a.heads + gh) * a.out_head_stride);
-  float mx = kNegBig, den = 0.0f, o0 = 0.0f, o1 = 0.0f;
-  const int r_end = int(int64_t(n) * (sidx + 1) / S);
-  for (int c0 = int(int64_t(n) * sidx / S); c0 < r_end; c0 += 64) {
-    const int cnt = min(64, r_end - c0);
+  const float* col = part + 2 * G + g * kHead + CPL * c;
+  float mx = kNegBig, den = 0.0f;
+  float o[CPL];
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) o[k] = 0.0f;
+  const int r_end = int(int64_t(n) * (w + 1) / S);
+  for (int c0 = int(int64_t(n) * w / S); c0 < r_end; c0 += L) {  // uniform over the wave
+    const int cnt = min(L, r_end - c0);
     float m = kNegBig, l = 0.0f;
-    if (lane < cnt) {
-      m = part[int64_t(c0 + lane) * rs + g];
-      l = part[int64_t(c0 + lane) * rs + G + g];
+    if (live && c < cnt) {
+      m = part[int64_t(c0 + c) * rs + g];
+      l = part[int64_t(c0 + c) * rs + G + g];
     }
-    f32x2 x[kCombineChunk];
+    const float cm = __builtin_fmaxf(mx, group_max<L>(m));
+    const float sc = __builtin_amdgcn_exp2f(mx - cm);
+    den *= sc;
 #pragma unroll
-    for (int i = 0; i < kCombineChunk; ++i)
-      x[i] = *reinterpret_cast<const f32x2*>(col + int64_t(c0 + min(i, cnt - 1)) * rs);
-    const float cm = __builtin_fmaxf(mx, wave_max(m));
-    const float c = __builtin_amdgcn_exp2f(mx - cm);
-    den *= c;
-    o0 *= c;
-    o1 *= c;
+    for (int k = 0; k < CPL; ++k) o[k] *= sc;
     mx = cm;
-    const float wl = __builtin_amdgcn_exp2f(m - cm);  // 0 past cnt
-    den += wave_sum(l * wl);
-    for (int s0 = 0; s0 < cnt; s0 += kCombineChunk) {
-      if (s0 > 0) {
+    const float wl = __builtin_amdgcn_exp2f(m - cm);  // 0 past cnt and on dead rows
+    den += group_sum<L>(l * wl);
+    for (int s0 = 0; s0 < cnt; s0 += NB) {
+      // 8-byte loads: records are G (kHead + 2) floats apart and their columns
+      // start 2 G floats in, so only 8-byte alignment holds for every G
+      f32x2 x[NB][CPL / 2];
 #pragma unroll
-        for (int i = 0; i < kCombineChunk; ++i)
-          x[i] = *reinterpret_cast<const f32x2*>(col + int64_t(c0 + min(s0 + i, cnt - 1)) * rs);
+      for (int i = 0; i < NB; ++i) {
+        // past cnt (or on a dead row) re-read a loaded record; its weight is 0
+        const int r = live ? c0 + min(s0 + i, cnt - 1) : 0;
+        const f32x2* src = reinterpret_cast<const f32x2*>(live ? col + int64_t(r) * rs : a.part);
+#pragma unroll
+        for (int k = 0; k < CPL / 2; ++k) x[i][k] = src[k];
       }
 #pragma unroll
-      for (int i = 0; i < kCombineChunk; ++i) {
-        const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), s0 + i));
-        o0 = __builtin_fmaf(x[i].x, w, o0);
-        o1 = __builtin_fmaf(x[i].y, w, o1);
+      for (int i = 0; i < NB; ++i) {
+        // record s0 + i's weight from lane s0 + i of the row (uniform: readlane)
+        const float wi = L == 64 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), min(s0 + i, L - 1)))
+                                 : __shfl(wl, (lane & ~(L - 1)) + min(s0 + i, L - 1));
+        const float wk = s0 + i < cnt ? wi : 0.0f;
+#pragma unroll
+        for (int k = 0; k < CPL / 2; ++k) {
+          o[2 * k] = __builtin_fmaf(x[i][k].x, wk, o[2 * k]);
+          o[2 * k + 1] = __builtin_fmaf(x[i][k].y, wk, o[2 * k + 1]);
+        }
       }
     }
   }
   if (S > 1) {
     // merge the S stretches (a stretch without records holds mx = kNegBig and
-    // zero sums, which weigh nothing)
-    __shared__ float s_mx[kCombineMaxWaves], s_den[kCombineMaxWaves];
-    __shared__ f32x2 s_o[kCombineMaxWaves][64];
-    if (lane == 0) {
-      s_mx[w] = mx;
-      s_den[w] = den;
+    // zero sums, which weigh nothing) through the launch's dynamic LDS
+    // (combine_lds_bytes): S x ROWS maxima and sums, then S x 64 lanes x CPL
+    // columns; a one-wave workgroup takes none, so many fit on a CU
+    extern __shared__ float s_dyn[];
+    float* s_mx = s_dyn;
+    float* s_den = s_mx + ROWS * S;
+    float* s_o = s_den + ROWS * S;
+    if (c == 0) {
+      s_mx[w * ROWS + rr] = mx;
+      s_den[w * ROWS + rr] = den;
     }
-    s_o[w][lane] = f32x2{o0, o1};
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) s_o[(w * 64 + lane) * CPL + k] = o[k];
     __syncthreads();
-    if (sidx != 0) return;
+    if (w != 0) return;
     float m_all = mx;
-    for (int t = 1; t < S; ++t) m_all = __builtin_fmaxf(m_all, s_mx[t]);
+    for (int t = 1; t < S; ++t) m_all = __builtin_fmaxf(m_all, s_mx[t * ROWS + rr]);
     den = 0.0f;
-    o0 = 0.0f;
-    o1 = 0.0f;
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) o[k] = 0.0f;
     for (int t = 0; t < S; ++t) {
-      const float c = __builtin_amdgcn_exp2f(s_mx[t] - m_all);
-      den += s_den[t] * c;
-      const f32x2 o = s_o[t][lane];
-      o0 += o.x * c;
-      o1 += o.y * c;
+      const float sc = __builtin_amdgcn_exp2f(s_mx[t * ROWS + rr] - m_all);
+      den += s_den[t * ROWS + rr] * sc;
+#pragma unroll
+      for (int k = 0; k < CPL; ++k) o[k] += s_o[(t * 64 + lane) * CPL + k] * sc;
     }
     mx = m_all;
   }
+  if (!live) return;
   // no records (an empty sequence): zeros and lse = -inf
   const float inv = den > 0.0f ? vd / den : 0.0f;
-  dst[2 * lane] = Elt<OUT_DT>::from_f32(o0 * inv);
-  dst[2 * lane + 1] = Elt<OUT_DT>::from_f32(o1 * inv);
+  using Bits = typename Elt<OUT_DT>::Bits;
+  Bits* dst = reinterpret_cast<Bits*>(a.out + tok * a.out_tok_stride + int64_t(h * a.heads + gh) * a.out_head_stride) +
+              CPL * c;
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) dst[k] = Elt<OUT_DT>::from_f32(o[k] * inv);
   // natural-log sum of exp(s): 2^mx * den in the exp2 domain
-  if (lane == 0 && a.lse)
+  if (c == 0 && a.lse)
     a.lse[int64_t(h * a.heads + gh) * a.lse_head_stride + tok] =
         den > 0.0f ? (mx + __builtin_log2f(den)) * 0.6931471805599453f : -__builtin_inff();
 }
@@ -1790,18 +1839,27 @@ int psk_paged_decode_attention(const void* q, int64_t q_tok_stride, int64_t q_he
   else launch_partials<true>(a, q_dtype, ng, runs, heads, num_kv_heads, grid, st, int(num_seqs));
   const int st1 = check_launch("decode partial kernel launch");
   if (st1 != PSK_OK) return st1;
-  const dim3 grid2{unsigned(num_kv_heads * G), unsigned(num_seqs), 1u};
-  // waves per query head in the combine: one per kCombineChunk records a
-  // sequence is expected to have (the balanced schedule spreads runs /
-  // sequences + 1 on average; the split schedule at most max_splits), at most
-  // kCombineMaxWaves
+  // waves per workgroup in the combine: one per combine_batch() records a
+  // sequence is expected to have, so that a wave's records take one round of
+  // loads (the balanced schedule spreads runs / sequences + 1 on average; the
+  // split schedule at most max_splits), at most kCombineMaxWaves.  Four rows
+  // per wave when one wave suffices, else one row per workgroup.
   const int64_t recs = runs > 0 ? runs / num_seqs + 1 : a.max_splits;
-  const int64_t waves = std::max<int64_t>(1, std::min<int64_t>(kCombineMaxWaves, ceil_div(recs, kCombineChunk)));
+  const bool quad = recs <= combine_batch<4>();
+  const int64_t waves = quad ? 1
+                             : std::max<int64_t>(1, std::min<int64_t>(kCombineMaxWaves,
+                                                                      ceil_div(recs, combine_batch<1>())));
+  const int rows = quad ? 4 : 1;
+  const dim3 grid2{unsigned(ceil_div(num_kv_heads * G, rows)), unsigned(num_seqs), 1u};
   const dim3 block2{unsigned(64 * waves), 1u, 1u};
-  if (out_dtype == PSK_DTYPE_BF16)
-    hipLaunchKernelGGL((decode_combine_kernel<PSK_DTYPE_BF16>), grid2, block2, 0, st, a);
-  else
-    hipLaunchKernelGGL((decode_combine_kernel<PSK_DTYPE_F32>), grid2, block2, 0, st, a);
+  const size_t lds2 = quad ? combine_lds_bytes<4>(waves) : combine_lds_bytes<1>(waves);
+  if (out_dtype == PSK_DTYPE_BF16) {
+    if (quad) hipLaunchKernelGGL((decode_combine_kernel<PSK_DTYPE_BF16, 4>), grid2, block2, lds2, st, a);
+    else hipLaunchKernelGGL((decode_combine_kernel<PSK_DTYPE_BF16, 1>), grid2, block2, lds2, st, a);
+  } else {
+    if (quad) hipLaunchKernelGGL((decode_combine_kernel<PSK_DTYPE_F32, 4>), grid2, block2, lds2, st, a);
+    else hipLaunchKernelGGL((decode_combine_kernel<PSK_DTYPE_F32, 1>), grid2, block2, lds2, st, a);
+  }
   return check_launch("decode_combine_kernel launch");
 }
 
