@@ -30,6 +30,10 @@ torch CPU baseline:
   decode_attention   one decode step of FP8 paged attention over config 2's cache
   decode_attention_q4  the same with 4 causal query tokens per sequence
                      (speculative decode: 16 MFMA rows per kv head)
+  fp8_prefill_append   the fused FP8 append at prefill size: 32768 tokens in
+                     config 2's geometry (--tokens to change; bf16_prefill_append
+                     without the quantizer), where HBM rather than the launch
+                     bounds it
   swap               config 5b: 8192 scattered blocks x 8 layers (4 GiB) D2H + H2D
   metadata           host us of prepare_kv_info (configs 2 and 3) and of the
                      graph static-metadata refresh, against the reference's way
@@ -182,6 +186,66 @@ def setup_append(args, device, fp8, rescale=False):
     }
     if rescale:
         info["config"]["amax_read_bytes"] = amax_bytes
+    return launch, info
+
+
+def setup_prefill_append(args, device, tokens=32768, fp8=True):
+    """The fused append at prefill size (workloads.prefill_append): `tokens`
+    new tokens of Llama-3-8B K/V into config 2's [65536, 16, 8, 128] cache,
+    FP8 with per-tensor scales (or bf16).  Inputs rotate over enough sets that
+    inputs and cache pages span >= 2 GiB, so neither L2 nor MALL holds them."""
+    import math
+
+    import torch
+
+    import workloads
+    from pipeswift_amd import cache_ops
+    from pipeswift_amd.reshape_and_cache import reshape_and_cache_flash
+
+    case = workloads.prefill_append(num_tokens=tokens, fp8=fp8)
+    ps, P = case.cache.shape[2], case.cache.shape[0]
+    N = tokens
+    row_bytes = case.qkv.shape[1] * 2
+    R = max(2, min(args.rotate, math.ceil(2.5e9 / (N * row_bytes))))
+    gen = torch.Generator().manual_seed(98)
+    dgen = torch.Generator(device=device).manual_seed(98)
+    qkv = torch.empty((R,) + tuple(case.qkv.shape), dtype=torch.bfloat16, device=device)
+    qkv.normal_(0.0, 2.0, generator=dgen)
+    qkv[0].copy_(case.qkv.to(device))
+    a, c = _affine_block_maps(R, P, gen, device)
+    base = case.slot_mapping.to(device)
+    slots = ((a.view(R, 1) * (base // ps).view(1, N) + c.view(R, 1)) % P) * ps + (base % ps).view(1, N)
+    slots[0].copy_(base)
+    cache = case.cache.to(device)
+    k_scale = v_scale = None
+    if fp8:
+        scales = torch.ones(2, dtype=torch.float32, device=device)
+        cache_ops.warmup(device)
+        cache_ops.compute_kv_scales(case.key(qkv[0]), case.value(qkv[0]), out=scales)
+        k_scale, v_scale = scales[0:1], scales[1:2]
+    kc, vc = cache[:, 0], cache[:, 1]
+
+    def launch(i):
+        q = qkv[i]
+        reshape_and_cache_flash(case.key(q), case.value(q), kc, vc, slots[i], k_scale, v_scale)
+
+    name = f"{'fp8' if fp8 else 'bf16'}_prefill_append" + ("" if tokens == 32768 else f"_{tokens}")
+    info = {
+        "name": name,
+        "kernel": "paged_scatter_kernel" if N >= 1024 else "paged_append_small_kernel",
+        "bytes": workloads.append_bytes(N, N, case.num_heads, case.head_size, 2, 1 if fp8 else 2),
+        "tokens": N,
+        "dtype": "fp8_e4m3fn" if fp8 else "bf16",
+        "rotate": R,
+        "config": {
+            "workload": f"fused {'FP8' if fp8 else 'bf16'} append of {N} prefill tokens (config 2's cache geometry)",
+            "tokens": N, "kv_heads": case.num_heads, "head_dim": case.head_size, "block_size": ps,
+            "num_blocks": P, "in_dtype": "bf16", "cache_dtype": "fp8_e4m3fn" if fp8 else "bf16",
+            "qkv_row_stride": case.qkv.shape[1], "scale": "per-tensor from amax" if fp8 else None,
+        },
+        "cpu": lambda b: cpu_append(case, fp8, b),
+        "cpu_torch": lambda b: torch_cpu_append(case, fp8, b),
+    }
     return launch, info
 
 
@@ -1460,6 +1524,8 @@ SETUPS = {
     "kv_scales": setup_kv_scales,
     "decode_attention": setup_decode_attention,
     "decode_attention_q4": lambda a, d: setup_decode_attention(a, d, q_len=4),
+    "fp8_prefill_append": lambda a, d: setup_prefill_append(a, d, tokens=a.tokens or 32768, fp8=True),
+    "bf16_prefill_append": lambda a, d: setup_prefill_append(a, d, tokens=a.tokens or 32768, fp8=False),
     "chunked_append": lambda a, d: setup_chunked(a, d, gather=False),
     "gather": lambda a, d: setup_chunked(a, d, gather=True),
     "mla_prefill": lambda a, d: setup_mla(a, d, decode=False),
@@ -1478,6 +1544,7 @@ SETUPS = {
 SECONDARY = (
     ("decode_attention", 256, 8),
     ("decode_attention_q4", 256, 8),
+    ("fp8_prefill_append", 256, 16),
     ("fp8_decode_write", 1024, 64),
     ("kv_scales", 1024, 64),
     ("bf16_append", 1024, 64),
@@ -1603,6 +1670,8 @@ def main():
     p.add_argument("--transports", default="blit,memcpy", help="swap workload: transports to compare")
     p.add_argument("--swap-reps", type=int, default=3)
     p.add_argument("--num-splits", type=int, default=0, help="decode_attention: splits of the longest sequence (0: auto)")
+    p.add_argument("--tokens", type=int, default=0,
+                   help="fp8_prefill_append / bf16_prefill_append: new tokens (0: 32768)")
     p.add_argument("--block-size", type=int, default=16,
                    help="chunked_append / gather: page size (16 is config 3; 128 is its sensitivity run)")
     args = p.parse_args()

@@ -243,6 +243,27 @@ def test_config2_fp8_decode_whole_cache(dev):
     assert np.array_equal(got, exp)
 
 
+def test_fp8_prefill_append_whole_cache(dev):
+    """The prefill-sized fused FP8 append (the bandwidth-bound shape the bench
+    times): 8192 consecutive tokens in whole pages of config 2's 2 GiB cache,
+    scales from the amax kernel, whole-cache compare against the oracle."""
+    case = workloads.prefill_append(num_tokens=8192)
+    print("fp8 prefill append: 8192 tokens, 65536 blocks", flush=True)
+    qd = case.qkv.to(dev)
+    scales = cache_ops.compute_kv_scales(case.key(qd), case.value(qd))
+    ks, _ = O.amax_scale(raw(case.key()), "bf16")
+    vs, _ = O.amax_scale(raw(case.value()), "bf16")
+    assert scales.cpu().tolist() == [float(ks), float(vs)]
+    cache_d = case.cache.to(dev)
+    reshape_and_cache_flash(case.key(qd), case.value(qd), cache_d[:, 0], cache_d[:, 1], case.slot_mapping.to(dev),
+                            scales[0:1], scales[1:2])
+    got = raw(cache_d)
+    exp = raw(case.cache).copy()
+    O.reshape_and_cache(raw(case.key()), raw(case.value()), exp[:, 0], exp[:, 1], case.slot_mapping.numpy(),
+                        "bf16", "fp8", ks, vs)
+    assert np.array_equal(got, exp)
+
+
 def test_append_offsets_beyond_2gib(dev):
     """A 4 GiB bf16 fused cache: blocks past byte 2^31 are addressed in 64 bits."""
     P, ps, H, D, N = 65536, 16, 8, 128, 256

@@ -109,6 +109,31 @@ def config2_fp8_decode(seed=SEEDS["2"], batch=128, num_blocks=65536, block_size=
     return AppendCase(qkv, q_size, heads, head_size, cache, slots, {"ctx": ctx, "tables": tables})
 
 
+def prefill_append(seed=SEEDS["2"] + 100, num_tokens=32768, num_blocks=65536, block_size=16, heads=8,
+                   head_size=128, q_size=4096, fp8=True) -> AppendCase:
+    """A prefill-sized append in config 2's geometry (Llama-3-8B K/V, bf16
+    ~N(0, 2) with 1% x20 outliers, qkv rows of 6144): num_tokens consecutive
+    positions of fresh sequences, whole pages drawn without replacement from
+    a [65536, 16, 8, 128] cache (FP8 E4M3FN, or bf16), in page order.  The
+    size where the append is bound by HBM, not by its launch."""
+    g = _gen(seed)
+    kv = heads * head_size
+    kvp = torch.randn(num_tokens, 2 * kv, generator=g) * 2.0
+    mask = torch.rand(num_tokens, 2 * kv, generator=g) < 0.01
+    qkv = torch.zeros(num_tokens, q_size + 2 * kv, dtype=torch.bfloat16)  # the query columns are not read
+    qkv[:, q_size:] = torch.where(mask, kvp * 20.0, kvp).to(torch.bfloat16)
+    pages = (num_tokens + block_size - 1) // block_size
+    assert pages < num_blocks
+    perm = torch.randperm(num_blocks - 1, generator=g)[:pages] + 1
+    t = torch.arange(num_tokens)
+    slots = (perm[t // block_size] * block_size + t % block_size).to(torch.int64)
+    dt = torch.float8_e4m3fn if fp8 else torch.bfloat16
+    cache = torch.zeros((num_blocks, 2, block_size, heads, head_size), dtype=torch.uint8 if fp8 else torch.bfloat16)
+    if fp8:
+        cache = cache.view(dt)
+    return AppendCase(qkv, q_size, heads, head_size, cache, slots)
+
+
 @dataclass
 class ChunkedCase:
     append: AppendCase
