@@ -202,7 +202,8 @@ def setup_prefill_append(args, device, tokens=32768, fp8=True):
     from pipeswift_amd import cache_ops
     from pipeswift_amd.reshape_and_cache import reshape_and_cache_flash
 
-    case = workloads.prefill_append(num_tokens=tokens, fp8=fp8)
+    q_size = 4096 if args.q_size < 0 else args.q_size
+    case = workloads.prefill_append(num_tokens=tokens, fp8=fp8, q_size=q_size)
     ps, P = case.cache.shape[2], case.cache.shape[0]
     N = tokens
     row_bytes = case.qkv.shape[1] * 2
@@ -246,6 +247,8 @@ def setup_prefill_append(args, device, tokens=32768, fp8=True):
         "cpu": lambda b: cpu_append(case, fp8, b),
         "cpu_torch": lambda b: torch_cpu_append(case, fp8, b),
     }
+    if q_size != 4096:
+        info["name"] += f"_q{q_size}"
     return launch, info
 
 
@@ -1670,6 +1673,9 @@ def main():
     p.add_argument("--transports", default="blit,memcpy", help="swap workload: transports to compare")
     p.add_argument("--swap-reps", type=int, default=3)
     p.add_argument("--num-splits", type=int, default=0, help="decode_attention: splits of the longest sequence (0: auto)")
+    p.add_argument("--q-size", type=int, default=-1,
+                   help="fp8_prefill_append / bf16_prefill_append: query columns ahead of K and V in each qkv "
+                        "row (-1: 4096, Llama-3-8B; 0: contiguous K/V rows)")
     p.add_argument("--tokens", type=int, default=0,
                    help="fp8_prefill_append / bf16_prefill_append: new tokens (0: 32768)")
     p.add_argument("--block-size", type=int, default=16,
