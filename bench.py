@@ -203,7 +203,9 @@ def setup_prefill_append(args, device, tokens=32768, fp8=True):
     from pipeswift_amd.reshape_and_cache import reshape_and_cache_flash
 
     q_size = 4096 if args.q_size < 0 else args.q_size
-    case = workloads.prefill_append(num_tokens=tokens, fp8=fp8, q_size=q_size)
+    bs = args.block_size  # 16 (config 2); larger pages as a sensitivity run over the same 2 GiB of slots
+    case = workloads.prefill_append(num_tokens=tokens, fp8=fp8, q_size=q_size, block_size=bs,
+                                    num_blocks=65536 * 16 // bs)
     ps, P = case.cache.shape[2], case.cache.shape[0]
     N = tokens
     row_bytes = case.qkv.shape[1] * 2
@@ -249,6 +251,8 @@ def setup_prefill_append(args, device, tokens=32768, fp8=True):
     }
     if q_size != 4096:
         info["name"] += f"_q{q_size}"
+    if bs != 16:
+        info["name"] += f"_bs{bs}"
     return launch, info
 
 
@@ -1679,7 +1683,8 @@ def main():
     p.add_argument("--tokens", type=int, default=0,
                    help="fp8_prefill_append / bf16_prefill_append: new tokens (0: 32768)")
     p.add_argument("--block-size", type=int, default=16,
-                   help="chunked_append / gather: page size (16 is config 3; 128 is its sensitivity run)")
+                   help="chunked_append / gather / *_prefill_append: page size (16 is configs 2 and 3; "
+                        "128 is config 3's sensitivity run)")
     args = p.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
