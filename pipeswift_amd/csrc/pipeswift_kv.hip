@@ -201,13 +201,25 @@ ScatterShape scatter_shape(int64_t num_tokens, int total_vecs) {
   return sh;
 }
 
+int64_t lds_per_cu();
+
 template <class C, int CH, int U, bool FAST, int WPB>
 int launch_scatter_shape(ScatterGeom g, const ScatterPart& p0, const ScatterPart& p1, int slice_shift,
                          hipStream_t st) {
   g.slice_shift = slice_shift;
   const int64_t waves = (ceil_div(g.num_tokens, CH) * g.nparts) << slice_shift;
   const int64_t grid = ceil_div(waves, WPB);
-  hipLaunchKernelGGL((paged_scatter_kernel<C, CH, U, FAST, WPB>), dim3(grid), dim3(WPB * kWave), 0, st, g, p0, p1);
+  // Prefill-sized copies (no quantizer) run best at two resident workgroups
+  // per CU, set through dynamic LDS: 32768 tokens of config 2's geometry 48.7
+  // against 50.4 us uncapped, 131072 tokens 185.5 against 196.3 (5.80 TB/s);
+  // one per CU is slower, and the quantizing append needs every wave it can
+  // get to cover its VALU work (2 per CU: 70.9 against 39.9 us).
+  size_t lds = 0;
+  if (C::OUT_B == C::IN_B && g.num_tokens >= 8192) {
+    const int64_t l = lds_per_cu();
+    if (l > 0) lds = size_t(l / 3 + 1024);
+  }
+  hipLaunchKernelGGL((paged_scatter_kernel<C, CH, U, FAST, WPB>), dim3(grid), dim3(WPB * kWave), lds, st, g, p0, p1);
   return check_launch("paged_scatter_kernel launch");
 }
 

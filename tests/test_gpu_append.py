@@ -264,6 +264,15 @@ def test_fp8_prefill_append_whole_cache(dev):
     assert np.array_equal(got, exp)
 
 
+def test_bf16_prefill_append_whole_cache(dev):
+    """The prefill-sized bf16 append (two resident workgroups per CU from 8192
+    tokens): 8192 consecutive tokens in whole pages of a 4 GiB bf16 cache,
+    whole-cache compare against the oracle."""
+    case = workloads.prefill_append(num_tokens=8192, fp8=False)
+    got, exp = _run_case(case, dev)
+    assert np.array_equal(got, exp)
+
+
 def test_append_offsets_beyond_2gib(dev):
     """A 4 GiB bf16 fused cache: blocks past byte 2^31 are addressed in 64 bits."""
     P, ps, H, D, N = 65536, 16, 8, 128, 256
