@@ -52,6 +52,17 @@ def test_config4_mla_fp8(dev, decode):
     assert np.array_equal(got, exp)
 
 
+@pytest.mark.parametrize("fp8", [False, True])
+def test_mla_prefill_sized_append(dev, fp8):
+    """A 16384-token MLA prefill (DeepSeek-V3 latent, pages of 64): the
+    prefill-sized launch (two resident workgroups per CU for the bf16 copy),
+    whole-cache compare."""
+    case = workloads.config4_mla(num_tokens=16384)
+    print(f"mla prefill append: 16384 tokens fp8={fp8}", flush=True)
+    got, exp = _mla(case, dev, fp8_scale=0.0371 if fp8 else None)
+    assert np.array_equal(got, exp)
+
+
 def test_mla_through_append_mla_kv_cache(dev):
     L, P, ps = 2, 300, 64
     mla = workloads.sentinel((L, P, ps, 576), torch.bfloat16, 31)
