@@ -260,6 +260,30 @@ def test_gather_large_mixed_sequences(dev, ps, H, D, dequant, pad):
         assert np.array_equal(raw(f), exp)
 
 
+def test_chunked_prefill_16k_append_then_gather(dev):
+    """Config 3's geometry with a 16384-token chunk over 6 sequences: the
+    prefill-sized append launch (two resident workgroups per CU for the bf16
+    copy), then the gather, against the oracle and as a round trip."""
+    cc = workloads.config3_chunked(batched_tokens=16384)
+    a = cc.append
+    print(f"chunked 16k: chunks={cc.chunk.tolist()} T={int(cc.cu_seq_lens[-1])}", flush=True)
+    qd = a.qkv.to(dev)
+    cache_d = a.cache.to(dev)
+    reshape_and_cache_flash(a.key(qd), a.value(qd), cache_d[:, 0], cache_d[:, 1], a.slot_mapping.to(dev))
+    exp = raw(a.cache).copy()
+    O.reshape_and_cache(raw(a.key()), raw(a.value()), exp[:, 0], exp[:, 1], a.slot_mapping.numpy())
+    assert np.array_equal(raw(cache_d), exp)
+    T = int(cc.cu_seq_lens[-1])
+    out_k = torch.empty(T, a.num_heads, a.head_size, dtype=torch.bfloat16, device=dev)
+    out_v = torch.empty_like(out_k)
+    cache_ops.gather_cache(cache_d[:, 0], out_k, cc.block_table.to(dev), cc.cu_seq_lens.to(dev),
+                           src_cache_v=cache_d[:, 1], dst_v=out_v)
+    cu = cc.cu_seq_lens.numpy()
+    rows_k = np.concatenate([raw(out_k)[cu[b] + int(cc.prefix[b]): cu[b + 1]] for b in range(len(cc.chunk))])
+    rows_v = np.concatenate([raw(out_v)[cu[b] + int(cc.prefix[b]): cu[b + 1]] for b in range(len(cc.chunk))])
+    assert np.array_equal(rows_k, raw(a.key())) and np.array_equal(rows_v, raw(a.value()))
+
+
 def test_config3_block_size_128_append_then_gather(dev):
     """Config 3's sensitivity run: the same chunked prefill at 128-token pages
     (4096 blocks, the same slot capacity), append then gather, against the
