@@ -1,10 +1,12 @@
 """FP8 (OCP E4M3FN) KV-cache settings.
 
-Mirrors the cache-side part of pipeswift/utils/fp8_kv.py: the dtype and
-saturation constants (:24-25), the global flag (:35-41), ``quantize``
-(:75-77) and the graph-safe warmup (:80-91).  The attention-reader loader and
-descale helpers of that file belong to the attention kernels and are not part
-of this package.
+Mirrors pipeswift/utils/fp8_kv.py: the dtype and saturation constants
+(:24-25), the global flag (:35-41), the attention-reader loader
+``attn_varlen_func`` (:44-62), ``quantize`` (:75-77), the graph-safe warmup
+(:80-91) and ``unit_descale`` (:94-103).  The loader hands back this
+package's reader (``attention.flash_attn_varlen_func``) in place of vLLM's FA3
+fork, so the reference's ``_fp8_paged_attn`` (attention.py:148-187) runs on it
+unchanged.
 
 gfx950 converts to the OCP E4M3FN format natively (max 448, 0x7F/0xFF NaN);
 this is not MI300's FNUZ variant (max 240).
@@ -48,6 +50,21 @@ def warmup(device) -> None:
     if device not in _scale_one:
         _scale_one[device] = torch.ones((1,), dtype=torch.float32, device=device)
     cache_ops.warmup(device)
+
+
+def attn_varlen_func():
+    """The FA3-style varlen entry point for the FP8 cache (fp8_kv.py:44-62):
+    this package's paged reader, same keywords."""
+    from .attention import flash_attn_varlen_func
+
+    return flash_attn_varlen_func
+
+
+def unit_descale(num_seqs: int, num_kv_heads: int, device) -> torch.Tensor:
+    """``{q,k,v}_descale`` of 1.0 shaped (num_seqs, num_kv_heads) as a
+    stride-0 view of one element: no allocation per call, graph safe
+    (fp8_kv.py:94-103)."""
+    return unit_scale(device).expand(num_seqs, num_kv_heads)
 
 
 def unit_scale(device) -> torch.Tensor:

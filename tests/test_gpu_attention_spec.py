@@ -221,3 +221,36 @@ def test_spec_decode_random_shapes(dev, seed):
           f"splits={num_splits}", flush=True)
     _spec_case(dev, 4000 + seed, lens, counts, G * Hkv, Hkv, ps, q_len, causal, q_dtype, out_dtype,
                num_splits=num_splits, ragged=ragged)
+
+
+def test_reference_fp8_paged_attn_call_through_fp8_kv(dev):
+    """The reference's _fp8_paged_attn (pipeswift/llms/layers/attention.py:
+    148-187) restated call for call on this package's fp8_kv: quantize the
+    query, unit descales as a stride-0 view, attn_varlen_func() with the FA3
+    keywords, decode and 2-token steps in one ragged batch."""
+    from pipeswift_amd import fp8_kv
+
+    g = torch.Generator().manual_seed(12)
+    P, ps, H, Hq = 300, 16, 4, 16
+    fused = torch.zeros(P, 2, ps, H, 128, dtype=torch.float8_e4m3fn)
+    fused[:, 0] = _fp8((P, ps, H, 128), 1.0, g)
+    fused[:, 1] = _fp8((P, ps, H, 128), 1.0, g)
+    fd = fused.to(dev)
+    B = 4
+    bt = torch.stack([torch.randperm(P, generator=g)[:40] for _ in range(B)]).to(torch.int32).to(dev)
+    lens = torch.tensor([17, 300, 640, 2], dtype=torch.int32, device=dev)
+    cu = torch.tensor([0, 1, 3, 5, 6], dtype=torch.int32, device=dev)
+    query = (torch.randn(6, Hq, 128, generator=g) * 2).to(torch.bfloat16).to(dev)
+    fp8_kv.warmup(dev)
+    descale = fp8_kv.unit_descale(cu.shape[0] - 1, fd.shape[3], dev)
+    assert descale.shape == (B, H) and descale.stride() == (0, 0)
+    print("reference-style fp8 paged attention call", flush=True)
+    out = fp8_kv.attn_varlen_func()(
+        q=fp8_kv.quantize(query), k=fd[:, 0], v=fd[:, 1], max_seqlen_q=2, cu_seqlens_q=cu, max_seqlen_k=None,
+        seqused_k=lens, block_table=bt, softmax_scale=0.0883883, causal=True, fa_version=3,
+        q_descale=descale, k_descale=descale, v_descale=descale, return_softmax_lse=False)
+    q8 = fp8_kv.quantize(query)
+    exp, _ = O.paged_decode_attention(raw(q8), "fp8", raw(fused[:, 0]), raw(fused[:, 1]), bt.cpu().numpy(),
+                                      lens.cpu().numpy(), 0.0883883, cu_seqlens_q=cu.cpu().numpy(), causal=True)
+    vmax = float(np.abs(O.e4m3fn_to_f32(raw(fused[:, 1]))).max())
+    _check(out, exp, vmax, True)
