@@ -2,7 +2,7 @@
 
 Mirrors pipeswift/utils/fp8_kv.py: the dtype and saturation constants
 (:24-25), the global flag (:35-41), the attention-reader loader
-``attn_varlen_func`` (:44-62), ``quantize`` (:75-77), the graph-safe warmup
+``attn_varlen_func`` (:44-62), ``check_available`` (:64-71), ``quantize`` (:75-77), the graph-safe warmup
 (:80-91) and ``unit_descale`` (:94-103).  The loader hands back this
 package's reader (``attention.flash_attn_varlen_func``) in place of vLLM's FA3
 fork, so the reference's ``_fp8_paged_attn`` (attention.py:148-187) runs on it
@@ -50,6 +50,18 @@ def warmup(device) -> None:
     if device not in _scale_one:
         _scale_one[device] = torch.ones((1,), dtype=torch.float32, device=device)
     cache_ops.warmup(device)
+
+
+def check_available() -> None:
+    """Fail at startup rather than in the first forward pass (fp8_kv.py:64-71):
+    the FP8 reader and append need a gfx950 GPU and this package's library."""
+    assert torch.cuda.is_available(), "--enable_fp8_kv needs a GPU"
+    arch = getattr(torch.cuda.get_device_properties(torch.cuda.current_device()), "gcnArchName", "")
+    assert arch.startswith("gfx950"), f"--enable_fp8_kv on this build needs gfx950 (MI355X), got {arch or 'unknown'}"
+    from ._lib import lib
+
+    lib()
+    attn_varlen_func()
 
 
 def attn_varlen_func():

@@ -241,6 +241,7 @@ def test_reference_fp8_paged_attn_call_through_fp8_kv(dev):
     lens = torch.tensor([17, 300, 640, 2], dtype=torch.int32, device=dev)
     cu = torch.tensor([0, 1, 3, 5, 6], dtype=torch.int32, device=dev)
     query = (torch.randn(6, Hq, 128, generator=g) * 2).to(torch.bfloat16).to(dev)
+    fp8_kv.check_available()
     fp8_kv.warmup(dev)
     descale = fp8_kv.unit_descale(cu.shape[0] - 1, fd.shape[3], dev)
     assert descale.shape == (B, H) and descale.stride() == (0, 0)
