@@ -38,7 +38,10 @@ torch CPU baseline:
   metadata           host us of prepare_kv_info (configs 2 and 3) and of the
                      graph static-metadata refresh, against the reference's way
 
-Each result carries:
+Output: plain-text progress lines, then ONE compact JSON result line, the
+last line of the run (nothing is written to stderr).  The full per-workload
+records go to --detail (default gpurun_out/bench_detail.json).  Each record
+carries:
   value            algorithmic HBM GB/s (bytes the kernel must move / time)
   roofline         the same per launch against MI355X's 8 TB/s peak, the HBM
                    traffic measured with rocprofv3 PMC counters (committed
@@ -49,17 +52,19 @@ Each result carries:
                    contiguous copy of the same bytes at the same size, timed
                    the same way (vs_launch > 1: the kernel beats that copy)
   wall_us_per_call_eager  host wall time per eager Python call (no graph)
-  cpu_baseline     the numpy oracle timed on this host on a bounded sample
-                   (headline only)
-  cpu_torch        the reference's CPU path (torch index_put_ / index_select /
-                   amax on host tensors of the same layout) on all host threads
-                   and on one
+  cpu_baseline     the reference's CPU path, timed on this host: torch
+                   index_put_ / index_select / amax (copy_blocks: a snapshot
+                   index copy; attention: torch fp32 softmax(QK^T)V) on host
+                   tensors of the same layout, on all the process's CPUs
+                   (`cores`) and on one (`value_1thread`)
+  cpu_oracle       the numpy oracle on one thread (headline only)
 
 Other workloads (--workload NAME runs one alone): any name above, and
   mla_fp8_tiles_prefill / mla_fp8_tiles_decode   config 4 into 656-byte FP8
                      entries with one scale per 128-element tile
   attention_shapes   decode attention on several batch shapes, balanced vs split
   l2_cycle           BlockManager store -> evict -> restore of an 8192-page prompt
+                     (the default run includes a 2048-page cycle)
   swap_sweep         host-link GB/s vs bytes per page, per transport
   hbm_copy           1 GiB device copy (achievable-bandwidth reference and the
                      PMC calibration run)
@@ -74,6 +79,7 @@ import os
 import platform
 import sys
 import time
+import warnings
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 if ROOT not in sys.path:
@@ -89,6 +95,26 @@ STEADY_STEPS = 2048  # launches per graph for the steady per-launch figure of th
 # graph: the queued method is the more faithful one below about 40 launches.
 QUEUED_MAX = 32
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def progress(msg):
+    """A plain-text progress line on stdout.  Only the final result line of a
+    run is JSON, and nothing goes to stderr, so the result line is the last
+    line of the run's combined output."""
+    print(f"[bench] {msg}", flush=True)
+
+
+def _cpu_threads():
+    """Host threads for the all-cores CPU baseline: the CPUs this process may
+    run on, capped by OMP_NUM_THREADS where the box sets it."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
 
 
 def _cpu_model():
@@ -183,6 +209,9 @@ def setup_append(args, device, fp8, rescale=False):
         },
         "cpu": lambda b: cpu_append(case, fp8, b),
         "cpu_torch": lambda b: torch_cpu_append(case, fp8, b, rescale=rescale),
+        "cpu_torch_what": (("torch amax/448 of K and V, then " if rescale else "torch ")
+                           + ("index_put_ of fp8_kv.quantize(x / scale) rows" if fp8 else "index_put_ of the K/V rows")
+                           + " into a host cache of the same layout"),
     }
     if rescale:
         info["config"]["amax_read_bytes"] = amax_bytes
@@ -248,6 +277,8 @@ def setup_prefill_append(args, device, tokens=32768, fp8=True):
         },
         "cpu": lambda b: cpu_append(case, fp8, b),
         "cpu_torch": lambda b: torch_cpu_append(case, fp8, b),
+        "cpu_torch_what": ("torch index_put_ of fp8_kv.quantize(x / scale) rows" if fp8
+                           else "torch index_put_ of the K/V rows") + " into a host cache of the same layout",
     }
     if q_size != 4096:
         info["name"] += f"_q{q_size}"
@@ -312,6 +343,9 @@ def setup_decode_attention(args, device, q_len=1):
         "rotate": R,
         "config": config,
         "cpu": lambda b: cpu_decode_attention(kc, vc, bt, ctx, q[0], scales, total * H * D * 2, b, q_len),
+        "cpu_torch": lambda b: torch_cpu_decode_attention(kc, vc, bt, ctx, q[0], scales, nbytes, b, q_len),
+        "cpu_torch_what": "torch fp32 attention (dequantized K/V pages, softmax(QK^T)V) over the first 16 "
+                          "sequences, scaled to the whole batch's bytes",
     }
     return launch, info
 
@@ -342,6 +376,7 @@ def setup_kv_scales(args, device):
         "config": {"workload": "FP8 per-tensor scale from amax, config 2 K and V", "tokens": case.qkv.shape[0]},
         "cpu": None,
         "cpu_torch": lambda b: torch_cpu_kv_scales(case, b),
+        "cpu_torch_what": "torch amax(|x|) / 448 of K and of V on the host",
     }
 
 
@@ -383,6 +418,7 @@ def setup_chunked(args, device, gather):
                        "head_dim": a.head_size, "block_size": ps, "num_blocks": P, "sequences": len(cc.chunk)},
             "cpu": lambda b: cpu_append(a, False, b),
             "cpu_torch": lambda b: torch_cpu_append(a, False, b),
+            "cpu_torch_what": "torch index_put_ of the K/V rows into a host cache of the same layout",
         }
     T = int(cc.cu_seq_lens[-1])
     bt = cc.block_table.to(device)
@@ -405,6 +441,7 @@ def setup_chunked(args, device, gather):
                    "pages": pages},
         "cpu": lambda b: cpu_gather(cc, b),
         "cpu_torch": lambda b: torch_cpu_gather(cc, b),
+        "cpu_torch_what": "torch index_select of each sequence's K and V pages, reshaped to rows",
     }
 
 
@@ -462,6 +499,8 @@ def setup_mla(args, device, decode, fp8=False):
                    "cache_dtype": "fp8_e4m3fn" if fp8 else "bf16"},
         "cpu": None,
         "cpu_torch": lambda b: torch_cpu_mla(case, host_scale, b),
+        "cpu_torch_what": ("torch index_put_ of the [kv_c | k_pe] rows" + (" after fp8_kv.quantize(x / scale)"
+                           if fp8 else "") + " into a host [P, 64, 576] cache"),
     }
 
 
@@ -523,6 +562,8 @@ def setup_copy_blocks(args, device):
                    "block_bytes": 65536},
         "cpu": lambda b: cpu_copy_blocks(nbytes, b),
         "cpu_torch": lambda b: torch_cpu_copy_blocks(nbytes, b),
+        "cpu_torch_what": "torch snapshot index copy stack[:, dst] = stack[:, src].clone() over 128 pairs of a "
+                          "61-layer 256-block host stack, scaled to config 5a's bytes",
     }
 
 
@@ -776,9 +817,11 @@ def measure_metadata(device):
         t_ref = (time.perf_counter() - t0) / rreps
         out[name] = {"tokens": int(info.slot_mapping.numel()), "pages_wide": int(info.page_table.shape[1]),
                      "ours_us": round(t_ours * 1e6, 1), "reference_style_python_us": round(t_ref * 1e6, 1)}
-        print(json.dumps({name: out[name]}), file=sys.stderr, flush=True)
+        progress(f"metadata {name}: ours {out[name]['ours_us']} us, reference-style loop "
+                 f"{out[name]['reference_style_python_us']} us")
     out["graph_refresh"] = measure_graph_refresh(device, cases["config2_decode"])
-    print(json.dumps({"graph_refresh": out["graph_refresh"]}), file=sys.stderr, flush=True)
+    progress(f"metadata graph_refresh: native {out['graph_refresh']['native']['us']} us, reference-style "
+             f"{out['graph_refresh']['reference_style']['us']} us")
     return {"value": out["config3_chunked"]["ours_us"], "unit": "us per step (host)",
             "config": {"workload": "metadata: prepare_kv_info and the graph static refresh", "cases": out},
             "roofline": None,
@@ -839,8 +882,14 @@ def measure_graph_refresh(device, case, reps=200):
 
 
 def run_l2_cycle(args, device):
-    """BlockManager's L2 path at config 5b scale: a 8192-page prompt (L=8 layers
-    of [2, 16, 8, 128] bf16, 512 KiB per page, 4 GiB) is stored to L2, evicted
+    line = dict({"metric": "L2 offload+restore GB/s through BlockManager (config 5b: 8192 scattered pages of 512 KiB, 4 GiB each way)", "n_gpus": 1, "steps": 1, "warmup": 0, "higher_is_better": True, "scaling": "weak",
+                 "vs_baseline": None, "dtype": "bytes", "data": "synthetic (seeded)"}, **measure_l2_cycle(device, 8192))
+    print(json.dumps(line), flush=True)
+
+
+def measure_l2_cycle(device, n=8192):
+    """BlockManager's L2 path: an n-page prompt (L=8 layers of [2, 16, 8, 128]
+    bf16, 512 KiB per page; n=8192 is config 5b's 4 GiB) is stored to L2, evicted
     from HBM, and restored by a second prompt with the same tokens, on pages
     drawn from seeded shuffles of both free lists (a churned pool, the case the
     deadline is priced for, block_manager.py:646-655).  Reports wall time and
@@ -862,13 +911,15 @@ def run_l2_cycle(args, device):
             self.seq_id, self.token_ids, self.offset = sid, array("i", toks), 0
             self.finished, self.l2_load_pending, self.page_hashes, self.l2_probe_resume = False, False, None, None
 
-    L, ps, n = 8, 16, 8192
+    L, ps = 8, 16
     P = n + 2
     cache = torch.zeros((L, P, 2, ps, 8, 128), dtype=torch.bfloat16, device=device)
     page_bytes = L * 2 * ps * 8 * 128 * 2
     t0 = time.perf_counter()
-    m = BlockManager(P, ps, [cache[:, :, 0], cache[:, :, 1]], None, kv_cache_tensor=cache,
-                     l2_cache_gb=n * page_bytes / 1024**3)
+    with warnings.catch_warnings():  # L2 holds n of the n + 2 GPU pages, by design of this cycle
+        warnings.simplefilter("ignore", RuntimeWarning)
+        m = BlockManager(P, ps, [cache[:, :, 0], cache[:, :, 1]], None, kv_cache_tensor=cache,
+                         l2_cache_gb=n * page_bytes / 1024**3)
     t_init = time.perf_counter() - t0
     rng = np.random.default_rng(1005)
     m.free_page_queue = deque(int(x) for x in rng.permutation(np.arange(1, P)))
@@ -956,22 +1007,25 @@ def run_l2_cycle(args, device):
         gc.enable()
     assert [h for h, _ in ref_keys] == [h for h, _ in m._prompt_page_hashes(Seq(9, prompt))]
     res["prompt_keys_ms"] = {"native": 1e3 * t_native, "reference_loop": 1e3 * t_ref, "first_prefill_ms": 1e3 * t_alloc}
-    print(json.dumps(res), file=sys.stderr, flush=True)
     stg, ldg = res["store"]["GB/s"], res["restore"]["GB/s"]
+    progress(f"l2_cycle {n} pages: store {stg:.2f} GB/s in {res['store']['wall_ms']:.1f} ms (deadline model "
+             f"{res['store']['predicted_ms']:.1f} ms), restore {ldg:.2f} GB/s in {res['restore']['wall_ms']:.1f} ms "
+             f"(model {res['restore']['predicted_ms']:.1f} ms)")
     value = 2.0 / (1.0 / stg + 1.0 / ldg)
-    line = {
-        "metric": "L2 offload+restore GB/s through BlockManager (4 GiB each way, 8192 scattered pages)",
-        "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": 1, "warmup": 0,
-        "ms_per_step": res["store"]["wall_ms"] + res["restore"]["wall_ms"], "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "bytes", "data": "synthetic (seeded)",
-        "config": {"workload": "l2_cycle (config 5b through BlockManager)", "results": res},
+    m.l2_copy_engine.close()
+    del m, cache
+    torch.cuda.empty_cache()
+    return {
+        "value": round(value, 2), "unit": "GB/s",
+        "ms_per_step": res["store"]["wall_ms"] + res["restore"]["wall_ms"],
+        "config": {"workload": f"l2_cycle: store -> evict -> restore of a {n}-page prompt through BlockManager",
+                   "results": res},
         "roofline": {"bound": "pcie", "achieved": round(value, 2), "peak": 64.0, "unit": "GB/s",
                      "frac": round(value / 64.0, 4), "traffic": None},
-        "cpu_baseline": {"value": round(1e3 * t_ref, 2), "unit": "ms to key the 8192-page prompt", "cores": 1,
-                         "kind": "port", "sample": "per-page xxhash loop of block_manager.py:678-693 (oracle)"},
+        "cpu_baseline": {"value": round(1e3 * t_ref, 2), "unit": f"ms to key the {n}-page prompt", "cores": 1,
+                         "kind": "port", "sample": "per-page xxhash loop of block_manager.py:678-693 (oracle), "
+                                                   f"native key chain {1e3 * t_native:.2f} ms"},
     }
-    m.l2_copy_engine.close()
-    print(json.dumps(line), flush=True)
 
 
 def run_attention_shapes(args, device):
@@ -1066,7 +1120,7 @@ def run_attention_shapes(args, device):
                 del graph
             row[label] = {"us": round(us, 2), "GB/s": round(kv_bytes / us / 1e3, 1), "eager_us": round(eager_us, 2)}
         results.append(row)
-        print(json.dumps(row), file=sys.stderr, flush=True)
+        progress("attention_shapes " + ", ".join(f"{k}={v}" for k, v in row.items()))
     print(json.dumps({"metric": "decode attention us per call, balanced vs split schedule", "unit": "us",
                       "calls_per_shape": reps, "shapes": results}), flush=True)
 
@@ -1112,7 +1166,7 @@ def run_swap_sweep(args, device):
             finally:
                 eng.close()
         rows.append(row)
-        print(json.dumps(row), file=sys.stderr, flush=True)
+        progress("swap_sweep " + ", ".join(f"{k}={v}" for k, v in row.items()))
     best = max(min(r[f"{t}_{d}_GBs"] for d in ("store", "load")) for r in rows for t in args.transports.split(","))
     line = {"metric": "host-link GB/s vs bytes per page (256 MiB scattered transfer)", "value": best, "unit": "GB/s",
             "n_gpus": 1, "higher_is_better": True, "vs_baseline": None, "dtype": "bytes", "data": "synthetic",
@@ -1166,6 +1220,52 @@ def cpu_decode_attention(kc, vc, bt, ctx, q, scales, kv_bytes, budget_s=10.0, q_
         done += 1
     el = time.perf_counter() - t0
     return nbytes / kv_bytes, el, f"float64 numpy oracle over the first {done} of 128 sequences"
+
+
+def torch_cpu_decode_attention_step(kc, vc, bt, ctx, q, scales, q_len=1, max_seqs=16):
+    """torch on the host for the decode attention: the first `max_seqs`
+    sequences' FP8 pages are copied to host memory once; a step dequantizes
+    them (x * descale, fp32) and computes causal softmax(Q K^T / sqrt(D)) V for
+    each kv head's query group.  Returns (step, outputs, sample bytes): outputs
+    holds each sequence's fp32 [q_len, Hq, D] after a step; sample bytes are
+    the algorithmic bytes of those sequences (K/V rows, page ids, queries and
+    outputs)."""
+    import torch
+
+    ks, vs = (float(x) for x in scales.cpu())
+    H, D = kc.shape[2], kc.shape[3]
+    Hq = q.shape[1]
+    G = Hq // H
+    seqs, sample_bytes = [], 0
+    for b in range(min(max_seqs, len(ctx))):
+        n = int(ctx[b])
+        pages = bt[b, : (n + 15) // 16].long()
+        seqs.append((kc[pages].cpu(), vc[pages].cpu(), q[b * q_len: (b + 1) * q_len].cpu(), n))
+        sample_bytes += n * H * D * 2 + pages.numel() * 4 + 2 * q_len * Hq * D * 2
+    scale = D ** -0.5
+    outs = [None] * len(seqs)
+
+    def step():
+        for i, (k8, v8, qb, n) in enumerate(seqs):
+            k = k8.float().reshape(-1, H, D)[:n].mul_(ks).permute(1, 2, 0)  # [H, D, n]
+            v = v8.float().reshape(-1, H, D)[:n].mul_(vs).transpose(0, 1)  # [H, n, D]
+            qf = qb.float().view(q_len, H, G, D).permute(1, 0, 2, 3).reshape(H, q_len * G, D)
+            s = torch.matmul(qf, k) * scale  # [H, q_len * G, n]
+            if q_len > 1:  # query row r sees keys 0 .. n - q_len + r
+                row = torch.arange(q_len).repeat_interleave(G).view(1, -1, 1)
+                s = s.masked_fill(torch.arange(n).view(1, 1, -1) > (n - q_len + row), float("-inf"))
+            o = torch.matmul(torch.softmax(s, -1), v)  # [H, q_len * G, D]
+            outs[i] = o.view(H, q_len, G, D).permute(1, 0, 2, 3).reshape(q_len, Hq, D)
+
+    return step, outs, sample_bytes
+
+
+def torch_cpu_decode_attention(kc, vc, bt, ctx, q, scales, full_bytes, budget_s=3.0, q_len=1):
+    """Times torch_cpu_decode_attention_step; returns (launch equivalents,
+    seconds): steps scaled by the sample's share of one launch's bytes."""
+    step, _, sample_bytes = torch_cpu_decode_attention_step(kc, vc, bt, ctx, q, scales, q_len)
+    n, el = _timed(step, budget_s)
+    return n * sample_bytes / full_bytes, el
 
 
 def cpu_append(case, fp8, budget_s=10.0):
@@ -1563,6 +1663,7 @@ SECONDARY = (
     ("mla_decode_fp8", 1024, 64),
     ("copy_blocks", 8, 2),
     ("swap", 2, 1),
+    ("l2_cycle", 2048, 0),  # (name, pages, -): the BlockManager store -> evict -> restore cycle, 1 GiB each way
     ("metadata", 0, 0),
 )
 
@@ -1598,26 +1699,27 @@ def measure_workload(args, device, name, steps, warmup, achievable, cpu_budget, 
         floor = measure_copy_floor(device, info["bytes"], steps)
     traffic = _load_traffic().get(name, {}).get("bytes_per_launch")
 
-    cpu = None
+    cpu_oracle = None
+    threads0 = torch.get_num_threads()
     if port_budget > 0 and info.get("cpu") is not None:
         torch.set_num_threads(1)
         n, el, sample = info["cpu"](port_budget)
-        cpu = {"value": info["bytes"] * n / el / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-               "sample": f"{sample}; {el:.1f} s on 1 thread of {_cpu_model()} ({os.cpu_count()} cpus visible)",
-               "tokens_per_s": info["tokens"] * n / el}
-    cpu_torch = None
+        cpu_oracle = {"value": round(info["bytes"] * n / el / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+                      "sample": f"{sample}; {el:.1f} s on 1 thread",
+                      "tokens_per_s": round(info["tokens"] * n / el, 1)}
+    cpu = None
     if cpu_budget > 0 and info.get("cpu_torch") is not None:
-        threads = os.cpu_count() or 1
+        threads = _cpu_threads()
         torch.set_num_threads(threads)
         n, el = info["cpu_torch"](cpu_budget)
         torch.set_num_threads(1)
         n1, el1 = info["cpu_torch"](cpu_budget)
-        cpu_torch = {"value": info["bytes"] * n / el / 1e9, "unit": "GB/s", "threads": threads,
-                     "value_1thread": info["bytes"] * n1 / el1 / 1e9,
-                     "tokens_per_s": info["tokens"] * n / el,
-                     "what": "the reference's CPU path: torch index_put_ / index_select / amax (copy_blocks: a "
-                             "snapshot index copy) on host tensors of the same layout, "
-                             f"{n:.3g} steps in {el:.1f} s on {threads} threads, {n1:.3g} in {el1:.1f} s on 1"}
+        cpu = {"value": round(info["bytes"] * n / el / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+               "value_1thread": round(info["bytes"] * n1 / el1 / 1e9, 4),
+               "tokens_per_s": round(info["tokens"] * n / el, 1),
+               "sample": f"{info.get('cpu_torch_what', 'torch on host tensors of the same layout')}: "
+                         f"{n:.3g} steps in {el:.1f} s on {threads} threads, {n1:.3g} in {el1:.1f} s on 1"}
+    torch.set_num_threads(threads0)
     res = {
         "value": round(achieved, 2),
         "unit": "GB/s",
@@ -1651,7 +1753,7 @@ def measure_workload(args, device, name, steps, warmup, achievable, cpu_budget, 
         },
         "wall_us_per_call_eager": round(t["eager_us"], 2),
         "cpu_baseline": cpu,
-        "cpu_torch": cpu_torch,
+        "cpu_oracle": cpu_oracle,
     }
     del launch, info
     gc.collect()
@@ -1674,6 +1776,8 @@ def main():
     p.add_argument("--rotate", type=int, default=512, help="rotation sets of inputs/slots")
     p.add_argument("--eager", action="store_true", help="time plain eager launches (host launch rate included)")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--detail", default=os.path.join("gpurun_out", "bench_detail.json"),
+                   help="file for the full per-workload records ('' for none); the result line stays compact")
     p.add_argument("--transports", default="blit,memcpy", help="swap workload: transports to compare")
     p.add_argument("--swap-reps", type=int, default=3)
     p.add_argument("--num-splits", type=int, default=0, help="decode_attention: splits of the longest sequence (0: auto)")
@@ -1689,7 +1793,7 @@ def main():
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the KV kernels are rank-local; see the sharding notes). Run with --gpus 1.", file=sys.stderr)
+              "(the KV kernels are rank-local; see the sharding notes). Run with --gpus 1.", flush=True)
         sys.exit(2)
     if args.steps < 1 or args.warmup < 0:
         raise SystemExit("--steps must be >= 1 and --warmup >= 0")
@@ -1708,11 +1812,11 @@ def main():
         raise SystemExit(f"unknown workload {name}")
 
     achievable = measure_device_copy(device)
+    progress(f"achievable device copy: {achievable:.1f} GB/s")
     nocpu = args.no_cpu_baseline
     res = measure_workload(args, device, headline, args.steps, args.warmup, achievable,
-                           cpu_budget=0 if nocpu else 3.0, port_budget=0 if nocpu else 10.0)
-    print(f"[bench] {headline}: {res['roofline']['us_per_launch']} us/launch, {res['value']} GB/s",
-          file=sys.stderr, flush=True)
+                           cpu_budget=0 if nocpu else 5.0, port_budget=0 if nocpu else 10.0)
+    progress(f"{headline}: {res['roofline']['us_per_launch']} us/launch, {res['value']} GB/s")
     secondary = None
     if name == "default" and not args.no_secondary:
         secondary = {}
@@ -1722,20 +1826,60 @@ def main():
                 r = measure_swap(device, ("blit",), reps=steps)
             elif sname == "metadata":
                 r = measure_metadata(device)
+            elif sname == "l2_cycle":
+                r = measure_l2_cycle(device, steps)
             else:
                 r = measure_workload(args, device, sname, steps, warmup, achievable,
                                      cpu_budget=0 if nocpu else 1.0, port_budget=0)
             secondary[sname] = r
-            print(f"[bench] {sname}: {r['value']} {r['unit']} ({time.perf_counter() - t0:.1f} s)",
-                  file=sys.stderr, flush=True)
+            progress(f"{sname}: {r['value']} {r['unit']} ({time.perf_counter() - t0:.1f} s)")
+    full = dict(headline=dict(res, name=headline), secondary=secondary, cpu_model=_cpu_model(),
+                cpus_visible=os.cpu_count(), args=vars(args))
+    detail = write_detail(args.detail, full)
+    print(json.dumps(result_line(res, args.warmup, secondary, detail), separators=(",", ":")), flush=True)
 
+
+def write_detail(path, full):
+    """Write the full per-workload records (configs, timings, copy floors, CPU
+    baselines) as JSON to `path`; returns the path written, or None."""
+    if not path:
+        return None
+    try:
+        os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)
+        with open(path, "w") as f:
+            json.dump(full, f, indent=1)
+        return path
+    except OSError as e:
+        progress(f"could not write {path}: {e}")
+        return None
+
+
+def _short_config(cfg):
+    keep = ("workload", "tokens", "valid_tokens", "kv_heads", "head_dim", "block_size", "num_blocks", "cache_dtype",
+            "scale", "rotation_sets", "timing")
+    return {k: cfg[k] for k in keep if k in cfg}
+
+
+def _short_cpu(cpu):
+    if not cpu:
+        return None
+    out = {k: cpu[k] for k in ("value", "unit", "cores", "kind", "value_1thread") if k in cpu}
+    out["sample"] = cpu.get("sample", "")[:160]
+    return out
+
+
+def result_line(res, warmup, secondary, detail=None):
+    """The one JSON result line (a few KB): the headline's fields in full, each
+    secondary workload as its value, roofline fraction, per-launch time and
+    CPU baseline.  The full records go to the detail file."""
+    rf = res["roofline"]
     line = {
         "metric": METRIC,
         "value": res["value"],
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": res["steps"],
-        "warmup": args.warmup,
+        "warmup": warmup,
         "ms_per_step": res["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
@@ -1744,16 +1888,38 @@ def main():
         "data": "synthetic (seeded)",
         "tokens_per_s": res["tokens_per_s"],
         "pct_of_peak": res["pct_of_peak"],
-        "config": res["config"],
-        "roofline": res["roofline"],
-        "copy_floor": res["copy_floor"],
-        "wall_us_per_call_eager": res["wall_us_per_call_eager"],
-        "cpu_baseline": res["cpu_baseline"],
-        "cpu_torch": res["cpu_torch"],
+        "config": _short_config(res["config"]),
+        "roofline": {k: rf[k] for k in ("bound", "kernel", "achieved", "peak", "unit", "frac", "traffic",
+                                        "bytes_per_launch", "us_per_launch", "steady_us_per_launch", "steady_frac",
+                                        "achievable", "frac_of_achievable") if k in rf},
+        "copy_floor_us": None if not res.get("copy_floor") else res["copy_floor"]["us"],
+        "cpu_baseline": _short_cpu(res.get("cpu_baseline")),
+        "cpu_oracle": _short_cpu(res.get("cpu_oracle")),
     }
     if secondary is not None:
-        line["secondary"] = secondary
-    print(json.dumps(line), flush=True)
+        sec = {}
+        for k, r in secondary.items():
+            rr = r.get("roofline") or {}
+            cpu = r.get("cpu_baseline") or {}
+            e = {"value": r["value"], "unit": r["unit"]}
+            if rr.get("frac") is not None:
+                e["frac"] = rr["frac"]
+            if rr.get("us_per_launch") is not None:
+                e["us"] = rr["us_per_launch"]
+            elif r.get("ms_per_step") is not None:
+                e["ms"] = round(r["ms_per_step"], 3)
+            if r.get("copy_floor"):
+                e["copy_us"] = r["copy_floor"]["us"]
+            if cpu:
+                e["cpu"] = cpu.get("value")
+                e["cpu_unit"] = cpu.get("unit")
+                if cpu.get("cores") is not None:
+                    e["cpu_cores"] = cpu["cores"]
+            sec[k] = e
+        line["secondary"] = sec
+    if detail:
+        line["detail"] = detail
+    return line
 
 
 if __name__ == "__main__":

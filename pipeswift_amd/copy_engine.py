@@ -6,38 +6,46 @@ BlockManager calls (block_manager.py:190-209, 288, 462, 534), with the transfer
 itself in ``psk_swap_blocks`` of libpipeswift_kv.so instead of a ctypes binding
 of cuMemcpyBatchAsync.
 
-What is the same as the reference:
+The contract kept from the reference:
   * one pinned host mirror per GPU cache tensor, shaped like the cache but
-    ``l2_num_pages`` deep;
-  * int8 ``[num_pages, bytes_per_page]`` views per (cache tensor, layer);
+    ``l2_num_pages`` deep, so page p of a layer spans the same byte range of
+    that layer on both tiers;
   * runs of pages that advance together on both tiers are coalesced on the
-    calling thread (the retire deadline is priced from the run count);
-  * transfers are ordered after the work already queued on the caller's
-    stream through an event, submitted by one daemon thread onto a dedicated
-    stream per direction, and signalled by an event on that stream;
-  * page indices are range-checked before anything is enqueued;
-  * ``calibrate`` fits the same ``t = descriptors/desc_rate + bytes/bw`` model.
+    calling thread, so ``CopyHandle.num_runs`` (what the caller prices the
+    retire deadline from) is known when ``store``/``load`` returns;
+  * a transfer starts after the work already queued on the caller's stream,
+    runs on a dedicated stream per direction and signals an event on it;
+  * page indices are validated before anything is enqueued;
+  * ``calibrate`` returns the ``t = descriptors/desc_rate + bytes/bw`` model
+    with integer rates per direction.
 
-What differs, by design for MI355X:
-  * the mirror is allocated with hipHostMalloc (mapped, portable) through the
-    library instead of torch's caching pinned allocator, which would round a
-    multi-GiB mirror up to the next power of two;
-  * two transports: ``"blit"`` (default) moves every (view, page) unit in ONE
-    kernel that reads/writes the mapped host mirror directly, so the cost per
-    descriptor that dominates the reference (copy_engine.py:15-36) disappears;
-    ``"memcpy"`` issues one hipMemcpyAsync per (view, run) on the SDMA engines
-    (the reference's batched-descriptor call, cuMemcpyBatchAsync, has a HIP
-    counterpart that this GPU's runtime does not export);
-  * both streams keep the default priority.
+The design underneath:
+  * the per-(tensor, layer) byte geometry of each direction is computed once
+    from the cache tensors' strides (``_Geometry``), as numpy arrays that go to
+    the library as they are;
+  * the mirror is hipHostMalloc'd (mapped, portable) by the library instead of
+    taken from torch's caching pinned allocator, which would round a multi-GiB
+    mirror up to the next power of two;
+  * two transports: ``"blit"`` (default) moves every (view, page) unit of a
+    transfer in ONE kernel that reads/writes the mapped host mirror directly,
+    so the cost per descriptor that dominates the reference
+    (copy_engine.py:15-36) disappears; ``"memcpy"`` issues one hipMemcpyAsync
+    per (view, run) on the SDMA engines (the batched-descriptor call the
+    reference uses has a HIP counterpart this GPU's runtime does not export);
+  * one ``_Submitter`` thread owns every runtime call of the transfers, so
+    the scheduler thread never blocks in the runtime; both copy streams keep
+    the default priority.
 """
 
 from __future__ import annotations
 
 import ctypes
+import math
 import os
 import queue
 import threading
 import time
+import weakref
 from collections import OrderedDict
 
 import numpy as np
@@ -48,6 +56,8 @@ from ._lib import check, lib
 
 TRANSPORTS = {"memcpy": _lib.SWAP_MEMCPY, "blit": _lib.SWAP_BLIT}
 DEFAULT_TRANSPORT = os.environ.get("PIPESWIFT_AMD_SWAP_TRANSPORT", "blit")
+# Pinned page-table staging buffers per direction (blit transport): a buffer is
+# reused only after the transfer that last read it has landed.
 _STAGING_SLOTS = 4
 # How long a submitter sleeps after queuing a transfer, so that the copy thread
 # takes the GIL and enqueues it (CopyEngine._submit).
@@ -58,29 +68,55 @@ _u64p = ctypes.POINTER(ctypes.c_uint64)
 
 
 # --------------------------------------------------------------------------- #
-# Cache tensor layout (copy_engine.py:121-142)
+# cache tensor layout (copy_engine.py:121-142)
 # --------------------------------------------------------------------------- #
 
 
 def page_bytes(caches):
-    """Bytes one page occupies across every layer of every cache tensor."""
-    return sum(cache[0, 0].numel() * cache.element_size() * cache.shape[0] for cache in caches)
+    """Bytes one page occupies across every layer of every cache tensor (a
+    cache is [layers, pages, ...])."""
+    total = 0
+    for cache in caches:
+        per_layer = math.prod(cache.shape[2:]) * cache.element_size()
+        total += cache.shape[0] * per_layer
+    return total
 
 
 def make_dma_views(caches, num_pages):
-    """Flatten each layer to an int8 [num_pages, page_bytes] view.
+    """``{"<tensor>.<layer>": int8 [num_pages, bytes per page]}`` over every
+    layer of every cache tensor.  The tensors must be contiguous, so a run of
+    consecutive pages of one layer is one byte range."""
+    out = OrderedDict()
+    for ci, cache in enumerate(caches):
+        if cache.shape[1] != num_pages or not cache.is_contiguous():
+            raise AssertionError(f"cache {ci}: need a contiguous [layers, {num_pages}, ...] tensor, "
+                                 f"got shape {tuple(cache.shape)}")
+        flat = cache.view(cache.shape[0], num_pages, -1)
+        for li in range(cache.shape[0]):
+            out[f"{ci}.{li}"] = flat[li].view(torch.int8)
+    return out
 
-    Contiguity is required: consecutive pages of a layer must be consecutive
-    bytes so that a run of pages is one byte range.
-    """
-    views = OrderedDict()
-    for cache_idx, cache in enumerate(caches):
-        assert cache.shape[1] == num_pages
-        assert cache.is_contiguous()
-        for layer_idx in range(cache.shape[0]):
-            layer = cache[layer_idx].reshape(num_pages, -1).view(torch.int8)
-            views[f"{cache_idx}.{layer_idx}"] = layer
-    return views
+
+class _Geometry:
+    """Byte geometry of one direction: for every (cache tensor, layer) view, the
+    source and destination address of page 0 and the bytes per page, read from
+    the tensors' strides (contiguous [layers, pages, ...] on both sides)."""
+
+    def __init__(self, src_caches, dst_caches):
+        src_b, dst_b, bpp = [], [], []
+        for src, dst in zip(src_caches, dst_caches):
+            if not (src.is_contiguous() and dst.is_contiguous()) or src.shape[0] != dst.shape[0] \
+                    or src.shape[2:] != dst.shape[2:] or src.dtype != dst.dtype:
+                raise AssertionError("mirror and cache tensors must be contiguous with matching page shapes")
+            es = src.element_size()
+            layers = np.arange(src.shape[0], dtype=np.uint64)
+            src_b.append(np.uint64(src.data_ptr()) + layers * np.uint64(src.stride(0) * es))
+            dst_b.append(np.uint64(dst.data_ptr()) + layers * np.uint64(dst.stride(0) * es))
+            bpp.append(np.full(src.shape[0], src.stride(1) * es, dtype=np.uint64))
+        self.src_bases = np.ascontiguousarray(np.concatenate(src_b))
+        self.dst_bases = np.ascontiguousarray(np.concatenate(dst_b))
+        self.bpb = np.ascontiguousarray(np.concatenate(bpp))
+        self.num_tensors = len(self.bpb)
 
 
 # --------------------------------------------------------------------------- #
@@ -108,73 +144,62 @@ class _HostBuffer:
 
 
 # --------------------------------------------------------------------------- #
-# Transport engine
+# page validation and coalescing
 # --------------------------------------------------------------------------- #
 
 
-class _TransferParams:
-    """One direction's geometry: per-view source/destination bases and bytes
-    per page, its stream, and (blit) a ring of pinned staging buffers."""
+def validate_pages(ids, limit, tier, what):
+    """AssertionError naming the offending ids when any of ``ids`` is not a page
+    of a ``limit``-page ``tier``; nothing is enqueued for such a transfer
+    (copy_engine.py:373-385 checks the same before the driver call)."""
+    ids = np.asarray(ids, dtype=np.int64)
+    if not len(ids) or (int(ids.min()) >= 0 and int(ids.max()) < limit):
+        return
+    bad = ids[(ids < 0) | (ids >= limit)]
+    shown = ", ".join(str(int(x)) for x in bad[:8]) + (", ..." if len(bad) > 8 else "")
+    raise AssertionError(f"{what}: {len(bad)} of {len(ids)} page ids are not pages of the {tier} tier "
+                         f"(it has {limit}): {shown}")
 
-    def __init__(self, src_views, dst_views, stream, src_limit, dst_limit, max_pages):
-        assert list(src_views.keys()) == list(dst_views.keys())
-        src_bases, dst_bases, bpb = [], [], []
-        for src, dst in zip(src_views.values(), dst_views.values()):
-            src_bpb = src.stride(0) * src.element_size()
-            assert src_bpb == dst.stride(0) * dst.element_size()
-            src_bases.append(src.data_ptr())
-            dst_bases.append(dst.data_ptr())
-            bpb.append(src_bpb)
-        self.src_bases = np.array(src_bases, dtype=np.uint64)
-        self.dst_bases = np.array(dst_bases, dtype=np.uint64)
-        self.bpb = np.array(bpb, dtype=np.uint64)
-        self.num_tensors = len(src_bases)
-        self.stream = stream
-        self.stream_handle = stream.cuda_stream
-        self.src_limit = src_limit
-        self.dst_limit = dst_limit
-        self.max_pages = max_pages
-        self.staging = []
-        self.desc_dev = None
-        self._slot = 0
 
-    def alloc_staging(self, device):
-        nbytes = int(lib().psk_swap_staging_bytes(self.num_tensors, self.max_pages))
-        self.staging = [[_HostBuffer(nbytes), None] for _ in range(_STAGING_SLOTS)]
-        # page tables are copied here before each blit (stream-ordered reuse)
-        self.desc_dev = torch.empty(nbytes, dtype=torch.uint8, device=device)
+def coalesce_runs(src_ids, dst_ids):
+    """Page pairs merged into runs that advance together on both tiers
+    (copy_engine.py:407-427): pairs ordered by source (stable), cut wherever
+    the source or the destination does not step by one.  The native radix
+    sort in libpipeswift_kv does it, since the submitting caller waits.
+    Returns (source starts, destination starts, lengths) as uint64 arrays."""
+    src = np.ascontiguousarray(src_ids, dtype=np.int64)
+    dst = np.ascontiguousarray(dst_ids, dtype=np.int64)
+    n = len(src)
+    out = np.empty((3, n), dtype=np.int64)
+    runs = lib().psk_coalesce_runs(src.ctypes.data_as(_i64p), dst.ctypes.data_as(_i64p), n,
+                                   out[0].ctypes.data_as(_i64p), out[1].ctypes.data_as(_i64p),
+                                   out[2].ctypes.data_as(_i64p))
+    if runs < 0:
+        check(int(runs), "coalesce page runs")
+    starts_s, starts_d, lengths = out[:, :runs].astype(np.uint64)
+    return starts_s, starts_d, lengths
 
-    def next_staging(self):
-        """A staging buffer no in-flight transfer still reads."""
-        slot = self.staging[self._slot]
-        self._slot = (self._slot + 1) % len(self.staging)
-        if slot[1] is not None:
-            slot[1].synchronize()
-        return slot
 
-    def free(self):
-        for buf, _ in self.staging:
-            buf.free()
-        self.staging = []
-        self.desc_dev = None
+# --------------------------------------------------------------------------- #
+# handles
+# --------------------------------------------------------------------------- #
 
 
 class CopyHandle:
+    """One submitted transfer (copy_engine.py:150-177): ``event`` is recorded
+    on the copy stream once the submitter has enqueued it; ``num_runs`` and
+    ``num_pages`` are set before ``store``/``load`` returns."""
+
     def __init__(self, pending=True):
-        # None until the copy thread has enqueued the batch; an empty transfer
-        # never gets one, hence the flag.
         self.event = None
-        self.pending = pending
+        self.pending = pending  # False for an empty transfer, which never gets an event
         self.error = None
-        # Set synchronously by _submit: the caller prices deadlines from them.
         self.num_runs = 0
         self.num_pages = 0
 
     def wait(self):
-        """Block until the transfer has landed (copy_engine.py:164-177).  Until
-        the copy thread has enqueued the transfer there is no event to wait on;
-        the loop sleeps rather than spins, because the copy thread needs the GIL
-        to get there and a spin with os.sched_yield keeps holding it."""
+        """Block until the transfer has landed.  The submitter needs the GIL to
+        enqueue it, so the wait for its event sleeps instead of spinning."""
         if not self.pending:
             return
         while self.event is None:
@@ -211,233 +236,258 @@ class JoinedCopyHandle:
             h.wait()
 
 
+# --------------------------------------------------------------------------- #
+# one direction of the transport
+# --------------------------------------------------------------------------- #
+
+
+class _Lane:
+    """One direction (store: GPU -> host, load: host -> GPU): its geometry, its
+    copy stream, the page-count limits of both ends, and for the blit transport
+    a ring of pinned page-table staging buffers plus the device buffer the
+    table is copied into before each blit."""
+
+    def __init__(self, name, geometry, stream, src_tier, dst_tier):
+        self.name = name
+        self.geometry = geometry
+        self.num_tensors = geometry.num_tensors
+        self.stream = stream
+        self.src_tier, self.src_limit = src_tier
+        self.dst_tier, self.dst_limit = dst_tier
+        self.max_pages = max(self.src_limit, self.dst_limit)
+        self._ring = []  # [host buffer, event of the last transfer that read it]
+        self._next = 0
+        self._desc = None
+
+    def enable_staging(self, device):
+        nbytes = int(lib().psk_swap_staging_bytes(self.num_tensors, self.max_pages))
+        self._ring = [[_HostBuffer(nbytes), None] for _ in range(_STAGING_SLOTS)]
+        self._desc = torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+    def check(self, src, dst):
+        what = f"L2 {self.name}"
+        validate_pages(src, self.src_limit, self.src_tier, f"{what} source")
+        validate_pages(dst, self.dst_limit, self.dst_tier, f"{what} destination")
+        if self._ring and len(src) > self.max_pages:
+            raise AssertionError(f"{what}: {len(src)} pages exceed one transfer's staging ({self.max_pages})")
+
+    def enqueue(self, runs, transport, timing):
+        """Enqueue one transfer of coalesced runs on this lane's stream (called
+        on the submitter thread, inside ``torch.cuda.stream(self.stream)``);
+        returns the event recorded after it."""
+        slot = None
+        if self._ring:
+            slot = self._ring[self._next]
+            self._next = (self._next + 1) % len(self._ring)
+            if slot[1] is not None:
+                slot[1].synchronize()  # the transfer that last read this table has landed
+        src_start, dst_start, run_len = (np.ascontiguousarray(a, dtype=np.int64) for a in runs)
+        g = self.geometry
+        if len(run_len):
+            status = lib().psk_swap_blocks(
+                transport, g.src_bases.ctypes.data_as(_u64p), g.dst_bases.ctypes.data_as(_u64p),
+                g.bpb.ctypes.data_as(_u64p), g.num_tensors,
+                src_start.ctypes.data_as(_i64p), dst_start.ctypes.data_as(_i64p), run_len.ctypes.data_as(_i64p),
+                len(run_len), self.src_limit, self.dst_limit,
+                slot[0].ptr if slot else None, slot[0].nbytes if slot else 0,
+                self._desc.data_ptr() if slot else None, self._desc.numel() if slot else 0,
+                self.stream.cuda_stream)
+            check(status, "L2 page transfer")
+        event = torch.cuda.Event(enable_timing=timing)
+        event.record(self.stream)
+        if slot is not None:
+            slot[1] = event
+        return event
+
+    def release(self):
+        """Drain the stream, then free the staging buffers."""
+        self.stream.synchronize()
+        for buf, _ in self._ring:
+            buf.free()
+        self._ring = []
+        self._desc = None
+
+
+class _Job:
+    __slots__ = ("lane", "runs", "after", "handle")
+
+    def __init__(self, lane, runs, after, handle):
+        self.lane, self.runs, self.after, self.handle = lane, runs, after, handle
+
+
+class _Submitter(threading.Thread):
+    """The daemon thread that makes every runtime call of the transfers: it
+    takes jobs in order, makes the lane's stream wait for the caller's event,
+    enqueues the transfer and hands the recorded event to the job's handle.  A
+    failure is parked on the handle and raised by its ``wait``."""
+
+    def __init__(self, device, transport, timing):
+        super().__init__(name="pipeswift-amd-l2-copy", daemon=True)
+        self.jobs = queue.SimpleQueue()
+        self._device = device
+        self._transport = transport
+        self._timing = timing
+
+    def run(self):
+        torch.cuda.set_device(self._device)
+        for job in iter(self.jobs.get, None):
+            try:
+                with torch.cuda.stream(job.lane.stream):
+                    if job.after is not None:
+                        job.lane.stream.wait_event(job.after)
+                    job.handle.event = job.lane.enqueue(job.runs, self._transport, self._timing)
+            except Exception as exc:  # deferred to CopyHandle.wait
+                job.handle.error = exc
+
+    def stop(self, timeout=30.0):
+        self.jobs.put(None)
+        self.join(timeout=timeout)
+
+
+def _shutdown(submitter, lanes, host_buffers):
+    """Stop the submitter, drain both lanes, then free the pinned memory (only
+    once nothing in flight can touch it).  Runs once: from ``close`` or when
+    the engine is collected."""
+    if submitter is not None and submitter.is_alive():
+        submitter.stop()
+    for lane in lanes:
+        lane.release()
+    for buf in host_buffers:
+        buf.free()
+    host_buffers.clear()
+
+
+# --------------------------------------------------------------------------- #
+# the engine
+# --------------------------------------------------------------------------- #
+
+
 class CopyEngine:
     """Pinned host mirror of the KV cache plus the page mover between tiers.
 
-    Transfers are submitted to one background thread so the scheduler never
-    blocks on a runtime call, and run on one dedicated stream per direction so
-    they overlap the forward pass.  Each returns a CopyHandle.
+    ``store``/``load`` validate and coalesce on the calling thread, queue the
+    transfer for the submitter thread, and return a CopyHandle at once; the
+    transfers run on one dedicated stream per direction, overlapping compute.
     """
 
     def __init__(self, gpu_caches, gpu_num_pages, l2_num_pages, transport=None, timing_events=False):
         """``timing_events`` makes each CopyHandle.event a timing event, so a
         caller can measure the transfer on the copy stream (benchmarks)."""
-        self.closed = False
-        self._host_buffers = []
-        self.thread = None
-        self.queue = queue.SimpleQueue()
+        transport = transport or DEFAULT_TRANSPORT
+        if transport not in TRANSPORTS:
+            raise AssertionError(f"unknown transport {transport!r}; pick one of {sorted(TRANSPORTS)}")
+        self.device = gpu_caches[0].device
+        if not all(c.is_cuda and c.device == self.device for c in gpu_caches):
+            raise AssertionError("every cache tensor must live on the same GPU")
+        self.transport = transport
         self.gpu_num_pages = gpu_num_pages
         self.l2_num_pages = l2_num_pages
-        transport = transport or DEFAULT_TRANSPORT
-        assert transport in TRANSPORTS, f"unknown transport {transport!r}; pick one of {sorted(TRANSPORTS)}"
-        self.transport = transport
-        self._transport_code = TRANSPORTS[transport]
-        self.device = gpu_caches[0].device
-        assert all(c.is_cuda and c.device == self.device for c in gpu_caches)
-        self.host_caches = [self._alloc_pinned_mirror(cache, l2_num_pages) for cache in gpu_caches]
-        gpu_views = make_dma_views(gpu_caches, gpu_num_pages)
-        cpu_views = make_dma_views(self.host_caches, l2_num_pages)
-        max_pages = max(gpu_num_pages, l2_num_pages)
-        self.load_params = _TransferParams(
-            cpu_views, gpu_views, torch.cuda.Stream(self.device), l2_num_pages, gpu_num_pages, max_pages
-        )
-        self.store_params = _TransferParams(
-            gpu_views, cpu_views, torch.cuda.Stream(self.device), gpu_num_pages, l2_num_pages, max_pages
-        )
-        if self._transport_code == _lib.SWAP_BLIT:
-            self.load_params.alloc_staging(self.device)
-            self.store_params.alloc_staging(self.device)
-        self.thread = threading.Thread(
-            target=self._copy_loop, args=(self.queue, self.device, self._transport_code, timing_events), daemon=True
-        )
-        self.thread.start()
-
-    def __del__(self):
-        self.close()
-
-    def _alloc_pinned_mirror(self, cache, num_pages):
-        """Host tensor shaped like ``cache`` but ``num_pages`` deep, pinned and
-        mapped into the GPU's address space."""
-        shape = list(cache.shape)
-        shape[1] = num_pages
-        nbytes = int(np.prod(shape, dtype=np.int64)) * cache.element_size()
-        buf = _HostBuffer(max(nbytes, 1))
-        self._host_buffers.append(buf)
-        return buf.tensor(cache.dtype, tuple(shape))
+        self.closed = False
+        self._buffers = []
+        self.host_caches = []
+        for cache in gpu_caches:
+            if cache.shape[1] != gpu_num_pages:
+                raise AssertionError(f"cache pages {cache.shape[1]} != gpu_num_pages {gpu_num_pages}")
+            shape = (cache.shape[0], l2_num_pages) + tuple(cache.shape[2:])
+            buf = _HostBuffer(max(1, math.prod(shape) * cache.element_size()))
+            self._buffers.append(buf)
+            self.host_caches.append(buf.tensor(cache.dtype, shape))
+        gpu_end, l2_end = ("gpu", gpu_num_pages), ("l2", l2_num_pages)
+        self.store_params = _Lane("store", _Geometry(gpu_caches, self.host_caches),
+                                  torch.cuda.Stream(self.device), gpu_end, l2_end)
+        self.load_params = _Lane("load", _Geometry(self.host_caches, gpu_caches),
+                                 torch.cuda.Stream(self.device), l2_end, gpu_end)
+        lanes = (self.store_params, self.load_params)
+        code = TRANSPORTS[transport]
+        if code == _lib.SWAP_BLIT:
+            for lane in lanes:
+                lane.enable_staging(self.device)
+        self._submitter = _Submitter(self.device, code, timing_events)
+        self._submitter.start()
+        self._finalizer = weakref.finalize(self, _shutdown, self._submitter, lanes, self._buffers)
 
     # -- submission ---------------------------------------------------------- #
 
     def store(self, gpu_page_idxs, l2_page_idxs):
         """D2H, ordered after the KV writes already queued on the current stream."""
-        compute_done = torch.cuda.Event()
-        compute_done.record(torch.cuda.current_stream(self.device))
-        return self._submit(gpu_page_idxs, l2_page_idxs, is_store=True, wait_event=compute_done)
-
-    def count_runs(self, src_ids, dst_ids):
-        """Runs one transfer of these page pairs would make (as CopyHandle.num_runs)."""
-        if not len(src_ids):
-            return 0
-        return len(self._coalesce(np.asarray(src_ids), np.asarray(dst_ids))[0])
+        return self._submit(self.store_params, gpu_page_idxs, l2_page_idxs)
 
     def load(self, l2_page_idxs, gpu_page_idxs):
         """H2D.  The caller must not read the GPU pages until the handle is waited on."""
-        compute_done = torch.cuda.Event()
-        compute_done.record(torch.cuda.current_stream(self.device))
-        return self._submit(l2_page_idxs, gpu_page_idxs, is_store=False, wait_event=compute_done)
+        return self._submit(self.load_params, l2_page_idxs, gpu_page_idxs)
 
-    def calibrate(self, num_pages=512):
-        """Per-direction ``{desc_rate, bw}``, solving ``t = descriptors/desc_rate + bytes/bw``
-        from a coalesced and a scattered transfer (copy_engine.py:286-333).
-        Overwrites the first ``num_pages`` pages of both tiers."""
-        n = min(num_pages, self.gpu_num_pages, self.l2_num_pages)
-        fwd = list(range(n))
-        rev = list(reversed(fwd))
-        model = {}
-        for direction, submit in (("store", self.store), ("load", self.load)):
-            params = self.store_params if direction == "store" else self.load_params
-            samples = {}
-            for tag, dst in (("coalesced", fwd), ("scattered", rev)):
-                for _ in range(2):  # the first pass pays warmup
-                    start = time.perf_counter()
-                    handle = submit(fwd, dst)
-                    handle.wait()
-                    elapsed = time.perf_counter() - start
-                samples[tag] = (
-                    handle.num_runs * params.num_tensors,
-                    handle.num_pages * int(params.bpb.sum()),
-                    elapsed,
-                )
-            (d_lo, nbytes, t_lo), (d_hi, _, t_hi) = samples["coalesced"], samples["scattered"]
-            t_desc = min(max((t_hi - t_lo) / max(1, d_hi - d_lo), 1e-9), 1.0)
-            link_s = max(t_lo - d_lo * t_desc, 1e-9)
-            model[direction] = {"desc_rate": int(1 / t_desc), "bw": int(nbytes / link_s)}
-        return model
+    def count_runs(self, src_ids, dst_ids):
+        """Runs one transfer of these page pairs would make (as CopyHandle.num_runs)."""
+        return len(coalesce_runs(src_ids, dst_ids)[2]) if len(src_ids) else 0
 
-    def close(self):
-        if getattr(self, "closed", True):
-            return
-        self.closed = True
-        if getattr(self, "thread", None) is not None:
-            self.queue.put(None)
-            self.thread.join(timeout=30.0)
-        # Free pinned memory only once nothing in flight can touch it.
-        for name in ("load_params", "store_params"):
-            params = getattr(self, name, None)
-            if params is not None:
-                params.stream.synchronize()
-                params.free()
-        self.host_caches = []
-        for buf in getattr(self, "_host_buffers", []):
-            buf.free()
-        self._host_buffers = []
-
-    def _submit(self, src_ids, dst_ids, is_store, wait_event=None):
-        assert not self.closed, "CopyEngine is closed"
-        params = self.store_params if is_store else self.load_params
+    def _submit(self, lane, src_ids, dst_ids):
+        if self.closed:
+            raise AssertionError("CopyEngine is closed")
         if not len(src_ids):
             return CopyHandle(pending=False)
-        src = np.array(src_ids, dtype=np.uint64)
-        dst = np.array(dst_ids, dtype=np.uint64)
-        assert src.shape == dst.shape, "source and destination page lists differ in length"
-        self._check_range(src, dst, params.src_limit, params.dst_limit, is_store)
-        if self._transport_code == _lib.SWAP_BLIT:
-            assert len(src) <= params.max_pages, f"{len(src)} pages exceed one transfer's staging ({params.max_pages})"
-        runs = self._coalesce(src, dst)
+        src = np.asarray(src_ids, dtype=np.int64)
+        dst = np.asarray(dst_ids, dtype=np.int64)
+        if src.shape != dst.shape:
+            raise AssertionError(f"L2 {lane.name}: {len(src)} source pages but {len(dst)} destination pages")
+        lane.check(src, dst)
+        runs = coalesce_runs(src, dst)
         handle = CopyHandle()
-        handle.num_runs = len(runs[0])
-        handle.num_pages = len(src_ids)
-        self.queue.put((runs, wait_event, handle, params))
-        # Hand the GIL to the copy thread so that it enqueues the transfer now: a
-        # caller that goes on with a long Python loop (the ledger walking a
-        # prompt) would otherwise hold it for up to the interpreter's 5 ms switch
-        # interval per piece.  sleep(0) returns before the thread has woken.
+        handle.num_runs, handle.num_pages = len(runs[2]), len(src)
+        after = torch.cuda.Event()
+        after.record(torch.cuda.current_stream(self.device))
+        self._submitter.jobs.put(_Job(lane, runs, after, handle))
+        # Hand the GIL to the submitter so that it enqueues the transfer now: a
+        # caller going on with a long Python loop (the ledger walking a prompt)
+        # would otherwise hold it for up to the interpreter's 5 ms switch
+        # interval.  sleep(0) returns before the thread has woken.
         time.sleep(GIL_HANDOFF_S)
         return handle
 
-    # -- copy thread --------------------------------------------------------- #
+    # -- cost model ---------------------------------------------------------- #
 
-    @staticmethod
-    def _check_range(src, dst, src_limit, dst_limit, is_store):
-        """Raise before anything is enqueued for an index no pool owns
-        (copy_engine.py:373-385)."""
-        for ids, limit, side in ((src, src_limit, "src"), (dst, dst_limit, "dst")):
-            if len(ids) and int(ids.max()) >= limit:
-                bad = np.flatnonzero(ids >= limit)
-                tier = ("gpu", "l2") if (side == "src") == is_store else ("l2", "gpu")
-                raise AssertionError(
-                    f"L2 {'store' if is_store else 'load'} {side} page index out of "
-                    f"range for the {tier[0]} tier: "
-                    f"{[int(ids[i]) for i in bad[:8]]} >= {limit} "
-                    f"({len(bad)} of {len(ids)} pages bad)"
-                )
+    def calibrate(self, num_pages=512):
+        """Per-direction ``{desc_rate, bw}`` (integers) of the model
+        ``seconds = descriptors / desc_rate + bytes / bw`` (copy_engine.py:286-333).
 
-    @classmethod
-    def _copy_loop(cls, q, device, transport, timing=False):
-        torch.cuda.set_device(device)
-        while True:
-            item = q.get()
-            if item is None:
-                return
-            runs, wait_event, handle, params = item
-            stream = params.stream
-            try:
-                with torch.cuda.stream(stream):
-                    if wait_event is not None:
-                        stream.wait_event(wait_event)
-                    slot = params.next_staging() if transport == _lib.SWAP_BLIT else None
-                    cls._copy_blocks(runs, params, transport, slot)
-                    event = torch.cuda.Event(enable_timing=timing)
-                    event.record(stream)
-                    if slot is not None:
-                        slot[1] = event
-                handle.event = event
-            except Exception as exc:  # deferred to CopyHandle.wait
-                handle.error = exc
+        Two transfers of the same n pages per direction: in order (few runs)
+        and reversed on the destination (one run per page).  Each is timed from
+        submission until its handle's wait returns (what a retire deadline has
+        to cover), best of three after a warmup; the difference of the two
+        times over the difference of their descriptor counts is the cost of a
+        descriptor, and what the ordered transfer spent beyond its descriptors
+        is the link time of its bytes.  Overwrites the first n pages of both
+        tiers."""
+        n = min(num_pages, self.gpu_num_pages, self.l2_num_pages)
+        ids = np.arange(n, dtype=np.int64)
+        model = {}
+        for lane in (self.store_params, self.load_params):
+            measured = []
+            for dst in (ids, ids[::-1].copy()):
+                self._time_transfer(lane, ids, dst)  # warmup
+                seconds = min(self._time_transfer(lane, ids, dst) for _ in range(3))
+                measured.append((self.count_runs(ids, dst) * lane.num_tensors, seconds))
+            (d_in_order, t_in_order), (d_scattered, t_scattered) = measured
+            per_desc = (t_scattered - t_in_order) / max(1, d_scattered - d_in_order)
+            per_desc = min(max(per_desc, 1e-9), 1.0)  # scattering never speeds a transfer up
+            link = max(t_in_order - d_in_order * per_desc, 1e-9)
+            nbytes = n * int(lane.geometry.bpb.sum())
+            model[lane.name] = {"desc_rate": int(1.0 / per_desc), "bw": int(nbytes / link)}
+        return model
 
-    @staticmethod
-    def _coalesce(src_ids, dst_ids):
-        """Merge page pairs that advance together on both tiers into runs
-        (copy_engine.py:407-427): order by source (stable), split wherever the
-        source or destination does not step by one.  Native (radix sort in
-        libpipeswift_kv) because the caller waits for it.  Returns run starts
-        on both sides and run lengths, in pages, as uint64 arrays."""
-        src = np.ascontiguousarray(src_ids, dtype=np.int64)
-        dst = np.ascontiguousarray(dst_ids, dtype=np.int64)
-        n = len(src)
-        rs = np.empty(n, dtype=np.int64)
-        rd = np.empty(n, dtype=np.int64)
-        rl = np.empty(n, dtype=np.int64)
-        runs = lib().psk_coalesce_runs(src.ctypes.data_as(_i64p), dst.ctypes.data_as(_i64p), n,
-                                       rs.ctypes.data_as(_i64p), rd.ctypes.data_as(_i64p), rl.ctypes.data_as(_i64p))
-        if runs < 0:
-            check(int(runs), "coalesce page runs")
-        return rs[:runs].astype(np.uint64), rd[:runs].astype(np.uint64), rl[:runs].astype(np.uint64)
+    def _time_transfer(self, lane, src, dst):
+        """Wall seconds from submitting one transfer until it has landed."""
+        torch.cuda.synchronize(self.device)
+        t0 = time.perf_counter()
+        self._submit(lane, src, dst).wait()
+        return time.perf_counter() - t0
 
-    @staticmethod
-    def _copy_blocks(runs, params, transport, slot=None):
-        """Enqueue the transfer of pre-coalesced page runs on params.stream."""
-        src_start, dst_start, run_len = (np.ascontiguousarray(a, dtype=np.int64) for a in runs)
-        if not len(run_len):
+    # -- shutdown ------------------------------------------------------------ #
+
+    def close(self):
+        """Stop the submitter, drain both copy streams, free the pinned mirror.
+        Idempotent; also runs when the engine is garbage-collected."""
+        if self.closed:
             return
-        staging, staging_bytes = (slot[0].ptr, slot[0].nbytes) if slot is not None else (None, 0)
-        desc = params.desc_dev
-        desc_ptr, desc_bytes = (desc.data_ptr(), desc.numel()) if (slot is not None and desc is not None) else (None, 0)
-        status = lib().psk_swap_blocks(
-            transport,
-            params.src_bases.ctypes.data_as(_u64p),
-            params.dst_bases.ctypes.data_as(_u64p),
-            params.bpb.ctypes.data_as(_u64p),
-            params.num_tensors,
-            src_start.ctypes.data_as(_i64p),
-            dst_start.ctypes.data_as(_i64p),
-            run_len.ctypes.data_as(_i64p),
-            len(run_len),
-            params.src_limit,
-            params.dst_limit,
-            staging,
-            staging_bytes,
-            desc_ptr,
-            desc_bytes,
-            params.stream_handle,
-        )
-        check(status, "L2 page transfer")
+        self.closed = True
+        self._finalizer()
+        self.host_caches = []

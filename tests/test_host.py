@@ -10,7 +10,7 @@ import torch
 
 from oracle import kv_oracle as O
 from pipeswift_amd import metadata
-from pipeswift_amd.copy_engine import CopyEngine, page_bytes
+from pipeswift_amd.copy_engine import coalesce_runs, page_bytes, validate_pages
 
 
 class Seq:
@@ -146,7 +146,7 @@ def test_copy_engine_coalesce_matches_oracle(seed):
     n = int(rng.integers(1, 300))
     src = rng.permutation(1000)[:n].astype(np.uint64)
     dst = (src + 3) if seed % 2 else rng.permutation(1000)[:n].astype(np.uint64)
-    got = CopyEngine._coalesce(src, dst)
+    got = coalesce_runs(src, dst)
     exp = O.coalesce(src, dst)
     for a, b in zip(got, exp):
         assert np.array_equal(a, b)
@@ -156,12 +156,17 @@ def test_copy_engine_coalesce_matches_oracle(seed):
     assert pairs == {(int(a), int(b)) for a, b in zip(src, dst)}
 
 
-def test_copy_engine_range_check_message():
-    with pytest.raises(AssertionError, match=r"L2 store src page index out of range for the gpu tier: \[10\] >= 10"):
-        CopyEngine._check_range(np.array([1, 10], np.uint64), np.array([0, 1], np.uint64), 10, 20, True)
-    with pytest.raises(AssertionError, match="L2 load dst page index out of range for the gpu tier"):
-        CopyEngine._check_range(np.array([0], np.uint64), np.array([50], np.uint64), 20, 10, False)
-    CopyEngine._check_range(np.array([9], np.uint64), np.array([19], np.uint64), 10, 20, True)
+def test_copy_engine_page_validation():
+    with pytest.raises(AssertionError, match=r"L2 store source: 1 of 2 page ids are not pages of the gpu tier "
+                                             r"\(it has 10\): 10$"):
+        validate_pages(np.array([1, 10]), 10, "gpu", "L2 store source")
+    with pytest.raises(AssertionError, match=r"2 of 3 page ids .* l2 tier \(it has 20\): -1, 50$"):
+        validate_pages(np.array([-1, 0, 50]), 20, "l2", "L2 load source")
+    long = np.arange(100, 120)
+    with pytest.raises(AssertionError, match=r"20 of 20 .*: 100, 101, 102, 103, 104, 105, 106, 107, \.\.\.$"):
+        validate_pages(long, 10, "gpu", "x")
+    validate_pages(np.array([9, 0]), 10, "gpu", "ok")
+    validate_pages(np.array([], dtype=np.int64), 0, "gpu", "empty")
 
 
 def test_page_bytes_matches_oracle():
