@@ -945,13 +945,13 @@ def measure_l2_cycle(device, n=8192):
     m.schedule_l2_stores_for_confirmed_seq(a)
     t_sched = time.perf_counter() - t0
     st = m.pending_l2_stores[-1]
-    st["copy"].wait()
+    st.copy.wait()
     t_store = time.perf_counter() - t0
     owed_store = m._l2_owed_s["store"] - 1 * m.l2_step_ms / 1000
     res["store"] = {"GB/s": n * page_bytes / t_store / 1e9, "wall_ms": 1e3 * t_store,
-                    "host_schedule_ms": 1e3 * t_sched, "runs": st["copy"].num_runs,
-                    "predicted_ms": 1e3 * owed_store, "due_step": st["due_step"]}
-    m.poll_l2_events(st["due_step"])
+                    "host_schedule_ms": 1e3 * t_sched, "runs": st.copy.num_runs,
+                    "predicted_ms": 1e3 * owed_store, "due_step": st.due_step}
+    m.poll_l2_events(st.due_step)
     m.deallocate(a)
     filler = Seq(2, [7] * (ps * (P - 1)))
     m.allocate_prefill(filler)
@@ -966,10 +966,10 @@ def measure_l2_cycle(device, n=8192):
     t_flush = time.perf_counter() - t0
     groups = list(m.pending_l2_loads)
     for g in groups:
-        g["copy"].wait()
+        g.copy.wait()
     t_load = time.perf_counter() - t0
     owed_load = m._l2_owed_s["load"] - step * m.l2_step_ms / 1000
-    m.poll_l2_events(groups[-1]["due_step"])
+    m.poll_l2_events(groups[-1].due_step)
     assert not b.l2_load_pending and b.offset == n * ps
     table_b = torch.tensor(list(m.kv_page_table[3])[:n], dtype=torch.int64, device=device)
     ok = True
@@ -981,8 +981,8 @@ def measure_l2_cycle(device, n=8192):
     assert ok, "restored pages differ"
     res["restore"] = {"GB/s": n * page_bytes / t_load / 1e9, "wall_ms": 1e3 * t_load,
                       "host_allocate_prefill_ms": 1e3 * t_alloc_b, "host_flush_ms": 1e3 * (t_flush - t_alloc_b),
-                      "transfers": len(groups), "runs": sum(g["copy"].num_runs for g in groups),
-                      "predicted_ms": 1e3 * owed_load, "last_due_step": groups[-1]["due_step"] - step}
+                      "transfers": len(groups), "runs": sum(g.copy.num_runs for g in groups),
+                      "predicted_ms": 1e3 * owed_load, "last_due_step": groups[-1].due_step - step}
     res["bytes_checked"] = True
 
     # host cost of keying the prompt: native chain against the reference's loop

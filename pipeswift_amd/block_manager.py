@@ -2,12 +2,18 @@
 prefix cache over them, and the pinned-host L2 tier with its deadline-priced
 transfers.
 
-Mirrors pipeswift/engine/block_manager.py -- ``L2PagePool`` (:22-121) and
+Drop-in for pipeswift/engine/block_manager.py -- ``L2PagePool`` (:22-121) and
 ``BlockManager`` (:124-885) -- with the same public names, arguments and
-behaviour.  What differs is underneath: the bytes move through the HIP
-``CopyEngine`` (a blit kernel over mapped pinned memory, one launch per batch)
-and the prefix-chained page keys come from one native call per prompt
-(``psk_page_hash_chain``) instead of one xxhash object per page.
+behaviour (page ids, eviction order, counters, retire steps).  The structure is
+this module's own: both tiers share one refcounted ``_PagePool``;
+``BlockManager`` is the HBM tier and owns an ``_L2Tier`` that holds everything
+behind it (pool, copy engine, agreed cost model, the ``_LinkClock`` that prices
+deadlines, staged requests, and one FIFO of in-flight ``_Transfer`` records per
+direction), exposing its state under the reference's attribute names.  The
+bytes move through the HIP ``CopyEngine`` (a blit kernel over mapped pinned
+memory, one launch per batch) and the prefix-chained page keys come from one
+native call per prompt (``psk_page_hash_chain``) instead of one xxhash object
+per page.
 
 Two deliberate departures, both confined to states in which the reference
 hands one page to two owners:
@@ -29,8 +35,10 @@ the reference's, call for call.
 from __future__ import annotations
 
 import ctypes
+import itertools
 import math
 import warnings
+import weakref
 from array import array
 from collections import OrderedDict, deque
 from typing import Dict, List
@@ -281,6 +289,287 @@ class L2PagePool(_PagePool):
 
 
 # --------------------------------------------------------------------------- #
+# the L2 tier: link clock, in-flight transfers, staged requests
+# --------------------------------------------------------------------------- #
+
+
+class _Transfer:
+    """A batched copy between the tiers that is in flight, and the scheduler
+    step by which it is due to have landed.  A store carries the pages it
+    reads and writes and the (key, tokens) of each; a restore carries the
+    (sequence, staged loads) pairs it serves."""
+
+    __slots__ = ("copy", "due_step", "gpu_page_idxs", "l2_page_idxs", "keys", "token_ids_list", "seq_loads")
+
+    def __init__(self, copy, due_step, gpu_page_idxs=(), l2_page_idxs=(), keys=(), token_ids_list=(), seq_loads=()):
+        self.copy = copy
+        self.due_step = due_step
+        self.gpu_page_idxs = gpu_page_idxs
+        self.l2_page_idxs = l2_page_idxs
+        self.keys = keys
+        self.token_ids_list = token_ids_list
+        self.seq_loads = seq_loads
+
+
+class _LinkClock:
+    """Per-direction water level of link-seconds the copy engine still owes.
+
+    A direction drains serially, so a transfer lands after everything queued
+    ahead of it: charging a transfer raises its direction's level (floored at
+    the current step, since time the engine has had counts as drained) by
+    ``runs * views / desc_rate + pages * page_bytes / bw`` and prices the due
+    step as the level in steps, rounded up (block_manager.py:617-636).  Every
+    input is agreed over ranks, so every rank predicts the same step."""
+
+    def __init__(self, cost_model, views, page_bytes, step_ms):
+        self.model = cost_model
+        self.views = views
+        self.page_bytes = page_bytes
+        self.step_s = step_ms / 1000
+        self.owed = {"store": 0.0, "load": 0.0}
+
+    def seconds(self, direction, runs, pages):
+        rates = self.model[direction]
+        return runs * self.views / rates["desc_rate"] + pages * self.page_bytes / rates["bw"]
+
+    def charge(self, direction, copy, now_step):
+        level = max(self.owed[direction], now_step * self.step_s) + self.seconds(direction, copy.num_runs,
+                                                                                   copy.num_pages)
+        self.owed[direction] = level
+        return int(math.ceil(level / self.step_s))
+
+    def scattered_page_seconds(self):
+        """One restored page priced fully scattered: a run per page per view
+        (:646-655)."""
+        return self.seconds("load", 1, 1)
+
+    def restore_backlog_steps(self, now_step, extra_pages):
+        """Steps until a restore of ``extra_pages`` more pages would land: the
+        load level still ahead of the current step plus those pages (:657-672)."""
+        ahead = max(self.owed["load"] - now_step * self.step_s, 0.0)
+        return int(math.ceil((ahead + extra_pages * self.scattered_page_seconds()) / self.step_s))
+
+
+def _step_sized_groups(staged, budget):
+    """Consecutive (sequence, loads) entries cut into groups of at most
+    ``budget`` pages, at whole sequences only; a sequence larger than the
+    budget forms a group of its own (:550-567)."""
+    group, room = [], budget
+    for entry in staged:
+        size = len(entry[1])
+        if group and size > room:
+            yield group
+            group, room = [], budget
+        group.append(entry)
+        room -= size
+    if group:
+        yield group
+
+
+def _due_prefix(transfers, now_step):
+    """How many transfers at the head of ``transfers`` are due at ``now_step``
+    (due steps never decrease along a direction's queue)."""
+    return sum(1 for _ in itertools.takewhile(lambda t: t.due_step <= now_step, transfers))
+
+
+class _L2Tier:
+    """The pinned-host tier behind the HBM pool: its page pool and copy engine,
+    the agreed cost model and geometry, the link clock, the stores and
+    restores staged for the step's flush, and the transfers in flight (one
+    FIFO per direction).  The BlockManager owning it keeps the HBM side."""
+
+    def __init__(self, owner, l2_cache_gb, step_ms):
+        # One tensor per layer stack where the layout allows it, so that a page
+        # of a layer is one contiguous run (:176-189).
+        if owner.mla_cache_tensor is not None:
+            caches = [owner.mla_cache_tensor]
+        elif owner.kv_cache_tensor is not None:
+            caches = [owner.kv_cache_tensor]
+        else:
+            caches = list(owner.kv_cache)
+        agree = owner._min_across_workers
+        self.num_pages = self._agreed_num_pages(owner.num_pages, l2_cache_gb, caches, agree)
+        self.engine = copy_engine.CopyEngine(caches, owner.num_pages, self.num_pages)
+        self.pool = L2PagePool(self.num_pages)
+        measured = self.engine.calibrate()
+        self.cost_model = {d: {term: max(1, agree(int(v))) for term, v in rates.items()}
+                           for d, rates in measured.items()}
+        self.page_bytes = max(1, agree(copy_engine.page_bytes(caches)))
+        self.views = max(1, agree(self.engine.load_params.num_tensors))
+        self.clock = _LinkClock(self.cost_model, self.views, self.page_bytes, step_ms)
+        self.now = 0  # the retire clock: the scheduler step
+        self.staged_stores = []  # (gpu page, (key, tuple(tokens)), tokens)
+        self.staged_loads = []  # (sequence, _StagedLoads)
+        self.stores = deque()  # _Transfer, in submission order
+        self.loads = deque()
+        # The engine is closed when the tier is collected, also without close().
+        weakref.finalize(self, self.engine.close)
+
+    @staticmethod
+    def _agreed_num_pages(gpu_pages, l2_cache_gb, caches, agree):
+        """Pages of the byte budget, the minimum over ranks (:233-267)."""
+        pb = copy_engine.page_bytes(caches)
+        budget = int(l2_cache_gb * 1024**3 + 0.5)
+        mine = budget // pb
+        if mine <= 0:
+            raise ValueError(f"L2 cache byte budget is too small: per_rank_budget={budget} bytes, page_bytes={pb}")
+        pages = agree(mine)
+        if pages < mine:
+            warnings.warn(f"L2 cache pages lowered to the minimum over ranks: local={mine}, agreed={pages}",
+                          RuntimeWarning)
+        if pages < gpu_pages:
+            warnings.warn("L2 cache holds fewer pages than the GPU pool, so only part of what L1 evicts fits; "
+                          f"num_pages={gpu_pages}, l2_pages={pages}, per_rank_budget={budget} bytes, "
+                          f"page_bytes={pb}", RuntimeWarning)
+        return pages
+
+    # -- stores (GPU -> host) ------------------------------------------------ #
+
+    def stage_store(self, page_idx, h, token_ids):
+        """Queue a store of a page decode just completed, for the step's flush,
+        unless its (key, tokens) is in L2 or already on its way (:393-404)."""
+        key = (h, tuple(token_ids))
+        if key in self.pool._pending_store_keys or self.pool._find(h, token_ids) is not None:
+            return False
+        self.pool.acquire_pending_key(key)
+        self.staged_stores.append((page_idx, key, token_ids))
+        return True
+
+    def submit_stores(self, owner, stores):
+        """One logical D2H transfer of every (page, key, tokens) of ``stores``
+        not resident or on its way, stopping at the first one no L2 page can
+        take (:433-474).  Each accepted page is pinned on both tiers and its
+        key claimed at once, so a duplicate later in the batch is skipped.
+
+        The transfer goes to the engine in pieces (L2_FIRST_PIECE pages,
+        doubling up to L2_STORE_CHUNK) while the batch is still being walked,
+        so the link starts on the first pages instead of after the whole
+        batch's bookkeeping (about 12 ms for an 8192-page prompt); its deadline
+        is priced from the whole batch's runs, as for a single submission.
+        Returns the pages sent."""
+        pending, find, take = self.pool._pending_store_keys, self.pool._find, self.pool.allocate_for_store
+        hold = owner._hold
+        src, dst, keys, toks, pieces = [], [], [], [], []
+        sent, piece = 0, min(L2_FIRST_PIECE, L2_STORE_CHUNK)
+        for page_idx, h, token_ids in stores:
+            key = (h, tuple(token_ids))
+            if h != -1 and (key in pending or find(h, token_ids) is not None):
+                continue
+            q = take()
+            if q is None:
+                break  # every L2 page is pinned by a transfer
+            pending[key] = pending.get(key, 0) + 1
+            hold(page_idx)
+            src.append(page_idx)
+            dst.append(q)
+            keys.append(key)
+            toks.append(token_ids)
+            if len(src) - sent >= piece:
+                pieces.append(self.engine.store(src[sent:], dst[sent:]))
+                sent, piece = len(src), min(2 * piece, L2_STORE_CHUNK)
+        if not src:
+            return 0
+        if sent < len(src):
+            pieces.append(self.engine.store(src[sent:], dst[sent:]))
+        copy = pieces[0] if len(pieces) == 1 else copy_engine.JoinedCopyHandle(
+            pieces, self.engine.count_runs(src, dst), len(src))
+        self.stores.append(_Transfer(copy, self.clock.charge("store", copy, self.now), gpu_page_idxs=src,
+                                     l2_page_idxs=dst, keys=keys, token_ids_list=toks))
+        owner.l2_store_cnt += len(src)
+        return len(src)
+
+    def retire_stores(self, owner, count):
+        """Land the ``count`` oldest stores (completion is FIFO): their L2 pages
+        become discoverable, their keys stop pending, and the GPU pages they
+        read are released suffix first (:476-491)."""
+        pool = self.pool
+        for _ in range(count):
+            t = self.stores.popleft()
+            t.copy.wait()
+            for q, key, token_ids in zip(t.l2_page_idxs, t.keys, t.token_ids_list):
+                pool.finish_store(q, key[0], token_ids)
+                pool.release_pending_key(key)
+            for p in reversed(t.gpu_page_idxs):
+                owner._drop(p)
+
+    # -- restores (host -> GPU) ---------------------------------------------- #
+
+    def pin_loads(self, owner, loads):
+        """Pin both pages of each restore: the GPU target and the L2 source."""
+        hold, hold2 = owner._hold, self.pool._hold
+        for load in loads:
+            hold(load["gpu_page_idx"])
+            hold2(load["l2_page_idx"])
+
+    def stage_loads(self, owner, seq, loads):
+        """Queue a sequence's restores for the batched flush (:497-507).  Their
+        pages are pinned now (or were, when their copies went out while the
+        prompt was allocated), so nothing recycles them before the flush."""
+        if not getattr(loads, "pinned", False):
+            self.pin_loads(owner, loads)
+        seq.l2_load_pending = True
+        self.staged_loads.append((seq, loads))
+
+    def flush_loads(self, owner):
+        """Send the staged restores as transfers of about one scheduler step of
+        fully scattered pages each, cut at whole sequences (:509-548).  Copies
+        that went out while their prompt was allocated join their group's
+        transfer as they are; the group's other pages go now.  Returns the
+        pages restored."""
+        staged, self.staged_loads = self.staged_loads, []
+        budget = max(1, int(self.clock.step_s / self.clock.scattered_page_seconds()))
+        total = 0
+        for group in _step_sized_groups(staged, budget):
+            handles, src, dst, late = [], [], [], []
+            for _, loads in group:
+                early = getattr(loads, "handles", None)
+                handles.extend(early or ())
+                for load in loads:
+                    src.append(load["l2_page_idx"])
+                    dst.append(load["gpu_page_idx"])
+                    if not early:
+                        late.append(load)
+            if late:
+                handles.append(self.engine.load([ld["l2_page_idx"] for ld in late],
+                                                [ld["gpu_page_idx"] for ld in late]))
+            copy = handles[0] if len(handles) == 1 else copy_engine.JoinedCopyHandle(
+                handles, self.engine.count_runs(src, dst), len(dst))
+            self.loads.append(_Transfer(copy, self.clock.charge("load", copy, self.now), seq_loads=group))
+            total += len(dst)
+        owner.l2_load_cnt += total
+        return total
+
+    def retire_loads(self, owner, count):
+        """Land the ``count`` oldest restores: key their GPU pages, unpin both
+        tiers (a GPU page reaches zero references only for a sequence released
+        mid-restore; suffix first), and move each live sequence past its
+        restored pages (:569-592)."""
+        ps = owner.page_size
+        for _ in range(count):
+            t = self.loads.popleft()
+            t.copy.wait()
+            for seq, loads in t.seq_loads:
+                live = seq.seq_id in owner.kv_page_table
+                for load in loads:
+                    owner._publish_gpu_page(load["gpu_page_idx"], load["hash"], load["token_ids"])
+                    self.pool.release_from_load(load["l2_page_idx"])
+                for load in reversed(loads):
+                    owner._drop(load["gpu_page_idx"])
+                if live:
+                    seq.offset += len(loads) * ps
+                seq.l2_load_pending = False
+
+    # -- the step clock ------------------------------------------------------ #
+
+    def advance(self, owner, step_idx):
+        """Step ``step_idx`` has run: land every transfer due by the next one,
+        stores before restores (:608-615)."""
+        self.now = step_idx + 1
+        self.retire_stores(owner, _due_prefix(self.stores, self.now))
+        self.retire_loads(owner, _due_prefix(self.loads, self.now))
+
+
+# --------------------------------------------------------------------------- #
 # block manager
 # --------------------------------------------------------------------------- #
 
@@ -303,86 +592,37 @@ class BlockManager(_PagePool):
         if l2_step_ms <= 0:
             raise ValueError(f"l2_step_ms must be positive, got {l2_step_ms}")
         super().__init__(num_pages, first_page=1)
+        self.page_size = page_size
         self.kv_page_table: Dict[int, array] = {}
         self.kv_cache: List[torch.Tensor] = kv_cache
         self.mla_cache_tensor: torch.Tensor = mla_cache_tensor
         # The fused [L, P, 2, ps, H, D] allocation ``kv_cache`` is viewed from.
         self.kv_cache_tensor: torch.Tensor = kv_cache_tensor
-        self.page_size = page_size
-        self.hit_cnt = 0
-
-        self.enable_l2_cache = l2_cache_gb > 0
-        # Assumed scheduler step: converts predicted link-seconds into the
-        # step count a retire deadline is expressed in.
+        # Assumed scheduler step: converts predicted link-seconds into the step
+        # count a retire deadline is expressed in.
         self.l2_step_ms = l2_step_ms
-        self.l2_hit_cnt = 0
-        self.l2_store_cnt = 0
-        self.l2_load_cnt = 0
-        self.pending_l2_stores = []
-        self.pending_l2_loads = []
-        self.l2_step = 0
-        # Link-seconds each direction's copy stream is predicted to still owe.
-        self._l2_owed_s = {"store": 0.0, "load": 0.0}
-        self._l2_pending_store_requests = []
-        self._l2_pending_load_requests = []
-        if self.enable_l2_cache:
-            # One tensor per layer stack where the layout allows it: a page of a
-            # layer is then one contiguous run (:176-189).
-            if self.mla_cache_tensor is not None:
-                gpu_caches = [self.mla_cache_tensor]
-            elif self.kv_cache_tensor is not None:
-                gpu_caches = [self.kv_cache_tensor]
-            else:
-                gpu_caches = list(self.kv_cache)
-            self.l2_num_pages = self._resolve_l2_num_pages(l2_cache_gb, gpu_caches)
-            self.l2_copy_engine = copy_engine.CopyEngine(gpu_caches, self.num_pages, self.l2_num_pages)
-            self.l2_pool = L2PagePool(self.l2_num_pages)
-            self.l2_cost_model = self._resolve_l2_cost_model()
-            self.l2_page_bytes = max(1, self._min_across_workers(copy_engine.page_bytes(gpu_caches)))
-            self.l2_views = max(1, self._min_across_workers(self.l2_copy_engine.load_params.num_tensors))
-        else:
-            self.l2_num_pages = 0
-            self.l2_page_bytes = 0
-            self.l2_views = 0
-            self.l2_pool = None
-            self.l2_copy_engine = None
-            self.l2_cost_model = None
+        # prefix-cache hits in L1, pages restored from L2, pages stored / restored
+        self.hit_cnt = self.l2_hit_cnt = self.l2_store_cnt = self.l2_load_cnt = 0
+        self.l2 = _L2Tier(self, l2_cache_gb, l2_step_ms) if l2_cache_gb > 0 else None
 
-    def __del__(self):
-        engine = getattr(self, "l2_copy_engine", None)
-        if engine is not None:
-            engine.close()
+    # The L2 tier's state under the reference's attribute names.
+    enable_l2_cache = property(lambda self: self.l2 is not None)
+    l2_pool = property(lambda self: self.l2.pool if self.l2 else None)
+    l2_copy_engine = property(lambda self: self.l2.engine if self.l2 else None)
+    l2_cost_model = property(lambda self: self.l2.cost_model if self.l2 else None)
+    l2_num_pages = property(lambda self: self.l2.num_pages if self.l2 else 0)
+    l2_page_bytes = property(lambda self: self.l2.page_bytes if self.l2 else 0)
+    l2_views = property(lambda self: self.l2.views if self.l2 else 0)
+    l2_step = property(lambda self: self.l2.now if self.l2 else 0)
+    pending_l2_stores = property(lambda self: self.l2.stores if self.l2 else ())
+    pending_l2_loads = property(lambda self: self.l2.loads if self.l2 else ())
+    _l2_pending_store_requests = property(lambda self: self.l2.staged_stores if self.l2 else [])
+    _l2_pending_load_requests = property(lambda self: self.l2.staged_loads if self.l2 else [])
+    _l2_owed_s = property(lambda self: self.l2.clock.owed if self.l2 else {"store": 0.0, "load": 0.0})
 
     @classmethod
     def compute_hash(cls, token_ids, prefix: int = -1):
         return page_key(token_ids, prefix)
-
-    # -- L2 capacity and cost model ---------------------------------------- #
-
-    def _resolve_l2_num_pages(self, l2_cache_gb, caches):
-        """Pages of the byte budget, agreed across ranks (:233-267)."""
-        pb = copy_engine.page_bytes(caches)
-        budget = int(l2_cache_gb * 1024**3 + 0.5)
-        local = budget // pb
-        if local <= 0:
-            raise ValueError(
-                f"L2 cache byte budget is too small: per_rank_budget={budget} bytes, page_bytes={pb}"
-            )
-        agreed = self._min_across_workers(local)
-        if agreed < local:
-            warnings.warn(
-                f"L2 cache pages lowered to the minimum over ranks: local={local}, agreed={agreed}",
-                RuntimeWarning,
-            )
-            local = agreed
-        if local < self.num_pages:
-            warnings.warn(
-                "L2 cache holds fewer pages than the GPU pool, so only part of what L1 "
-                f"evicts fits; num_pages={self.num_pages}, l2_pages={local}, "
-                f"per_rank_budget={budget} bytes, page_bytes={pb}",
-                RuntimeWarning,
-            )
-        return local
 
     @staticmethod
     def _min_across_workers(value):
@@ -394,15 +634,6 @@ class BlockManager(_PagePool):
         t = torch.tensor([value], dtype=torch.int64, device=device)
         dist.all_reduce(t, op=dist.ReduceOp.MIN)
         return int(t.item())
-
-    def _resolve_l2_cost_model(self):
-        """Per-direction integer ``{desc_rate, bw}`` from the engine's
-        calibration, reduced to the minimum over ranks (:270-288)."""
-        model = self.l2_copy_engine.calibrate()
-        return {
-            direction: {term: max(1, self._min_across_workers(int(v))) for term, v in terms.items()}
-            for direction, terms in model.items()
-        }
 
     # -- L1 pool ------------------------------------------------------------ #
 
@@ -444,15 +675,6 @@ class BlockManager(_PagePool):
         if self.page_idx2hash[page_idx] == -1:
             self._key_page(page_idx, h, token_ids)
 
-    def _retain_gpu_page_for_transfer(self, page_idx):
-        self._hold(page_idx)
-
-    def _release_gpu_pages_from_transfer(self, ordered_page_idxs):
-        """Drop a transfer's reference on each page, in eviction order: a page
-        reaching zero joins the tail of its queue (:372-387)."""
-        for p in ordered_page_idxs:
-            self._drop(p)
-
     def reset_page(self, page_idx):
         self._unkey_page(page_idx)
 
@@ -461,276 +683,75 @@ class BlockManager(_PagePool):
         also staged for L2 (:814-832)."""
         assert h != -1 and self.page_idx2hash[page_idx] == -1 and self.ref_counts[page_idx] == 1
         self._key_page(page_idx, h, token_ids)
-        if from_decode and self.enable_l2_cache:
-            self._stage_l2_store(page_idx, h, token_ids)
+        if from_decode and self.l2 is not None:
+            self.l2.stage_store(page_idx, h, token_ids)
 
     def get_usage(self):
         return 1 - (len(self.free_page_queue) + len(self.cached_pages)) / self.num_pages
 
     def get_l2_usage(self):
-        return self.l2_pool.get_usage() if self.enable_l2_cache else 0.0
+        return self.l2.pool.get_usage() if self.l2 else 0.0
 
-    # -- L2 stores (GPU -> host) ------------------------------------------- #
-
-    def _stage_l2_store(self, page_idx, h, token_ids):
-        """Queue a store for the step's batched flush (:393-404)."""
-        if not self.enable_l2_cache or self.l2_pool.has_page_or_pending(h, token_ids):
-            return False
-        key = (h, tuple(token_ids))
-        self._l2_pending_store_requests.append((page_idx, h, token_ids, key))
-        self.l2_pool.acquire_pending_key(key)
-        return True
+    # -- L2 calls of the scheduler (block_manager.py:393-672) --------------- #
 
     def flush_l2_stores(self):
-        """Send the staged stores whose page still carries the staged key (:406-418)."""
-        if not self._l2_pending_store_requests:
+        """Send the staged stores whose page still carries the staged key (a
+        page can be merged away or recycled in between); returns the pages
+        sent."""
+        if self.l2 is None or not self.l2.staged_stores:
             return 0
-        staged, self._l2_pending_store_requests = self._l2_pending_store_requests, []
+        staged, self.l2.staged_stores = self.l2.staged_stores, []
         live = []
-        for page_idx, h, token_ids, key in staged:
-            self.l2_pool.release_pending_key(key)
-            if self.page_idx2hash[page_idx] == h:
-                live.append((page_idx, h, token_ids))
-        return self._schedule_l2_store_batch(live)
+        for page_idx, key, token_ids in staged:
+            self.l2.pool.release_pending_key(key)
+            if self.page_idx2hash[page_idx] == key[0]:
+                live.append((page_idx, key[0], token_ids))
+        return self.l2.submit_stores(self, live)
 
     def schedule_l2_stores_for_confirmed_seq(self, seq):
         """Store the keyed pages of the sequence's confirmed tokens (:420-431)."""
-        if not self.enable_l2_cache or seq.seq_id not in self.kv_page_table:
+        if self.l2 is None or seq.seq_id not in self.kv_page_table:
             return
         table = self.kv_page_table[seq.seq_id]
-        confirmed = min(len(seq.token_ids) // self.page_size, len(table))
-        stores = []
-        for p in table[:confirmed]:
-            h = self.page_idx2hash[p]
-            if h != -1:
-                stores.append((p, h, self.page_idx2token_ids[p]))
-        self._schedule_l2_store_batch(stores)
-
-    def _schedule_l2_store_batch(self, stores):
-        """One D2H transfer for every store not already resident or on its way;
-        stops at the first store no L2 page can take (:433-474).
-
-        The transfer is one logical copy, as in the reference, but it is
-        submitted in pieces (L2_FIRST_PIECE pages, doubling up to
-        L2_STORE_CHUNK) while this loop is still walking the batch, so the link
-        starts moving the first pages instead of waiting for the host's per-page
-        bookkeeping of the whole batch (about 12 ms for an 8192-page prompt).  Page ids, order and the deadline
-        priced from the whole batch's runs are those of a single submission."""
-        if not self.enable_l2_cache:
-            return 0
-        gpu, l2, keys, toks = [], [], [], []
-        handles = []
-        sent = 0
-        pool = self.l2_pool
-        engine = self.l2_copy_engine
-        # pool.has_page_or_pending / acquire_pending_key and self._hold,
-        # inlined with the key tuple built once: this runs once per page
-        pending, find, take = pool._pending_store_keys, pool._find, pool.allocate_for_store
-        rc, cached = self.ref_counts, self.cached_pages
-        piece = min(L2_FIRST_PIECE, L2_STORE_CHUNK)
-        for page_idx, h, token_ids in stores:
-            key = (h, tuple(token_ids))
-            if h != -1 and (key in pending or find(h, token_ids) is not None):
-                continue
-            dst = take()
-            if dst is None:
-                break
-            # Claimed now, so a duplicate later in this batch is caught above.
-            pending[key] = pending.get(key, 0) + 1
-            if rc[page_idx] == 0 and page_idx in cached:
-                del cached[page_idx]
-            rc[page_idx] += 1
-            gpu.append(page_idx)
-            l2.append(dst)
-            keys.append(h)
-            toks.append(token_ids)
-            if len(gpu) - sent >= piece:
-                handles.append(engine.store(gpu[sent:], l2[sent:]))
-                sent = len(gpu)
-                piece = min(2 * piece, L2_STORE_CHUNK)
-        if not gpu:
-            return 0
-        if sent < len(gpu):
-            handles.append(engine.store(gpu[sent:], l2[sent:]))
-        if len(handles) == 1:
-            copy = handles[0]
-        else:
-            copy = copy_engine.JoinedCopyHandle(handles, engine.count_runs(gpu, l2), len(gpu))
-        self.pending_l2_stores.append(
-            {
-                "copy": copy,
-                "due_step": self._l2_retire_step(copy, "store"),
-                "gpu_page_idxs": gpu,
-                "l2_page_idxs": l2,
-                "hashes": keys,
-                "token_ids_list": toks,
-            }
-        )
-        self.l2_store_cnt += len(gpu)
-        return len(gpu)
-
-    def _retire_l2_stores(self, n_ready):
-        """Retire the first ``n_ready`` stores (completion is FIFO): key their L2
-        pages, then drop the GPU pins suffix first (:476-491)."""
-        for pending in self.pending_l2_stores[:n_ready]:
-            pending["copy"].wait()
-            for dst, h, token_ids in zip(pending["l2_page_idxs"], pending["hashes"], pending["token_ids_list"]):
-                self.l2_pool.finish_store(dst, h, token_ids)
-                self.l2_pool.release_pending_key((h, tuple(token_ids)))
-            self._release_gpu_pages_from_transfer(reversed(pending["gpu_page_idxs"]))
-        self.pending_l2_stores = self.pending_l2_stores[n_ready:]
-
-    # -- L2 loads (host -> GPU) -------------------------------------------- #
-
-    def _pin_loads(self, loads):
-        """Pin both pages of each restore (_hold on both tiers, inlined: this
-        runs once per restored page)."""
-        rc, cached = self.ref_counts, self.cached_pages
-        l2 = self.l2_pool
-        rc2, cached2 = l2.ref_counts, l2.cached_pages
-        for load in loads:
-            g, q = load["gpu_page_idx"], load["l2_page_idx"]
-            if rc[g] == 0 and g in cached:
-                del cached[g]
-            rc[g] += 1
-            if rc2[q] == 0 and q in cached2:
-                del cached2[q]
-            rc2[q] += 1
-
-    def _stage_l2_loads(self, seq, loads):
-        """Queue a sequence's restore for the batched flush (:497-507).  Its
-        pages are pinned here (or already, where its copies went out early), so
-        nothing recycles them before the flush."""
-        if not getattr(loads, "pinned", False):
-            self._pin_loads(loads)
-        seq.l2_load_pending = True
-        self._l2_pending_load_requests.append((seq, loads))
+        confirmed = table[: min(len(seq.token_ids) // self.page_size, len(table))]
+        key_of, tokens_of = self.page_idx2hash, self.page_idx2token_ids
+        self.l2.submit_stores(self, [(p, key_of[p], tokens_of[p]) for p in confirmed if key_of[p] != -1])
 
     def flush_l2_loads(self):
-        """Send the staged restores as transfers of about one scheduler step
-        each, split at whole sequences (:509-548)."""
-        if not self._l2_pending_load_requests:
+        """Send the staged restores (see _L2Tier.flush_loads); returns the pages."""
+        if self.l2 is None or not self.l2.staged_loads:
             return 0
-        staged, self._l2_pending_load_requests = self._l2_pending_load_requests, []
-        total = 0
-        engine = self.l2_copy_engine
-        for group in self._split_l2_loads(staged):
-            # pages whose copies already went out (submitted while their prompt
-            # was allocated) join the transfer as they are; the rest go now
-            src, dst, handles, late_src, late_dst = [], [], [], [], []
-            for _, loads in group:
-                early = getattr(loads, "handles", None)
-                if early:
-                    handles.extend(early)
-                for load in loads:
-                    src.append(load["l2_page_idx"])
-                    dst.append(load["gpu_page_idx"])
-                    if not early:
-                        late_src.append(load["l2_page_idx"])
-                        late_dst.append(load["gpu_page_idx"])
-            if late_src:
-                handles.append(engine.load(late_src, late_dst))
-            # one transfer, priced from the whole group's runs as one submission
-            copy = handles[0] if len(handles) == 1 else copy_engine.JoinedCopyHandle(
-                handles, engine.count_runs(src, dst), len(dst))
-            self.pending_l2_loads.append(
-                {"copy": copy, "due_step": self._l2_retire_step(copy, "load"), "seq_loads": group}
-            )
-            total += len(dst)
-        self.l2_load_cnt += total
-        return total
-
-    def _split_l2_loads(self, staged):
-        """Greedy groups of at most one step's worth of fully scattered pages;
-        a sequence larger than that goes alone (:550-567)."""
-        budget = max(1, int((self.l2_step_ms / 1000) / self.l2_page_s))
-        groups, cur, acc = [], [], 0
-        for entry in staged:
-            n = len(entry[1])
-            if cur and acc + n > budget:
-                groups.append(cur)
-                cur, acc = [], 0
-            cur.append(entry)
-            acc += n
-        if cur:
-            groups.append(cur)
-        return groups
-
-    def _retire_l2_loads(self, n_ready):
-        """Retire the first ``n_ready`` restores: key the GPU pages, unpin both
-        tiers, advance each live sequence past its restored pages (:569-592)."""
-        ps = self.page_size
-        for pending in self.pending_l2_loads[:n_ready]:
-            pending["copy"].wait()
-            for seq, loads in pending["seq_loads"]:
-                alive = seq.seq_id in self.kv_page_table
-                for load in loads:
-                    self._publish_gpu_page(load["gpu_page_idx"], load["hash"], load["token_ids"])
-                    self.l2_pool.release_from_load(load["l2_page_idx"])
-                # Reaches zero only for a sequence released mid-load; suffix first.
-                self._release_gpu_pages_from_transfer([load["gpu_page_idx"] for load in reversed(loads)])
-                if alive:
-                    seq.offset += len(loads) * ps
-                seq.l2_load_pending = False
-        self.pending_l2_loads = self.pending_l2_loads[n_ready:]
+        return self.l2.flush_loads(self)
 
     def reclaim_l2_store_pages(self):
-        """Retire the oldest in-flight store ahead of its deadline; True if
-        there was one (:594-606)."""
-        if not self.pending_l2_stores:
+        """Land the oldest in-flight store ahead of its deadline, freeing the GPU
+        pages it pins; True if there was one (:594-606)."""
+        if self.l2 is None or not self.l2.stores:
             return False
-        self._retire_l2_stores(1)
+        self.l2.retire_stores(self, 1)
         return True
 
     def poll_l2_events(self, step_idx):
-        """Once per scheduler step: retire every transfer whose deadline step
-        has arrived (:608-615)."""
-        if not self.enable_l2_cache:
-            return
-        self.l2_step = step_idx + 1
-        if not self.pending_l2_stores and not self.pending_l2_loads:
-            return
-        self._retire_l2_stores(self._l2_num_due(self.pending_l2_stores))
-        self._retire_l2_loads(self._l2_num_due(self.pending_l2_loads))
-
-    def _l2_retire_step(self, copy, direction):
-        """Step by which ``copy`` is due.  A direction drains serially, so the
-        transfer lands after everything queued ahead of it: a water level of
-        link-seconds owed, floored at the current step, plus this transfer's
-        ``runs * views / desc_rate + pages * page_bytes / bw`` (:617-636)."""
-        model = self.l2_cost_model[direction]
-        cost_s = copy.num_runs * self.l2_views / model["desc_rate"] + copy.num_pages * self.l2_page_bytes / model["bw"]
-        step_s = self.l2_step_ms / 1000
-        owed_s = max(self._l2_owed_s[direction], self.l2_step * step_s) + cost_s
-        self._l2_owed_s[direction] = owed_s
-        return int(math.ceil(owed_s / step_s))
-
-    def _l2_num_due(self, pendings):
-        """Length of the due prefix (deadlines increase along the list)."""
-        for i, pending in enumerate(pendings):
-            if pending["due_step"] > self.l2_step:
-                return i
-        return len(pendings)
+        """Once per scheduler step: land every transfer whose deadline step has
+        arrived."""
+        if self.l2 is not None:
+            self.l2.advance(self, step_idx)
 
     @property
     def l2_page_s(self):
-        """Link-seconds of one restored page priced fully scattered: one
-        descriptor per page per view (:646-655)."""
-        model = self.l2_cost_model["load"]
-        return self.l2_views / model["desc_rate"] + self.l2_page_bytes / model["bw"]
+        """Link-seconds of one restored page priced fully scattered."""
+        return self.l2.clock.scattered_page_seconds()
 
     def l2_load_horizon_steps(self):
-        """Steps until a restore staged now would be due: what the load water
-        level still owes past the current step plus the staged, unflushed pages
-        (:657-672)."""
-        if not self.enable_l2_cache:
+        """Steps until a restore staged now would be due: the load level still
+        owed past the current step plus the staged, unflushed pages."""
+        if self.l2 is None:
             return 0
-        pages = sum(len(loads) for _, loads in self._l2_pending_load_requests)
-        step_s = self.l2_step_ms / 1000
-        owed_s = max(self._l2_owed_s["load"] - self.l2_step * step_s, 0.0)
-        return int(math.ceil((owed_s + pages * self.l2_page_s) / step_s))
+        staged = sum(len(loads) for _, loads in self.l2.staged_loads)
+        return self.l2.clock.restore_backlog_steps(self.l2.now, staged)
 
     # -- sequence-level allocation ----------------------------------------- #
+
 
     def _prompt_page_hashes(self, seq):
         """``[(key, page tokens)]`` for every page of the prompt, -1 for a
@@ -794,7 +815,7 @@ class BlockManager(_PagePool):
             loads = self._prefill_pages_one_by_one(pages, matched, table)
         self.kv_page_table[seq.seq_id] = table
         if loads:
-            self._stage_l2_loads(seq, loads)
+            self.l2.stage_loads(self, seq, loads)
 
     def _prefill_pages_batched(self, pages, matched, table):
         """Pages past the L1 match when the free and cached queues serve every
@@ -829,7 +850,7 @@ class BlockManager(_PagePool):
                 for j, src in enumerate(srcs):
                     h, token_ids = pages[i + j]
                     piece.append({"gpu_page_idx": got[j], "l2_page_idx": src, "hash": h, "token_ids": token_ids})
-                self._pin_loads(piece)
+                self.l2.pin_loads(self, piece)
                 loads.extend(piece)
                 loads.handles.append(engine.load(srcs, got))
                 table.extend(got)

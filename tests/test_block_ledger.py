@@ -137,10 +137,10 @@ def state_product(m):
             "l2_keys": list(pool.page_idx2hash),
             "l2_index": {h: list(v) for h, v in pool.hash2page_idx_list.items()},
             "pending_keys": dict(pool._pending_store_keys),
-            "stores": [(x["gpu_page_idxs"], x["l2_page_idxs"], x["due_step"]) for x in m.pending_l2_stores],
-            "loads": [(x["due_step"], [(s.seq_id, [(ld["gpu_page_idx"], ld["l2_page_idx"]) for ld in lds])
-                                       for s, lds in x["seq_loads"]]) for x in m.pending_l2_loads],
-            "staged_stores": [(p, h) for p, h, _, _ in m._l2_pending_store_requests],
+            "stores": [(x.gpu_page_idxs, x.l2_page_idxs, x.due_step) for x in m.pending_l2_stores],
+            "loads": [(x.due_step, [(s.seq_id, [(ld["gpu_page_idx"], ld["l2_page_idx"]) for ld in lds])
+                                    for s, lds in x.seq_loads]) for x in m.pending_l2_loads],
+            "staged_stores": [(p, key[0]) for p, key, _ in m._l2_pending_store_requests],
             "owed": dict(m._l2_owed_s),
             "step": m.l2_step,
         })
@@ -201,10 +201,10 @@ def check_product_invariants(m):
         for p in t:
             holders[p] += 1
     for x in m.pending_l2_stores:
-        for p in x["gpu_page_idxs"]:
+        for p in x.gpu_page_idxs:
             holders[p] += 1
     staged = [lds for _, lds in m._l2_pending_load_requests] + [
-        lds for x in m.pending_l2_loads for _, lds in x["seq_loads"]]
+        lds for x in m.pending_l2_loads for _, lds in x.seq_loads]
     for lds in staged:
         for ld in lds:
             holders[ld["gpu_page_idx"]] += 1
@@ -217,7 +217,7 @@ def check_product_invariants(m):
         t2.index = [(h, p) for h, ps in pool.hash2page_idx_list.items() for p in ps]
         holders = [0] * pool.num_pages
         for x in m.pending_l2_stores:
-            for q in x["l2_page_idxs"]:
+            for q in x.l2_page_idxs:
                 holders[q] += 1
         for lds in staged:
             for ld in lds:
@@ -507,7 +507,7 @@ def test_allocate_drains_in_flight_stores_before_failing(monkeypatch):
     m.allocate_prefill(Seq(2, [9]))  # takes 3
     assert m.free_pages() == 0 and len(m.pending_l2_stores) == 1
     p = m.allocate_a_page()  # retires the store: cached [2, 1], evicts 2
-    assert m.pending_l2_stores == [] and p == 2 and list(m.cached_pages) == [1]
+    assert not m.pending_l2_stores and p == 2 and list(m.cached_pages) == [1]
 
 
 @pytest.mark.parametrize("kind", IMPLS)
@@ -572,7 +572,7 @@ def run_trace(monkeypatch, seed, steps=600, num_pages=32, ps=4, l2_pages=64, adm
             toks = d[:cut] + [rng.randrange(40) for _ in range(n - cut)]
             need = (n + ps - 1) // ps
             # past the free count only as far as in-flight stores pin pages
-            pinned = sum(len(x["gpu_page_idxs"]) for x in m.pending_l2_stores)
+            pinned = sum(len(x.gpu_page_idxs) for x in m.pending_l2_stores)
             past_free = rng.random() < admit_past_free and m.free_pages() + pinned >= need
             if not past_free and m.free_pages() < need:
                 continue

@@ -86,7 +86,7 @@ def test_l2_store_evict_restore_round_trip(kind, dev):
 
     m.poll_l2_events(0)
     m.schedule_l2_stores_for_confirmed_seq(a)
-    assert m.l2_store_cnt == 20 and m.pending_l2_stores[0]["due_step"] >= 1
+    assert m.l2_store_cnt == 20 and m.pending_l2_stores[0].due_step >= 1
     step = _run_until(m, lambda: not m.pending_l2_stores, 0)
     m.deallocate(a)
 
