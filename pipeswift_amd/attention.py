@@ -24,6 +24,7 @@ cache is not covered.
 
 from __future__ import annotations
 
+import os
 from typing import Optional
 
 import torch
@@ -32,6 +33,8 @@ from ._lib import check, dtype_code, i64_array, lib, ptr, stream_handle
 
 HEAD_DIM = 128
 MAX_ROWS = 16  # query tokens x query heads per kv head
+# Opt-in argument checks that need a host synchronization (check_cu_seqlens_q).
+_CHECK_ARGS = os.environ.get("PIPESWIFT_AMD_CHECK_ARGS", "0") == "1"
 
 _OUT_CODES = {torch.bfloat16: 2, torch.float32: 0}
 
@@ -59,6 +62,27 @@ def _descale(t: Optional[torch.Tensor], num_seqs: int, num_kv_heads: int, device
     return t, t.stride(0), t.stride(1)
 
 
+def check_cu_seqlens_q(cu_seqlens_q: torch.Tensor, total_q: int, q_len: int) -> None:
+    """Validate a ragged query layout against what the reader assumes (an
+    AssertionError naming the first violation): ``cu_seqlens_q`` is int32
+    [B + 1], starts at 0, never decreases, ends at most at ``total_q`` (the
+    query rows), and gives no sequence more than ``q_len`` rows.  The reader
+    itself trusts the layout: a longer sequence is cut to its first ``q_len``
+    rows (the others of a fresh output stay unwritten), and an end past
+    ``total_q`` writes output rows past the tensor.  This check copies the
+    array to the host (a synchronization), so it is opt-in."""
+    cu = cu_seqlens_q.detach().to("cpu", torch.int64)
+    assert cu.dim() == 1 and cu.numel() >= 1, f"cu_seqlens_q must be 1-D [B + 1], got shape {tuple(cu.shape)}"
+    assert int(cu[0]) == 0, f"cu_seqlens_q[0] = {int(cu[0])}, must be 0"
+    n = cu[1:] - cu[:-1]
+    if n.numel():
+        b = int(torch.argmin(n))
+        assert int(n[b]) >= 0, f"cu_seqlens_q decreases at sequence {b}: {int(cu[b])} -> {int(cu[b + 1])}"
+        b = int(torch.argmax(n))
+        assert int(n[b]) <= q_len, f"sequence {b} has {int(n[b])} query rows, more than max_seqlen_q = {q_len}"
+    assert int(cu[-1]) <= total_q, f"cu_seqlens_q[-1] = {int(cu[-1])} exceeds the {total_q} query rows"
+
+
 def paged_decode_attention(
     q: torch.Tensor,
     k_cache: torch.Tensor,
@@ -77,6 +101,7 @@ def paged_decode_attention(
     q_len: int = 1,
     cu_seqlens_q: Optional[torch.Tensor] = None,
     causal: bool = True,
+    validate: bool = False,
 ):
     """One decode step of attention for every sequence.
 
@@ -95,6 +120,12 @@ def paged_decode_attention(
     balances the work instead: one workgroup per resident slot, each streaming
     an equal run of the batch's 16-token tiles of one kv head across sequence
     boundaries.
+
+    Contract of a ragged ``cu_seqlens_q`` (not checked on the fast path):
+    cu[-1] <= total_q and every sequence has at most ``q_len`` rows.
+    ``validate=True`` (or PIPESWIFT_AMD_CHECK_ARGS=1) checks it with a host
+    synchronization first (``check_cu_seqlens_q``); the check is skipped while
+    the stream is being captured into a graph.
     """
     assert q.is_cuda and k_cache.is_cuda and v_cache.is_cuda
     assert q.dim() == 3 and q.shape[2] == HEAD_DIM and q.stride(2) == 1, "q must be [B, Hq, 128] with unit last stride"
@@ -112,6 +143,8 @@ def paged_decode_attention(
         assert cu_seqlens_q.dtype == torch.int32 and cu_seqlens_q.is_contiguous() and cu_seqlens_q.dim() == 1
         assert cu_seqlens_q.device == q.device
         B = cu_seqlens_q.shape[0] - 1
+        if (validate or _CHECK_ARGS) and not torch.cuda.is_current_stream_capturing():
+            check_cu_seqlens_q(cu_seqlens_q, TQ, q_len)
     assert Hq % Hkv == 0 and q_len * (Hq // Hkv) <= MAX_ROWS, \
         f"{q_len} query tokens x {Hq // Hkv} heads per kv head (at most {MAX_ROWS} rows)"
     assert block_table.dtype == torch.int32 and block_table.dim() == 2 and block_table.stride(1) == 1
@@ -173,7 +206,18 @@ def flash_attn_varlen_func(
     ``causal`` each sees the keys up to its own position.  ``max_seqlen_k``
     bounds the lengths when given, else the block table's width does.
     ``num_splits`` is the flash-decoding split count (0: the balanced
-    schedule); ``fa_version`` is accepted for signature compatibility."""
+    schedule); ``fa_version`` is accepted for signature compatibility.
+
+    Prefill over the paged FP8 cache is not covered: a call whose
+    ``max_seqlen_q * Hq / Hkv`` exceeds 16 raises NotImplementedError before
+    touching the device (the reference routes prefill through the same entry,
+    attention.py:577-585)."""
+    group = q.shape[1] // k.shape[2] if k.shape[2] else 0
+    if int(max_seqlen_q) * max(group, 1) > MAX_ROWS:
+        raise NotImplementedError(
+            f"prefill over the paged FP8 cache is not implemented: max_seqlen_q={int(max_seqlen_q)} query tokens x "
+            f"{group} query heads per kv head exceed the {MAX_ROWS} rows of the decode reader, which covers decode "
+            f"and speculative decode up to {MAX_ROWS // max(group, 1)} tokens per sequence")
     assert seqused_k is not None and block_table is not None, "paged decode needs seqused_k and block_table"
     B = seqused_k.shape[0]
     assert cu_seqlens_q is not None and cu_seqlens_q.shape[0] == B + 1

@@ -54,7 +54,12 @@ def warmup(device) -> None:
 
 def check_available() -> None:
     """Fail at startup rather than in the first forward pass (fp8_kv.py:64-71):
-    the FP8 reader and append need a gfx950 GPU and this package's library."""
+    the FP8 reader and append need a gfx950 GPU and this package's library.
+
+    The reader covers decode and speculative decode (``max_seqlen_q`` times
+    the query heads per kv head at most 16); a prefill forward over the FP8
+    cache raises NotImplementedError from ``attn_varlen_func()``'s function,
+    so an engine that prefills through it must keep --enable_fp8_kv off."""
     assert torch.cuda.is_available(), "--enable_fp8_kv needs a GPU"
     arch = getattr(torch.cuda.get_device_properties(torch.cuda.current_device()), "gcnArchName", "")
     assert arch.startswith("gfx950"), f"--enable_fp8_kv on this build needs gfx950 (MI355X), got {arch or 'unknown'}"
@@ -66,7 +71,8 @@ def check_available() -> None:
 
 def attn_varlen_func():
     """The FA3-style varlen entry point for the FP8 cache (fp8_kv.py:44-62):
-    this package's paged reader, same keywords."""
+    this package's paged reader, same keywords, for decode and speculative
+    decode (prefill-sized calls raise NotImplementedError)."""
     from .attention import flash_attn_varlen_func
 
     return flash_attn_varlen_func

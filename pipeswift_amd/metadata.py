@@ -232,9 +232,12 @@ def derive_kvcache_info_next_decode_step(
         ptrs[i], plen[i] = _page_ptr(kv_page_table[seq.seq_id], keep)
         pos[i] = seq.offset
     prev_kv = np.ascontiguousarray(prev.actual_lens_kv_cpu.numpy(), dtype=np.int32)
-    assert prev_kv.shape[0] >= num_seqs, "previous step has fewer sequences"
+    K = prev_kv.shape[0]
+    assert K >= num_seqs, "previous step has fewer sequences"
     B = num_seqs
-    nbytes = 8 * B + 4 * B
+    # lens_kv keeps all K entries of the previous step, the first B advanced
+    # (the reference copies the whole previous array, metadata.py:367-369)
+    nbytes = 8 * B + 4 * K
     on_gpu = device.type == "cuda"
     stager = _stagers.setdefault(device if on_gpu else "cpu", _PinnedStager())
     slot, blk = stager.acquire(nbytes)
@@ -248,6 +251,8 @@ def derive_kvcache_info_next_decode_step(
             raise IndexError(lib().psk_last_error().decode())
         check(int(got), "derive_kvcache_info_next_decode_step")
     host = blk[:nbytes]
+    if K > B:
+        host[8 * B + 4 * B:].view(torch.int32).copy_(torch.from_numpy(prev_kv[B:]))
     if on_gpu:
         dev = torch.empty(nbytes, dtype=torch.uint8, device=device)
         dev.copy_(host, non_blocking=True)

@@ -75,6 +75,26 @@ def test_next_decode_step_metadata():
     assert nxt.actual_lens_kv.tolist() == [41, 17]
 
 
+def test_next_decode_step_keeps_the_previous_steps_longer_lens():
+    """A draft step over the first sequences of a longer previous step: lens_kv
+    keeps every previous entry and advances only the stepped ones, as the
+    reference's copy of the whole previous array does (metadata.py:367-369),
+    so it stays as long as the lens_q / cu_seqlens_q taken from that step."""
+    ps = 16
+    seqs = [Seq(0, 40, 39), Seq(1, 16, 15), Seq(2, 70, 69)]
+    table = {0: [5, 9, 2, 7], 1: [4, 8], 2: [1, 3, 6, 10, 11]}
+    info = metadata.prepare_kv_info(seqs, table, ps, None, None, is_decode=True, device="cpu")
+    assert info.actual_lens_kv_cpu.tolist() == [40, 16, 70]
+    stepped = seqs[:2]
+    for s in stepped:
+        s.offset += 1
+        s.token_ids.append(0)
+    nxt = metadata.derive_kvcache_info_next_decode_step(info, stepped, table, ps, device="cpu")
+    assert nxt.slot_mapping.tolist() == [2 * 16 + 8, 8 * 16 + 0]
+    assert nxt.actual_lens_kv_cpu.tolist() == [41, 17, 70] == nxt.actual_lens_kv.tolist()
+    assert nxt.actual_lens_kv.shape[0] == nxt.actual_lens_q.shape[0] == nxt.cu_seqlens_q.shape[0] - 1
+
+
 def test_graph_refresh_oracle_hand_worked():
     """The oracle of set_graph_kvcacheinfo (cudagraph.py:75-118) on a case
     worked out by hand: 2 live sequences in a graph of 4, static buffers of 5
@@ -186,3 +206,43 @@ def test_shim_asserts_fire_before_device_calls():
         reshape_and_cache_flash(k.view(4, 1024)[None], k, c, c, torch.zeros(4, dtype=torch.int64))
     with pytest.raises(AssertionError):
         reshape_and_cache_flash_diffkv(k, k, torch.zeros(2, 16, 8, 100), torch.zeros(4, dtype=torch.int64))
+
+
+def test_fp8_reader_refuses_prefill_before_any_device_call():
+    """The FA3-style entry covers decode and speculative decode; a prefill-sized
+    call (the reference routes prefill through the same entry when
+    --enable_fp8_kv is on) raises NotImplementedError naming prefill, before
+    any device work (these are host tensors)."""
+    from pipeswift_amd import fp8_kv
+
+    f = fp8_kv.attn_varlen_func()
+    q = torch.zeros(6 * 8, 32, 128, dtype=torch.bfloat16)
+    k = torch.zeros(10, 16, 8, 128, dtype=torch.float8_e4m3fn)
+    cu = torch.tensor([0, 8, 16, 24, 32, 40, 48], dtype=torch.int32)
+    lens = torch.full((6,), 100, dtype=torch.int32)
+    bt = torch.zeros(6, 8, dtype=torch.int32)
+    with pytest.raises(NotImplementedError, match=r"prefill over the paged FP8 cache.*max_seqlen_q=8 query tokens x 4"):
+        f(q=q, k=k, v=k, max_seqlen_q=8, cu_seqlens_q=cu, seqused_k=lens, block_table=bt, causal=True)
+    # group 8: two query tokens per sequence are the most the reader takes
+    with pytest.raises(NotImplementedError, match="up to 2 tokens per sequence"):
+        f(q=torch.zeros(18, 64, 128, dtype=torch.bfloat16), k=k, v=k, max_seqlen_q=3, cu_seqlens_q=cu[:7],
+          seqused_k=lens, block_table=bt, causal=True)
+
+
+def test_ragged_query_layout_check():
+    """check_cu_seqlens_q, the reader's opt-in validation of a ragged query
+    layout: each violation the reader would not survive is named."""
+    from pipeswift_amd.attention import check_cu_seqlens_q
+
+    ok = torch.tensor([0, 4, 5, 9], dtype=torch.int32)
+    check_cu_seqlens_q(ok, 9, 4)
+    check_cu_seqlens_q(ok, 12, 4)  # spare rows past the last sequence are allowed
+    check_cu_seqlens_q(torch.tensor([0], dtype=torch.int32), 0, 1)
+    with pytest.raises(AssertionError, match=r"sequence 2 has 5 query rows, more than max_seqlen_q = 4"):
+        check_cu_seqlens_q(torch.tensor([0, 4, 5, 10], dtype=torch.int32), 10, 4)
+    with pytest.raises(AssertionError, match=r"cu_seqlens_q\[-1\] = 9 exceeds the 8 query rows"):
+        check_cu_seqlens_q(ok, 8, 4)
+    with pytest.raises(AssertionError, match="decreases at sequence 1"):
+        check_cu_seqlens_q(torch.tensor([0, 4, 3, 6], dtype=torch.int32), 8, 4)
+    with pytest.raises(AssertionError, match=r"cu_seqlens_q\[0\] = 1"):
+        check_cu_seqlens_q(torch.tensor([1, 4], dtype=torch.int32), 8, 4)

@@ -31,11 +31,22 @@ def _gen(seed):
     return torch.Generator().manual_seed(seed)
 
 
+_SENTINEL_TILE = 64 << 20
+
+
 def sentinel(shape, dtype, seed) -> torch.Tensor:
-    """Seeded random bytes viewed as ``dtype``: pre-fill for whole-buffer compares."""
+    """Seeded random bytes viewed as ``dtype``: pre-fill for whole-buffer
+    compares, so that a stray store of any byte value shows.  Buffers over
+    64 MiB repeat one seeded 64 MiB tile, each repeat XORed with its index
+    (a 2 GiB cache in about a second instead of a quarter of a minute)."""
     nbytes = math.prod(shape) * torch.empty((), dtype=dtype).element_size()
-    b = torch.randint(0, 256, (nbytes,), generator=_gen(seed), dtype=torch.uint8)
-    return b.view(dtype).view(shape)
+    rng = np.random.default_rng(seed)
+    tile = rng.integers(0, 256, min(nbytes, _SENTINEL_TILE), dtype=np.uint8)
+    out = np.empty(nbytes, dtype=np.uint8)
+    for i, start in enumerate(range(0, nbytes, len(tile) or 1)):
+        n = min(len(tile), nbytes - start)
+        np.bitwise_xor(tile[:n], np.uint8(i & 0xFF), out=out[start:start + n])
+    return torch.from_numpy(out).view(dtype).view(shape)
 
 
 @dataclass
@@ -105,7 +116,7 @@ def config2_fp8_decode(seed=SEEDS["2"], batch=128, num_blocks=65536, block_size=
         tables.append(table)
         p = int(ctx[b]) - 1
         slots[b] = int(table[p // block_size]) * block_size + p % block_size
-    cache = torch.zeros((num_blocks, 2, block_size, heads, head_size), dtype=torch.uint8).view(torch.float8_e4m3fn)
+    cache = sentinel((num_blocks, 2, block_size, heads, head_size), torch.float8_e4m3fn, seed + 1)
     return AppendCase(qkv, q_size, heads, head_size, cache, slots, {"ctx": ctx, "tables": tables})
 
 
@@ -128,9 +139,7 @@ def prefill_append(seed=SEEDS["2"] + 100, num_tokens=32768, num_blocks=65536, bl
     t = torch.arange(num_tokens)
     slots = (perm[t // block_size] * block_size + t % block_size).to(torch.int64)
     dt = torch.float8_e4m3fn if fp8 else torch.bfloat16
-    cache = torch.zeros((num_blocks, 2, block_size, heads, head_size), dtype=torch.uint8 if fp8 else torch.bfloat16)
-    if fp8:
-        cache = cache.view(dt)
+    cache = sentinel((num_blocks, 2, block_size, heads, head_size), dt, seed + 1)
     return AppendCase(qkv, q_size, heads, head_size, cache, slots)
 
 
