@@ -98,8 +98,10 @@ def test_copy_engine_round_trip(dev, transport):
         assert np.array_equal(got[:, back], src[:, gpu_ids])
         untouched = np.setdiff1d(np.arange(P), back)
         assert not got[:, untouched].any()
-        with pytest.raises(AssertionError, match="out of range"):
+        with pytest.raises(AssertionError, match="not pages of the gpu tier"):
             eng.store([P], [0])
+        with pytest.raises(AssertionError, match="not pages of the l2 tier"):
+            eng.load([-1], [0])
         assert eng.load([], []).pending is False
     finally:
         eng.close()
