@@ -276,6 +276,74 @@ __global__ void __launch_bounds__(64 * WPB) paged_append_small_kernel(SmallAppen
   }
 }
 
+// Prefill-sized two-part rows whose second part is short (the MLA latent row:
+// kv_c 64 vectors + k_pe 8 vectors of 16 input bytes).  One wave per (token
+// chunk, part) would leave 7/8 of every k_pe wave's lanes idle while it pays
+// the whole wave's instructions, which for the quantizing append is the
+// dominant cost.  Here the lanes are packed over the flat (token, vector)
+// space of both parts -- vector j of token t is number t * V + j, the first
+// V0 from part 0 -- so every lane of every wave moves a vector.  Each lane
+// loads its U vectors, then its tokens' slots (a lane-varying load; lanes of
+// one token share the line), then stores.  Both parts write one cache (same
+// block and slot strides) with one scale, as the MLA entry passes them.
+template <class C, int V, int V0, int U>
+__global__ void __launch_bounds__(256) packed_row_scatter_kernel(ScatterGeom g, ScatterPart p0, ScatterPart p1) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const uint32_t wave = blockIdx.x * 4u + uint32_t(__builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave));
+  const uint32_t total = uint32_t(g.num_tokens) * uint32_t(V);
+  typename C::In v[U];
+  uint32_t tok[U];
+  int vec[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const uint32_t f = wave * uint32_t(kWave * U) + uint32_t(u * kWave + lane);
+    const uint32_t fc = f < total ? f : total - 1;  // lanes past the end re-read the last vector
+    tok[u] = fc / uint32_t(V);
+    vec[u] = f < total ? int(fc - tok[u] * uint32_t(V)) : -1;
+    const int j = int(fc - tok[u] * uint32_t(V));
+    const char* src = j < V0 ? p0.src + int64_t(tok[u]) * p0.src_stride + int64_t(j) * C::IN_B
+                             : p1.src + int64_t(tok[u]) * p1.src_stride + int64_t(j - V0) * C::IN_B;
+    v[u] = vload_nt<C::IN_B>(src);
+  }
+  int64_t slot[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) slot[u] = g.slots[tok[u]];
+  const QScale qs = make_qscale_uniform(p0.scale ? *p0.scale : 1.0f);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int j = vec[u];
+    if (j >= 0 && slot[u] >= 0 && slot[u] < g.num_slots) {
+      const int64_t s = slot[u];
+      char* row = p0.dst + (s >> g.bs_shift) * p0.blk_stride + (s & (g.block_size - 1)) * p0.page_stride;
+      const int64_t o = j < V0 ? int64_t(j) * C::OUT_B : p1.dst_off + int64_t(j - V0) * C::OUT_B;
+      vstore_nt<C::OUT_B>(row + o, C::apply(v[u], qs));
+    }
+  }
+}
+
+// The packed launch applies to the quantizing append of flat two-part rows of
+// 64 + 8 vectors into one cache with power-of-two pages and one scale, from
+// 1024 tokens up (decode-sized batches take paged_append_small_kernel).  One
+// vector per lane: config 4's FP8 prefill (4096 tokens) 3.20 us against 3.54
+// with one wave per (2 tokens, part), and 3.49 / 4.14 at two / four vectors
+// per lane.  The bf16 copy of the same rows stays on the per-part waves
+// (3.10 us against 3.68 packed), where no per-wave arithmetic is saved.
+template <class C>
+bool launch_packed_rows(const ScatterGeom& g, const ScatterPart& p0, const ScatterPart& p1, hipStream_t st,
+                        int* status) {
+  constexpr int U = 1;
+  if (C::OUT_B >= C::IN_B || g.nparts != 2 || g.bs_shift < 0 || g.num_tokens < 1024 || p0.seg_vecs != 64 ||
+      p1.seg_vecs != 8 || p0.dst != p1.dst || p0.dst_off != 0 || p0.blk_stride != p1.blk_stride ||
+      p0.page_stride != p1.page_stride || p0.scale != p1.scale ||
+      g.num_tokens > (int64_t(INT32_MAX) - 4 * kWave * U) / 72)
+    return false;
+  const int64_t waves = ceil_div(g.num_tokens * 72, kWave * U);
+  hipLaunchKernelGGL((packed_row_scatter_kernel<C, 72, 64, U>), dim3(ceil_div(waves, 4)), dim3(4 * kWave), 0, st,
+                     g, p0, p1);
+  *status = check_launch("packed_row_scatter_kernel launch");
+  return true;
+}
+
 bool part_flat(const ScatterPart& p, int out_b) { return p.nseg == 1 && p.inner_stride == out_b; }
 
 template <class C>
@@ -313,11 +381,14 @@ int launch_scatter(const ScatterGeom& g, const ScatterPart& p0, const ScatterPar
     return check_launch("paged_append_small_kernel launch");
   }
   if (sh.ch == 1) return launch_scatter_shape<C, 1, 1, true, 1>(g, p0, p1, sh.slice_shift, st);
-  // A quantizing append spends VALU time per element: twice the waves of
-  // two tokens each overlap it better (config 4's FP8 MLA prefill 3.71 us
-  // against 4.02 at four tokens and two vectors per lane, which stays best
-  // for the plain copies: bf16 MLA prefill 3.29 against 3.77).
-  if constexpr (C::OUT_B < C::IN_B) return launch_scatter_shape<C, 2, 1, true, 4>(g, p0, p1, 0, st);
+  int packed_status;
+  if (launch_packed_rows<C>(g, p0, p1, st, &packed_status)) return packed_status;
+  // A quantizing append gets one token per wave and one vector per lane (a row
+  // longer than 64 vectors loops): 32768 prefill tokens of config 2's geometry
+  // 38.6 us against 39.8 at two tokens per wave, 40.9 at two vectors per lane
+  // (a whole row in one pass), and 150.0 against 152.7 us at 131072 tokens.
+  // Four tokens and two vectors per lane stay best for the plain copies.
+  if constexpr (C::OUT_B < C::IN_B) return launch_scatter_shape<C, 1, 1, true, 4>(g, p0, p1, 0, st);
   return launch_scatter_shape<C, 4, 2, true, 4>(g, p0, p1, sh.slice_shift, st);
 }
 
