@@ -246,8 +246,14 @@ def setup_prefill_append(args, device, tokens=32768, fp8=True):
     qkv[0].copy_(case.qkv.to(device))
     a, c = _affine_block_maps(R, P, gen, device)
     base = case.slot_mapping.to(device)
-    slots = ((a.view(R, 1) * (base // ps).view(1, N) + c.view(R, 1)) % P) * ps + (base % ps).view(1, N)
-    slots[0].copy_(base)
+    if args.slots == "contiguous":
+        # every rotation set writes one run of consecutive slots (pages in
+        # order): the same kernel without the page scatter
+        start = (torch.arange(R, device=device) * N) % (P * ps - N + 1)
+        slots = start.view(R, 1) + torch.arange(N, device=device).view(1, N)
+    else:
+        slots = ((a.view(R, 1) * (base // ps).view(1, N) + c.view(R, 1)) % P) * ps + (base % ps).view(1, N)
+        slots[0].copy_(base)
     cache = case.cache.to(device)
     k_scale = v_scale = None
     if fp8:
@@ -284,6 +290,9 @@ def setup_prefill_append(args, device, tokens=32768, fp8=True):
         info["name"] += f"_q{q_size}"
     if bs != 16:
         info["name"] += f"_bs{bs}"
+    if args.slots == "contiguous":
+        info["name"] += "_contiguous"
+        info["config"]["slots"] = "one run of consecutive slots per rotation set"
     return launch, info
 
 
@@ -1786,6 +1795,9 @@ def main():
                         "row (-1: 4096, Llama-3-8B; 0: contiguous K/V rows)")
     p.add_argument("--tokens", type=int, default=0,
                    help="fp8_prefill_append / bf16_prefill_append: new tokens (0: 32768)")
+    p.add_argument("--slots", default="pages", choices=("pages", "contiguous"),
+                   help="*_prefill_append: 'pages' scatters the prompt's pages over the cache (the config); "
+                        "'contiguous' writes consecutive slots (the same kernel without the page scatter)")
     p.add_argument("--block-size", type=int, default=16,
                    help="chunked_append / gather / *_prefill_append: page size (16 is configs 2 and 3; "
                         "128 is config 3's sensitivity run)")
