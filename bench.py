@@ -464,7 +464,7 @@ def setup_mla(args, device, decode, fp8=False):
     from pipeswift_amd import cache_ops
     from pipeswift_amd.reshape_and_cache import reshape_and_cache_flash_diffkv
 
-    n = 128 if decode else 4096
+    n = args.tokens or (128 if decode else 4096)
     case = workloads.config4_mla(num_tokens=n, decode=decode)
     P, ps = case.cache.shape[0], case.cache.shape[1]
     R = args.rotate
@@ -496,7 +496,7 @@ def setup_mla(args, device, decode, fp8=False):
 
     nbytes = workloads.mla_bytes(n, 576, 2, 1 if fp8 else 2)
     kind = "decode" if decode else "prefill"
-    name = f"mla_{kind}" + ("_fp8" if fp8 else "")
+    name = f"mla_{kind}" + ("_fp8" if fp8 else "") + ("" if n == (128 if decode else 4096) else f"_{n}")
     host_scale = None if scale is None else float(scale.cpu())
     return launch, {
         "rotate": R,
@@ -1794,7 +1794,8 @@ def main():
                    help="fp8_prefill_append / bf16_prefill_append: query columns ahead of K and V in each qkv "
                         "row (-1: 4096, Llama-3-8B; 0: contiguous K/V rows)")
     p.add_argument("--tokens", type=int, default=0,
-                   help="fp8_prefill_append / bf16_prefill_append: new tokens (0: 32768)")
+                   help="fp8_prefill_append / bf16_prefill_append: new tokens (0: 32768); mla_*: tokens "
+                        "(0: config 4's 4096 prefill / 128 decode)")
     p.add_argument("--slots", default="pages", choices=("pages", "contiguous"),
                    help="*_prefill_append: 'pages' scatters the prompt's pages over the cache (the config); "
                         "'contiguous' writes consecutive slots (the same kernel without the page scatter)")

@@ -179,6 +179,45 @@ def paged_decode_attention(
     return (out, lse) if return_softmax_lse else out
 
 
+def _chunked_queries(cu_seqlens_q, total_q, seqused_k, block_table, chunk, causal, descales):
+    """Query tokens of each sequence cut into chunks of at most ``chunk``
+    consecutive tokens, each chunk a sequence of its own for the reader, built
+    on the device (no host synchronization).
+
+    Chunk j of sequence b covers its query tokens [j*chunk, i1), consecutive
+    rows of q, so q and the output keep their layout.  Its key length is the
+    sequence's length minus the sequence's tokens after the chunk when causal
+    (the reader's bottom-right alignment then shows each token the keys up to
+    its own position), else the whole sequence.  How many chunks there are
+    depends on the lengths, so the layout has a fixed bound of
+    ceil(total_q / chunk) + B chunk slots; slots past the last chunk have no
+    query rows and no keys.  Returns (cu_seqlens_q, seq_lens, block_table,
+    descales) of the chunk sequences."""
+    dev = cu_seqlens_q.device
+    B = seqused_k.shape[0]
+    cu = cu_seqlens_q.to(torch.int64)
+    n = cu[1:] - cu[:-1]
+    chunks = (n + chunk - 1) // chunk
+    ends = torch.cumsum(chunks, 0)
+    V = (total_q + chunk - 1) // chunk + B
+    v = torch.arange(V, device=dev)
+    b = torch.searchsorted(ends, v, right=True).clamp_(max=B - 1)
+    live = v < ends[-1]
+    j = v - (ends[b] - chunks[b])
+    i1 = torch.minimum((j + 1) * chunk, n[b])
+    cu2 = torch.empty(V + 1, dtype=torch.int32, device=dev)
+    cu2[:V] = torch.where(live, cu[b] + j * chunk, cu[-1]).to(torch.int32)
+    cu2[V] = cu[-1].to(torch.int32)
+    L = seqused_k.to(torch.int64)[b]
+    lens = (L - n[b] + i1) if causal else L
+    lens = torch.where(live, lens, torch.zeros_like(lens)).clamp_(min=0).to(torch.int32)
+    bt = block_table.index_select(0, b)
+    out = []
+    for d in descales:
+        out.append(d.index_select(0, b) if d is not None and d.dim() == 2 and d.numel() > 1 else d)
+    return cu2, lens, bt, out
+
+
 def flash_attn_varlen_func(
     q,
     k,
@@ -199,33 +238,42 @@ def flash_attn_varlen_func(
     num_splits=0,
 ):
     """The FA3 entry the reference's ``_fp8_paged_attn`` calls
-    (attention.py:166-184), for decode and speculative decode: q is
+    (attention.py:166-184) for decode, speculative decode and prefill: q is
     [total_q, Hq, D], sequence b's query tokens at rows
-    [cu_seqlens_q[b], cu_seqlens_q[b+1]), at most ``max_seqlen_q`` of them
-    (``max_seqlen_q * Hq / Hkv <= 16``), the sequence's last positions; with
-    ``causal`` each sees the keys up to its own position.  ``max_seqlen_k``
-    bounds the lengths when given, else the block table's width does.
-    ``num_splits`` is the flash-decoding split count (0: the balanced
-    schedule); ``fa_version`` is accepted for signature compatibility.
+    [cu_seqlens_q[b], cu_seqlens_q[b+1]), at most ``max_seqlen_q`` of them,
+    the sequence's last positions; with ``causal`` each sees the keys up to
+    its own position.  ``max_seqlen_k`` bounds the lengths when given, else
+    the block table's width does.  ``num_splits`` is the flash-decoding split
+    count (0: the balanced schedule); ``fa_version`` is accepted for signature
+    compatibility.
 
-    Prefill over the paged FP8 cache is not covered: a call whose
-    ``max_seqlen_q * Hq / Hkv`` exceeds 16 raises NotImplementedError before
-    touching the device (the reference routes prefill through the same entry,
-    attention.py:577-585)."""
-    group = q.shape[1] // k.shape[2] if k.shape[2] else 0
-    if int(max_seqlen_q) * max(group, 1) > MAX_ROWS:
-        raise NotImplementedError(
-            f"prefill over the paged FP8 cache is not implemented: max_seqlen_q={int(max_seqlen_q)} query tokens x "
-            f"{group} query heads per kv head exceed the {MAX_ROWS} rows of the decode reader, which covers decode "
-            f"and speculative decode up to {MAX_ROWS // max(group, 1)} tokens per sequence")
-    assert seqused_k is not None and block_table is not None, "paged decode needs seqused_k and block_table"
+    A sequence's query tokens and the query heads of a kv head share the 16
+    rows of one MFMA tile.  When ``max_seqlen_q * Hq / Hkv`` exceeds 16 (a
+    prefill or chunked-prefill step, which the reference routes through this
+    same entry, attention.py:577-585), each sequence's query tokens are cut
+    into chunks of 16 / (Hq / Hkv) tokens, each read as a sequence of its own
+    (``_chunked_queries``): exact, but every chunk streams its sequence's keys
+    again, so a prefill of n tokens over L keys reads about n / chunk times
+    the cache bytes a decode step reads.  More than 16 query heads per kv
+    head raise NotImplementedError."""
+    assert seqused_k is not None and block_table is not None, "paged attention needs seqused_k and block_table"
     B = seqused_k.shape[0]
     assert cu_seqlens_q is not None and cu_seqlens_q.shape[0] == B + 1
+    group = q.shape[1] // k.shape[2] if k.shape[2] else 0
+    if group > MAX_ROWS:
+        raise NotImplementedError(f"{group} query heads per kv head exceed the reader's {MAX_ROWS} rows")
     q_len = int(max_seqlen_q)
-    # B rows of at most one token each: one per sequence, cu_seqlens_q is 0..B
-    cu = None if q_len == 1 and q.shape[0] == B else cu_seqlens_q
     ps = k.shape[1]
     bound = block_table.shape[1] * ps if max_seqlen_k is None else min(int(max_seqlen_k), block_table.shape[1] * ps)
+    if q_len * max(group, 1) > MAX_ROWS:
+        chunk = MAX_ROWS // max(group, 1)
+        cu2, lens2, bt2, (qd, kd, vd) = _chunked_queries(cu_seqlens_q, q.shape[0], seqused_k, block_table, chunk,
+                                                         causal, (q_descale, k_descale, v_descale))
+        return paged_decode_attention(q, k, v, bt2, lens2, softmax_scale, qd, kd, vd, out=out,
+                                      return_softmax_lse=return_softmax_lse, max_seq_len=bound,
+                                      num_splits=num_splits, q_len=chunk, cu_seqlens_q=cu2, causal=causal)
+    # B rows of at most one token each: one per sequence, cu_seqlens_q is 0..B
+    cu = None if q_len == 1 and q.shape[0] == B else cu_seqlens_q
     return paged_decode_attention(q, k, v, block_table, seqused_k, softmax_scale, q_descale, k_descale, v_descale,
                                   out=out, return_softmax_lse=return_softmax_lse, max_seq_len=bound,
                                   num_splits=num_splits, q_len=q_len, cu_seqlens_q=cu, causal=causal)

@@ -299,8 +299,9 @@ def test_flash_attn_varlen_func_matches_direct_call(dev):
     assert torch.equal(a, b)
     with pytest.raises(AssertionError):  # no cu_seqlens_q
         attention.flash_attn_varlen_func(q, fd[:, 0], fd[:, 1], 2, None, seqused_k=lens, block_table=bt)
-    with pytest.raises(NotImplementedError, match="prefill"):  # 5 tokens x 4 heads: more than 16 rows per kv head
-        attention.flash_attn_varlen_func(q, fd[:, 0], fd[:, 1], 5, torch.arange(B + 1, dtype=torch.int32, device=dev),
+    with pytest.raises(NotImplementedError, match="query heads per kv head"):  # 32 heads over one kv head
+        attention.flash_attn_varlen_func(torch.zeros(B, 32, 128, dtype=torch.bfloat16, device=dev), fd[:, 0, :, :1],
+                                         fd[:, 1, :, :1], 1, torch.arange(B + 1, dtype=torch.int32, device=dev),
                                          seqused_k=lens, block_table=bt)
 
 

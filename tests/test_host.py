@@ -208,25 +208,51 @@ def test_shim_asserts_fire_before_device_calls():
         reshape_and_cache_flash_diffkv(k, k, torch.zeros(2, 16, 8, 100), torch.zeros(4, dtype=torch.int64))
 
 
-def test_fp8_reader_refuses_prefill_before_any_device_call():
-    """The FA3-style entry covers decode and speculative decode; a prefill-sized
-    call (the reference routes prefill through the same entry when
-    --enable_fp8_kv is on) raises NotImplementedError naming prefill, before
-    any device work (these are host tensors)."""
+def test_fp8_reader_refuses_more_than_16_heads_per_kv_head_before_any_device_call():
+    """The FA3-style entry covers decode, speculative decode and (in chunks)
+    prefill; a group of more than 16 query heads per kv head does not fit the
+    reader's 16 MFMA rows and raises NotImplementedError before any device
+    work (these are host tensors)."""
     from pipeswift_amd import fp8_kv
 
     f = fp8_kv.attn_varlen_func()
-    q = torch.zeros(6 * 8, 32, 128, dtype=torch.bfloat16)
-    k = torch.zeros(10, 16, 8, 128, dtype=torch.float8_e4m3fn)
-    cu = torch.tensor([0, 8, 16, 24, 32, 40, 48], dtype=torch.int32)
-    lens = torch.full((6,), 100, dtype=torch.int32)
-    bt = torch.zeros(6, 8, dtype=torch.int32)
-    with pytest.raises(NotImplementedError, match=r"prefill over the paged FP8 cache.*max_seqlen_q=8 query tokens x 4"):
-        f(q=q, k=k, v=k, max_seqlen_q=8, cu_seqlens_q=cu, seqused_k=lens, block_table=bt, causal=True)
-    # group 8: two query tokens per sequence are the most the reader takes
-    with pytest.raises(NotImplementedError, match="up to 2 tokens per sequence"):
-        f(q=torch.zeros(18, 64, 128, dtype=torch.bfloat16), k=k, v=k, max_seqlen_q=3, cu_seqlens_q=cu[:7],
-          seqused_k=lens, block_table=bt, causal=True)
+    k = torch.zeros(10, 16, 2, 128, dtype=torch.float8_e4m3fn)
+    cu = torch.tensor([0, 8, 16], dtype=torch.int32)
+    with pytest.raises(NotImplementedError, match="32 query heads per kv head exceed the reader's 16 rows"):
+        f(q=torch.zeros(16, 64, 128, dtype=torch.bfloat16), k=k, v=k, max_seqlen_q=8, cu_seqlens_q=cu,
+          seqused_k=torch.full((2,), 100, dtype=torch.int32), block_table=torch.zeros(2, 8, dtype=torch.int32),
+          causal=True)
+
+
+def test_chunked_prefill_layout():
+    """The chunk sequences a prefill is read as (attention._chunked_queries), on
+    the host: rows, causal key lengths and table rows of every chunk, against a
+    direct enumeration."""
+    from pipeswift_amd.attention import _chunked_queries
+
+    counts = [5, 0, 1, 9, 4]
+    lens = [5 + 30, 3, 1 + 7, 9, 4 + 100]
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(counts)]), dtype=torch.int32)
+    bt = torch.arange(5 * 3, dtype=torch.int32).view(5, 3)
+    ds = torch.arange(10, dtype=torch.float32).view(5, 2)
+    for causal in (True, False):
+        cu2, lens2, bt2, (qd, kd, vd) = _chunked_queries(cu, 21, torch.tensor(lens, dtype=torch.int32), bt, 4,
+                                                           causal, (ds, None, ds[:1, :1]))
+        exp_rows, exp_lens, exp_b = [], [], []
+        for b, (n, L) in enumerate(zip(counts, lens)):
+            for i0 in range(0, n, 4):
+                i1 = min(i0 + 4, n)
+                exp_rows.append((int(cu[b]) + i0, int(cu[b]) + i1))
+                exp_lens.append(L - n + i1 if causal else L)
+                exp_b.append(b)
+        V = (21 + 3) // 4 + 5
+        assert cu2.shape[0] == V + 1 and lens2.shape[0] == V and bt2.shape[0] == V
+        k = len(exp_rows)
+        assert [(int(cu2[i]), int(cu2[i + 1])) for i in range(k)] == exp_rows
+        assert all(int(cu2[i]) == int(cu2[i + 1]) == 19 for i in range(k, V))  # empty slots at the end
+        assert lens2[:k].tolist() == exp_lens and not lens2[k:].any()
+        assert torch.equal(bt2[:k], bt[exp_b]) and torch.equal(qd[:k], ds[exp_b])
+        assert kd is None and vd.shape == (1, 1)
 
 
 def test_ragged_query_layout_check():
