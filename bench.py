@@ -62,6 +62,8 @@ carries:
 Other workloads (--workload NAME runs one alone): any name above, and
   mla_fp8_tiles_prefill / mla_fp8_tiles_decode   config 4 into 656-byte FP8
                      entries with one scale per 128-element tile
+  prefill_attention  a chunked-prefill step of FP8 paged attention (config 3
+                     geometry: 4096 query tokens, prefixes 0-60k)
   attention_shapes   decode attention on several batch shapes, balanced vs split
   l2_cycle           BlockManager store -> evict -> restore of an 8192-page prompt
                      (the default run includes a 2048-page cycle)
@@ -359,6 +361,58 @@ def setup_decode_attention(args, device, q_len=1):
     return launch, info
 
 
+def setup_prefill_attention(args, device):
+    """A chunked-prefill step of attention over an FP8 paged cache, in config
+    3's geometry: 4096 new query tokens over 6 sequences with page-aligned
+    prefixes of 0-60k cached tokens, 32 query heads over 4 kv heads (16 / 8 = 2
+    query tokens per chunk), random FP8 pages, causal, per-tensor descales,
+    through ``flash_attn_varlen_func`` as the reference's ``_fp8_paged_attn``
+    calls it for prefill.  Algorithmic bytes: every sequence's K and V rows
+    once, the page ids, the bf16 queries and outputs; the chunked reader
+    streams each sequence's keys once per chunk, so its effective rate is
+    reported against those bytes."""
+    import torch
+
+    import workloads
+    from pipeswift_amd import attention
+
+    cc = workloads.config3_chunked()
+    H, D, Hq, ps = 4, 128, 32, 16
+    P = cc.append.cache.shape[0]
+    dgen = torch.Generator(device=device).manual_seed(76)
+    cache = (torch.randn((P, 2, ps, H, D), device=device, generator=dgen) * 2.0).to(torch.float8_e4m3fn)
+    kc, vc = cache[:, 0], cache[:, 1]
+    bt = cc.block_table.to(device)
+    chunk = cc.chunk
+    N = int(chunk.sum())
+    cu = torch.zeros(len(chunk) + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(chunk, 0).to(torch.int32)
+    cu = cu.to(device)
+    lens = (cc.prefix + cc.chunk).to(torch.int32).to(device)
+    R = min(args.rotate, 4)
+    q = (torch.randn(R, N, Hq, D, device=device, generator=dgen) * 2.0).to(torch.bfloat16)
+    scales = torch.tensor([0.01, 0.02], dtype=torch.float32, device=device)
+    out = torch.empty(N, Hq, D, dtype=torch.bfloat16, device=device)
+    maxq = int(chunk.max())
+
+    def launch(i):
+        attention.flash_attn_varlen_func(q[i], kc, vc, maxq, cu, seqused_k=lens, block_table=bt,
+                                         softmax_scale=D ** -0.5, causal=True, k_descale=scales[0:1],
+                                         v_descale=scales[1:2], out=out)
+
+    total = int(lens.sum())
+    pages = int(((cc.prefix + cc.chunk + ps - 1) // ps).sum())
+    nbytes = total * H * D * 2 + pages * 4 + 2 * N * Hq * D * 2
+    return launch, {
+        "name": "prefill_attention", "kernel": "decode_partial_ring_kernel + decode_combine_kernel",
+        "bytes": nbytes, "tokens": N, "dtype": "fp8_e4m3fn", "rotate": R,
+        "config": {"workload": "chunked-prefill attention over an FP8 paged cache (config 3 geometry)",
+                   "query_tokens": N, "context_tokens": total, "q_heads": Hq, "kv_heads": H, "head_dim": D,
+                   "block_size": ps, "chunk_tokens": 16 // (Hq // H)},
+        "cpu": None,
+    }
+
+
 def setup_kv_scales(args, device):
     """Per-tensor FP8 scales of config 2's K and V (amax / 448), one launch."""
     import torch
@@ -501,7 +555,8 @@ def setup_mla(args, device, decode, fp8=False):
     return launch, {
         "rotate": R,
         "name": name,
-        "kernel": "paged_append_small_kernel" if decode else "paged_scatter_kernel", "bytes": nbytes,
+        "kernel": ("paged_append_small_kernel" if n < 1024 else
+                   "packed_row_scatter_kernel" if fp8 else "paged_scatter_kernel"), "bytes": nbytes,
         "tokens": n, "dtype": "fp8_e4m3fn" if fp8 else "bf16",
         "config": {"workload": f"MLA latent append, {kind}" + (", per-tensor FP8" if fp8 else "") + " (config 4)",
                    "tokens": n, "row": 576, "block_size": ps, "num_blocks": P,
@@ -1640,6 +1695,7 @@ SETUPS = {
     "kv_scales": setup_kv_scales,
     "decode_attention": setup_decode_attention,
     "decode_attention_q4": lambda a, d: setup_decode_attention(a, d, q_len=4),
+    "prefill_attention": setup_prefill_attention,
     "fp8_prefill_append": lambda a, d: setup_prefill_append(a, d, tokens=a.tokens or 32768, fp8=True),
     "bf16_prefill_append": lambda a, d: setup_prefill_append(a, d, tokens=a.tokens or 32768, fp8=False),
     "chunked_append": lambda a, d: setup_chunked(a, d, gather=False),

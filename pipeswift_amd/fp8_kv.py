@@ -56,10 +56,10 @@ def check_available() -> None:
     """Fail at startup rather than in the first forward pass (fp8_kv.py:64-71):
     the FP8 reader and append need a gfx950 GPU and this package's library.
 
-    The reader covers decode and speculative decode (``max_seqlen_q`` times
-    the query heads per kv head at most 16); a prefill forward over the FP8
-    cache raises NotImplementedError from ``attn_varlen_func()``'s function,
-    so an engine that prefills through it must keep --enable_fp8_kv off."""
+    The reader covers decode, speculative decode and prefill (prefill reads
+    each sequence's query tokens in chunks of 16 / G tokens, G query heads
+    per kv head, each chunk streaming the sequence's keys again); groups of
+    more than 16 query heads per kv head raise NotImplementedError."""
     assert torch.cuda.is_available(), "--enable_fp8_kv needs a GPU"
     arch = getattr(torch.cuda.get_device_properties(torch.cuda.current_device()), "gcnArchName", "")
     assert arch.startswith("gfx950"), f"--enable_fp8_kv on this build needs gfx950 (MI355X), got {arch or 'unknown'}"
@@ -71,8 +71,8 @@ def check_available() -> None:
 
 def attn_varlen_func():
     """The FA3-style varlen entry point for the FP8 cache (fp8_kv.py:44-62):
-    this package's paged reader, same keywords, for decode and speculative
-    decode (prefill-sized calls raise NotImplementedError)."""
+    this package's paged reader, same keywords, for decode, speculative
+    decode and prefill."""
     from .attention import flash_attn_varlen_func
 
     return flash_attn_varlen_func
