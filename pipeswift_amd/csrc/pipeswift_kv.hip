@@ -286,8 +286,15 @@ __global__ void __launch_bounds__(64 * WPB) paged_append_small_kernel(SmallAppen
 // loads its U vectors, then its tokens' slots (a lane-varying load; lanes of
 // one token share the line), then stores.  Both parts write one cache (same
 // block and slot strides) with one scale, as the MLA entry passes them.
-template <class C, int V, int V0, int U>
+// a * b for a, b < 2^24, product taken modulo 2^32 (v_mul_u32_u24: full rate)
+__device__ __forceinline__ uint32_t mul24(uint32_t a, uint32_t b) { return uint32_t(__umul24(a, b)); }
+
+template <class C, int V, int V0, int U, bool NARROW>
 __global__ void __launch_bounds__(256) packed_row_scatter_kernel(ScatterGeom g, ScatterPart p0, ScatterPart p1) {
+  // NARROW: every input part and the cache span less than 4 GiB and every
+  // stride, token index and block count fits 24 bits (checked on the host),
+  // so offsets are 32-bit and come from full-rate 24-bit multiply-adds instead
+  // of the quarter-rate 64-bit products, a third of the kernel's VALU time.
   const int lane = threadIdx.x & (kWave - 1);
   const uint32_t wave = blockIdx.x * 4u + uint32_t(__builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave));
   const uint32_t total = uint32_t(g.num_tokens) * uint32_t(V);
@@ -299,10 +306,17 @@ __global__ void __launch_bounds__(256) packed_row_scatter_kernel(ScatterGeom g, 
     const uint32_t f = wave * uint32_t(kWave * U) + uint32_t(u * kWave + lane);
     const uint32_t fc = f < total ? f : total - 1;  // lanes past the end re-read the last vector
     tok[u] = fc / uint32_t(V);
-    vec[u] = f < total ? int(fc - tok[u] * uint32_t(V)) : -1;
     const int j = int(fc - tok[u] * uint32_t(V));
-    const char* src = j < V0 ? p0.src + int64_t(tok[u]) * p0.src_stride + int64_t(j) * C::IN_B
-                             : p1.src + int64_t(tok[u]) * p1.src_stride + int64_t(j - V0) * C::IN_B;
+    vec[u] = f < total ? j : -1;
+    const bool first = j < V0;
+    const char* src;
+    if constexpr (NARROW) {
+      const uint32_t stride = uint32_t(first ? p0.src_stride : p1.src_stride);
+      src = (first ? p0.src : p1.src) + (mul24(tok[u], stride) + uint32_t(first ? j : j - V0) * C::IN_B);
+    } else {
+      src = first ? p0.src + int64_t(tok[u]) * p0.src_stride + int64_t(j) * C::IN_B
+                  : p1.src + int64_t(tok[u]) * p1.src_stride + int64_t(j - V0) * C::IN_B;
+    }
     v[u] = vload_nt<C::IN_B>(src);
   }
   int64_t slot[U];
@@ -312,11 +326,19 @@ __global__ void __launch_bounds__(256) packed_row_scatter_kernel(ScatterGeom g, 
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int j = vec[u];
-    if (j >= 0 && slot[u] >= 0 && slot[u] < g.num_slots) {
-      const int64_t s = slot[u];
-      char* row = p0.dst + (s >> g.bs_shift) * p0.blk_stride + (s & (g.block_size - 1)) * p0.page_stride;
-      const int64_t o = j < V0 ? int64_t(j) * C::OUT_B : p1.dst_off + int64_t(j - V0) * C::OUT_B;
-      vstore_nt<C::OUT_B>(row + o, C::apply(v[u], qs));
+    if (j >= 0 && uint64_t(slot[u]) < uint64_t(g.num_slots)) {
+      char* dst;
+      if constexpr (NARROW) {
+        const uint32_t s32 = uint32_t(slot[u]);
+        const uint32_t o = j < V0 ? uint32_t(j) * C::OUT_B : uint32_t(p1.dst_off) + uint32_t(j - V0) * C::OUT_B;
+        dst = p0.dst + (mul24(s32 >> g.bs_shift, uint32_t(p0.blk_stride)) +
+                        mul24(s32 & uint32_t(g.block_size - 1), uint32_t(p0.page_stride)) + o);
+      } else {
+        const int64_t sl = slot[u];
+        const int64_t o = j < V0 ? int64_t(j) * C::OUT_B : p1.dst_off + int64_t(j - V0) * C::OUT_B;
+        dst = p0.dst + (sl >> g.bs_shift) * p0.blk_stride + (sl & (g.block_size - 1)) * p0.page_stride + o;
+      }
+      vstore_nt<C::OUT_B>(dst, C::apply(v[u], qs));
     }
   }
 }
@@ -338,8 +360,23 @@ bool launch_packed_rows(const ScatterGeom& g, const ScatterPart& p0, const Scatt
       g.num_tokens > (int64_t(INT32_MAX) - 4 * kWave * U) / 72)
     return false;
   const int64_t waves = ceil_div(g.num_tokens * 72, kWave * U);
-  hipLaunchKernelGGL((packed_row_scatter_kernel<C, 72, 64, U>), dim3(ceil_div(waves, 4)), dim3(4 * kWave), 0, st,
-                     g, p0, p1);
+  // 32-bit offsets when every span fits (see the kernel)
+  constexpr int64_t k24 = int64_t(1) << 24, k32 = int64_t(1) << 32;
+  const int64_t num_blocks = g.num_slots >> g.bs_shift;
+  const int64_t row_in = int64_t(p0.seg_vecs) * C::IN_B, row_k = int64_t(p1.seg_vecs) * C::IN_B;
+  const int64_t cache_span = (num_blocks - 1) * p0.blk_stride + (g.block_size - 1) * p0.page_stride +
+                             p1.dst_off + int64_t(p1.seg_vecs) * C::OUT_B;
+  const bool narrow = g.num_tokens <= k24 && g.num_slots < (int64_t(1) << 31) && num_blocks < k24 &&
+                      g.block_size < k24 && p0.blk_stride >= 0 && p0.blk_stride < k24 && p0.page_stride >= 0 && p0.page_stride < k24 &&
+                      p0.src_stride >= 0 && p0.src_stride < k24 && p1.src_stride >= 0 && p1.src_stride < k24 &&
+                      (g.num_tokens - 1) * p0.src_stride + row_in < k32 &&
+                      (g.num_tokens - 1) * p1.src_stride + row_k < k32 && cache_span < k32 && p1.dst_off < k24;
+  if (narrow)
+    hipLaunchKernelGGL((packed_row_scatter_kernel<C, 72, 64, U, true>), dim3(ceil_div(waves, 4)), dim3(4 * kWave), 0,
+                       st, g, p0, p1);
+  else
+    hipLaunchKernelGGL((packed_row_scatter_kernel<C, 72, 64, U, false>), dim3(ceil_div(waves, 4)), dim3(4 * kWave), 0,
+                       st, g, p0, p1);
   *status = check_launch("packed_row_scatter_kernel launch");
   return true;
 }

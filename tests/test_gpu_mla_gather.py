@@ -63,6 +63,31 @@ def test_mla_prefill_sized_append(dev, fp8):
     assert np.array_equal(got, exp)
 
 
+def test_mla_fp8_append_wide_block_stride(dev):
+    """Pages 16 MiB + 4 KiB apart: a block stride past 24 bits, so the packed
+    FP8 append takes its 64-bit offset path (the narrow one needs every stride
+    below 2^24 bytes); 1280 tokens, every slot of the 20 pages."""
+    g = torch.Generator().manual_seed(35)
+    P, ps, n = 20, 64, 1280
+    pitch = (1 << 24) + 4096
+    latent = torch.randn(n, 1536 + 576, generator=g).to(torch.bfloat16)
+    ckv = torch.randn(n, 512, generator=g).to(torch.bfloat16)
+    slots = torch.randperm(P * ps, generator=g).to(torch.int64)
+    slots[::17] = -1
+    base = torch.zeros(P, pitch, dtype=torch.uint8, device=dev)
+    cache = base[:, : ps * 576].view(P, ps, 1, 576).view(torch.float8_e4m3fn)
+    assert cache.stride(0) == pitch
+    print(f"mla fp8 wide stride: N={n} pitch={pitch}", flush=True)
+    ld = latent.to(dev)
+    sc = torch.tensor([0.0371], dtype=torch.float32, device=dev)
+    reshape_and_cache_flash_diffkv(ckv.to(dev).unsqueeze(1), ld[:, 2048:].unsqueeze(1), cache, slots.to(dev), sc)
+    exp = np.zeros((P, ps, 576), np.uint8)
+    O.concat_and_cache_mla(raw(ckv), raw(latent[:, 2048:]), exp, slots.numpy(), "bf16", "fp8", 0.0371)
+    got = base.cpu().numpy()
+    assert np.array_equal(got[:, : ps * 576].reshape(P, ps, 576), exp)
+    assert not got[:, ps * 576 :].any()
+
+
 def test_mla_through_append_mla_kv_cache(dev):
     L, P, ps = 2, 300, 64
     mla = workloads.sentinel((L, P, ps, 576), torch.bfloat16, 31)
