@@ -38,6 +38,8 @@
  *   psk_paged_decode_attention  decode over the FP8 cache; the reference calls
  *                             vLLM's FA3 flash_attn_varlen_func for it
  *                             (pipeswift/llms/layers/attention.py:148-187)
+ *   psk_paged_prefill_attention  prefill over the FP8 cache, through the same
+ *                             FA3 entry (attention.py:166-184, 577-585)
  *   psk_concat_and_cache_mla_fp8_tiles,  the FP8 MLA entry with per-128-element
  *   psk_gather_mla_fp8_tiles  tile scales that the reference's MLA reader would
  *                             need; it rejects FP8 MLA for lack of it
@@ -349,6 +351,39 @@ int psk_paged_decode_attention(const void* q, int64_t q_tok_stride, int64_t q_he
 
 int64_t psk_paged_decode_workspace_len(int64_t num_seqs, int64_t q_len, int64_t num_q_heads,
                                        int64_t num_kv_heads, int64_t max_seq_len, int64_t num_splits);
+
+/*
+ * Paged prefill attention over an FP8 E4M3FN KV cache: what
+ * psk_paged_decode_attention computes (same q~, s_j, out, lse, descales,
+ * causal rule, page addressing and zero rows for missing pages), for any
+ * number of query tokens per sequence -- the prefill and chunked-prefill steps
+ * the reference sends through the same FA3 entry
+ * (pipeswift/llms/layers/attention.py:166-184, called for prefill at
+ * :577-585).  Sequence b has n_b = min(max_seqlen_q, cu_seqlens_q[b+1] -
+ * cu_seqlens_q[b]) query tokens at rows [cu_seqlens_q[b], ...) of q and out
+ * (cu_seqlens_q NULL: max_seqlen_q rows each, total_q = num_seqs *
+ * max_seqlen_q); total_q is the rows of q and bounds cu_seqlens_q[num_seqs].
+ * num_q_heads / num_kv_heads is at most 256.  Each workgroup reads its keys
+ * once for 256 / (num_q_heads / num_kv_heads) query tokens of one kv head.
+ * out rows (bf16 or f32) need 4-element alignment.  workspace: device int32,
+ * at least psk_paged_prefill_workspace_len(num_seqs) words, no initial
+ * contents needed.  Two launches.
+ */
+int psk_paged_prefill_attention(const void* q, int64_t q_tok_stride, int64_t q_head_stride, int q_dtype,
+                                const void* k_cache, const void* v_cache, const int64_t* k_strides,
+                                const int64_t* v_strides, const int32_t* block_table,
+                                int64_t block_table_stride, int64_t block_table_width,
+                                const int32_t* seq_lens, int64_t num_seqs, int64_t num_q_heads,
+                                int64_t num_kv_heads, int64_t head_size, int64_t block_size,
+                                int64_t num_blocks, int64_t total_q, int64_t max_seqlen_q,
+                                const int32_t* cu_seqlens_q, int causal, float softmax_scale,
+                                const float* q_descale, const float* k_descale,
+                                const float* v_descale, const int64_t* descale_strides, void* out,
+                                int64_t out_tok_stride, int64_t out_head_stride, int out_dtype,
+                                float* lse, int64_t lse_head_stride, int32_t* workspace,
+                                int64_t workspace_len, void* stream);
+
+int64_t psk_paged_prefill_workspace_len(int64_t num_seqs);
 
 /*
  * FP8 MLA latent entries with one scale per 128-element tile (build-defined;

@@ -93,6 +93,13 @@ _SIGNATURES = {
          _i64, _vp, _i64, _vp],
     ),
     "psk_paged_decode_workspace_len": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64]),
+    "psk_paged_prefill_attention": (
+        _int,
+        [_vp, _i64, _i64, _int, _vp, _vp, _c_int64_p, _c_int64_p, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64,
+         _i64, _i64, _i64, _vp, _int, ctypes.c_float, _vp, _vp, _vp, _c_int64_p, _vp, _i64, _i64, _int, _vp, _i64,
+         _vp, _i64, _vp],
+    ),
+    "psk_paged_prefill_workspace_len": (_i64, [_i64]),
     "psk_mla_fp8_tile_entry_bytes": (_i64, [_i64, _i64]),
     "psk_concat_and_cache_mla_fp8_tiles": (
         _int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp],

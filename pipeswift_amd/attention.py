@@ -17,9 +17,11 @@ kv head) -- for instance the per-tensor
 scales ``cache_ops.compute_kv_scales`` gave the append.
 
 The query tokens of a sequence and the query heads of a kv head share the
-16 rows of one MFMA tile: ``max_seqlen_q * Hq / Hkv`` must be at most 16
-(e.g. 4 draft positions at 4 heads per kv head).  Prefill over the paged
-cache is not covered.
+16 rows of one MFMA tile of the decode reader: ``max_seqlen_q * Hq / Hkv`` at
+most 16 (e.g. 4 draft positions at 4 heads per kv head).  Larger steps --
+prefill and chunked prefill, which the reference sends through the same entry
+-- run ``psk_paged_prefill_attention`` (``paged_prefill_attention``): the same
+arithmetic, with each kv head's keys read once per 256 query rows.
 """
 
 from __future__ import annotations
@@ -179,6 +181,91 @@ def paged_decode_attention(
     return (out, lse) if return_softmax_lse else out
 
 
+def prefill_workspace_words(num_seqs: int) -> int:
+    n = int(lib().psk_paged_prefill_workspace_len(num_seqs))
+    if n < 0:
+        check(n, "paged prefill workspace")
+    return n
+
+
+def paged_prefill_attention(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    cu_seqlens_q: Optional[torch.Tensor],
+    max_seqlen_q: int,
+    softmax_scale: Optional[float] = None,
+    q_descale: Optional[torch.Tensor] = None,
+    k_descale: Optional[torch.Tensor] = None,
+    v_descale: Optional[torch.Tensor] = None,
+    out: Optional[torch.Tensor] = None,
+    return_softmax_lse: bool = False,
+    causal: bool = True,
+    workspace: Optional[torch.Tensor] = None,
+    validate: bool = False,
+):
+    """Attention of a prefill (or chunked-prefill) step over the paged FP8
+    cache: ``paged_decode_attention``'s arguments and results (q~, scores,
+    descales, FA's bottom-right causal rule, zero rows for missing pages, bf16
+    or float32 ``out``, lse [Hq, total_q]) for any number of query tokens per
+    sequence, at most ``max_seqlen_q`` each, and up to 256 query heads per kv
+    head.  One workgroup per (kv head, block of 256 / (Hq / Hkv) query tokens
+    of one sequence) streams the sequence's keys once for the whole block
+    through LDS; Q K^T and P V run on the bf16 MFMA over exactly converted FP8
+    values, P in bf16 hi + lo parts, fp32 sums.  ``workspace``: int32 of at
+    least ``prefill_workspace_words(B)`` (allocated when absent).  The ragged
+    layout contract, and ``validate``, are ``paged_decode_attention``'s."""
+    assert q.is_cuda and k_cache.is_cuda and v_cache.is_cuda
+    assert q.dim() == 3 and q.shape[2] == HEAD_DIM and q.stride(2) == 1, "q must be [T, Hq, 128] with unit last stride"
+    assert k_cache.dtype == torch.float8_e4m3fn and v_cache.dtype == torch.float8_e4m3fn, "the cache must be fp8 e4m3fn"
+    assert k_cache.dim() == 4 and k_cache.shape == v_cache.shape and k_cache.shape[3] == HEAD_DIM
+    assert k_cache.stride(3) == 1 and v_cache.stride(3) == 1
+    TQ, Hq, _ = q.shape
+    P, ps, Hkv, _ = k_cache.shape
+    q_len = int(max_seqlen_q)
+    assert q_len >= 1
+    if cu_seqlens_q is None:
+        assert TQ % q_len == 0, f"{TQ} query rows are not {q_len} per sequence"
+        B = TQ // q_len
+    else:
+        assert cu_seqlens_q.dtype == torch.int32 and cu_seqlens_q.is_contiguous() and cu_seqlens_q.dim() == 1
+        assert cu_seqlens_q.device == q.device
+        B = cu_seqlens_q.shape[0] - 1
+        if (validate or _CHECK_ARGS) and not torch.cuda.is_current_stream_capturing():
+            check_cu_seqlens_q(cu_seqlens_q, TQ, q_len)
+    assert Hkv > 0 and Hq % Hkv == 0, f"{Hq} query heads over {Hkv} kv heads"
+    assert block_table.dtype == torch.int32 and block_table.dim() == 2 and block_table.stride(1) == 1
+    assert block_table.shape[0] >= B
+    assert seq_lens.dtype == torch.int32 and seq_lens.is_contiguous() and seq_lens.numel() >= B
+    device = q.device
+    if softmax_scale is None:
+        softmax_scale = HEAD_DIM ** -0.5
+    if out is None:
+        out = torch.empty(TQ, Hq, HEAD_DIM, dtype=torch.bfloat16, device=device)
+    assert out.dtype in _OUT_CODES and out.shape == (TQ, Hq, HEAD_DIM) and out.stride(2) == 1
+    lse = torch.empty(Hq, TQ, dtype=torch.float32, device=device) if return_softmax_lse else None
+    need = prefill_workspace_words(B)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.int32, device=device)
+    assert workspace.dtype == torch.int32 and workspace.device == device
+    qd, qsb, qsh = _descale(q_descale, B, Hkv, device)
+    kd, ksb, ksh = _descale(k_descale, B, Hkv, device)
+    vd, vsb, vsh = _descale(v_descale, B, Hkv, device)
+    st = lib().psk_paged_prefill_attention(
+        q.data_ptr(), q.stride(0), q.stride(1), dtype_code(q.dtype),
+        k_cache.data_ptr(), v_cache.data_ptr(), i64_array(k_cache.stride()[:3]), i64_array(v_cache.stride()[:3]),
+        block_table.data_ptr(), block_table.stride(0), block_table.shape[1], seq_lens.data_ptr(), B, Hq, Hkv,
+        HEAD_DIM, ps, P, TQ, q_len, ptr(cu_seqlens_q), 1 if causal else 0, float(softmax_scale),
+        ptr(qd), ptr(kd), ptr(vd), i64_array([qsb, qsh, ksb, ksh, vsb, vsh]), out.data_ptr(), out.stride(0),
+        out.stride(1), _OUT_CODES[out.dtype], ptr(lse), TQ if lse is not None else 0, workspace.data_ptr(),
+        workspace.numel(), stream_handle(device),
+    )
+    check(st, "paged_prefill_attention")
+    return (out, lse) if return_softmax_lse else out
+
+
 def _chunked_queries(cu_seqlens_q, total_q, seqused_k, block_table, chunk, causal, descales):
     """Query tokens of each sequence cut into chunks of at most ``chunk``
     consecutive tokens, each chunk a sequence of its own for the reader, built
@@ -218,6 +305,26 @@ def _chunked_queries(cu_seqlens_q, total_q, seqused_k, block_table, chunk, causa
     return cu2, lens, bt, out
 
 
+def chunked_prefill_attention(q, k, v, max_seqlen_q, cu_seqlens_q, seqused_k, block_table, softmax_scale=None,
+                              causal=False, q_descale=None, k_descale=None, v_descale=None,
+                              return_softmax_lse=False, out=None, num_splits=0):
+    """A prefill step read by the decode reader instead of the prefill kernel:
+    each sequence's query tokens cut into chunks of 16 / (Hq / Hkv) tokens,
+    each read as a sequence of its own (``_chunked_queries``).  Exact, but
+    every chunk streams its sequence's keys again, so a prefill of n tokens
+    over L keys reads about n / chunk times the cache bytes of one pass; kept
+    as an independent second path for cross-checks and as the prefill
+    kernel's measured baseline.  At most 16 query heads per kv head."""
+    group = q.shape[1] // k.shape[2]
+    assert 1 <= group <= MAX_ROWS, f"{group} query heads per kv head: the decode reader takes at most {MAX_ROWS}"
+    chunk = MAX_ROWS // group
+    cu2, lens2, bt2, (qd, kd, vd) = _chunked_queries(cu_seqlens_q, q.shape[0], seqused_k, block_table, chunk,
+                                                     causal, (q_descale, k_descale, v_descale))
+    return paged_decode_attention(q, k, v, bt2, lens2, softmax_scale, qd, kd, vd, out=out,
+                                  return_softmax_lse=return_softmax_lse, max_seq_len=block_table.shape[1] * k.shape[1],
+                                  num_splits=num_splits, q_len=chunk, cu_seqlens_q=cu2, causal=causal)
+
+
 def flash_attn_varlen_func(
     q,
     k,
@@ -248,30 +355,23 @@ def flash_attn_varlen_func(
     compatibility.
 
     A sequence's query tokens and the query heads of a kv head share the 16
-    rows of one MFMA tile.  When ``max_seqlen_q * Hq / Hkv`` exceeds 16 (a
-    prefill or chunked-prefill step, which the reference routes through this
-    same entry, attention.py:577-585), each sequence's query tokens are cut
-    into chunks of 16 / (Hq / Hkv) tokens, each read as a sequence of its own
-    (``_chunked_queries``): exact, but every chunk streams its sequence's keys
-    again, so a prefill of n tokens over L keys reads about n / chunk times
-    the cache bytes a decode step reads.  More than 16 query heads per kv
-    head raise NotImplementedError."""
+    rows of one MFMA tile of the decode reader.  When ``max_seqlen_q * Hq /
+    Hkv`` exceeds 16 (a prefill or chunked-prefill step, which the reference
+    routes through this same entry, attention.py:577-585, or more than 16
+    query heads per kv head) the step runs ``paged_prefill_attention``, which
+    reads each kv head's keys once per block of 256 query rows; ``num_splits``
+    and ``max_seqlen_k`` do not apply there."""
     assert seqused_k is not None and block_table is not None, "paged attention needs seqused_k and block_table"
     B = seqused_k.shape[0]
     assert cu_seqlens_q is not None and cu_seqlens_q.shape[0] == B + 1
     group = q.shape[1] // k.shape[2] if k.shape[2] else 0
-    if group > MAX_ROWS:
-        raise NotImplementedError(f"{group} query heads per kv head exceed the reader's {MAX_ROWS} rows")
     q_len = int(max_seqlen_q)
     ps = k.shape[1]
     bound = block_table.shape[1] * ps if max_seqlen_k is None else min(int(max_seqlen_k), block_table.shape[1] * ps)
     if q_len * max(group, 1) > MAX_ROWS:
-        chunk = MAX_ROWS // max(group, 1)
-        cu2, lens2, bt2, (qd, kd, vd) = _chunked_queries(cu_seqlens_q, q.shape[0], seqused_k, block_table, chunk,
-                                                         causal, (q_descale, k_descale, v_descale))
-        return paged_decode_attention(q, k, v, bt2, lens2, softmax_scale, qd, kd, vd, out=out,
-                                      return_softmax_lse=return_softmax_lse, max_seq_len=bound,
-                                      num_splits=num_splits, q_len=chunk, cu_seqlens_q=cu2, causal=causal)
+        return paged_prefill_attention(q, k, v, block_table, seqused_k, cu_seqlens_q, q_len, softmax_scale,
+                                       q_descale, k_descale, v_descale, out=out,
+                                       return_softmax_lse=return_softmax_lse, causal=causal)
     # B rows of at most one token each: one per sequence, cu_seqlens_q is 0..B
     cu = None if q_len == 1 and q.shape[0] == B else cu_seqlens_q
     return paged_decode_attention(q, k, v, block_table, seqused_k, softmax_scale, q_descale, k_descale, v_descale,

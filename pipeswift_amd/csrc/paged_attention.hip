@@ -1514,6 +1514,341 @@ __global__ void __launch_bounds__(64 * kCombineMaxWaves) decode_combine_kernel(D
         den > 0.0f ? (mx + __builtin_log2f(den)) * 0.6931471805599453f : -__builtin_inff();
 }
 
+// ---- Prefill: many query tokens per sequence ----
+//
+// psk_paged_prefill_attention computes what the decode reader computes, for
+// sequences with more query rows per kv head than one 16-row MFMA tile holds
+// (prefill, chunked prefill, long speculative drafts, groups of more than 16
+// query heads).  One workgroup per (query block, kv head): kPfWaves waves of
+// kPfSets sets of 16 MFMA rows, kPfRows rows in all; row r is query token
+// i0 + r / G, query head g = r % G of the block's tq = kPfRows / G tokens, so
+// every K/V row of the block's keys is read from the cache once per tq query
+// tokens.  The keys stream through two LDS stages of kPfKeys keys, filled by
+// every thread (one 16-byte chunk of K and one of V each) and consumed by
+// every wave:
+//   * K as bf16, converted once by the thread that loaded it, 256-byte rows
+//     whose 16-byte chunk c of key t sits at chunk c ^ (t & 15): the eight
+//     lanes of one ds_read_b128 phase (eight keys, one chunk) hit distinct
+//     banks;
+//   * V as loaded (FP8) in 2 KiB tiles of 16 keys with the decode ring's
+//     layout (see pv_offsets), read transposed by ds_read_b64_tr_b8.
+// Per 32 keys and 16 rows: S^T = K Q^T on v_mfma_f32_16x16x32_bf16 (two
+// 16-key tiles, four MFMAs each, exactly converted FP8 operands as in the
+// decode reader), the running softmax in the exp2 domain with the lazily
+// raised maximum, then O^T = V^T P^T on the same MFMA with P split into bf16
+// hi + lo.  Transposed products leave each lane one query row (lane % 16):
+// its scores, running maximum and sum, and output columns 16 b + 4 (lane /
+// 16) + r, so a rescale stays inside the lane.  The 32-key MFMA step takes as
+// its k = 8 s + j (s = lane / 16) key 4 s + j of the first 16-key tile for
+// j < 4 and key 4 s + j - 4 of the second for j >= 4: the lane's S^T results
+// of the two tiles are then its P^T operand as they stand, and one transposed
+// V read per tile gives the matching V^T operand.
+constexpr int kPfWaves = 8;
+constexpr int kPfSets = 2;
+constexpr int kPfRows = kPfWaves * kPfSets * 16;
+constexpr int kPfKeys = 64;
+constexpr int kPfThreads = kPfWaves * 64;
+static_assert(kPfKeys * 8 == kPfThreads, "each thread loads one 16-byte chunk of K and one of V per stage");
+
+struct PrefillArgs {
+  DecodeArgs a;
+  const int32_t* blocks;  // [num_seqs + 1]: query blocks of the sequences before b; the total last
+  int32_t num_seqs;
+  int32_t tq;             // query tokens per block
+};
+
+// blocks[b] = sum over b' < b of ceil(n_b' / tq) query blocks, blocks[num_seqs]
+// the total: one workgroup of 1024 threads.
+__global__ void __launch_bounds__(1024) prefill_blocks_kernel(DecodeArgs a, int num_seqs, int tq, int32_t* blocks) {
+  __shared__ int32_t s_wave[16];
+  const int lane = int(threadIdx.x) & 63, wave = int(threadIdx.x) >> 6;
+  int carry = 0;
+  for (int c0 = 0; c0 < num_seqs; c0 += 1024) {
+    const int b = c0 + int(threadIdx.x);
+    const int nb = b < num_seqs ? (q_count(a, b) + tq - 1) / tq : 0;
+    int x = nb;  // inclusive prefix over the wave
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x, o);
+      if (lane >= o) x += y;
+    }
+    if (lane == 63) s_wave[wave] = x;
+    __syncthreads();
+    int before = 0, total = 0;
+    for (int w = 0; w < 16; ++w) {
+      const int t = s_wave[w];
+      before += w < wave ? t : 0;
+      total += t;
+    }
+    if (b < num_seqs) blocks[b] = carry + before + x - nb;
+    carry += total;
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) blocks[num_seqs] = carry;
+}
+
+// The sequence of query block u (blocks[0] = 0 <= u < blocks[num_seqs]): the
+// last b with blocks[b] <= u, by a 64-way search of the wave (one round up to
+// 64 sequences, two up to 4096).
+__device__ __forceinline__ int block_sequence(const int32_t* blocks, int num_seqs, int u, int lane) {
+  int lo = 0, n = num_seqs;  // the answer lies in [lo, lo + n) and blocks[lo] <= u
+  while (n > 1) {
+    const int step = (n + 63) / 64;
+    const bool le = lane * step < n && blocks[lo + lane * step] <= u;  // true on a prefix of the lanes
+    const uint64_t m = __ballot(le);
+    const int last = 63 - __builtin_clzll(m);
+    lo += last * step;
+    n = min(step, n - last * step);
+  }
+  return lo;
+}
+
+// Byte offsets, from a 16-key V tile of a stage, of this lane's four
+// transposed reads (pv_offsets without the ring slot's K half).
+__device__ __forceinline__ void pf_v_offsets(int lane, uint32_t (&off)[4]) {
+  const int r = lane & 15, s = lane >> 4;
+  const int tok = 4 * s + ((r >> 1) & 3);
+  const uint32_t row = uint32_t(1024 * (tok >> 3) + 128 * (tok & 7) + 8 * (r & 1));
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int c = 2 * k + (r >= 8 ? 1 : 0);
+    off[k] = row + uint32_t(16 * (c ^ (tok & 7)));
+  }
+}
+
+template <int OUT_DT>
+__device__ __forceinline__ void store_row4(char* dst, f32x4 v);
+template <>
+__device__ __forceinline__ void store_row4<PSK_DTYPE_F32>(char* dst, f32x4 v) {
+  *reinterpret_cast<f32x4*>(dst) = v;
+}
+template <>
+__device__ __forceinline__ void store_row4<PSK_DTYPE_BF16>(char* dst, f32x4 v) {
+  using E = Elt<PSK_DTYPE_BF16>;
+  const uint32_t lo = uint32_t(E::from_f32(v[0])) | (uint32_t(E::from_f32(v[1])) << 16);
+  const uint32_t hi = uint32_t(E::from_f32(v[2])) | (uint32_t(E::from_f32(v[3])) << 16);
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  *reinterpret_cast<u32x2*>(dst) = u32x2{lo, hi};
+}
+
+template <int Q_DT, int OUT_DT>
+__global__ void __launch_bounds__(kPfThreads) prefill_attention_kernel(PrefillArgs p) {
+  const DecodeArgs& a = p.a;
+  __shared__ u32x4 s_k[2][kPfKeys * 16];  // bf16 K rows
+  __shared__ u32x4 s_v[2][kPfKeys * 8];   // FP8 V, 16-key tiles of 2 KiB
+  const int lane = int(threadIdx.x) & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+  const int Hkv = a.num_kv_heads;
+  const int total = p.blocks[p.num_seqs];
+  const int idx = int(blockIdx.x) / Hkv, h = int(blockIdx.x) - idx * Hkv;
+  if (idx >= total) return;
+  // the last blocks of a sequence see the most keys: launched first
+  const int u = total - 1 - idx;
+  const int b = __builtin_amdgcn_readfirstlane(block_sequence(p.blocks, p.num_seqs, u, lane));
+  const int i0 = (u - p.blocks[b]) * p.tq;
+  const int n = q_count(a, b);
+  const int ni = min(p.tq, n - i0);
+  const int64_t qf = q_first(a, b);
+  const int L = max(a.seq_lens[b], 0);
+  const int G = a.heads;
+  // causal: query token i sees keys below base + i (FA's bottom-right alignment)
+  const int base = a.causal ? L - n + 1 : L;
+  const int key_end = a.causal ? min(max(base + i0 + ni - 1, 0), L) : L;  // keys any row of the block sees
+  const int mask_from = a.causal ? min(max(base + i0, 0), L) : L;         // keys every row sees
+  const float qd = descale(a.qd, a.qd_b, a.qd_h, b, h);
+  const float kd = descale(a.kd, a.kd_b, a.kd_h, b, h);
+  const float vd = descale(a.vd, a.vd_b, a.vd_h, b, h);
+  const float sl = a.scale_log2 * qd * kd;
+
+  int row_lim[kPfSets];
+  bf16x8 qop[kPfSets][4];
+#pragma unroll
+  for (int s = 0; s < kPfSets; ++s) {
+    const int r = (wave * kPfSets + s) * 16 + (lane & 15);
+    const int ti = r / G, g = r - ti * G;
+    const bool live = ti < ni;
+    row_lim[s] = live ? (a.causal ? min(max(base + i0 + ti, 0), L) : L) : 0;
+    uint32_t qw[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qw[i] = 0;
+    if (live)
+      load_query_as<Q_DT>(a.q + (qf + i0 + ti) * a.q_tok_stride + int64_t(h * G + g) * a.q_head_stride, qd,
+                          32 * (lane >> 4), qw);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) qop[s][c] = e4m3x8_to_bf16(qw[2 * c], qw[2 * c + 1]);
+  }
+  float m[kPfSets], mth[kPfSets], l[kPfSets];
+  f32x4 o[kPfSets][8];
+#pragma unroll
+  for (int s = 0; s < kPfSets; ++s) {
+    m[s] = kNegBig;
+    mth[s] = kNegBig + kLazy;
+    l[s] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) o[s][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+
+  // loads: thread t takes chunk t & 7 (16 bytes) of key t >> 3 of a stage, of
+  // K and of V; keys past key_end and rows on missing pages load as zeros
+  const int lk = int(threadIdx.x) >> 3, lc = int(threadIdx.x) & 7;
+  const int32_t* bt_row = a.block_table + int64_t(b) * a.bt_stride;
+  auto page_id = [&](int t) -> int32_t {
+    const int key = t * kPfKeys + lk;
+    return key < key_end ? checked_page(a, bt_row, page_index(a, key)) : -1;
+  };
+  auto fetch = [&](int t, int32_t pid, u32x4& kr, u32x4& vr) {
+    kr = u32x4(0);
+    vr = u32x4(0);
+    if (pid >= 0) {
+      const int key = t * kPfKeys + lk;
+      const int64_t row = key - int64_t(page_index(a, key)) * a.block_size;
+      kr = *reinterpret_cast<const u32x4*>(a.k + int64_t(pid) * a.k_blk + row * a.k_row + int64_t(h) * a.k_head +
+                                           16 * lc);
+      vr = *reinterpret_cast<const u32x4*>(a.v + int64_t(pid) * a.v_blk + row * a.v_row + int64_t(h) * a.v_head +
+                                           16 * lc);
+    }
+  };
+  auto stage_store = [&](int st, const u32x4& kr, const u32x4& vr) {
+    const int sw = lk & 15;
+    s_k[st][lk * 16 + ((2 * lc) ^ sw)] = __builtin_bit_cast(u32x4, e4m3x8_to_bf16(kr[0], kr[1]));
+    s_k[st][lk * 16 + ((2 * lc + 1) ^ sw)] = __builtin_bit_cast(u32x4, e4m3x8_to_bf16(kr[2], kr[3]));
+    s_v[st][(lk >> 4) * 128 + ((lk >> 3) & 1) * 64 + (lk & 7) * 8 + (lc ^ (lk & 7))] = vr;
+  };
+
+  uint32_t voff[4];
+  pf_v_offsets(lane, voff);
+  const int kx = lane & 15, kc0 = 4 * (lane >> 4);
+  auto compute = [&](int st, int t) {
+#pragma unroll
+    for (int kb = 0; kb < kPfKeys / 32; ++kb) {
+      const int key0 = t * kPfKeys + 32 * kb;
+      if (key0 >= key_end) break;
+      bf16x8 kop[2][4];
+      uint32_t vw[2][8];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int kk = 32 * kb + 16 * j + kx;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) kop[j][c] = __builtin_bit_cast(bf16x8, s_k[st][kk * 16 + ((kc0 + c) ^ kx)]);
+        const char* vt = reinterpret_cast<const char*>(&s_v[st][0]) + 2048 * (2 * kb + j);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const i32x2 w = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+              (__attribute__((address_space(3))) i32x2*)(vt + voff[k]));
+          vw[j][2 * k] = uint32_t(w[0]);
+          vw[j][2 * k + 1] = uint32_t(w[1]);
+        }
+      }
+      f32x4 sc[kPfSets][2];
+#pragma unroll
+      for (int s = 0; s < kPfSets; ++s) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int c = 0; c < 4; ++c) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[j][c], qop[s][c], acc, 0, 0, 0);
+          sc[s][j] = acc;
+        }
+      }
+      bf16x8 vop[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) vop[c] = e4m3x8_to_bf16(vw[0][c], vw[1][c]);
+      const bool masked = key0 + 32 > mask_from;
+#pragma unroll
+      for (int s = 0; s < kPfSets; ++s) {
+        float x[8];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float v = sc[s][j][r] * sl;
+            x[4 * j + r] = !masked || key0 + 16 * j + kc0 + r < row_lim[s] ? v : -__builtin_inff();
+          }
+        }
+        float mx = __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(x[0], x[1]), __builtin_fmaxf(x[2], x[3])),
+                                   __builtin_fmaxf(__builtin_fmaxf(x[4], x[5]), __builtin_fmaxf(x[6], x[7])));
+        mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16));
+        mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32));  // the row's maximum, in its four lanes
+        if (__any(mx > mth[s])) {
+          const float mn = __builtin_fmaxf(m[s], mx);
+          const float cr = __builtin_amdgcn_exp2f(m[s] - mn);
+          l[s] *= cr;
+#pragma unroll
+          for (int c = 0; c < 8; ++c) o[s][c] *= cr;
+          m[s] = mn;
+          mth[s] = mn + kLazy;
+        }
+        bf16x8 hi, lo;
+        float ps = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float pv = __builtin_amdgcn_exp2f(x[i] - m[s]);
+          ps += pv;
+          hi[i] = (__bf16)pv;
+          lo[i] = (__bf16)(pv - (float)hi[i]);
+        }
+        l[s] += ps;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          o[s][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop[c], hi, o[s][c], 0, 0, 0);
+          o[s][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop[c], lo, o[s][c], 0, 0, 0);
+        }
+      }
+    }
+  };
+
+  // two stages: the loads of stage t + 1 fly while stage t is consumed, and
+  // the page id of stage t + 2 while those land
+  const int n_tiles = (key_end + kPfKeys - 1) / kPfKeys;
+  u32x4 kr = u32x4(0), vr = u32x4(0);
+  int32_t pid_next = -1;
+  if (n_tiles > 0) {
+    const int32_t pid0 = page_id(0);
+    pid_next = n_tiles > 1 ? page_id(1) : -1;
+    fetch(0, pid0, kr, vr);
+    stage_store(0, kr, vr);
+  }
+  __syncthreads();
+  for (int t = 0; t < n_tiles; ++t) {
+    const bool more = t + 1 < n_tiles;
+    if (more) {
+      fetch(t + 1, pid_next, kr, vr);
+      pid_next = t + 2 < n_tiles ? page_id(t + 2) : -1;
+    }
+    compute(t & 1, t);
+    if (more) stage_store((t + 1) & 1, kr, vr);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int s = 0; s < kPfSets; ++s) {
+    float lt = l[s];
+    lt += __shfl_xor(lt, 16);
+    lt += __shfl_xor(lt, 32);
+    const int r = (wave * kPfSets + s) * 16 + (lane & 15);
+    const int ti = r / G, g = r - ti * G;
+    if (ti < ni) {
+      const int64_t tok = qf + i0 + ti;
+      const float inv = lt > 0.0f ? vd / lt : 0.0f;  // a row that sees no key: zeros and lse = -inf
+      char* dst = a.out + tok * a.out_tok_stride + int64_t(h * G + g) * a.out_head_stride;
+      constexpr int kEsz = Elt<OUT_DT>::kSize;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) store_row4<OUT_DT>(dst + (16 * c + kc0) * kEsz, o[s][c] * inv);
+      if (lane < 16 && a.lse)
+        a.lse[int64_t(h * G + g) * a.lse_head_stride + tok] =
+            lt > 0.0f ? (m[s] + __builtin_log2f(lt)) * 0.6931471805599453f : -__builtin_inff();
+    }
+  }
+}
+
+template <int Q_DT>
+void launch_prefill_q(const PrefillArgs& p, int out_dtype, dim3 grid, hipStream_t st) {
+  if (out_dtype == PSK_DTYPE_BF16)
+    hipLaunchKernelGGL((prefill_attention_kernel<Q_DT, PSK_DTYPE_BF16>), grid, dim3(kPfThreads), 0, st, p);
+  else
+    hipLaunchKernelGGL((prefill_attention_kernel<Q_DT, PSK_DTYPE_F32>), grid, dim3(kPfThreads), 0, st, p);
+}
+
 // Tokens per workgroup.  num_splits > 0 asks for that many splits of the
 // longest sequence; 0 aims at 20 splits of it (measured best for config 2's
 // 128 x 8 sequence-heads, within 1% from 17 to 20 and up to 20% slower from 31
@@ -1861,6 +2196,124 @@ int psk_paged_decode_attention(const void* q, int64_t q_tok_stride, int64_t q_he
     else hipLaunchKernelGGL((decode_combine_kernel<PSK_DTYPE_F32, 1>), grid2, block2, lds2, st, a);
   }
   return check_launch("decode_combine_kernel launch");
+}
+
+
+int64_t psk_paged_prefill_workspace_len(int64_t num_seqs) { return num_seqs < 0 ? PSK_E_ARG : num_seqs + 1; }
+
+int psk_paged_prefill_attention(const void* q, int64_t q_tok_stride, int64_t q_head_stride, int q_dtype,
+                                const void* k_cache, const void* v_cache, const int64_t* k_strides,
+                                const int64_t* v_strides, const int32_t* block_table, int64_t block_table_stride,
+                                int64_t block_table_width, const int32_t* seq_lens, int64_t num_seqs,
+                                int64_t num_q_heads, int64_t num_kv_heads, int64_t head_size, int64_t block_size,
+                                int64_t num_blocks, int64_t total_q, int64_t max_seqlen_q,
+                                const int32_t* cu_seqlens_q, int causal, float softmax_scale, const float* q_descale,
+                                const float* k_descale, const float* v_descale, const int64_t* descale_strides,
+                                void* out, int64_t out_tok_stride, int64_t out_head_stride, int out_dtype, float* lse,
+                                int64_t lse_head_stride, int32_t* workspace, int64_t workspace_len, void* stream) {
+  begin_device_call();
+  if (num_seqs < 0 || num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads)
+    return fail(PSK_E_ARG, "bad head counts (q %lld, kv %lld)", (long long)num_q_heads, (long long)num_kv_heads);
+  const int64_t group = num_q_heads / num_kv_heads;
+  if (group > kPfRows)
+    return fail(PSK_E_ARG, "at most %d query heads per kv head (got %lld)", kPfRows, (long long)group);
+  if (max_seqlen_q <= 0 || max_seqlen_q > INT32_MAX) return fail(PSK_E_ARG, "max_seqlen_q %lld", (long long)max_seqlen_q);
+  if (total_q < 0 || total_q > INT32_MAX) return fail(PSK_E_ARG, "total_q %lld", (long long)total_q);
+  if (!cu_seqlens_q && total_q != num_seqs * max_seqlen_q)
+    return fail(PSK_E_ARG, "without cu_seqlens_q every sequence has max_seqlen_q rows (%lld != %lld x %lld)",
+                (long long)total_q, (long long)num_seqs, (long long)max_seqlen_q);
+  if (head_size != kHead) return fail(PSK_E_ARG, "head_size must be %d (got %lld)", kHead, (long long)head_size);
+  if (block_size <= 0 || block_size > INT32_MAX || num_blocks <= 0 || num_blocks > INT32_MAX ||
+      block_table_width <= 0)
+    return fail(PSK_E_ARG, "bad cache geometry");
+  if (q_dtype != PSK_DTYPE_FP8_E4M3FN && q_dtype != PSK_DTYPE_BF16 && q_dtype != PSK_DTYPE_F16 &&
+      q_dtype != PSK_DTYPE_F32)
+    return fail(PSK_E_DTYPE, "query dtype %d", q_dtype);
+  if (out_dtype != PSK_DTYPE_BF16 && out_dtype != PSK_DTYPE_F32)
+    return fail(PSK_E_DTYPE, "output dtype %d (bf16 or f32)", out_dtype);
+  if (num_seqs == 0 || total_q == 0) return PSK_OK;
+  if (!q || !k_cache || !v_cache || !k_strides || !v_strides || !block_table || !seq_lens || !out || !workspace)
+    return fail(PSK_E_ARG, "NULL pointer");
+  if (!std::isfinite(softmax_scale)) return fail(PSK_E_ARG, "softmax_scale is not finite");
+  if (workspace_len < num_seqs + 1)
+    return fail(PSK_E_WORKSPACE, "workspace of %lld words, need %lld", (long long)workspace_len,
+                (long long)(num_seqs + 1));
+  const int qsz = dtype_size(q_dtype), osz = dtype_size(out_dtype);
+  const uint64_t kv_align[8] = {uint64_t(uintptr_t(k_cache)), uint64_t(uintptr_t(v_cache)), uint64_t(k_strides[0]),
+                                uint64_t(k_strides[1]),       uint64_t(k_strides[2]),       uint64_t(v_strides[0]),
+                                uint64_t(v_strides[1]),       uint64_t(v_strides[2])};
+  if (common_align(kv_align, 8, 16) < 16) return fail(PSK_E_ARG, "K/V caches need 16-byte aligned bases and strides");
+  const uint64_t q_align[3] = {uint64_t(uintptr_t(q)), uint64_t(q_tok_stride * qsz), uint64_t(q_head_stride * qsz)};
+  if (common_align(q_align, 3, 16) < 16) return fail(PSK_E_ARG, "query rows need 16-byte alignment");
+  const uint64_t o_align[3] = {uint64_t(uintptr_t(out)), uint64_t(out_tok_stride * osz),
+                               uint64_t(out_head_stride * osz)};
+  if (common_align(o_align, 3, 4 * osz) < 4 * osz)
+    return fail(PSK_E_ARG, "output rows need %d-byte alignment", 4 * osz);
+
+  PrefillArgs p{};
+  DecodeArgs& a = p.a;
+  a.q = static_cast<const char*>(q);
+  a.q_tok_stride = q_tok_stride * qsz;
+  a.q_head_stride = q_head_stride * qsz;
+  a.k = static_cast<const uint8_t*>(k_cache);
+  a.v = static_cast<const uint8_t*>(v_cache);
+  a.k_blk = k_strides[0];
+  a.k_row = k_strides[1];
+  a.k_head = k_strides[2];
+  a.v_blk = v_strides[0];
+  a.v_row = v_strides[1];
+  a.v_head = v_strides[2];
+  a.block_table = block_table;
+  a.bt_stride = block_table_stride;
+  a.bt_width = block_table_width;
+  a.seq_lens = seq_lens;
+  a.num_blocks = int32_t(num_blocks);
+  a.block_size = int32_t(block_size);
+  a.bs_shift = log2_exact(block_size);
+  a.num_kv_heads = int32_t(num_kv_heads);
+  a.group = int32_t(group);
+  a.heads = int32_t(group);
+  a.q_len = int32_t(max_seqlen_q);
+  a.cu_q = cu_seqlens_q;
+  a.causal = causal ? 1 : 0;
+  a.scale_log2 = softmax_scale * 1.4426950408889634f;
+  const int64_t zero[6] = {0, 0, 0, 0, 0, 0};
+  const int64_t* ds = descale_strides ? descale_strides : zero;
+  a.qd = q_descale;
+  a.qd_b = ds[0];
+  a.qd_h = ds[1];
+  a.kd = k_descale;
+  a.kd_b = ds[2];
+  a.kd_h = ds[3];
+  a.vd = v_descale;
+  a.vd_b = ds[4];
+  a.vd_h = ds[5];
+  a.out = static_cast<char*>(out);
+  a.out_tok_stride = out_tok_stride * osz;
+  a.out_head_stride = out_head_stride * osz;
+  a.lse = lse;
+  a.lse_head_stride = lse_head_stride;
+  p.blocks = workspace;
+  p.num_seqs = int32_t(num_seqs);
+  p.tq = int32_t(kPfRows / group);
+  // query blocks: at most ceil(total_q / tq) whole ones plus one partial per sequence
+  const int64_t max_blocks = ceil_div(total_q, p.tq) + num_seqs;
+  if (num_seqs > INT32_MAX - 1 || max_blocks * num_kv_heads > INT32_MAX)
+    return fail(PSK_E_ARG, "too many query blocks (%lld x %lld kv heads)", (long long)max_blocks,
+                (long long)num_kv_heads);
+
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(prefill_blocks_kernel, dim3(1), dim3(1024), 0, st, a, int(num_seqs), int(p.tq), workspace);
+  const int st1 = check_launch("prefill_blocks_kernel launch");
+  if (st1 != PSK_OK) return st1;
+  const dim3 grid{unsigned(max_blocks * num_kv_heads), 1u, 1u};
+  switch (q_dtype) {
+    case PSK_DTYPE_FP8_E4M3FN: launch_prefill_q<PSK_DTYPE_FP8_E4M3FN>(p, out_dtype, grid, st); break;
+    case PSK_DTYPE_BF16: launch_prefill_q<PSK_DTYPE_BF16>(p, out_dtype, grid, st); break;
+    case PSK_DTYPE_F16: launch_prefill_q<PSK_DTYPE_F16>(p, out_dtype, grid, st); break;
+    default: launch_prefill_q<PSK_DTYPE_F32>(p, out_dtype, grid, st); break;
+  }
+  return check_launch("prefill_attention_kernel launch");
 }
 
 }  // extern "C"

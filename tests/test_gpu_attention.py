@@ -299,10 +299,13 @@ def test_flash_attn_varlen_func_matches_direct_call(dev):
     assert torch.equal(a, b)
     with pytest.raises(AssertionError):  # no cu_seqlens_q
         attention.flash_attn_varlen_func(q, fd[:, 0], fd[:, 1], 2, None, seqused_k=lens, block_table=bt)
-    with pytest.raises(NotImplementedError, match="query heads per kv head"):  # 32 heads over one kv head
-        attention.flash_attn_varlen_func(torch.zeros(B, 32, 128, dtype=torch.bfloat16, device=dev), fd[:, 0, :, :1],
-                                         fd[:, 1, :, :1], 1, torch.arange(B + 1, dtype=torch.int32, device=dev),
-                                         seqused_k=lens, block_table=bt)
+    # 32 heads over one kv head: past the decode reader's 16 rows, the prefill kernel reads it
+    q32 = q.to(torch.float32).repeat(1, 8, 1)[:, :32].to(torch.bfloat16)
+    c = attention.flash_attn_varlen_func(q32, fd[:, 0, :, :1], fd[:, 1, :, :1], 1,
+                                         torch.arange(B + 1, dtype=torch.int32, device=dev), seqused_k=lens,
+                                         block_table=bt, softmax_scale=0.1, causal=True)
+    d = attention.paged_prefill_attention(q32, fd[:, 0, :, :1], fd[:, 1, :, :1], bt, lens, None, 1, 0.1)
+    assert torch.equal(c, d)
 
 
 @pytest.mark.parametrize("Hq,Hkv,length", [(8, 2, 20000), (64, 8, 9000), (3, 1, 33000)])

@@ -1,15 +1,18 @@
 """GPU parity of prefill over the paged FP8 cache: ``flash_attn_varlen_func``
-with more query tokens per sequence than one MFMA tile holds
-(``max_seqlen_q * Hq / Hkv > 16``), which the reference's
+with more query rows per kv head than one MFMA tile of the decode reader
+holds (``max_seqlen_q * Hq / Hkv > 16``), which the reference's
 ``_fp8_paged_attn`` passes for every prefill step (attention.py:577-585).
-Each sequence's query tokens are read in chunks of 16 / G tokens, each a
-sequence of its own, so the arithmetic per row is the decode reader's and
-so are the tolerances (see test_gpu_attention.py):
-  * fp32 output: |got - oracle| <= 3e-4 * max|V * vd| + 1e-4 * |oracle|
-  * lse:         |got - oracle| <= 5e-4 + 1e-5 * |oracle|
+Those steps run ``psk_paged_prefill_attention``; its arithmetic per row is
+the decode reader's (exact FP8 -> bf16 operands, fp32 MFMA sums, P in bf16
+hi + lo), and so are the tolerances (see test_gpu_attention.py):
+  * output: |got - oracle| <= 3e-4 * max|V * vd| + 1e-4 * |oracle|
+    (bf16 output: plus the bf16 rounding of the oracle, 2^-8 |oracle|)
+  * lse:    |got - oracle| <= 5e-4 + 1e-5 * |oracle|
 The oracle (oracle/kv_oracle.py: paged_decode_attention) runs in float64 over
 the same ragged layout and is pinned against torch SDPA under torch's
-lower-right causal mask.
+lower-right causal mask.  The decode reader run over chunks of the same step
+(``attention.chunked_prefill_attention``) is a second, independent GPU path
+that must agree with both.
 """
 
 import numpy as np
@@ -17,13 +20,20 @@ import pytest
 import torch
 
 from oracle import kv_oracle as O
-from pipeswift_amd import fp8_kv
+from pipeswift_amd import attention, fp8_kv
 from tests.conftest import raw
 
 pytestmark = pytest.mark.gpu
 
 
-def _prefill_case(dev, seed, lens, counts, Hq, Hkv, ps, causal, descales=True, num_splits=0, spare_rows=0):
+_Q_NAMES = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32", torch.float8_e4m3fn: "fp8"}
+
+
+def _prefill_case(dev, seed, lens, counts, Hq, Hkv, ps, causal, descales=True, num_splits=0, spare_rows=0,
+                  out_dtype=torch.float32, q_dtype=torch.bfloat16, path="entry"):
+    """One ragged step through ``path`` ("entry": flash_attn_varlen_func as
+    the reference calls it; "prefill": paged_prefill_attention directly;
+    "chunks": the decode reader over chunks), checked against the oracle."""
     g = torch.Generator().manual_seed(seed)
     B = len(lens)
     P = max(64, sum(-(-x // ps) for x in lens) + 8)
@@ -34,31 +44,42 @@ def _prefill_case(dev, seed, lens, counts, Hq, Hkv, ps, causal, descales=True, n
     bt = torch.stack([torch.randperm(P, generator=g)[:W] for _ in range(B)]).to(torch.int32)
     cu = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
     TQ = int(cu[-1]) + spare_rows
-    q = (torch.randn(TQ, Hq, 128, generator=g) * 3).to(torch.bfloat16)
+    q = (torch.randn(TQ, Hq, 128, generator=g) * 3)
+    q = q.clamp(-448, 448).to(q_dtype)
     rng = np.random.default_rng(seed)
     ds = [torch.from_numpy(rng.uniform(0.5, 2.0, (B, Hkv)).astype(np.float32)) for _ in range(3)] if descales \
         else [None] * 3
     fd = fused.to(dev)
-    out = torch.full((TQ, Hq, 128), 7.0, dtype=torch.float32, device=dev)
+    out = torch.full((TQ, Hq, 128), 7.0, dtype=out_dtype, device=dev)
     print(f"prefill case seed={seed} B={B} counts={list(counts)[:8]} Hq={Hq} Hkv={Hkv} ps={ps} causal={causal} "
-          f"splits={num_splits}", flush=True)
-    f = fp8_kv.attn_varlen_func()
-    got, lse = f(q=q.to(dev), k=fd[:, 0], v=fd[:, 1], max_seqlen_q=int(max(counts)),
-                 cu_seqlens_q=torch.from_numpy(cu).to(dev), max_seqlen_k=None,
-                 seqused_k=torch.tensor(lens, dtype=torch.int32, device=dev), block_table=bt.to(dev),
-                 softmax_scale=128 ** -0.5, causal=causal, q_descale=None if ds[0] is None else ds[0].to(dev),
-                 k_descale=None if ds[1] is None else ds[1].to(dev), v_descale=None if ds[2] is None else ds[2].to(dev),
-                 return_softmax_lse=True, out=out, num_splits=num_splits)
+          f"splits={num_splits} out={out_dtype} q={q_dtype} path={path}", flush=True)
+    dd = [None if d is None else d.to(dev) for d in ds]
+    kw = dict(softmax_scale=128 ** -0.5, causal=causal, q_descale=dd[0], k_descale=dd[1], v_descale=dd[2],
+              return_softmax_lse=True, out=out)
+    cu_d = torch.from_numpy(cu).to(dev)
+    lens_d = torch.tensor(lens, dtype=torch.int32, device=dev)
+    if path == "entry":
+        f = fp8_kv.attn_varlen_func()
+        got, lse = f(q=q.to(dev), k=fd[:, 0], v=fd[:, 1], max_seqlen_q=int(max(counts)), cu_seqlens_q=cu_d,
+                     max_seqlen_k=None, seqused_k=lens_d, block_table=bt.to(dev), num_splits=num_splits, **kw)
+    elif path == "prefill":
+        got, lse = attention.paged_prefill_attention(q.to(dev), fd[:, 0], fd[:, 1], bt.to(dev), lens_d, cu_d,
+                                                     int(max(counts)), **kw)
+    else:
+        got, lse = attention.chunked_prefill_attention(q.to(dev), fd[:, 0], fd[:, 1], int(max(counts)), cu_d, lens_d,
+                                                       bt.to(dev), num_splits=num_splits, **kw)
     npd = [None if d is None else d.numpy() for d in ds]
-    exp, lse_exp = O.paged_decode_attention(raw(q[: int(cu[-1])]), "bf16", raw(fused[:, 0]), raw(fused[:, 1]),
-                                            bt.numpy(), np.array(lens), 128 ** -0.5, *npd, cu_seqlens_q=cu,
-                                            causal=causal)
+    exp, lse_exp = O.paged_decode_attention(raw(q[: int(cu[-1])]), _Q_NAMES[q_dtype], raw(fused[:, 0]),
+                                            raw(fused[:, 1]), bt.numpy(), np.array(lens), 128 ** -0.5, *npd,
+                                            cu_seqlens_q=cu, causal=causal)
     n = int(cu[-1])
     vd_max = 1.0 if npd[2] is None else float(np.max(npd[2]))
     vmax = float(np.abs(O.e4m3fn_to_f32(raw(fused[:, 1]))).max()) * vd_max
     gotn = got[:n].double().cpu().numpy()
     err = np.abs(gotn - exp)
     tol = 3e-4 * vmax + 1e-4 * np.abs(exp)
+    if out_dtype == torch.bfloat16:
+        tol = tol + 2.0 ** -8 * np.abs(exp)
     assert (err <= tol).all(), f"max err {err.max():.3e} at {np.unravel_index(err.argmax(), err.shape)}"
     lse_got = lse.cpu().numpy().T.astype(np.float64)[:n]
     fin = np.isfinite(lse_exp)
@@ -70,12 +91,14 @@ def _prefill_case(dev, seed, lens, counts, Hq, Hkv, ps, causal, descales=True, n
     return got
 
 
-@pytest.mark.parametrize("Hq,Hkv", [(32, 8), (64, 8), (8, 8), (16, 1)])
+@pytest.mark.parametrize("Hq,Hkv", [(32, 8), (64, 8), (8, 8), (16, 1), (32, 1), (6, 2), (256, 2)])
 @pytest.mark.parametrize("causal", [True, False])
-def test_prefill_ragged_chunks(dev, Hq, Hkv, causal):
+def test_prefill_ragged(dev, Hq, Hkv, causal):
     """Prefill and chunked prefill: sequences with 1 to 200 query tokens over
     prefixes of 0 to 900 cached tokens (the query tokens are each sequence's
-    last positions), every group size's chunk length (16 / G tokens)."""
+    last positions), groups of 1 to 128 query heads per kv head (3: rows of a
+    token straddle MFMA row sets; 128: two query tokens per block), so one to
+    a hundred query blocks per sequence."""
     rng = np.random.default_rng(Hq * 10 + Hkv + causal)
     B = 7
     counts = [int(x) for x in rng.integers(1, 200, B)]
@@ -86,28 +109,58 @@ def test_prefill_ragged_chunks(dev, Hq, Hkv, causal):
 
 
 @pytest.mark.parametrize("ps", [16, 24, 64])
-def test_prefill_block_sizes_and_splits(dev, ps):
-    """Other page sizes (24: the general-page reader) and an explicit split
-    count, with empty sequences and spare query rows past the last one."""
+def test_prefill_block_sizes(dev, ps):
+    """Other page sizes (24: page rows found by division), empty sequences
+    and spare query rows past the last one; the decode reader over chunks of
+    the same step (with an explicit split count) agrees as well."""
     counts = [40, 0, 130, 17, 0, 64]
     lens = [40 + 300, 12, 130, 17 + 5, 0, 64 + 1000]
-    _prefill_case(dev, 600 + ps, lens, counts, 32, 8, ps, True, spare_rows=5)
-    _prefill_case(dev, 650 + ps, lens, counts, 32, 8, ps, True, num_splits=3)
+    a = _prefill_case(dev, 600 + ps, lens, counts, 32, 8, ps, True, spare_rows=5)
+    b = _prefill_case(dev, 600 + ps, lens, counts, 32, 8, ps, True, spare_rows=5, path="chunks", num_splits=3)
+    n = sum(counts)
+    assert float((a[:n] - b[:n]).abs().max()) <= 1e-3
 
 
-def test_prefill_more_chunks_than_the_balanced_schedule_takes(dev):
+def test_prefill_group_16_over_1100_tokens(dev):
     """A chunked-prefill step of 1100 new tokens over 6 sequences with prefixes
-    up to 1500 tokens at 16 query heads over one kv head: chunks of one token,
-    so 1100+ chunk sequences, past the balanced schedule's 1024, and the split
-    schedule reads them; unit descales, as the reference passes them."""
+    up to 1500 tokens at 16 query heads over one kv head (16-token query
+    blocks); unit descales, as the reference passes them.  Through the decode
+    reader the same step is 1100+ one-token chunk sequences, past its balanced
+    schedule's 1024, which its split schedule reads."""
     rng = np.random.default_rng(77)
     cuts = np.sort(rng.choice(np.arange(1, 1100), 5, replace=False))
     counts = np.diff(np.concatenate([[0], cuts, [1100]])).tolist()
     lens = [int(c) + int(p) * 16 for c, p in zip(counts, rng.integers(0, 94, 6))]
     _prefill_case(dev, 700, lens, counts, 16, 1, 16, True, descales=False)
+    _prefill_case(dev, 700, lens, counts, 16, 1, 16, True, descales=False, path="chunks")
 
 
 def test_prefill_shorter_sequence_than_its_queries(dev):
     """Query tokens past the sequence's keys see no key: zeros and lse -inf, as
     in the decode reader (FA's bottom-right alignment)."""
     _prefill_case(dev, 800, [5, 300], [20, 40], 32, 8, 16, True)
+
+
+@pytest.mark.parametrize("q_dtype,out_dtype", [(torch.float8_e4m3fn, torch.float32), (torch.float16, torch.float32),
+                                               (torch.float32, torch.bfloat16), (torch.bfloat16, torch.bfloat16)])
+def test_prefill_query_and_output_dtypes(dev, q_dtype, out_dtype):
+    """An FP8 query is used as is, the others quantized as e4m3(q / qd);
+    bf16 or float32 output; through paged_prefill_attention directly."""
+    _prefill_case(dev, 900, [300, 77, 500], [120, 77, 33], 32, 4, 16, True, q_dtype=q_dtype, out_dtype=out_dtype,
+                  path="prefill")
+
+
+def test_prefill_many_sequences(dev):
+    """150 sequences of 1 to 40 query tokens (the block search's two rounds),
+    at 8 query heads per kv head."""
+    rng = np.random.default_rng(91)
+    counts = [int(x) for x in rng.integers(1, 40, 150)]
+    lens = [c + int(p) for c, p in zip(counts, rng.integers(0, 200, 150))]
+    _prefill_case(dev, 901, lens, counts, 16, 2, 16, True)
+
+
+def test_prefill_long_prefix(dev):
+    """Config 3's shape at a smaller scale: 600 and 900 new tokens over
+    prefixes of 2000 and 4000 cached tokens, 32 query heads over 4 kv heads,
+    many stages per workgroup and the causal band across two of them."""
+    _prefill_case(dev, 902, [2600, 4900], [600, 900], 32, 4, 16, True)

@@ -208,20 +208,32 @@ def test_shim_asserts_fire_before_device_calls():
         reshape_and_cache_flash_diffkv(k, k, torch.zeros(2, 16, 8, 100), torch.zeros(4, dtype=torch.int64))
 
 
-def test_fp8_reader_refuses_more_than_16_heads_per_kv_head_before_any_device_call():
-    """The FA3-style entry covers decode, speculative decode and (in chunks)
-    prefill; a group of more than 16 query heads per kv head does not fit the
-    reader's 16 MFMA rows and raises NotImplementedError before any device
-    work (these are host tensors)."""
-    from pipeswift_amd import fp8_kv
+def test_fp8_reader_routes_steps_by_rows_per_kv_head(monkeypatch):
+    """The FA3-style entry sends a step whose query tokens x query heads per
+    kv head fit the decode reader's 16 MFMA rows to paged_decode_attention
+    (decode, speculative decode) and every larger one -- prefill, chunked
+    prefill, groups of more than 16 heads -- to paged_prefill_attention, with
+    the caller's arguments (host tensors: the calls are intercepted)."""
+    from pipeswift_amd import attention, fp8_kv
 
+    calls = []
+    monkeypatch.setattr(attention, "paged_decode_attention", lambda *a, **k: calls.append(("decode", a, k)) or "d")
+    monkeypatch.setattr(attention, "paged_prefill_attention", lambda *a, **k: calls.append(("prefill", a, k)) or "p")
     f = fp8_kv.attn_varlen_func()
-    k = torch.zeros(10, 16, 2, 128, dtype=torch.float8_e4m3fn)
+    bt = torch.zeros(2, 8, dtype=torch.int32)
+    lens = torch.full((2,), 100, dtype=torch.int32)
     cu = torch.tensor([0, 8, 16], dtype=torch.int32)
-    with pytest.raises(NotImplementedError, match="32 query heads per kv head exceed the reader's 16 rows"):
-        f(q=torch.zeros(16, 64, 128, dtype=torch.bfloat16), k=k, v=k, max_seqlen_q=8, cu_seqlens_q=cu,
-          seqused_k=torch.full((2,), 100, dtype=torch.int32), block_table=torch.zeros(2, 8, dtype=torch.int32),
-          causal=True)
+    for Hq, Hkv, q_len, want in [(32, 8, 4, "decode"), (32, 8, 5, "prefill"), (8, 8, 16, "decode"),
+                                 (8, 8, 17, "prefill"), (64, 2, 1, "prefill"), (16, 1, 1, "decode")]:
+        k = torch.zeros(10, 16, Hkv, 128, dtype=torch.float8_e4m3fn)
+        q = torch.zeros(16, Hq, 128, dtype=torch.bfloat16)
+        got = f(q=q, k=k, v=k, max_seqlen_q=q_len, cu_seqlens_q=cu, seqused_k=lens, block_table=bt, causal=True,
+                softmax_scale=0.25)
+        assert got == want[0], (Hq, Hkv, q_len)
+        kind, args, kw = calls[-1]
+        assert kind == want
+        if kind == "prefill":
+            assert args[5] is cu and args[6] == q_len and args[7] == 0.25 and kw["causal"] is True
 
 
 def test_chunked_prefill_layout():
