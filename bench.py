@@ -35,6 +35,11 @@ torch CPU baseline:
                      without the quantizer), where HBM rather than the launch
                      bounds it
   swap               config 5b: 8192 scattered blocks x 8 layers (4 GiB) D2H + H2D
+  prefill_attention  a chunked-prefill step of FP8 paged attention (config 3
+                     geometry: 4096 query tokens over prefixes of 14k-45k),
+                     the prefill kernel; MFMA-bound, so its value is TFLOP/s
+                     against the 2.5 PFLOP/s dense bf16 peak (--chunked: the
+                     decode reader over 2-token chunks of the same step)
   metadata           host us of prepare_kv_info (configs 2 and 3) and of the
                      graph static-metadata refresh, against the reference's way
 
@@ -62,8 +67,6 @@ carries:
 Other workloads (--workload NAME runs one alone): any name above, and
   mla_fp8_tiles_prefill / mla_fp8_tiles_decode   config 4 into 656-byte FP8
                      entries with one scale per 128-element tile
-  prefill_attention  a chunked-prefill step of FP8 paged attention (config 3
-                     geometry: 4096 query tokens, prefixes 0-60k)
   attention_shapes   decode attention on several batch shapes, balanced vs split
   l2_cycle           BlockManager store -> evict -> restore of an 8192-page prompt
                      (the default run includes a 2048-page cycle)
@@ -88,6 +91,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0
+PEAK_BF16_TFS = 2500.0  # MI355X dense bf16 MFMA
 PUBLISHED_H2D_64K_GBPS = 47.9  # the reference's H2D at 64 KiB per descriptor, H100 (copy_engine.py:15-21)
 SPIN_CYCLES = 2_000_000  # shader clocks of the pre-timing spin (~1 ms at 2.4 GHz)
 STEADY_STEPS = 2048  # launches per graph for the steady per-launch figure of the us workloads
@@ -364,13 +368,15 @@ def setup_decode_attention(args, device, q_len=1):
 def setup_prefill_attention(args, device):
     """A chunked-prefill step of attention over an FP8 paged cache, in config
     3's geometry: 4096 new query tokens over 6 sequences with page-aligned
-    prefixes of 0-60k cached tokens, 32 query heads over 4 kv heads (16 / 8 = 2
-    query tokens per chunk), random FP8 pages, causal, per-tensor descales,
-    through ``flash_attn_varlen_func`` as the reference's ``_fp8_paged_attn``
-    calls it for prefill.  Algorithmic bytes: every sequence's K and V rows
-    once, the page ids, the bf16 queries and outputs; the chunked reader
-    streams each sequence's keys once per chunk, so its effective rate is
-    reported against those bytes."""
+    prefixes of 14k-45k cached tokens, 32 query heads over 4 kv heads, random
+    FP8 pages, causal, per-tensor descales, through ``flash_attn_varlen_func``
+    as the reference's ``_fp8_paged_attn`` calls it for prefill (the prefill
+    kernel).  MFMA-bound: algorithmic FLOPs are 4 * 128 per visible (query
+    head, key) pair (Q K^T and P V, 2 * 128 each), counted once; the kernel's
+    bf16 hi + lo split of P runs P V twice on the matrix cores.  Algorithmic
+    bytes: every sequence's K and V rows once, the page ids, the bf16 queries
+    and outputs.  ``--chunked`` times the decode reader over 2-token chunks of
+    the same step instead."""
     import torch
 
     import workloads
@@ -395,21 +401,41 @@ def setup_prefill_attention(args, device):
     out = torch.empty(N, Hq, D, dtype=torch.bfloat16, device=device)
     maxq = int(chunk.max())
 
+    fn = attention.chunked_prefill_attention if getattr(args, "chunked", False) else attention.flash_attn_varlen_func
+    ws = torch.empty(attention.prefill_workspace_words(len(chunk)), dtype=torch.int32, device=device)
+
     def launch(i):
-        attention.flash_attn_varlen_func(q[i], kc, vc, maxq, cu, seqused_k=lens, block_table=bt,
-                                         softmax_scale=D ** -0.5, causal=True, k_descale=scales[0:1],
-                                         v_descale=scales[1:2], out=out)
+        if fn is attention.flash_attn_varlen_func:
+            attention.paged_prefill_attention(q[i], kc, vc, bt, lens, cu, maxq, D ** -0.5, None, scales[0:1],
+                                              scales[1:2], out=out, causal=True, workspace=ws)
+        else:
+            fn(q[i], kc, vc, maxq, cu, lens, bt, softmax_scale=D ** -0.5, causal=True, k_descale=scales[0:1],
+               v_descale=scales[1:2], out=out)
 
     total = int(lens.sum())
     pages = int(((cc.prefix + cc.chunk + ps - 1) // ps).sum())
     nbytes = total * H * D * 2 + pages * 4 + 2 * N * Hq * D * 2
+    p, c = cc.prefix.double(), cc.chunk.double()
+    pairs = float((c * p + c * (c + 1) / 2).sum()) * Hq  # visible (query head, key) pairs, causal
+    kernel = ("decode_partial_ring_kernel + decode_combine_kernel" if fn is not attention.flash_attn_varlen_func
+              else "prefill_attention_kernel")
+    flops = 4.0 * D * pairs
+
+    def cpu_torch(budget):
+        # the last 32 query tokens of sequence 0, every head, scaled by FLOPs
+        L0, e0 = int(lens[0]), int(cu[1])
+        step, _, _ = torch_cpu_decode_attention_step(kc, vc, bt[:1], lens[:1].cpu(), q[0][e0 - 32:e0], scales, 32, 1)
+        n, el = _timed(step, budget)
+        return n * 4.0 * D * Hq * sum(L0 - 31 + r for r in range(32)) / flops, el
     return launch, {
-        "name": "prefill_attention", "kernel": "decode_partial_ring_kernel + decode_combine_kernel",
+        "name": "prefill_attention", "kernel": kernel, "flops": flops, "cpu_torch": cpu_torch,
+        "cpu_torch_what": "torch fp32 causal attention on host tensors (the last 32 query tokens of sequence 0, "
+                          "all heads; scaled by FLOPs)",
         "bytes": nbytes, "tokens": N, "dtype": "fp8_e4m3fn", "rotate": R,
         "config": {"workload": "chunked-prefill attention over an FP8 paged cache (config 3 geometry)",
                    "query_tokens": N, "context_tokens": total, "q_heads": Hq, "kv_heads": H, "head_dim": D,
-                   "block_size": ps, "chunk_tokens": 16 // (Hq // H)},
-        "cpu": None,
+                   "block_size": ps, "path": "chunked decode reader" if kernel.startswith("decode") else
+                   "prefill kernel"},
     }
 
 
@@ -1729,6 +1755,7 @@ SECONDARY = (
     ("copy_blocks", 8, 2),
     ("swap", 2, 1),
     ("l2_cycle", 2048, 0),  # (name, pages, -): the BlockManager store -> evict -> restore cycle, 1 GiB each way
+    ("prefill_attention", 16, 2),
     ("metadata", 0, 0),
 )
 
@@ -1779,8 +1806,10 @@ def measure_workload(args, device, name, steps, warmup, achievable, cpu_budget, 
         n, el = info["cpu_torch"](cpu_budget)
         torch.set_num_threads(1)
         n1, el1 = info["cpu_torch"](cpu_budget)
-        cpu = {"value": round(info["bytes"] * n / el / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
-               "value_1thread": round(info["bytes"] * n1 / el1 / 1e9, 4),
+        # per launch: bytes (GB/s) or, for a matrix-core-bound workload, FLOPs (TFLOP/s)
+        work, div, unit = (info["flops"], 1e12, "TFLOP/s") if info.get("flops") else (info["bytes"], 1e9, "GB/s")
+        cpu = {"value": round(work * n / el / div, 4), "unit": unit, "cores": threads, "kind": "port",
+               "value_1thread": round(work * n1 / el1 / div, 4),
                "tokens_per_s": round(info["tokens"] * n / el, 1),
                "sample": f"{info.get('cpu_torch_what', 'torch on host tensors of the same layout')}: "
                          f"{n:.3g} steps in {el:.1f} s on {threads} threads, {n1:.3g} in {el1:.1f} s on 1"}
@@ -1820,6 +1849,18 @@ def measure_workload(args, device, name, steps, warmup, achievable, cpu_budget, 
         "cpu_baseline": cpu,
         "cpu_oracle": cpu_oracle,
     }
+    if info.get("flops"):
+        # a matrix-core-bound workload: the roofline is MFMA throughput, the
+        # value in TFLOP/s; the HBM rate stays in the record
+        tf = info["flops"] / per_launch_s / 1e12
+        res["hbm_gbs"] = res["value"]
+        res["value"] = round(tf, 2)
+        res["unit"] = "TFLOP/s"
+        res["pct_of_peak"] = round(100.0 * tf / PEAK_BF16_TFS, 3)
+        rf = res["roofline"]
+        rf.update({"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK_BF16_TFS, "unit": "TFLOP/s",
+                   "frac": round(tf / PEAK_BF16_TFS, 5), "flops_per_launch": info["flops"],
+                   "achievable": None, "frac_of_achievable": None, "steady_frac": None})
     del launch, info
     gc.collect()
     torch.cuda.synchronize()
@@ -1855,6 +1896,8 @@ def main():
     p.add_argument("--slots", default="pages", choices=("pages", "contiguous"),
                    help="*_prefill_append: 'pages' scatters the prompt's pages over the cache (the config); "
                         "'contiguous' writes consecutive slots (the same kernel without the page scatter)")
+    p.add_argument("--chunked", action="store_true",
+                   help="prefill_attention: the decode reader over 2-token chunks instead of the prefill kernel")
     p.add_argument("--block-size", type=int, default=16,
                    help="chunked_append / gather / *_prefill_append: page size (16 is configs 2 and 3; "
                         "128 is config 3's sensitivity run)")
@@ -1945,7 +1988,7 @@ def result_line(res, warmup, secondary, detail=None):
     line = {
         "metric": METRIC,
         "value": res["value"],
-        "unit": "GB/s",
+        "unit": res.get("unit", "GB/s"),
         "n_gpus": 1,
         "steps": res["steps"],
         "warmup": warmup,
@@ -1981,7 +2024,8 @@ def result_line(res, warmup, secondary, detail=None):
                 e["copy_us"] = r["copy_floor"]["us"]
             if cpu:
                 e["cpu"] = cpu.get("value")
-                e["cpu_unit"] = cpu.get("unit")
+                if cpu.get("unit") != r["unit"]:
+                    e["cpu_unit"] = cpu.get("unit")
                 if cpu.get("cores") is not None:
                     e["cpu_cores"] = cpu["cores"]
             sec[k] = e

@@ -1550,22 +1550,50 @@ constexpr int kPfKeys = 64;
 constexpr int kPfThreads = kPfWaves * 64;
 static_assert(kPfKeys * 8 == kPfThreads, "each thread loads one 16-byte chunk of K and one of V per stage");
 
+constexpr int kPfSortMax = 1024;  // sequences the pre-pass orders by length (more: batch order)
+
 struct PrefillArgs {
   DecodeArgs a;
-  const int32_t* blocks;  // [num_seqs + 1]: query blocks of the sequences before b; the total last
+  const int32_t* blocks;  // [num_seqs + 1]: query blocks before launch position k; the total last
+  const int32_t* order;   // [num_seqs]: the sequence at launch position k
   int32_t num_seqs;
   int32_t tq;             // query tokens per block
 };
 
-// blocks[b] = sum over b' < b of ceil(n_b' / tq) query blocks, blocks[num_seqs]
-// the total: one workgroup of 1024 threads.
-__global__ void __launch_bounds__(1024) prefill_blocks_kernel(DecodeArgs a, int num_seqs, int tq, int32_t* blocks) {
+// The launch order of the query blocks, in one workgroup of 1024 threads:
+// sequences by decreasing length (the keys their last block reads; without
+// query tokens last), ties in batch order, then each sequence's blocks from
+// its last (the most keys, when causal) to its first.  Writes order[k] and
+// the exclusive prefix blocks[k] of ceil(n_b / tq) over launch positions,
+// blocks[num_seqs] = the total.  Past kPfSortMax sequences the batch order is
+// kept.
+__global__ void __launch_bounds__(1024) prefill_blocks_kernel(DecodeArgs a, int num_seqs, int tq, int32_t* blocks,
+                                                              int32_t* order) {
+  __shared__ int32_t s_key[kPfSortMax];
+  __shared__ int32_t s_order[kPfSortMax];
   __shared__ int32_t s_wave[16];
-  const int lane = int(threadIdx.x) & 63, wave = int(threadIdx.x) >> 6;
+  const int tid = int(threadIdx.x), lane = tid & 63, wave = tid >> 6;
+  const bool sorted = num_seqs <= kPfSortMax;
+  if (sorted) {
+    int key = -1;
+    if (tid < num_seqs) key = q_count(a, tid) > 0 ? max(a.seq_lens[tid], 0) : -1;
+    s_key[tid] = key;
+    __syncthreads();
+    if (tid < num_seqs) {
+      int rank = 0;
+      for (int j = 0; j < num_seqs; ++j) {
+        const int kj = s_key[j];
+        rank += (kj > key || (kj == key && j < tid)) ? 1 : 0;
+      }
+      s_order[rank] = tid;
+    }
+    __syncthreads();
+  }
   int carry = 0;
   for (int c0 = 0; c0 < num_seqs; c0 += 1024) {
-    const int b = c0 + int(threadIdx.x);
-    const int nb = b < num_seqs ? (q_count(a, b) + tq - 1) / tq : 0;
+    const int k = c0 + tid;
+    const int b = k < num_seqs ? (sorted ? s_order[k] : k) : 0;
+    const int nb = k < num_seqs ? (q_count(a, b) + tq - 1) / tq : 0;
     int x = nb;  // inclusive prefix over the wave
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
@@ -1580,16 +1608,19 @@ __global__ void __launch_bounds__(1024) prefill_blocks_kernel(DecodeArgs a, int 
       before += w < wave ? t : 0;
       total += t;
     }
-    if (b < num_seqs) blocks[b] = carry + before + x - nb;
+    if (k < num_seqs) {
+      blocks[k] = carry + before + x - nb;
+      order[k] = b;
+    }
     carry += total;
     __syncthreads();
   }
-  if (threadIdx.x == 0) blocks[num_seqs] = carry;
+  if (tid == 0) blocks[num_seqs] = carry;
 }
 
-// The sequence of query block u (blocks[0] = 0 <= u < blocks[num_seqs]): the
-// last b with blocks[b] <= u, by a 64-way search of the wave (one round up to
-// 64 sequences, two up to 4096).
+// The launch position of query block u (blocks[0] = 0 <= u < blocks[num_seqs]):
+// the last k with blocks[k] <= u, by a 64-way search of the wave (one round up
+// to 64 sequences, two up to 4096).
 __device__ __forceinline__ int block_sequence(const int32_t* blocks, int num_seqs, int u, int lane) {
   int lo = 0, n = num_seqs;  // the answer lies in [lo, lo + n) and blocks[lo] <= u
   while (n > 1) {
@@ -1642,10 +1673,10 @@ __global__ void __launch_bounds__(kPfThreads) prefill_attention_kernel(PrefillAr
   const int total = p.blocks[p.num_seqs];
   const int idx = int(blockIdx.x) / Hkv, h = int(blockIdx.x) - idx * Hkv;
   if (idx >= total) return;
-  // the last blocks of a sequence see the most keys: launched first
-  const int u = total - 1 - idx;
-  const int b = __builtin_amdgcn_readfirstlane(block_sequence(p.blocks, p.num_seqs, u, lane));
-  const int i0 = (u - p.blocks[b]) * p.tq;
+  const int k = __builtin_amdgcn_readfirstlane(block_sequence(p.blocks, p.num_seqs, idx, lane));
+  const int b = p.order[k];
+  // a sequence's blocks from its last (the most keys, when causal) to its first
+  const int i0 = (p.blocks[k + 1] - 1 - idx) * p.tq;
   const int n = q_count(a, b);
   const int ni = min(p.tq, n - i0);
   const int64_t qf = q_first(a, b);
@@ -1692,14 +1723,19 @@ __global__ void __launch_bounds__(kPfThreads) prefill_attention_kernel(PrefillAr
   // K and of V; keys past key_end and rows on missing pages load as zeros
   const int lk = int(threadIdx.x) >> 3, lc = int(threadIdx.x) & 7;
   const int32_t* bt_row = a.block_table + int64_t(b) * a.bt_stride;
+  // the table entry as stored (range-checked where it is used, a stage
+  // later: a check here would wait for the load, and with it for the K/V
+  // loads issued before it)
   auto page_id = [&](int t) -> int32_t {
     const int key = t * kPfKeys + lk;
-    return key < key_end ? checked_page(a, bt_row, page_index(a, key)) : -1;
+    if (key >= key_end) return -1;
+    const int pi = page_index(a, key);
+    return pi < a.bt_width ? bt_row[pi] : -1;
   };
   auto fetch = [&](int t, int32_t pid, u32x4& kr, u32x4& vr) {
     kr = u32x4(0);
     vr = u32x4(0);
-    if (pid >= 0) {
+    if (pid >= 0 && pid < a.num_blocks) {
       const int key = t * kPfKeys + lk;
       const int64_t row = key - int64_t(page_index(a, key)) * a.block_size;
       kr = *reinterpret_cast<const u32x4*>(a.k + int64_t(pid) * a.k_blk + row * a.k_row + int64_t(h) * a.k_head +
@@ -1767,9 +1803,11 @@ __global__ void __launch_bounds__(kPfThreads) prefill_attention_kernel(PrefillAr
         }
         float mx = __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(x[0], x[1]), __builtin_fmaxf(x[2], x[3])),
                                    __builtin_fmaxf(__builtin_fmaxf(x[4], x[5]), __builtin_fmaxf(x[6], x[7])));
-        mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16));
-        mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32));  // the row's maximum, in its four lanes
+        // the four lanes of a row hold the same threshold, so a lane's own
+        // maximum decides; the row's maximum is formed only to raise it
         if (__any(mx > mth[s])) {
+          mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16));
+          mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32));
           const float mn = __builtin_fmaxf(m[s], mx);
           const float cr = __builtin_amdgcn_exp2f(m[s] - mn);
           l[s] *= cr;
@@ -2199,7 +2237,7 @@ int psk_paged_decode_attention(const void* q, int64_t q_tok_stride, int64_t q_he
 }
 
 
-int64_t psk_paged_prefill_workspace_len(int64_t num_seqs) { return num_seqs < 0 ? PSK_E_ARG : num_seqs + 1; }
+int64_t psk_paged_prefill_workspace_len(int64_t num_seqs) { return num_seqs < 0 ? PSK_E_ARG : 2 * num_seqs + 1; }
 
 int psk_paged_prefill_attention(const void* q, int64_t q_tok_stride, int64_t q_head_stride, int q_dtype,
                                 const void* k_cache, const void* v_cache, const int64_t* k_strides,
@@ -2235,9 +2273,9 @@ int psk_paged_prefill_attention(const void* q, int64_t q_tok_stride, int64_t q_h
   if (!q || !k_cache || !v_cache || !k_strides || !v_strides || !block_table || !seq_lens || !out || !workspace)
     return fail(PSK_E_ARG, "NULL pointer");
   if (!std::isfinite(softmax_scale)) return fail(PSK_E_ARG, "softmax_scale is not finite");
-  if (workspace_len < num_seqs + 1)
+  if (workspace_len < 2 * num_seqs + 1)
     return fail(PSK_E_WORKSPACE, "workspace of %lld words, need %lld", (long long)workspace_len,
-                (long long)(num_seqs + 1));
+                (long long)(2 * num_seqs + 1));
   const int qsz = dtype_size(q_dtype), osz = dtype_size(out_dtype);
   const uint64_t kv_align[8] = {uint64_t(uintptr_t(k_cache)), uint64_t(uintptr_t(v_cache)), uint64_t(k_strides[0]),
                                 uint64_t(k_strides[1]),       uint64_t(k_strides[2]),       uint64_t(v_strides[0]),
@@ -2294,16 +2332,18 @@ int psk_paged_prefill_attention(const void* q, int64_t q_tok_stride, int64_t q_h
   a.lse = lse;
   a.lse_head_stride = lse_head_stride;
   p.blocks = workspace;
+  p.order = workspace + num_seqs + 1;
   p.num_seqs = int32_t(num_seqs);
   p.tq = int32_t(kPfRows / group);
   // query blocks: at most ceil(total_q / tq) whole ones plus one partial per sequence
   const int64_t max_blocks = ceil_div(total_q, p.tq) + num_seqs;
-  if (num_seqs > INT32_MAX - 1 || max_blocks * num_kv_heads > INT32_MAX)
+  if (num_seqs > (INT32_MAX - 1) / 2 || max_blocks * num_kv_heads > INT32_MAX)
     return fail(PSK_E_ARG, "too many query blocks (%lld x %lld kv heads)", (long long)max_blocks,
                 (long long)num_kv_heads);
 
   hipStream_t st = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(prefill_blocks_kernel, dim3(1), dim3(1024), 0, st, a, int(num_seqs), int(p.tq), workspace);
+  hipLaunchKernelGGL(prefill_blocks_kernel, dim3(1), dim3(1024), 0, st, a, int(num_seqs), int(p.tq), workspace,
+                     workspace + num_seqs + 1);
   const int st1 = check_launch("prefill_blocks_kernel launch");
   if (st1 != PSK_OK) return st1;
   const dim3 grid{unsigned(max_blocks * num_kv_heads), 1u, 1u};
