@@ -1543,12 +1543,20 @@ __global__ void __launch_bounds__(64 * kCombineMaxWaves) decode_combine_kernel(D
 // j < 4 and key 4 s + j - 4 of the second for j >= 4: the lane's S^T results
 // of the two tiles are then its P^T operand as they stand, and one transposed
 // V read per tile gives the matching V^T operand.
-constexpr int kPfWaves = 8;
+#ifndef PSK_PF_WAVES
+#define PSK_PF_WAVES 8
+#endif
+#ifndef PSK_PF_KEYS
+#define PSK_PF_KEYS 64
+#endif
+constexpr int kPfWaves = PSK_PF_WAVES;
 constexpr int kPfSets = 2;
 constexpr int kPfRows = kPfWaves * kPfSets * 16;
-constexpr int kPfKeys = 64;
+constexpr int kPfKeys = PSK_PF_KEYS;  // keys per LDS stage
 constexpr int kPfThreads = kPfWaves * 64;
-static_assert(kPfKeys * 8 == kPfThreads, "each thread loads one 16-byte chunk of K and one of V per stage");
+constexpr int kPfLoads = kPfKeys * 8 / kPfThreads;  // 16-byte chunks of K (and of V) per thread per stage
+static_assert(kPfKeys % 32 == 0 && kPfLoads >= 1 && kPfLoads * kPfThreads == kPfKeys * 8,
+              "a stage is whole 32-key blocks, its chunks spread evenly over the threads");
 
 constexpr int kPfSortMax = 1024;  // sequences the pre-pass orders by length (more: batch order)
 
@@ -1558,6 +1566,7 @@ struct PrefillArgs {
   const int32_t* order;   // [num_seqs]: the sequence at launch position k
   int32_t num_seqs;
   int32_t tq;             // query tokens per block
+  int32_t narrow;         // K/V page and row strides below 2^32: offsets from 32 x 32-bit products
 };
 
 // The launch order of the query blocks, in one workgroup of 1024 threads:
@@ -1663,10 +1672,11 @@ __device__ __forceinline__ void store_row4<PSK_DTYPE_BF16>(char* dst, f32x4 v) {
 }
 
 template <int Q_DT, int OUT_DT>
-__global__ void __launch_bounds__(kPfThreads) prefill_attention_kernel(PrefillArgs p) {
+__global__ void __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(2)))
+prefill_attention_kernel(PrefillArgs p) {
   const DecodeArgs& a = p.a;
-  __shared__ u32x4 s_k[2][kPfKeys * 16];  // bf16 K rows
-  __shared__ u32x4 s_v[2][kPfKeys * 8];   // FP8 V, 16-key tiles of 2 KiB
+  __shared__ u32x4 s_k[2][kPfKeys * 16];  // bf16 K rows, chunk c of key t at c ^ (t & 15)
+  __shared__ u32x4 s_v[2][kPfKeys * 16];  // bf16 V rows, chunk c of key t at c ^ (2 (t & 7))
   const int lane = int(threadIdx.x) & 63;
   const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
   const int Hkv = a.num_kv_heads;
@@ -1689,7 +1699,9 @@ __global__ void __launch_bounds__(kPfThreads) prefill_attention_kernel(PrefillAr
   const float qd = descale(a.qd, a.qd_b, a.qd_h, b, h);
   const float kd = descale(a.kd, a.kd_b, a.kd_h, b, h);
   const float vd = descale(a.vd, a.vd_b, a.vd_h, b, h);
-  const float sl = a.scale_log2 * qd * kd;
+  // exp2-domain score scale; a negative one is applied as -q~ (exact) times |sl|
+  const float sl_signed = a.scale_log2 * qd * kd;
+  const float sl = __builtin_fabsf(sl_signed);
 
   int row_lim[kPfSets];
   bf16x8 qop[kPfSets][4];
@@ -1705,157 +1717,272 @@ __global__ void __launch_bounds__(kPfThreads) prefill_attention_kernel(PrefillAr
     if (live)
       load_query_as<Q_DT>(a.q + (qf + i0 + ti) * a.q_tok_stride + int64_t(h * G + g) * a.q_head_stride, qd,
                           32 * (lane >> 4), qw);
+    if (sl_signed < 0.0f) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qw[i] ^= 0x80808080u;  // -q~: E4M3 sign bits
+    }
 #pragma unroll
     for (int c = 0; c < 4; ++c) qop[s][c] = e4m3x8_to_bf16(qw[2 * c], qw[2 * c + 1]);
   }
-  float m[kPfSets], mth[kPfSets], l[kPfSets];
+  // Softmax state per row set.  m is fixed by the row's first 32 keys and
+  // never raised: p = 2^(x - m) with x up to m + kPfHeadroom keeps every p,
+  // sum and accumulator finite, so the hot loop has no rescale.  A score past
+  // that (`ex`) makes the workgroup redo the row with exact maxima: a pass
+  // for the maxima, then the accumulation again.  Rows without a query token
+  // keep m = +kBig (every p is 0).
+  constexpr float kPfHeadroom = 64.0f;
+  constexpr float kBig = 1.0e30f;
+  float m[kPfSets], l[kPfSets];
   f32x4 o[kPfSets][8];
+  bool live_row[kPfSets];
 #pragma unroll
-  for (int s = 0; s < kPfSets; ++s) {
-    m[s] = kNegBig;
-    mth[s] = kNegBig + kLazy;
-    l[s] = 0.0f;
+  for (int s = 0; s < kPfSets; ++s) live_row[s] = ((wave * kPfSets + s) * 16 + (lane & 15)) / G < ni;
+  auto reset = [&](float m0) {
 #pragma unroll
-    for (int c = 0; c < 8; ++c) o[s][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  }
+    for (int s = 0; s < kPfSets; ++s) {
+      m[s] = live_row[s] ? m0 : kBig;
+      l[s] = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) o[s][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  };
+  bool ex = false;
 
-  // loads: thread t takes chunk t & 7 (16 bytes) of key t >> 3 of a stage, of
-  // K and of V; keys past key_end and rows on missing pages load as zeros
-  const int lk = int(threadIdx.x) >> 3, lc = int(threadIdx.x) & 7;
+  // loads: chunk i = threadIdx.x + u * kPfThreads of a stage (u < kPfLoads)
+  // is 16-byte chunk i & 7 of key i >> 3, of K and of V; keys past key_end
+  // and rows on missing pages load as zeros
+  const int lc = int(threadIdx.x) & 7;
+  auto lkey = [&](int u) { return (int(threadIdx.x) + u * kPfThreads) >> 3; };
   const int32_t* bt_row = a.block_table + int64_t(b) * a.bt_stride;
   // the table entry as stored (range-checked where it is used, a stage
   // later: a check here would wait for the load, and with it for the K/V
   // loads issued before it)
-  auto page_id = [&](int t) -> int32_t {
-    const int key = t * kPfKeys + lk;
+  auto page_id = [&](int t, int u) -> int32_t {
+    const int key = t * kPfKeys + lkey(u);
     if (key >= key_end) return -1;
     const int pi = page_index(a, key);
     return pi < a.bt_width ? bt_row[pi] : -1;
   };
-  auto fetch = [&](int t, int32_t pid, u32x4& kr, u32x4& vr) {
+  const uint8_t* kbase = a.k + int64_t(h) * a.k_head + 16 * lc;
+  const uint8_t* vbase = a.v + int64_t(h) * a.v_head + 16 * lc;
+  auto fetch = [&](int t, int u, int32_t pid, u32x4& kr, u32x4& vr) {
     kr = u32x4(0);
     vr = u32x4(0);
     if (pid >= 0 && pid < a.num_blocks) {
-      const int key = t * kPfKeys + lk;
-      const int64_t row = key - int64_t(page_index(a, key)) * a.block_size;
-      kr = *reinterpret_cast<const u32x4*>(a.k + int64_t(pid) * a.k_blk + row * a.k_row + int64_t(h) * a.k_head +
-                                           16 * lc);
-      vr = *reinterpret_cast<const u32x4*>(a.v + int64_t(pid) * a.v_blk + row * a.v_row + int64_t(h) * a.v_head +
-                                           16 * lc);
+      const int key = t * kPfKeys + lkey(u);
+      const int row = a.bs_shift >= 0 ? key & (a.block_size - 1) : key - page_index(a, key) * a.block_size;
+      uint64_t ko, vo;
+      if (p.narrow) {  // two v_mad_u64_u32 each
+        ko = uint64_t(uint32_t(pid)) * uint32_t(a.k_blk) + uint64_t(uint32_t(row)) * uint32_t(a.k_row);
+        vo = uint64_t(uint32_t(pid)) * uint32_t(a.v_blk) + uint64_t(uint32_t(row)) * uint32_t(a.v_row);
+      } else {
+        ko = uint64_t(int64_t(pid) * a.k_blk + int64_t(row) * a.k_row);
+        vo = uint64_t(int64_t(pid) * a.v_blk + int64_t(row) * a.v_row);
+      }
+      kr = *reinterpret_cast<const u32x4*>(kbase + ko);
+      vr = *reinterpret_cast<const u32x4*>(vbase + vo);
     }
   };
-  auto stage_store = [&](int st, const u32x4& kr, const u32x4& vr) {
-    const int sw = lk & 15;
-    s_k[st][lk * 16 + ((2 * lc) ^ sw)] = __builtin_bit_cast(u32x4, e4m3x8_to_bf16(kr[0], kr[1]));
-    s_k[st][lk * 16 + ((2 * lc + 1) ^ sw)] = __builtin_bit_cast(u32x4, e4m3x8_to_bf16(kr[2], kr[3]));
-    s_v[st][(lk >> 4) * 128 + ((lk >> 3) & 1) * 64 + (lk & 7) * 8 + (lc ^ (lk & 7))] = vr;
+  // both as bf16 (exact), converted once here for every wave
+  auto stage_store = [&](int st, int u, const u32x4& kr, const u32x4& vr) {
+    const int lk = lkey(u);
+    const int ks = lk & 15, vs = 2 * (lk & 7);
+    s_k[st][lk * 16 + ((2 * lc) ^ ks)] = __builtin_bit_cast(u32x4, e4m3x8_to_bf16(kr[0], kr[1]));
+    s_k[st][lk * 16 + ((2 * lc + 1) ^ ks)] = __builtin_bit_cast(u32x4, e4m3x8_to_bf16(kr[2], kr[3]));
+    s_v[st][lk * 16 + ((2 * lc) ^ vs)] = __builtin_bit_cast(u32x4, e4m3x8_to_bf16(vr[0], vr[1]));
+    s_v[st][lk * 16 + ((2 * lc + 1) ^ vs)] = __builtin_bit_cast(u32x4, e4m3x8_to_bf16(vr[2], vr[3]));
   };
 
-  uint32_t voff[4];
-  pf_v_offsets(lane, voff);
+  // read side.  K (the A operand of S^T): key kx = lane % 16 of a 16-key
+  // tile, chunk 4 (lane / 16) + c for MFMA c.  V^T (the A operand of O^T):
+  // ds_read_b64_tr_b16 gives lane i of a 16-lane group element j of the row
+  // that lane 4 j + i / 4 of the group addressed, at its element i % 4; lane
+  // r of group s addresses key 4 s + r / 4 of the tile, columns 16 c + 4 (r %
+  // 4) .. + 3 (chunk 2 c + (r % 4) / 2, half r % 2), so lane i receives column
+  // 16 c + i of keys 4 s .. 4 s + 3.
   const int kx = lane & 15, kc0 = 4 * (lane >> 4);
-  auto compute = [&](int st, int t) {
+  const int vkey = 4 * (lane >> 4) + (kx >> 2);  // this lane's V row in a 16-key tile
+  const uint32_t vrow = uint32_t(256 * vkey + 8 * (kx & 1));
+  const int vq = (kx & 3) >> 1, vsw = 2 * (vkey & 7);  // keys 16 j + vkey: (vkey & 7) is the tile-free swizzle
+
+  // raw scores y = q~ . K of the 32 keys from key0 (-inf where masked), the
+  // lane's 8 of each row set
+  auto scores = [&](auto masked_tag, int st, int key0, int kb, float (&y)[kPfSets][8]) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int kk = 32 * kb + 16 * j + kx;
+      bf16x8 kop[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) kop[c] = __builtin_bit_cast(bf16x8, s_k[st][kk * 16 + ((kc0 + c) ^ kx)]);
+#pragma unroll
+      for (int s = 0; s < kPfSets; ++s) {
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[c], qop[s][c], acc, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          y[s][4 * j + r] = !MASKED || key0 + 16 * j + kc0 + r < row_lim[s] ? acc[r] : -__builtin_inff();
+      }
+    }
+  };
+  // a lane's largest scaled score of a set (sl >= 0: max(y) * sl); IEEE
+  // maximum, so no canonicalizing moves, and a NaN score propagates
+  auto lane_max = [&](const float (&y)[8]) {
+    return __builtin_elementwise_maximum(
+               __builtin_elementwise_maximum(__builtin_elementwise_maximum(y[0], y[1]),
+                                             __builtin_elementwise_maximum(y[2], y[3])),
+               __builtin_elementwise_maximum(__builtin_elementwise_maximum(y[4], y[5]),
+                                             __builtin_elementwise_maximum(y[6], y[7]))) * sl;
+  };
+  auto row_max = [&](float v) {
+    v = __builtin_fmaxf(v, __shfl_xor(v, 16));
+    return __builtin_fmaxf(v, __shfl_xor(v, 32));
+  };
+  // FIRST: the block fixes m (the row's maximum of these keys); CHECK: flag a
+  // score past m + kPfHeadroom
+  auto block = [&](auto masked_tag, auto first_tag, auto check_tag, int st, int key0, int kb) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
+    constexpr bool FIRST = decltype(first_tag)::value;
+    constexpr bool CHECK = decltype(check_tag)::value;
+    float y[kPfSets][8];
+    scores(masked_tag, st, key0, kb, y);
+    const char* vb = reinterpret_cast<const char*>(&s_v[st][0]) + 256 * 32 * kb;
+    // set by set: set s + 1's softmax (VALU) is independent of set s's P V
+    // (MFMA), so the two overlap; V^T is read again for each set rather than
+    // held in registers
+#pragma unroll
+    for (int s = 0; s < kPfSets; ++s) {
+      if constexpr (FIRST) {
+        m[s] = live_row[s] ? __builtin_fmaxf(row_max(lane_max(y[s])), kNegBig) : kBig;
+      } else if constexpr (CHECK) {
+        ex |= lane_max(y[s]) > m[s] + kPfHeadroom;
+      }
+      // P = hi + lo: hi the top 16 bits of p (a bf16 value), lo = p - hi
+      // (exact in fp32) rounded to bf16; hi + lo carries ~16 bits of p
+      float pv[8], ps = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float e = __builtin_fmaf(y[s][i], sl, -m[s]);
+        pv[i] = __builtin_amdgcn_exp2f(MASKED && y[s][i] == -__builtin_inff() ? -__builtin_inff() : e);
+        ps += pv[i];
+      }
+      l[s] += ps;
+      uint32_t hw[4], lw[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t u0 = __float_as_uint(pv[2 * i]), u1 = __float_as_uint(pv[2 * i + 1]);
+        hw[i] = __builtin_amdgcn_perm(u1, u0, 0x07060302u);
+        const f32x2 lo2 = {pv[2 * i] - __uint_as_float(u0 & 0xFFFF0000u),
+                           pv[2 * i + 1] - __uint_as_float(u1 & 0xFFFF0000u)};
+        lw[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(lo2, bf16x2));
+      }
+      const bf16x8 hi = __builtin_bit_cast(bf16x8, u32x4{hw[0], hw[1], hw[2], hw[3]});
+      const bf16x8 lo = __builtin_bit_cast(bf16x8, u32x4{lw[0], lw[1], lw[2], lw[3]});
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const uint32_t off = vrow + uint32_t(16 * ((2 * c + vq) ^ vsw));
+        const s16x4 t0 =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(vb + off));
+        const s16x4 t1 =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(vb + 256 * 16 + off));
+        const bf16x8 vop = __builtin_bit_cast(bf16x8, __builtin_shufflevector(t0, t1, 0, 1, 2, 3, 4, 5, 6, 7));
+        o[s][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, hi, o[s][c], 0, 0, 0);
+        o[s][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, lo, o[s][c], 0, 0, 0);
+      }
+    }
+  };
+  // the maxima pass of a redo: the lane's largest scaled score per set into m
+  auto block_max = [&](auto masked_tag, int st, int key0, int kb) {
+    float y[kPfSets][8];
+    scores(masked_tag, st, key0, kb, y);
+#pragma unroll
+    for (int s = 0; s < kPfSets; ++s) m[s] = __builtin_fmaxf(m[s], lane_max(y[s]));
+  };
+
+  // The keys of the block stream through two LDS stages: the loads of stage
+  // t + 1 fly while stage t is consumed, and the page id of stage t + 2 while
+  // those land.  Stage 0, the stages every row sees whole and the rest (the
+  // causal band and the end of the keys) each run as straight-line code over
+  // their 32-key blocks; every wave takes the same (uniform) path, so the
+  // barriers match.
+  const int n_tiles = (key_end + kPfKeys - 1) / kPfKeys;
+  const int t_open = min(n_tiles, mask_from / kPfKeys);  // stages [0, t_open) need no mask
+  using T = std::true_type;
+  using F = std::false_type;
+  // one stage's 32-key blocks.  MODE 0: the pass with m fixed by the first
+  // block (FIRST) and the headroom check; 1: the maxima of a redo; 2: the
+  // accumulation of a redo (m exact, no check)
+  auto run_stage = [&](auto mode, auto masked_tag, auto first_tag, int st, int t) {
+    constexpr int MODE = decltype(mode)::value;
 #pragma unroll
     for (int kb = 0; kb < kPfKeys / 32; ++kb) {
       const int key0 = t * kPfKeys + 32 * kb;
-      if (key0 >= key_end) break;
-      bf16x8 kop[2][4];
-      uint32_t vw[2][8];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int kk = 32 * kb + 16 * j + kx;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) kop[j][c] = __builtin_bit_cast(bf16x8, s_k[st][kk * 16 + ((kc0 + c) ^ kx)]);
-        const char* vt = reinterpret_cast<const char*>(&s_v[st][0]) + 2048 * (2 * kb + j);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const i32x2 w = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-              (__attribute__((address_space(3))) i32x2*)(vt + voff[k]));
-          vw[j][2 * k] = uint32_t(w[0]);
-          vw[j][2 * k + 1] = uint32_t(w[1]);
-        }
-      }
-      f32x4 sc[kPfSets][2];
-#pragma unroll
-      for (int s = 0; s < kPfSets; ++s) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-          for (int c = 0; c < 4; ++c) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[j][c], qop[s][c], acc, 0, 0, 0);
-          sc[s][j] = acc;
-        }
-      }
-      bf16x8 vop[8];
-#pragma unroll
-      for (int c = 0; c < 8; ++c) vop[c] = e4m3x8_to_bf16(vw[0][c], vw[1][c]);
-      const bool masked = key0 + 32 > mask_from;
-#pragma unroll
-      for (int s = 0; s < kPfSets; ++s) {
-        float x[8];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float v = sc[s][j][r] * sl;
-            x[4 * j + r] = !masked || key0 + 16 * j + kc0 + r < row_lim[s] ? v : -__builtin_inff();
-          }
-        }
-        float mx = __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(x[0], x[1]), __builtin_fmaxf(x[2], x[3])),
-                                   __builtin_fmaxf(__builtin_fmaxf(x[4], x[5]), __builtin_fmaxf(x[6], x[7])));
-        // the four lanes of a row hold the same threshold, so a lane's own
-        // maximum decides; the row's maximum is formed only to raise it
-        if (__any(mx > mth[s])) {
-          mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16));
-          mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32));
-          const float mn = __builtin_fmaxf(m[s], mx);
-          const float cr = __builtin_amdgcn_exp2f(m[s] - mn);
-          l[s] *= cr;
-#pragma unroll
-          for (int c = 0; c < 8; ++c) o[s][c] *= cr;
-          m[s] = mn;
-          mth[s] = mn + kLazy;
-        }
-        bf16x8 hi, lo;
-        float ps = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float pv = __builtin_amdgcn_exp2f(x[i] - m[s]);
-          ps += pv;
-          hi[i] = (__bf16)pv;
-          lo[i] = (__bf16)(pv - (float)hi[i]);
-        }
-        l[s] += ps;
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          o[s][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop[c], hi, o[s][c], 0, 0, 0);
-          o[s][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop[c], lo, o[s][c], 0, 0, 0);
-        }
+      if (decltype(masked_tag)::value && key0 >= key_end) break;
+      if constexpr (MODE == 1) {
+        block_max(masked_tag, st, key0, kb);
+      } else if (kb == 0) {
+        block(masked_tag, first_tag, std::integral_constant<bool, MODE == 0>{}, st, key0, kb);
+      } else {
+        block(masked_tag, F{}, std::integral_constant<bool, MODE == 0>{}, st, key0, kb);
       }
     }
   };
-
-  // two stages: the loads of stage t + 1 fly while stage t is consumed, and
-  // the page id of stage t + 2 while those land
-  const int n_tiles = (key_end + kPfKeys - 1) / kPfKeys;
-  u32x4 kr = u32x4(0), vr = u32x4(0);
-  int32_t pid_next = -1;
-  if (n_tiles > 0) {
-    const int32_t pid0 = page_id(0);
-    pid_next = n_tiles > 1 ? page_id(1) : -1;
-    fetch(0, pid0, kr, vr);
-    stage_store(0, kr, vr);
-  }
-  __syncthreads();
-  for (int t = 0; t < n_tiles; ++t) {
-    const bool more = t + 1 < n_tiles;
-    if (more) {
-      fetch(t + 1, pid_next, kr, vr);
-      pid_next = t + 2 < n_tiles ? page_id(t + 2) : -1;
+  auto stream = [&](auto mode) {
+    u32x4 kr[kPfLoads], vr[kPfLoads];
+    int32_t pid_next[kPfLoads];
+#pragma unroll
+    for (int u = 0; u < kPfLoads; ++u) pid_next[u] = -1;
+    if (n_tiles > 0) {
+      int32_t pid0[kPfLoads];
+#pragma unroll
+      for (int u = 0; u < kPfLoads; ++u) {
+        pid0[u] = page_id(0, u);
+        pid_next[u] = n_tiles > 1 ? page_id(1, u) : -1;
+      }
+#pragma unroll
+      for (int u = 0; u < kPfLoads; ++u) fetch(0, u, pid0[u], kr[u], vr[u]);
+#pragma unroll
+      for (int u = 0; u < kPfLoads; ++u) stage_store(0, u, kr[u], vr[u]);
     }
-    compute(t & 1, t);
-    if (more) stage_store((t + 1) & 1, kr, vr);
     __syncthreads();
+    auto stage = [&](int t, auto masked_tag, auto first_tag) {
+      const bool more = t + 1 < n_tiles;
+      if (more) {
+#pragma unroll
+        for (int u = 0; u < kPfLoads; ++u) fetch(t + 1, u, pid_next[u], kr[u], vr[u]);
+#pragma unroll
+        for (int u = 0; u < kPfLoads; ++u) pid_next[u] = t + 2 < n_tiles ? page_id(t + 2, u) : -1;
+      }
+      run_stage(mode, masked_tag, first_tag, t & 1, t);
+      if (more) {
+#pragma unroll
+        for (int u = 0; u < kPfLoads; ++u) stage_store((t + 1) & 1, u, kr[u], vr[u]);
+      }
+      __syncthreads();
+    };
+    constexpr bool kFirst = decltype(mode)::value == 0;
+    if (n_tiles > 0) {
+      if (t_open > 0) stage(0, F{}, std::integral_constant<bool, kFirst>{});
+      else stage(0, T{}, std::integral_constant<bool, kFirst>{});
+    }
+    int t = 1;
+    for (; t < t_open; ++t) stage(t, F{}, F{});
+    for (; t < n_tiles; ++t) stage(t, T{}, F{});
+  };
+  reset(kNegBig);
+  stream(std::integral_constant<int, 0>{});
+  if (__syncthreads_or(ex ? 1 : 0)) {
+    // a score past the headroom: exact maxima, then the accumulation again
+    reset(kNegBig);
+    stream(std::integral_constant<int, 1>{});
+    float mx[kPfSets];
+#pragma unroll
+    for (int s = 0; s < kPfSets; ++s) mx[s] = live_row[s] ? __builtin_fmaxf(row_max(m[s]), kNegBig) : kBig;
+    reset(kNegBig);
+#pragma unroll
+    for (int s = 0; s < kPfSets; ++s) m[s] = mx[s];
+    stream(std::integral_constant<int, 2>{});
   }
 
 #pragma unroll
@@ -2335,6 +2462,9 @@ int psk_paged_prefill_attention(const void* q, int64_t q_tok_stride, int64_t q_h
   p.order = workspace + num_seqs + 1;
   p.num_seqs = int32_t(num_seqs);
   p.tq = int32_t(kPfRows / group);
+  constexpr int64_t k32 = int64_t(1) << 32;
+  p.narrow = k_strides[0] >= 0 && k_strides[0] < k32 && k_strides[1] >= 0 && k_strides[1] < k32 &&
+             v_strides[0] >= 0 && v_strides[0] < k32 && v_strides[1] >= 0 && v_strides[1] < k32;
   // query blocks: at most ceil(total_q / tq) whole ones plus one partial per sequence
   const int64_t max_blocks = ceil_div(total_q, p.tq) + num_seqs;
   if (num_seqs > (INT32_MAX - 1) / 2 || max_blocks * num_kv_heads > INT32_MAX)
