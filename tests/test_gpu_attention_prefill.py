@@ -30,7 +30,7 @@ _Q_NAMES = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32", 
 
 
 def _prefill_case(dev, seed, lens, counts, Hq, Hkv, ps, causal, descales=True, num_splits=0, spare_rows=0,
-                  out_dtype=torch.float32, q_dtype=torch.bfloat16, path="entry"):
+                  out_dtype=torch.float32, q_dtype=torch.bfloat16, path="entry", scale=128 ** -0.5, k_sign=1.0):
     """One ragged step through ``path`` ("entry": flash_attn_varlen_func as
     the reference calls it; "prefill": paged_prefill_attention directly;
     "chunks": the decode reader over chunks), checked against the oracle."""
@@ -49,12 +49,14 @@ def _prefill_case(dev, seed, lens, counts, Hq, Hkv, ps, causal, descales=True, n
     rng = np.random.default_rng(seed)
     ds = [torch.from_numpy(rng.uniform(0.5, 2.0, (B, Hkv)).astype(np.float32)) for _ in range(3)] if descales \
         else [None] * 3
+    if k_sign != 1.0:
+        ds[1] = ds[1] * k_sign
     fd = fused.to(dev)
     out = torch.full((TQ, Hq, 128), 7.0, dtype=out_dtype, device=dev)
     print(f"prefill case seed={seed} B={B} counts={list(counts)[:8]} Hq={Hq} Hkv={Hkv} ps={ps} causal={causal} "
           f"splits={num_splits} out={out_dtype} q={q_dtype} path={path}", flush=True)
     dd = [None if d is None else d.to(dev) for d in ds]
-    kw = dict(softmax_scale=128 ** -0.5, causal=causal, q_descale=dd[0], k_descale=dd[1], v_descale=dd[2],
+    kw = dict(softmax_scale=scale, causal=causal, q_descale=dd[0], k_descale=dd[1], v_descale=dd[2],
               return_softmax_lse=True, out=out)
     cu_d = torch.from_numpy(cu).to(dev)
     lens_d = torch.tensor(lens, dtype=torch.int32, device=dev)
@@ -70,7 +72,7 @@ def _prefill_case(dev, seed, lens, counts, Hq, Hkv, ps, causal, descales=True, n
                                                        bt.to(dev), num_splits=num_splits, **kw)
     npd = [None if d is None else d.numpy() for d in ds]
     exp, lse_exp = O.paged_decode_attention(raw(q[: int(cu[-1])]), _Q_NAMES[q_dtype], raw(fused[:, 0]),
-                                            raw(fused[:, 1]), bt.numpy(), np.array(lens), 128 ** -0.5, *npd,
+                                            raw(fused[:, 1]), bt.numpy(), np.array(lens), scale, *npd,
                                             cu_seqlens_q=cu, causal=causal)
     n = int(cu[-1])
     vd_max = 1.0 if npd[2] is None else float(np.max(npd[2]))
@@ -164,3 +166,16 @@ def test_prefill_long_prefix(dev):
     prefixes of 2000 and 4000 cached tokens, 32 query heads over 4 kv heads,
     many stages per workgroup and the causal band across two of them."""
     _prefill_case(dev, 902, [2600, 4900], [600, 900], 32, 4, 16, True)
+
+
+def test_prefill_steep_scores_take_the_exact_redo(dev):
+    """Scores spread over hundreds of binary orders of magnitude (softmax
+    scale 4): rows pass the prefill kernel's 2^64 headroom above the maximum
+    of their first 32 keys, so their workgroups recompute with exact row
+    maxima; results still match the float64 oracle."""
+    _prefill_case(dev, 903, [700, 90, 1500], [300, 90, 64], 32, 4, 16, True, scale=4.0)
+
+
+def test_prefill_negative_score_scale(dev):
+    """A negative k descale (the score scale's sign applied to q~, exactly)."""
+    _prefill_case(dev, 904, [400, 250], [120, 250], 16, 2, 16, True, k_sign=-1.0)
