@@ -56,10 +56,10 @@ def check_available() -> None:
     """Fail at startup rather than in the first forward pass (fp8_kv.py:64-71):
     the FP8 reader and append need a gfx950 GPU and this package's library.
 
-    The reader covers decode, speculative decode and prefill (prefill reads
-    each sequence's query tokens in chunks of 16 / G tokens, G query heads
-    per kv head, each chunk streaming the sequence's keys again); groups of
-    more than 16 query heads per kv head raise NotImplementedError."""
+    The reader covers decode, speculative decode and prefill: steps of at
+    most 16 query rows per kv head (query tokens x G query heads per kv head)
+    run the decode kernels, larger ones the prefill kernel, for groups of up
+    to 256 query heads per kv head."""
     assert torch.cuda.is_available(), "--enable_fp8_kv needs a GPU"
     arch = getattr(torch.cuda.get_device_properties(torch.cuda.current_device()), "gcnArchName", "")
     assert arch.startswith("gfx950"), f"--enable_fp8_kv on this build needs gfx950 (MI355X), got {arch or 'unknown'}"
