@@ -1543,16 +1543,10 @@ __global__ void __launch_bounds__(64 * kCombineMaxWaves) decode_combine_kernel(D
 // j < 4 and key 4 s + j - 4 of the second for j >= 4: the lane's S^T results
 // of the two tiles are then its P^T operand as they stand, and one transposed
 // V read per tile gives the matching V^T operand.
-#ifndef PSK_PF_WAVES
-#define PSK_PF_WAVES 8
-#endif
-#ifndef PSK_PF_KEYS
-#define PSK_PF_KEYS 64
-#endif
-constexpr int kPfWaves = PSK_PF_WAVES;
+constexpr int kPfWaves = 8;
 constexpr int kPfSets = 2;
 constexpr int kPfRows = kPfWaves * kPfSets * 16;
-constexpr int kPfKeys = PSK_PF_KEYS;  // keys per LDS stage
+constexpr int kPfKeys = 64;  // keys per LDS stage
 constexpr int kPfThreads = kPfWaves * 64;
 constexpr int kPfLoads = kPfKeys * 8 / kPfThreads;  // 16-byte chunks of K (and of V) per thread per stage
 static_assert(kPfKeys % 32 == 0 && kPfLoads >= 1 && kPfLoads * kPfThreads == kPfKeys * 8,
