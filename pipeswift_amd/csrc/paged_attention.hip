@@ -1524,25 +1524,23 @@ __global__ void __launch_bounds__(64 * kCombineMaxWaves) decode_combine_kernel(D
 // i0 + r / G, query head g = r % G of the block's tq = kPfRows / G tokens, so
 // every K/V row of the block's keys is read from the cache once per tq query
 // tokens.  The keys stream through two LDS stages of kPfKeys keys, filled by
-// every thread (one 16-byte chunk of K and one of V each) and consumed by
-// every wave:
-//   * K as bf16, converted once by the thread that loaded it, 256-byte rows
-//     whose 16-byte chunk c of key t sits at chunk c ^ (t & 15): the eight
-//     lanes of one ds_read_b128 phase (eight keys, one chunk) hit distinct
-//     banks;
-//   * V as loaded (FP8) in 2 KiB tiles of 16 keys with the decode ring's
-//     layout (see pv_offsets), read transposed by ds_read_b64_tr_b8.
+// every thread (one 16-byte chunk of K and one of V each, converted once to
+// bf16, exactly) and consumed by every wave, as 256-byte rows:
+//   * K: 16-byte chunk c of key t at chunk c ^ (t & 15), so the lanes of one
+//     ds_read_b128 phase (consecutive keys, one chunk) hit distinct banks;
+//   * V: chunk c of key t at c ^ (2 (t & 7)), read transposed by
+//     ds_read_b64_tr_b16 (four keys of one column per lane and read).
 // Per 32 keys and 16 rows: S^T = K Q^T on v_mfma_f32_16x16x32_bf16 (two
 // 16-key tiles, four MFMAs each, exactly converted FP8 operands as in the
-// decode reader), the running softmax in the exp2 domain with the lazily
-// raised maximum, then O^T = V^T P^T on the same MFMA with P split into bf16
-// hi + lo.  Transposed products leave each lane one query row (lane % 16):
-// its scores, running maximum and sum, and output columns 16 b + 4 (lane /
-// 16) + r, so a rescale stays inside the lane.  The 32-key MFMA step takes as
-// its k = 8 s + j (s = lane / 16) key 4 s + j of the first 16-key tile for
-// j < 4 and key 4 s + j - 4 of the second for j >= 4: the lane's S^T results
-// of the two tiles are then its P^T operand as they stand, and one transposed
-// V read per tile gives the matching V^T operand.
+// decode reader), the softmax in the exp2 domain, then O^T = V^T P^T on the
+// same MFMA with P split into bf16 hi + lo.  Transposed products leave each
+// lane one query row (lane % 16): its scores, maximum and sum, and output
+// columns 16 b + 4 (lane / 16) + r.  The 32-key MFMA step takes as its
+// k = 8 s + j (s = lane / 16) key 4 s + j of the first 16-key tile for j < 4
+// and key 4 s + j - 4 of the second for j >= 4: the lane's S^T results of the
+// two tiles are then its P^T operand as they stand, and one transposed V read
+// per tile gives the matching V^T operand.  A row's maximum is fixed by its
+// first 32 keys (see the kernel), so the loop has no rescale.
 constexpr int kPfWaves = 8;
 constexpr int kPfSets = 2;
 constexpr int kPfRows = kPfWaves * kPfSets * 16;
