@@ -30,7 +30,8 @@ _Q_NAMES = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32", 
 
 
 def _prefill_case(dev, seed, lens, counts, Hq, Hkv, ps, causal, descales=True, num_splits=0, spare_rows=0,
-                  out_dtype=torch.float32, q_dtype=torch.bfloat16, path="entry", scale=128 ** -0.5, k_sign=1.0):
+                  out_dtype=torch.float32, q_dtype=torch.bfloat16, path="entry", scale=128 ** -0.5, k_sign=1.0,
+                  bad_ids=False):
     """One ragged step through ``path`` ("entry": flash_attn_varlen_func as
     the reference calls it; "prefill": paged_prefill_attention directly;
     "chunks": the decode reader over chunks), checked against the oracle."""
@@ -42,6 +43,11 @@ def _prefill_case(dev, seed, lens, counts, Hq, Hkv, ps, causal, descales=True, n
     fused[:, 1] = (torch.randn((P, ps, Hkv, 128), generator=g) * 2.0).to(torch.float8_e4m3fn)
     W = max(1, max(-(-x // ps) for x in lens))
     bt = torch.stack([torch.randperm(P, generator=g)[:W] for _ in range(B)]).to(torch.int32)
+    if bad_ids:  # missing pages inside the sequences: their rows read as zeros
+        for b in range(B):
+            used = -(-lens[b] // ps)
+            if used > 1:
+                bt[b, 1] = -3 if b % 2 else P + 5
     cu = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
     TQ = int(cu[-1]) + spare_rows
     q = (torch.randn(TQ, Hq, 128, generator=g) * 3)
@@ -179,3 +185,36 @@ def test_prefill_steep_scores_take_the_exact_redo(dev):
 def test_prefill_negative_score_scale(dev):
     """A negative k descale (the score scale's sign applied to q~, exactly)."""
     _prefill_case(dev, 904, [400, 250], [120, 250], 16, 2, 16, True, k_sign=-1.0)
+
+
+def test_prefill_missing_pages_read_as_zero_rows(dev):
+    """Block-table entries outside [0, num_blocks) inside the sequences read
+    as zero K and V rows (scores 0), as in the decode reader and the oracle."""
+    _prefill_case(dev, 905, [300, 200, 90], [100, 200, 40], 32, 8, 16, True, bad_ids=True)
+
+
+def test_prefill_page_stride_past_32_bits(dev):
+    """Pages 4 GiB + 32 KiB apart (a strided view over one allocation): the
+    loader's 64-bit offset path, which strides below 2^32 never take."""
+    Hkv, Hq, ps, D = 2, 16, 16, 128
+    stride = (1 << 32) + (1 << 15)
+    base = torch.zeros(stride + 2 * ps * Hkv * D * 2, dtype=torch.uint8, device=dev)
+    g = torch.Generator().manual_seed(906)
+    pages = (torch.randn(2, 2, ps, Hkv, D, generator=g) * 2).to(torch.float8_e4m3fn)  # [page, K/V, row, head, d]
+    for p in range(2):
+        base[p * stride: p * stride + 2 * ps * Hkv * D].copy_(pages[p].reshape(-1).view(torch.uint8).to(dev))
+    kc = base.view(torch.float8_e4m3fn).as_strided((2, ps, Hkv, D), (stride, Hkv * D, D, 1))
+    vc = base.view(torch.float8_e4m3fn).as_strided((2, ps, Hkv, D), (stride, Hkv * D, D, 1), ps * Hkv * D)
+    L, n = 30, 20
+    q = (torch.randn(n, Hq, D, generator=g) * 3).to(torch.bfloat16)
+    bt = torch.tensor([[1, 0]], dtype=torch.int32)
+    cu = torch.tensor([0, n], dtype=torch.int32)
+    print(f"prefill wide page stride: stride={stride}", flush=True)
+    got = attention.paged_prefill_attention(q.to(dev), kc, vc, bt.to(dev), torch.tensor([L], dtype=torch.int32,
+                                            device=dev), cu.to(dev), n, 128 ** -0.5,
+                                            out=torch.zeros(n, Hq, D, dtype=torch.float32, device=dev))
+    exp, _ = O.paged_decode_attention(raw(q), "bf16", raw(pages[:, 0]), raw(pages[:, 1]), bt.numpy(), np.array([L]),
+                                      128 ** -0.5, cu_seqlens_q=cu.numpy(), causal=True)
+    vmax = float(np.abs(O.e4m3fn_to_f32(raw(pages[:, 1]))).max())
+    err = np.abs(got.double().cpu().numpy() - exp)
+    assert (err <= 3e-4 * vmax + 1e-4 * np.abs(exp)).all(), f"max err {err.max():.3e}"
