@@ -1717,12 +1717,14 @@ prefill_attention_kernel(PrefillArgs p) {
     for (int c = 0; c < 4; ++c) qop[s][c] = e4m3x8_to_bf16(qw[2 * c], qw[2 * c + 1]);
   }
   // Softmax state per row set.  m is fixed by the row's first 32 keys and
-  // never raised: p = 2^(x - m) with x up to m + kPfHeadroom keeps every p,
-  // sum and accumulator finite, so the hot loop has no rescale.  A score past
-  // that (`ex`) makes the workgroup redo the row with exact maxima: a pass
-  // for the maxima, then the accumulation again.  Rows without a query token
-  // keep m = +kBig (every p is 0).
-  constexpr float kPfHeadroom = 64.0f;
+  // never raised, so the hot loop has no rescale and checks nothing: while
+  // every lane's share of a row's sum stays below 2^kPfHeadroom, every p
+  // (each below that too), sum and accumulator is finite and exact.  A score
+  // far above the first keys' maximum makes a share reach it (or overflow),
+  // and the workgroup then redoes the row with exact maxima: a pass for the
+  // maxima, then the accumulation again.  Rows without a query token keep
+  // m = +kBig (every p is 0).
+  constexpr float kPfHeadroom = 94.0f;
   constexpr float kBig = 1.0e30f;
   float m[kPfSets], l[kPfSets];
   f32x4 o[kPfSets][8];
@@ -1738,7 +1740,6 @@ prefill_attention_kernel(PrefillArgs p) {
       for (int c = 0; c < 8; ++c) o[s][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
   };
-  bool ex = false;
 
   // loads: chunk i = threadIdx.x + u * kPfThreads of a stage (u < kPfLoads)
   // is 16-byte chunk i & 7 of key i >> 3, of K and of V; keys past key_end
@@ -1831,12 +1832,10 @@ prefill_attention_kernel(PrefillArgs p) {
     v = __builtin_fmaxf(v, __shfl_xor(v, 16));
     return __builtin_fmaxf(v, __shfl_xor(v, 32));
   };
-  // FIRST: the block fixes m (the row's maximum of these keys); CHECK: flag a
-  // score past m + kPfHeadroom
-  auto block = [&](auto masked_tag, auto first_tag, auto check_tag, int st, int key0, int kb) {
+  // FIRST: the block fixes m (the row's maximum of these keys)
+  auto block = [&](auto masked_tag, auto first_tag, int st, int key0, int kb) {
     constexpr bool MASKED = decltype(masked_tag)::value;
     constexpr bool FIRST = decltype(first_tag)::value;
-    constexpr bool CHECK = decltype(check_tag)::value;
     float y[kPfSets][8];
     scores(masked_tag, st, key0, kb, y);
     const char* vb = reinterpret_cast<const char*>(&s_v[st][0]) + 256 * 32 * kb;
@@ -1845,11 +1844,7 @@ prefill_attention_kernel(PrefillArgs p) {
     // held in registers
 #pragma unroll
     for (int s = 0; s < kPfSets; ++s) {
-      if constexpr (FIRST) {
-        m[s] = live_row[s] ? __builtin_fmaxf(row_max(lane_max(y[s])), kNegBig) : kBig;
-      } else if constexpr (CHECK) {
-        ex |= lane_max(y[s]) > m[s] + kPfHeadroom;
-      }
+      if constexpr (FIRST) m[s] = live_row[s] ? __builtin_fmaxf(row_max(lane_max(y[s])), kNegBig) : kBig;
       // P = hi + lo: hi the top 16 bits of p (a bf16 value), lo = p - hi
       // (exact in fp32) rounded to bf16; hi + lo carries ~16 bits of p
       float pv[8], ps = 0.0f;
@@ -1903,8 +1898,8 @@ prefill_attention_kernel(PrefillArgs p) {
   using T = std::true_type;
   using F = std::false_type;
   // one stage's 32-key blocks.  MODE 0: the pass with m fixed by the first
-  // block (FIRST) and the headroom check; 1: the maxima of a redo; 2: the
-  // accumulation of a redo (m exact, no check)
+  // block (FIRST); 1: the maxima of a redo; 2: the accumulation of a redo (m
+  // exact)
   auto run_stage = [&](auto mode, auto masked_tag, auto first_tag, int st, int t) {
     constexpr int MODE = decltype(mode)::value;
 #pragma unroll
@@ -1914,9 +1909,9 @@ prefill_attention_kernel(PrefillArgs p) {
       if constexpr (MODE == 1) {
         block_max(masked_tag, st, key0, kb);
       } else if (kb == 0) {
-        block(masked_tag, first_tag, std::integral_constant<bool, MODE == 0>{}, st, key0, kb);
+        block(masked_tag, first_tag, st, key0, kb);
       } else {
-        block(masked_tag, F{}, std::integral_constant<bool, MODE == 0>{}, st, key0, kb);
+        block(masked_tag, F{}, st, key0, kb);
       }
     }
   };
@@ -1964,6 +1959,9 @@ prefill_attention_kernel(PrefillArgs p) {
   };
   reset(kNegBig);
   stream(std::integral_constant<int, 0>{});
+  bool ex = false;  // NaN shares also fail the test
+#pragma unroll
+  for (int s = 0; s < kPfSets; ++s) ex |= !(l[s] < __builtin_ldexpf(1.0f, int(kPfHeadroom)));
   if (__syncthreads_or(ex ? 1 : 0)) {
     // a score past the headroom: exact maxima, then the accumulation again
     reset(kNegBig);
