@@ -218,3 +218,15 @@ def test_prefill_page_stride_past_32_bits(dev):
     vmax = float(np.abs(O.e4m3fn_to_f32(raw(pages[:, 1]))).max())
     err = np.abs(got.double().cpu().numpy() - exp)
     assert (err <= 3e-4 * vmax + 1e-4 * np.abs(exp)).all(), f"max err {err.max():.3e}"
+
+
+def test_prefill_more_sequences_than_the_pre_pass_orders(dev):
+    """1100 sequences of 2 to 4 query tokens (past the pre-pass's 1024, which
+    then keeps batch order; the block search takes two rounds), a few of them
+    without query tokens."""
+    rng = np.random.default_rng(907)
+    counts = [int(x) for x in rng.integers(2, 5, 1100)]
+    for b in (5, 600, 1099):
+        counts[b] = 0
+    lens = [c + int(p) for c, p in zip(counts, rng.integers(0, 60, 1100))]
+    _prefill_case(dev, 907, lens, counts, 32, 4, 16, True)
