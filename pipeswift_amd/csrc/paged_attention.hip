@@ -1719,7 +1719,7 @@ prefill_attention_kernel(PrefillArgs p) {
   // Softmax state per row set.  m is fixed by the row's first 32 keys and
   // never raised, so the hot loop has no rescale and checks nothing: while
   // every lane's share of a row's sum stays below 2^kPfHeadroom, every p
-  // (each below that too), sum and accumulator is finite and exact.  A score
+  // (each below that too), sum and accumulator is finite.  A score
   // far above the first keys' maximum makes a share reach it (or overflow),
   // and the workgroup then redoes the row with exact maxima: a pass for the
   // maxima, then the accumulation again.  Rows without a query token keep
