@@ -1546,9 +1546,14 @@ constexpr int kPfSets = 2;
 constexpr int kPfRows = kPfWaves * kPfSets * 16;
 constexpr int kPfKeys = 64;  // keys per LDS stage
 constexpr int kPfThreads = kPfWaves * 64;
-constexpr int kPfLoads = kPfKeys * 8 / kPfThreads;  // 16-byte chunks of K (and of V) per thread per stage
-static_assert(kPfKeys % 32 == 0 && kPfLoads >= 1 && kPfLoads * kPfThreads == kPfKeys * 8,
-              "a stage is whole 32-key blocks, its chunks spread evenly over the threads");
+// The first wave of each SIMD loads, converts and stores the stages.  Waves
+// w and w + kPfWaves / 2 share a SIMD; the older one issues first and ends
+// its blocks of a stage about a quarter of a stage early, so giving it all
+// the staging work evens the two out at the barrier.
+constexpr int kPfLoaders = kPfThreads / 2;
+constexpr int kPfLoads = kPfKeys * 8 / kPfLoaders;  // 16-byte chunks of K (and of V) per loader per stage
+static_assert(kPfKeys % 32 == 0 && kPfLoads >= 1 && kPfLoads * kPfLoaders == kPfKeys * 8,
+              "a stage is whole 32-key blocks, its chunks spread evenly over the loaders");
 
 constexpr int kPfSortMax = 1024;  // sequences the pre-pass orders by length (more: batch order)
 
@@ -1741,11 +1746,13 @@ prefill_attention_kernel(PrefillArgs p) {
     }
   };
 
-  // loads: chunk i = threadIdx.x + u * kPfThreads of a stage (u < kPfLoads)
-  // is 16-byte chunk i & 7 of key i >> 3, of K and of V; keys past key_end
-  // and rows on missing pages load as zeros
+  // loads, by the loader waves (threads below kPfLoaders): chunk i =
+  // threadIdx.x + u * kPfLoaders of a stage (u < kPfLoads) is 16-byte chunk
+  // i & 7 of key i >> 3, of K and of V; keys past key_end and rows on
+  // missing pages load as zeros
   const int lc = int(threadIdx.x) & 7;
-  auto lkey = [&](int u) { return (int(threadIdx.x) + u * kPfThreads) >> 3; };
+  auto lkey = [&](int u) { return (int(threadIdx.x) + u * kPfLoaders) >> 3; };
+  const bool loader = wave < kPfLoaders / 64;
   const int32_t* bt_row = a.block_table + int64_t(b) * a.bt_stride;
   // the table entry as stored (range-checked where it is used, a stage
   // later: a check here would wait for the load, and with it for the K/V
@@ -1920,7 +1927,7 @@ prefill_attention_kernel(PrefillArgs p) {
     int32_t pid_next[kPfLoads];
 #pragma unroll
     for (int u = 0; u < kPfLoads; ++u) pid_next[u] = -1;
-    if (n_tiles > 0) {
+    if (n_tiles > 0 && loader) {
       int32_t pid0[kPfLoads];
 #pragma unroll
       for (int u = 0; u < kPfLoads; ++u) {
@@ -1934,7 +1941,7 @@ prefill_attention_kernel(PrefillArgs p) {
     }
     __syncthreads();
     auto stage = [&](int t, auto masked_tag, auto first_tag) {
-      const bool more = t + 1 < n_tiles;
+      const bool more = t + 1 < n_tiles && loader;
       if (more) {
 #pragma unroll
         for (int u = 0; u < kPfLoads; ++u) fetch(t + 1, u, pid_next[u], kr[u], vr[u]);
