@@ -16,7 +16,9 @@
  *   byte = e4m3fn_rne(min(m, 448)) | (sign(x) ^ sign(s))
  *          (min: the kernel's unsigned min on the bits of m >= +0 or NaN,
  *           the same as IEEE minNum there: NaN and +inf -> 448)
- *   NaN quotient (fast: x is NaN; else: m is NaN) -> policy byte:
+ *   NaN quotient (fast: the bits of y read as unsigned exceed +inf's, i.e.
+ *   y is NaN, which with r finite and positive is exactly x NaN; else: m is
+ *   NaN) -> policy byte:
  *          0xFE (clamp_min, the reference's Triton clamp) or 0x7F | sign(x) (torch)
  * The IEEE path: q = x / s; NaN -> the same policy byte; else
  *   byte = e4m3fn_rne(clamp(q, -448, 448)).
@@ -119,7 +121,7 @@ static inline uint8_t kernel_byte(float x, const qscale* q, int policy, float* m
       const float e = fmaf(-y, q->s, a);
       m = fmaf(e, q->r, y);
     }
-    nanq = isnan(x);
+    nanq = fbits(y) > 0x7F800000u;
   } else {
     m = fabsf(x) / q->s;
     nanq = isnan(m);

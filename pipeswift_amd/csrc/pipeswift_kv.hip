@@ -283,9 +283,10 @@ __global__ void __launch_bounds__(64 * WPB) paged_append_small_kernel(SmallAppen
 // dominant cost.  Here the lanes are packed over the flat (token, vector)
 // space of both parts -- vector j of token t is number t * V + j, the first
 // V0 from part 0 -- so every lane of every wave moves a vector.  Each lane
-// loads its U vectors, then its tokens' slots (a lane-varying load; lanes of
-// one token share the line), then stores.  Both parts write one cache (same
+// loads its tokens' slots (a lane-varying load; lanes of one token share the
+// line), then its U vectors, then stores.  Both parts write one cache (same
 // block and slot strides) with one scale, as the MLA entry passes them.
+//
 // a * b for a, b < 2^24, product taken modulo 2^32 (v_mul_u32_u24: full rate)
 __device__ __forceinline__ uint32_t mul24(uint32_t a, uint32_t b) { return uint32_t(__umul24(a, b)); }
 
@@ -298,9 +299,9 @@ __global__ void __launch_bounds__(256) packed_row_scatter_kernel(ScatterGeom g, 
   const int lane = threadIdx.x & (kWave - 1);
   const uint32_t wave = blockIdx.x * 4u + uint32_t(__builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave));
   const uint32_t total = uint32_t(g.num_tokens) * uint32_t(V);
-  typename C::In v[U];
   uint32_t tok[U];
   int vec[U];
+  const char* src[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const uint32_t f = wave * uint32_t(kWave * U) + uint32_t(u * kWave + lane);
@@ -309,38 +310,49 @@ __global__ void __launch_bounds__(256) packed_row_scatter_kernel(ScatterGeom g, 
     const int j = int(fc - tok[u] * uint32_t(V));
     vec[u] = f < total ? j : -1;
     const bool first = j < V0;
-    const char* src;
     if constexpr (NARROW) {
       const uint32_t stride = uint32_t(first ? p0.src_stride : p1.src_stride);
-      src = (first ? p0.src : p1.src) + (mul24(tok[u], stride) + uint32_t(first ? j : j - V0) * C::IN_B);
+      src[u] = (first ? p0.src : p1.src) + (mul24(tok[u], stride) + uint32_t(first ? j : j - V0) * C::IN_B);
     } else {
-      src = first ? p0.src + int64_t(tok[u]) * p0.src_stride + int64_t(j) * C::IN_B
-                  : p1.src + int64_t(tok[u]) * p1.src_stride + int64_t(j - V0) * C::IN_B;
+      src[u] = first ? p0.src + int64_t(tok[u]) * p0.src_stride + int64_t(j) * C::IN_B
+                     : p1.src + int64_t(tok[u]) * p1.src_stride + int64_t(j - V0) * C::IN_B;
     }
-    v[u] = vload_nt<C::IN_B>(src);
   }
+  // The slots load before the rows: loads return in order, so the store
+  // offsets are formed while the rows are still in flight.
   int64_t slot[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) slot[u] = g.slots[tok[u]];
-  const QScale qs = make_qscale_uniform(p0.scale ? *p0.scale : 1.0f);
+  typename C::In v[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) v[u] = vload_nt<C::IN_B>(src[u]);
+  QScale qs = make_qscale_uniform(p0.scale ? *p0.scale : 1.0f);
+  // The empty asm statements keep the reciprocal's division and the store
+  // offsets here, under the row loads: left alone, the compiler moves both
+  // into the store's branch, behind the wait for the rows.
+  asm volatile("" : "+v"(qs.r));
+  char* dst[U];
+  bool ok[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int j = vec[u];
-    if (j >= 0 && uint64_t(slot[u]) < uint64_t(g.num_slots)) {
-      char* dst;
-      if constexpr (NARROW) {
-        const uint32_t s32 = uint32_t(slot[u]);
-        const uint32_t o = j < V0 ? uint32_t(j) * C::OUT_B : uint32_t(p1.dst_off) + uint32_t(j - V0) * C::OUT_B;
-        dst = p0.dst + (mul24(s32 >> g.bs_shift, uint32_t(p0.blk_stride)) +
-                        mul24(s32 & uint32_t(g.block_size - 1), uint32_t(p0.page_stride)) + o);
-      } else {
-        const int64_t sl = slot[u];
-        const int64_t o = j < V0 ? int64_t(j) * C::OUT_B : p1.dst_off + int64_t(j - V0) * C::OUT_B;
-        dst = p0.dst + (sl >> g.bs_shift) * p0.blk_stride + (sl & (g.block_size - 1)) * p0.page_stride + o;
-      }
-      vstore_nt<C::OUT_B>(dst, C::apply(v[u], qs));
+    ok[u] = j >= 0 && uint64_t(slot[u]) < uint64_t(g.num_slots);
+    if constexpr (NARROW) {
+      const uint32_t s32 = uint32_t(slot[u]);
+      const uint32_t o = j < V0 ? uint32_t(j) * C::OUT_B : uint32_t(p1.dst_off) + uint32_t(j - V0) * C::OUT_B;
+      uint32_t off = mul24(s32 >> g.bs_shift, uint32_t(p0.blk_stride)) +
+                     mul24(s32 & uint32_t(g.block_size - 1), uint32_t(p0.page_stride)) + o;
+      asm volatile("" : "+v"(off));
+      dst[u] = p0.dst + off;
+    } else {
+      const int64_t sl = slot[u];
+      const int64_t o = j < V0 ? int64_t(j) * C::OUT_B : p1.dst_off + int64_t(j - V0) * C::OUT_B;
+      dst[u] = p0.dst + (sl >> g.bs_shift) * p0.blk_stride + (sl & (g.block_size - 1)) * p0.page_stride + o;
     }
   }
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    if (ok[u]) vstore_nt<C::OUT_B>(dst[u], C::apply(v[u], qs));
 }
 
 // The packed launch applies to the quantizing append of flat two-part rows of

@@ -288,29 +288,21 @@ struct QuantConv {
     float m[E];
     bool any_nan = false;
     if (__builtin_expect(qs.fast, 1)) {
-      if constexpr (EltT::kSize == 2 && E >= 2) {
-        // NaN inputs, from the raw 16-bit words: |h| above the infinity's bits.
-        // A packed 16-bit integer max over the words, then one test per half
-        // (a per-element float compare costs one instruction per element plus
-        // the per-lane bookkeeping of each result).
-        typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
-        constexpr uint16_t kInf = IN_DT == PSK_DTYPE_BF16 ? 0x7F80u : 0x7C00u;
-        uint32_t w[E / 2];
-        __builtin_memcpy(w, &v, sizeof(w));
-        u16x2 mx = __builtin_bit_cast(u16x2, w[0] & 0x7FFF7FFFu);
-#pragma unroll
-        for (int k = 1; k < E / 2; ++k) mx = __builtin_elementwise_max(mx, __builtin_bit_cast(u16x2, w[k] & 0x7FFF7FFFu));
-        any_nan = (mx.x > kInf) | (mx.y > kInf);
-      }
+      // NaN inputs: with r finite and positive, y = |x| r is NaN exactly
+      // when x is (an infinite x gives an infinite y), and y's bits read as
+      // unsigned exceed the infinity's only for a NaN -- one integer maximum
+      // over the y (three-input v_max3_u32), then one compare
+      uint32_t ymax = 0;
 #pragma unroll
       for (int i = 0; i < E; ++i) {
         const float x = EltT::to_f32(e[i]);
-        if constexpr (!(EltT::kSize == 2 && E >= 2)) any_nan |= __builtin_isnan(x);
         const float a = __builtin_fabsf(x);
         const float y = a * qs.r;
+        ymax = __builtin_elementwise_max(ymax, __float_as_uint(y));
         const float r = __builtin_fmaf(-y, qs.s, a);
         m[i] = __builtin_fmaf(r, qs.r, y);
       }
+      any_nan = ymax > 0x7F800000u;
     } else {
       // scales outside [2^-80, 2^100) (0, inf, NaN, subnormal): IEEE division.
       // The empty volatile asm keeps this a branch: otherwise the compiler
