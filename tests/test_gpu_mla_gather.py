@@ -88,6 +88,34 @@ def test_mla_fp8_append_wide_block_stride(dev):
     assert not got[:, ps * 576 :].any()
 
 
+@pytest.mark.parametrize("scale", [1.0, 0.0371, -0.5, 2.0 ** -90])
+def test_mla_fp8_prefill_every_bf16_pattern(dev, scale):
+    """Every bf16 bit pattern (NaNs, infinities, subnormals, signed zeros)
+    through the packed FP8 MLA append (1152 tokens: the prefill-sized launch),
+    k_pe a column slice of the latent, at scales on the quantizer's fast
+    path, negative, and below its range (the IEEE division); whole cache
+    against the oracle."""
+    rng = np.random.default_rng(36)
+    n, P, ps = 1152, 24, 64
+    pats = np.tile(np.arange(65536, dtype=np.uint16), (n * 576) // 65536 + 1)[: n * 576]
+    rng.shuffle(pats)
+    rows = pats.reshape(n, 576)
+    latent = np.zeros((n, 2112), np.uint16)
+    latent[:, 2048:] = rows[:, 512:]
+    latent_t = torch.from_numpy(latent.view(np.int16)).view(torch.bfloat16)
+    ckv_t = torch.from_numpy(np.ascontiguousarray(rows[:, :512]).view(np.int16)).view(torch.bfloat16)
+    slots = torch.from_numpy(rng.permutation(P * ps)[:n].astype(np.int64))
+    slots[::19] = -1
+    cache = torch.zeros(P, ps, 1, 576, dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
+    sc = torch.tensor([scale], dtype=torch.float32, device=dev)
+    print(f"mla fp8 every bf16 pattern: N={n} scale={scale}", flush=True)
+    ld = latent_t.to(dev)
+    reshape_and_cache_flash_diffkv(ckv_t.to(dev).unsqueeze(1), ld[:, 2048:].unsqueeze(1), cache, slots.to(dev), sc)
+    exp = np.zeros((P, ps, 576), np.uint8)
+    O.concat_and_cache_mla(raw(ckv_t), raw(latent_t[:, 2048:]), exp, slots.numpy(), "bf16", "fp8", scale)
+    assert np.array_equal(raw(cache.cpu()).reshape(P, ps, 576), exp)
+
+
 def test_mla_through_append_mla_kv_cache(dev):
     L, P, ps = 2, 300, 64
     mla = workloads.sentinel((L, P, ps, 576), torch.bfloat16, 31)
