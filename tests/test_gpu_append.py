@@ -224,6 +224,34 @@ def test_fp8_nan_policy(dev):
         assert raw(cache)[:, 0].reshape(-1).tolist() == want, scale
 
 
+@pytest.mark.parametrize("scale", [1.0, 7.77, -0.25, 1e-39])
+def test_fp8_prefill_sized_every_bf16_pattern(dev, scale):
+    """Every bf16 bit pattern (128 times each) through the prefill-sized FP8
+    append: 4096 tokens of 8 x 128 K and V as column slices of 6144-wide qkv
+    rows into 16-token pages in random order (the multi-token-per-wave
+    scatter kernel), V at three times K's scale; whole cache against the
+    oracle."""
+    rng = np.random.default_rng(37)
+    N, H, D, P, ps = 4096, 8, 128, 512, 16
+    pats = np.tile(np.arange(65536, dtype=np.uint16), (2 * N * H * D) // 65536)
+    rng.shuffle(pats)
+    qkv = np.zeros((N, 6144), np.uint16)
+    qkv[:, 4096:] = pats.reshape(N, 2 * H * D)
+    qkv_t = torch.from_numpy(qkv.view(np.int16)).view(torch.bfloat16).to(dev)
+    k, v = qkv_t[:, 4096:5120].view(N, H, D), qkv_t[:, 5120:].view(N, H, D)
+    slots = torch.from_numpy(rng.permutation(P * ps)[:N].astype(np.int64))
+    slots[::23] = -1
+    cache = torch.zeros(P, 2, ps, H, D, dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
+    ks = torch.tensor([scale], dtype=torch.float32, device=dev)
+    vs = torch.tensor([scale * 3.0], dtype=torch.float32, device=dev)
+    print(f"fp8 prefill-sized every bf16 pattern: N={N} scale={scale}", flush=True)
+    reshape_and_cache_flash(k, v, cache[:, 0], cache[:, 1], slots.to(dev), ks, vs)
+    exp = np.zeros((P, 2, ps, H, D), np.uint8)
+    O.reshape_and_cache(raw(k), raw(v), exp[:, 0], exp[:, 1], slots.numpy(), "bf16", "fp8",
+                        float(ks.cpu()), float(vs.cpu()))
+    assert np.array_equal(raw(cache), exp)
+
+
 def test_config2_fp8_decode_whole_cache(dev):
     """65536-block E4M3 cache (2 GiB fused; 64-bit offsets), scales from the
     amax kernel, whole-cache compare."""
