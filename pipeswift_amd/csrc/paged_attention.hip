@@ -1524,8 +1524,9 @@ __global__ void __launch_bounds__(64 * kCombineMaxWaves) decode_combine_kernel(D
 // i0 + r / G, query head g = r % G of the block's tq = kPfRows / G tokens, so
 // every K/V row of the block's keys is read from the cache once per tq query
 // tokens.  The keys stream through two LDS stages of kPfKeys keys, filled by
-// every thread (one 16-byte chunk of K and one of V each, converted once to
-// bf16, exactly) and consumed by every wave, as 256-byte rows:
+// the first wave of each SIMD (two 16-byte chunks of K and two of V per
+// thread, converted once to bf16, exactly) and consumed by every wave, as
+// 256-byte rows:
 //   * K: 16-byte chunk c of key t at chunk c ^ (t & 15), so the lanes of one
 //     ds_read_b128 phase (consecutive keys, one chunk) hit distinct banks;
 //   * V: chunk c of key t at c ^ (2 (t & 7)), read transposed by
