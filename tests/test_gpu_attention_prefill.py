@@ -230,3 +230,40 @@ def test_prefill_more_sequences_than_the_pre_pass_orders(dev):
         counts[b] = 0
     lens = [c + int(p) for c, p in zip(counts, rng.integers(0, 60, 1100))]
     _prefill_case(dev, 907, lens, counts, 32, 4, 16, True)
+
+
+def test_prefill_bench_step_matches_decode_reader(dev):
+    """The bench's prefill_attention step at full size (config 3 geometry:
+    4096 query tokens over 6 sequences with 14k-45k cached keys, 32 query
+    heads over 4 kv heads, random FP8 pages, per-tensor descales, the bench's
+    seeds): the prefill kernel against the decode reader over 2-token chunks
+    of the same step, float32 outputs.  Two independent kernels, each pinned
+    to the oracle at smaller sizes, agree to 1e-3 of the largest output."""
+    import workloads
+
+    cc = workloads.config3_chunked()
+    H, D, Hq, ps = 4, 128, 32, 16
+    P = cc.append.cache.shape[0]
+    g = torch.Generator(device=dev).manual_seed(76)
+    cache = (torch.randn((P, 2, ps, H, D), device=dev, generator=g) * 2.0).to(torch.float8_e4m3fn)
+    kc, vc = cache[:, 0], cache[:, 1]
+    bt = cc.block_table.to(dev)
+    N = int(cc.chunk.sum())
+    cu = torch.zeros(len(cc.chunk) + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(cc.chunk, 0).to(torch.int32)
+    cu = cu.to(dev)
+    lens = (cc.prefix + cc.chunk).to(torch.int32).to(dev)
+    q = (torch.randn(N, Hq, D, device=dev, generator=g) * 2.0).to(torch.bfloat16)
+    kd = torch.tensor([0.01], dtype=torch.float32, device=dev)
+    vd = torch.tensor([0.02], dtype=torch.float32, device=dev)
+    maxq = int(cc.chunk.max())
+    print(f"prefill bench step: N={N} keys={int(lens.sum())} P={P}", flush=True)
+    a = torch.empty(N, Hq, D, dtype=torch.float32, device=dev)
+    b = torch.empty_like(a)
+    attention.paged_prefill_attention(q, kc, vc, bt, lens, cu, maxq, D ** -0.5, None, kd, vd, out=a, causal=True)
+    attention.chunked_prefill_attention(q, kc, vc, maxq, cu, lens, bt, softmax_scale=D ** -0.5, causal=True,
+                                        k_descale=kd, v_descale=vd, out=b)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(a).all())
+    ref = float(b.abs().max())
+    assert ref > 0.0 and float((a - b).abs().max()) <= 1e-3 * ref
