@@ -1886,6 +1886,16 @@ prefill_attention_kernel(PrefillArgs p) {
         o[s][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, lo, o[s][c], 0, 0, 0);
       }
     }
+    // Ask the scheduler to alternate one MFMA with up to four VALU
+    // instructions over the block's 48 MFMAs, so that each wave's softmax
+    // issues under its own matrix work as well as under the other wave's:
+    // 2-3 % faster on three boxes (2.55-2.65 ms against 2.60-2.71 without;
+    // one MFMA to two VALU: slower; to five: slower; to six or eight: level).
+#pragma unroll
+    for (int i = 0; i < 48; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // up to four VALU
+    }
   };
   // the maxima pass of a redo: the lane's largest scaled score per set into m
   auto block_max = [&](auto masked_tag, int st, int key0, int kb) {
