@@ -45,7 +45,8 @@ torch CPU baseline:
 
 Output: plain-text progress lines, then ONE compact JSON result line, the
 last line of the run (nothing is written to stderr).  The full per-workload
-records go to --detail (default gpurun_out/bench_detail.json).  Each record
+records go to the --detail file (by default bench_detail.json in the output
+folder that the box's results are copied back from).  Each record
 carries:
   value            algorithmic HBM GB/s (bytes the kernel must move / time)
   roofline         the same per launch against MI355X's 8 TB/s peak, the HBM
