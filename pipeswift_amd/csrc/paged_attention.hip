@@ -1891,8 +1891,9 @@ prefill_attention_kernel(PrefillArgs p) {
     // issues under its own matrix work as well as under the other wave's:
     // 2-3 % faster on three boxes (2.55-2.65 ms against 2.60-2.71 without;
     // one MFMA to two VALU: slower; to five: slower; to six or eight: level).
+    constexpr int kBlockMfmas = kPfSets * (8 + 16);  // per set: S^T 2 x 4, then P V 8 x (hi, lo)
 #pragma unroll
-    for (int i = 0; i < 48; ++i) {
+    for (int i = 0; i < kBlockMfmas; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
       __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // up to four VALU
     }
