@@ -373,8 +373,8 @@ def setup_prefill_attention(args, device):
     FP8 pages, causal, per-tensor descales, through ``flash_attn_varlen_func``
     as the reference's ``_fp8_paged_attn`` calls it for prefill (the prefill
     kernel).  MFMA-bound: algorithmic FLOPs are 4 * 128 per visible (query
-    head, key) pair (Q K^T and P V, 2 * 128 each), counted once; the kernel's
-    bf16 hi + lo split of P runs P V twice on the matrix cores.  Algorithmic
+    head, key) pair (Q K^T and P V, 2 * 128 each), counted once, as the
+    kernel runs them (P V once, on fp16 P).  Algorithmic
     bytes: every sequence's K and V rows once, the page ids, the bf16 queries
     and outputs.  ``--chunked`` times the decode reader over 2-token chunks of
     the same step instead."""

@@ -213,8 +213,10 @@ def paged_prefill_attention(
     sequence, at most ``max_seqlen_q`` each, and up to 256 query heads per kv
     head.  One workgroup per (kv head, block of 256 / (Hq / Hkv) query tokens
     of one sequence) streams the sequence's keys once for the whole block
-    through LDS; Q K^T and P V run on the bf16 MFMA over exactly converted FP8
-    values, P in bf16 hi + lo parts, fp32 sums.  ``workspace``: int32 of at
+    through LDS; Q K^T runs on the bf16 MFMA over exactly converted FP8
+    values and P V on the fp16 MFMA with V exact and P rounded once to fp16
+    (at most (2^-11 + K 2^-25) max|V vd| more error for K keys), fp32 sums.
+    ``workspace``: int32 of at
     least ``prefill_workspace_words(B)`` (allocated when absent).  The ragged
     layout contract, and ``validate``, are ``paged_decode_attention``'s."""
     assert q.is_cuda and k_cache.is_cuda and v_cache.is_cuda

@@ -64,6 +64,8 @@ namespace {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kHead = 128;    // head_dim of the MFMA tiling
 constexpr int kTile = 16;     // tokens per tile (N of the 16x16x32 MFMA)
@@ -147,6 +149,16 @@ __device__ __forceinline__ bf16x8 e4m3x8_to_bf16(uint32_t w0, uint32_t w1) {
   const bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false);
   const bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true);
   return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+// The same to fp16, exactly: E4M3FN's 3-bit mantissas and exponents 2^-9 ..
+// 2^8 (448 at most) all lie in fp16's range and precision.
+__device__ __forceinline__ f16x8 e4m3x8_to_f16(uint32_t w0, uint32_t w1) {
+  const f16x2 a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, false);
+  const f16x2 b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, true);
+  const f16x2 c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, false);
+  const f16x2 d = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, true);
+  return f16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
 
 template <int CTRL>
@@ -1525,16 +1537,18 @@ __global__ void __launch_bounds__(64 * kCombineMaxWaves) decode_combine_kernel(D
 // every K/V row of the block's keys is read from the cache once per tq query
 // tokens.  The keys stream through two LDS stages of kPfKeys keys, filled by
 // the first wave of each SIMD (two 16-byte chunks of K and two of V per
-// thread, converted once to bf16, exactly) and consumed by every wave, as
-// 256-byte rows:
+// thread, converted once, exactly, K to bf16 and V to fp16) and consumed by
+// every wave, as 256-byte rows:
 //   * K: 16-byte chunk c of key t at chunk c ^ (t & 15), so the lanes of one
 //     ds_read_b128 phase (consecutive keys, one chunk) hit distinct banks;
 //   * V: chunk c of key t at c ^ (2 (t & 7)), read transposed by
 //     ds_read_b64_tr_b16 (four keys of one column per lane and read).
 // Per 32 keys and 16 rows: S^T = K Q^T on v_mfma_f32_16x16x32_bf16 (two
 // 16-key tiles, four MFMAs each, exactly converted FP8 operands as in the
-// decode reader), the softmax in the exp2 domain, then O^T = V^T P^T on the
-// same MFMA with P split into bf16 hi + lo.  Transposed products leave each
+// decode reader), the softmax in the exp2 domain, then O^T = V^T P^T on
+// v_mfma_f32_16x16x32_f16 with P rounded to fp16 once (11 significant bits,
+// where the decode reader keeps ~16 in a bf16 hi + lo pair and runs P V
+// twice; FA3's FP8 path keeps 4).  Transposed products leave each
 // lane one query row (lane % 16): its scores, maximum and sum, and output
 // columns 16 b + 4 (lane / 16) + r.  The 32-key MFMA step takes as its
 // k = 8 s + j (s = lane / 16) key 4 s + j of the first 16-key tile for j < 4
@@ -1674,7 +1688,7 @@ __global__ void __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu
 prefill_attention_kernel(PrefillArgs p) {
   const DecodeArgs& a = p.a;
   __shared__ u32x4 s_k[2][kPfKeys * 16];  // bf16 K rows, chunk c of key t at c ^ (t & 15)
-  __shared__ u32x4 s_v[2][kPfKeys * 16];  // bf16 V rows, chunk c of key t at c ^ (2 (t & 7))
+  __shared__ u32x4 s_v[2][kPfKeys * 16];  // fp16 V rows, chunk c of key t at c ^ (2 (t & 7))
   const int lane = int(threadIdx.x) & 63;
   const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
   const int Hkv = a.num_kv_heads;
@@ -1725,12 +1739,13 @@ prefill_attention_kernel(PrefillArgs p) {
   // Softmax state per row set.  m is fixed by the row's first 32 keys and
   // never raised, so the hot loop has no rescale and checks nothing: while
   // every lane's share of a row's sum stays below 2^kPfHeadroom, every p
-  // (each below that too), sum and accumulator is finite.  A score
+  // (each below that too) is a finite fp16 value (at most 65504) and every
+  // sum and accumulator is finite.  A score
   // far above the first keys' maximum makes a share reach it (or overflow),
   // and the workgroup then redoes the row with exact maxima: a pass for the
   // maxima, then the accumulation again.  Rows without a query token keep
   // m = +kBig (every p is 0).
-  constexpr float kPfHeadroom = 94.0f;
+  constexpr float kPfHeadroom = 15.0f;
   constexpr float kBig = 1.0e30f;
   float m[kPfSets], l[kPfSets];
   f32x4 o[kPfSets][8];
@@ -1784,14 +1799,14 @@ prefill_attention_kernel(PrefillArgs p) {
       vr = *reinterpret_cast<const u32x4*>(vbase + vo);
     }
   };
-  // both as bf16 (exact), converted once here for every wave
+  // K as bf16 and V as fp16 (both exact), converted once here for every wave
   auto stage_store = [&](int st, int u, const u32x4& kr, const u32x4& vr) {
     const int lk = lkey(u);
     const int ks = lk & 15, vs = 2 * (lk & 7);
     s_k[st][lk * 16 + ((2 * lc) ^ ks)] = __builtin_bit_cast(u32x4, e4m3x8_to_bf16(kr[0], kr[1]));
     s_k[st][lk * 16 + ((2 * lc + 1) ^ ks)] = __builtin_bit_cast(u32x4, e4m3x8_to_bf16(kr[2], kr[3]));
-    s_v[st][lk * 16 + ((2 * lc) ^ vs)] = __builtin_bit_cast(u32x4, e4m3x8_to_bf16(vr[0], vr[1]));
-    s_v[st][lk * 16 + ((2 * lc + 1) ^ vs)] = __builtin_bit_cast(u32x4, e4m3x8_to_bf16(vr[2], vr[3]));
+    s_v[st][lk * 16 + ((2 * lc) ^ vs)] = __builtin_bit_cast(u32x4, e4m3x8_to_f16(vr[0], vr[1]));
+    s_v[st][lk * 16 + ((2 * lc + 1) ^ vs)] = __builtin_bit_cast(u32x4, e4m3x8_to_f16(vr[2], vr[3]));
   };
 
   // read side.  K (the A operand of S^T): key kx = lane % 16 of a 16-key
@@ -1853,8 +1868,8 @@ prefill_attention_kernel(PrefillArgs p) {
 #pragma unroll
     for (int s = 0; s < kPfSets; ++s) {
       if constexpr (FIRST) m[s] = live_row[s] ? __builtin_fmaxf(row_max(lane_max(y[s])), kNegBig) : kBig;
-      // P = hi + lo: hi the top 16 bits of p (a bf16 value), lo = p - hi
-      // (exact in fp32) rounded to bf16; hi + lo carries ~16 bits of p
+      // P rounded to fp16 (RNE, relative error <= 2^-11 from 2^-14 up; every
+      // p is below 2^15 in the pass that is kept, see the headroom)
       float pv[8], ps = 0.0f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -1863,17 +1878,11 @@ prefill_attention_kernel(PrefillArgs p) {
         ps += pv[i];
       }
       l[s] += ps;
-      uint32_t hw[4], lw[4];
+      uint32_t pw[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t u0 = __float_as_uint(pv[2 * i]), u1 = __float_as_uint(pv[2 * i + 1]);
-        hw[i] = __builtin_amdgcn_perm(u1, u0, 0x07060302u);
-        const f32x2 lo2 = {pv[2 * i] - __uint_as_float(u0 & 0xFFFF0000u),
-                           pv[2 * i + 1] - __uint_as_float(u1 & 0xFFFF0000u)};
-        lw[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(lo2, bf16x2));
-      }
-      const bf16x8 hi = __builtin_bit_cast(bf16x8, u32x4{hw[0], hw[1], hw[2], hw[3]});
-      const bf16x8 lo = __builtin_bit_cast(bf16x8, u32x4{lw[0], lw[1], lw[2], lw[3]});
+      for (int i = 0; i < 4; ++i)
+        pw[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{pv[2 * i], pv[2 * i + 1]}), f16x2));
+      const f16x8 pop = __builtin_bit_cast(f16x8, u32x4{pw[0], pw[1], pw[2], pw[3]});
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
         const uint32_t off = vrow + uint32_t(16 * ((2 * c + vq) ^ vsw));
@@ -1881,17 +1890,17 @@ prefill_attention_kernel(PrefillArgs p) {
             __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(vb + off));
         const s16x4 t1 =
             __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(vb + 256 * 16 + off));
-        const bf16x8 vop = __builtin_bit_cast(bf16x8, __builtin_shufflevector(t0, t1, 0, 1, 2, 3, 4, 5, 6, 7));
-        o[s][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, hi, o[s][c], 0, 0, 0);
-        o[s][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, lo, o[s][c], 0, 0, 0);
+        const f16x8 vop = __builtin_bit_cast(f16x8, __builtin_shufflevector(t0, t1, 0, 1, 2, 3, 4, 5, 6, 7));
+        o[s][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop, o[s][c], 0, 0, 0);
       }
     }
     // Ask the scheduler to alternate one MFMA with up to four VALU
-    // instructions over the block's 48 MFMAs, so that each wave's softmax
-    // issues under its own matrix work as well as under the other wave's:
-    // 2-3 % faster on three boxes (2.55-2.65 ms against 2.60-2.71 without;
-    // one MFMA to two VALU: slower; to five: slower; to six or eight: level).
-    constexpr int kBlockMfmas = kPfSets * (8 + 16);  // per set: S^T 2 x 4, then P V 8 x (hi, lo)
+    // instructions over the block's 32 MFMAs, so that each wave's softmax
+    // issues under its own matrix work as well as under the other wave's.
+    // With P V run twice (P as bf16 hi + lo) this was 2-3 % faster on three
+    // boxes; with P in fp16, one MFMA to 2, 3 or 4 VALU and no hint measure
+    // within 1.5 % of each other and six VALU 2 % slower.
+    constexpr int kBlockMfmas = kPfSets * (8 + 8);  // per set: S^T 2 x 4, then P V 8
 #pragma unroll
     for (int i = 0; i < kBlockMfmas; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA

@@ -3,11 +3,20 @@ with more query rows per kv head than one MFMA tile of the decode reader
 holds (``max_seqlen_q * Hq / Hkv > 16``), which the reference's
 ``_fp8_paged_attn`` passes for every prefill step (attention.py:577-585).
 Those steps run ``psk_paged_prefill_attention``; its arithmetic per row is
-the decode reader's (exact FP8 -> bf16 operands, fp32 MFMA sums, P in bf16
-hi + lo), and so are the tolerances (see test_gpu_attention.py):
-  * output: |got - oracle| <= 3e-4 * max|V * vd| + 1e-4 * |oracle|
+the decode reader's (exact FP8 -> bf16 Q K^T operands, fp32 MFMA sums) except
+that P V takes P rounded once to fp16 (V exactly as fp16) where the decode
+reader keeps ~16 bits of P in a bf16 hi + lo pair.  The tolerances are the
+decode reader's (see test_gpu_attention.py) plus what the fp16 rounding of
+P can add:
+  * output: |got - oracle| <= 3e-4 * vmax + 1e-4 * |oracle|, vmax = max|V * vd|
     (bf16 output: plus the bf16 rounding of the oracle, 2^-8 |oracle|)
-  * lse:    |got - oracle| <= 5e-4 + 1e-5 * |oracle|
+    + for the prefill kernel (2^-11 + K * 2^-25) * vmax, K the most keys a
+    row sees: each weight p <= 2^15 (relative to the maximum of its row's
+    first 32 keys, whose key has p = 1, so the row's sum l >= 1) rounds with
+    relative error <= 2^-11 from 2^-14 up and absolute error <= 2^-25 below,
+    so sum_i |dp_i| |v_i| / l <= 2^-11 vmax + K 2^-25 vmax
+  * lse:    |got - oracle| <= 5e-4 + 1e-5 * |oracle| (the sum l is taken
+    over the unrounded p)
 The oracle (oracle/kv_oracle.py: paged_decode_attention) runs in float64 over
 the same ragged layout and is pinned against torch SDPA under torch's
 lower-right causal mask.  The decode reader run over chunks of the same step
@@ -86,6 +95,8 @@ def _prefill_case(dev, seed, lens, counts, Hq, Hkv, ps, causal, descales=True, n
     gotn = got[:n].double().cpu().numpy()
     err = np.abs(gotn - exp)
     tol = 3e-4 * vmax + 1e-4 * np.abs(exp)
+    if _runs_prefill_kernel(path, counts, Hq, Hkv):
+        tol = tol + p_rounding_bound(max(lens), vmax)
     if out_dtype == torch.bfloat16:
         tol = tol + 2.0 ** -8 * np.abs(exp)
     assert (err <= tol).all(), f"max err {err.max():.3e} at {np.unravel_index(err.argmax(), err.shape)}"
@@ -96,7 +107,19 @@ def _prefill_case(dev, seed, lens, counts, Hq, Hkv, ps, causal, descales=True, n
     assert (lse_err <= 5e-4 + 1e-5 * np.abs(lse_exp[fin])).all(), f"lse max err {lse_err.max():.3e}"
     if spare_rows:  # rows past the last sequence are not written
         assert bool((got[n:] == 7.0).all())
-    return got
+    return got, vmax
+
+
+def _runs_prefill_kernel(path, counts, Hq, Hkv):
+    """Whether the step runs the prefill kernel (flash_attn_varlen_func's
+    routing: more than 16 query rows per kv head)."""
+    return path == "prefill" or (path == "entry" and max(counts) * max(Hq // Hkv, 1) > 16)
+
+
+def p_rounding_bound(keys, vmax):
+    """What rounding P to fp16 can add to an output of the prefill kernel
+    (the module docstring derives it)."""
+    return (2.0 ** -11 + keys * 2.0 ** -25) * vmax
 
 
 @pytest.mark.parametrize("Hq,Hkv", [(32, 8), (64, 8), (8, 8), (16, 1), (32, 1), (6, 2), (256, 2)])
@@ -123,10 +146,12 @@ def test_prefill_block_sizes(dev, ps):
     the same step (with an explicit split count) agrees as well."""
     counts = [40, 0, 130, 17, 0, 64]
     lens = [40 + 300, 12, 130, 17 + 5, 0, 64 + 1000]
-    a = _prefill_case(dev, 600 + ps, lens, counts, 32, 8, ps, True, spare_rows=5)
-    b = _prefill_case(dev, 600 + ps, lens, counts, 32, 8, ps, True, spare_rows=5, path="chunks", num_splits=3)
+    a, vmax = _prefill_case(dev, 600 + ps, lens, counts, 32, 8, ps, True, spare_rows=5)
+    b, _ = _prefill_case(dev, 600 + ps, lens, counts, 32, 8, ps, True, spare_rows=5, path="chunks", num_splits=3)
     n = sum(counts)
-    assert float((a[:n] - b[:n]).abs().max()) <= 1e-3
+    # each within its tolerance of the oracle, so within their sum of each other
+    bound = 2 * (3e-4 * vmax + 1e-4 * float(b[:n].abs().max())) + p_rounding_bound(max(lens), vmax)
+    assert float((a[:n] - b[:n]).abs().max()) <= bound
 
 
 def test_prefill_group_16_over_1100_tokens(dev):
@@ -176,7 +201,7 @@ def test_prefill_long_prefix(dev):
 
 def test_prefill_steep_scores_take_the_exact_redo(dev):
     """Scores spread over hundreds of binary orders of magnitude (softmax
-    scale 4): rows pass the prefill kernel's 2^64 headroom above the maximum
+    scale 4): rows pass the prefill kernel's 2^15 headroom above the maximum
     of their first 32 keys, so their workgroups recompute with exact row
     maxima; results still match the float64 oracle."""
     _prefill_case(dev, 903, [700, 90, 1500], [300, 90, 64], 32, 4, 16, True, scale=4.0)
@@ -217,7 +242,47 @@ def test_prefill_page_stride_past_32_bits(dev):
                                       128 ** -0.5, cu_seqlens_q=cu.numpy(), causal=True)
     vmax = float(np.abs(O.e4m3fn_to_f32(raw(pages[:, 1]))).max())
     err = np.abs(got.double().cpu().numpy() - exp)
-    assert (err <= 3e-4 * vmax + 1e-4 * np.abs(exp)).all(), f"max err {err.max():.3e}"
+    assert (err <= 3e-4 * vmax + p_rounding_bound(L, vmax) + 1e-4 * np.abs(exp)).all(), f"max err {err.max():.3e}"
+
+
+def test_prefill_weights_at_the_edge_of_fp16(dev):
+    """A key 2^14.9, 2^15.8 and 2^17 times heavier than the first 32 keys of
+    its row (one sequence each): the first weight is a large but finite fp16
+    value on the pass without rescale; the second is finite in fp16 but past
+    the 2^15 headroom, and the third overflows fp16, so those workgroups
+    must take the exact redo.  Scores are q~0 * K0 * kd in the exp2 domain
+    (softmax scale ln 2, every other q and K element 0): K0 = 16 at key 40
+    of 64 and 0 elsewhere, q~0 the E4M3 query from -1 to 1 over a sequence's
+    rows, kd = 14.9/16, 15.8/16, 17/16 by sequence.  Results match the
+    float64 oracle, finite everywhere."""
+    ps, D, L, n = 16, 128, 64, 20
+    g = torch.Generator().manual_seed(908)
+    P = 3 * L // ps + 2
+    kf = torch.zeros(P, ps, 1, D)
+    for b in range(3):
+        kf[b * 4 + 2, 40 - 32, 0, 0] = 16.0  # key 40 of sequence b (page 2 of its 4)
+    kc8 = kf.to(torch.float8_e4m3fn)
+    vc8 = (torch.randn(P, ps, 1, D, generator=g) * 2).to(torch.float8_e4m3fn)
+    q = torch.zeros(3 * n, 1, D)
+    q[:, 0, 0] = torch.linspace(-1.0, 1.0, n).repeat(3)
+    q = q.to(torch.bfloat16)
+    kd = torch.tensor([[14.9 / 16], [15.8 / 16], [17.0 / 16]], dtype=torch.float32)
+    bt = torch.arange(12, dtype=torch.int32).view(3, 4)
+    cu = torch.tensor([0, n, 2 * n, 3 * n], dtype=torch.int32)
+    lens = torch.full((3,), L, dtype=torch.int32)
+    scale = float(np.log(2.0))
+    print("prefill fp16 weight edge: 3 sequences, key 40 at 14.9/15.8/17 binades", flush=True)
+    got = attention.paged_prefill_attention(q.to(dev), kc8.to(dev), vc8.to(dev), bt.to(dev), lens.to(dev), cu.to(dev),
+                                            n, scale, None, kd.to(dev), None,
+                                            out=torch.zeros(3 * n, 1, D, dtype=torch.float32, device=dev),
+                                            causal=False)
+    exp, _ = O.paged_decode_attention(raw(q), "bf16", raw(kc8), raw(vc8), bt.numpy(), lens.numpy(), scale, None,
+                                      kd.numpy(), None, cu_seqlens_q=cu.numpy(), causal=False)
+    gotn = got.double().cpu().numpy()
+    assert np.isfinite(gotn).all()
+    vmax = float(np.abs(O.e4m3fn_to_f32(raw(vc8))).max())
+    err = np.abs(gotn - exp)
+    assert (err <= 3e-4 * vmax + p_rounding_bound(L, vmax) + 1e-4 * np.abs(exp)).all(), f"max err {err.max():.3e}"
 
 
 def test_prefill_more_sequences_than_the_pre_pass_orders(dev):
