@@ -35,6 +35,8 @@ the reference's, call for call.
 from __future__ import annotations
 
 import ctypes
+import functools
+import gc
 import itertools
 import math
 import warnings
@@ -62,6 +64,29 @@ L2_LOAD_CHUNK = 1024
 # and each later one twice the one before, up to the chunk: the link starts
 # after the host has walked 128 pages (~0.2 ms) instead of 1024 (~1.4 ms).
 L2_FIRST_PIECE = 128
+
+
+def _collector_paused(fn):
+    """Run a ledger walk with Python's cyclic garbage collector held off, its
+    previous state restored afterwards (on an error too).  A walk over a long
+    prompt allocates a few containers per page (page keys, restore records);
+    with the collector on, their allocations trigger collections that rescan
+    them and the rest of the heap every few hundred pages, which made a
+    16000-page store or restore walk about 3x slower on the host (114 / 122 ms
+    against 37 / 41 ms).  Reference counting frees objects as usual meanwhile;
+    only the detection of reference cycles waits for the walk to end."""
+
+    @functools.wraps(fn)
+    def run(*args, **kwargs):
+        if not gc.isenabled():
+            return fn(*args, **kwargs)
+        gc.disable()
+        try:
+            return fn(*args, **kwargs)
+        finally:
+            gc.enable()
+
+    return run
 
 
 class _StagedLoads(list):
@@ -708,6 +733,7 @@ class BlockManager(_PagePool):
                 live.append((page_idx, key[0], token_ids))
         return self.l2.submit_stores(self, live)
 
+    @_collector_paused
     def schedule_l2_stores_for_confirmed_seq(self, seq):
         """Store the keyed pages of the sequence's confirmed tokens (:420-431)."""
         if self.l2 is None or seq.seq_id not in self.kv_page_table:
@@ -717,6 +743,7 @@ class BlockManager(_PagePool):
         key_of, tokens_of = self.page_idx2hash, self.page_idx2token_ids
         self.l2.submit_stores(self, [(p, key_of[p], tokens_of[p]) for p in confirmed if key_of[p] != -1])
 
+    @_collector_paused
     def flush_l2_loads(self):
         """Send the staged restores (see _L2Tier.flush_loads); returns the pages."""
         if self.l2 is None or not self.l2.staged_loads:
@@ -788,6 +815,7 @@ class BlockManager(_PagePool):
         seq.l2_probe_resume = (n, max(0, len(pages) - 1))
         return False
 
+    @_collector_paused
     def allocate_prefill(self, seq):
         """Page table for a prompt: the contiguous L1 prefix match (never the
         last page: a sequence must run at least one token), then the L2 matches
@@ -893,6 +921,7 @@ class BlockManager(_PagePool):
             table.append(p)
         return loads
 
+    @_collector_paused
     def deallocate(self, seq):
         """Release every page of the sequence, suffix first, so its suffix is
         evicted before its prefix (:784-794)."""

@@ -700,3 +700,36 @@ def test_random_traces_with_restores_submitted_while_allocating(monkeypatch):
     assert loads and all(len(c[1]) <= 2 for c in loads)
     staged = sum(len(lds) for _, m in runs for _, lds in m._l2_pending_load_requests)
     assert sum(len(c[1]) for c in loads) == sum(m.l2_load_cnt for _, m in runs) + staged
+
+
+def test_ledger_walks_pause_the_collector_and_restore_its_state():
+    """The bulk walks (prefill allocation, store scheduling, restore flush,
+    release) run with Python's cyclic collector held off and leave it as they
+    found it: enabled after a walk, enabled after a walk that raised, and
+    still disabled when it was disabled before."""
+    import gc
+
+    from pipeswift_amd import block_manager as bm
+
+    for name in ("allocate_prefill", "schedule_l2_stores_for_confirmed_seq", "flush_l2_loads", "deallocate"):
+        assert getattr(getattr(bm.BlockManager, name), "__wrapped__", None) is not None, name
+    seen = []
+
+    @bm._collector_paused
+    def walk(fail=False):
+        seen.append(gc.isenabled())
+        if fail:
+            raise RuntimeError("walk failed")
+        return 5
+
+    was = gc.isenabled()
+    try:
+        gc.enable()
+        assert walk() == 5 and seen[-1] is False and gc.isenabled()
+        with pytest.raises(RuntimeError):
+            walk(fail=True)
+        assert seen[-1] is False and gc.isenabled()
+        gc.disable()
+        assert walk() == 5 and seen[-1] is False and not gc.isenabled()
+    finally:
+        (gc.enable if was else gc.disable)()
