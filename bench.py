@@ -152,13 +152,15 @@ def _affine_block_maps(R, num_blocks, gen, device):
 def setup_append(args, device, fp8, rescale=False):
     """Config 1 (bf16) or config 2 (FP8 decode) append.  With ``rescale`` a
     step is the whole FP8 write of a caller that recomputes its per-tensor
-    scales every step: amax -> scale of K and V (two launches), then the fused
-    append (one launch); its bytes add the amax read of K and V."""
+    scales every step: ``reshape_and_cache_flash_amax``, the amax partials of
+    K and V, then the fused append that finishes the scales itself (two
+    launches; before it, amax partials, finalize and append took three); its
+    bytes add the amax read of K and V."""
     import torch
 
     import workloads
     from pipeswift_amd import cache_ops
-    from pipeswift_amd.reshape_and_cache import reshape_and_cache_flash
+    from pipeswift_amd.reshape_and_cache import reshape_and_cache_flash, reshape_and_cache_flash_amax
 
     case = workloads.config2_fp8_decode() if fp8 else workloads.config1_append()
     ps, P = case.cache.shape[2], case.cache.shape[0]
@@ -188,8 +190,7 @@ def setup_append(args, device, fp8, rescale=False):
     if rescale:
         def launch(i):
             q = qkv[i]
-            cache_ops.compute_kv_scales(case.key(q), case.value(q), out=scales)
-            reshape_and_cache_flash(case.key(q), case.value(q), kc, vc, slots[i], k_scale, v_scale)
+            reshape_and_cache_flash_amax(case.key(q), case.value(q), kc, vc, slots[i], scales_out=scales)
     else:
         def launch(i):
             q = qkv[i]
@@ -200,7 +201,7 @@ def setup_append(args, device, fp8, rescale=False):
     name = "fp8_decode_write" if rescale else ("fp8_decode_append" if fp8 else "bf16_append")
     info = {
         "name": name,
-        "kernel": ("amax_partial_kernel + amax_finalize_kernel + paged_append_small_kernel" if rescale
+        "kernel": ("amax_partial_kernel + paged_append_small_amax_kernel" if rescale
                    else "paged_append_small_kernel"),  # the launch for batches under 1024 tokens
         "bytes": nbytes + (amax_bytes if rescale else 0),
         "tokens": case.num_valid,

@@ -33,7 +33,8 @@
  *                             reference (pipeswift/llms/layers/attention.py:189-211)
  *   psk_copy_blocks           prefix-cache page copy; the reference remaps instead
  *                             (pipeswift/engine/block_manager.py:841-877)
- *   psk_kv_amax_scale         per-tensor FP8 scale; the reference fixes it at 1.0
+ *   psk_kv_amax_scale,        per-tensor FP8 scale, and the FP8 append with that
+ *   psk_reshape_and_cache_amax  scale; the reference fixes it at 1.0
  *                             (pipeswift/utils/fp8_kv.py:1-3, 75-77)
  *   psk_paged_decode_attention  decode over the FP8 cache; the reference calls
  *                             vLLM's FA3 flash_attn_varlen_func for it
@@ -228,6 +229,26 @@ int64_t psk_kv_amax_workspace_len(void);
 int psk_kv_amax_scale_noalloc(const void* x0, const void* x1, int64_t rows, int64_t row_len,
                               int64_t row_stride0, int64_t row_stride1, int dtype, float qmax,
                               float* scale_out, float* amax_out, void* stream);
+
+/*
+ * The FP8 append with per-tensor scales from this step's own K and V
+ * (build-defined; the reference appends with scale 1.0,
+ * pipeswift/utils/fp8_kv.py:1-3, 75-77): psk_kv_amax_scale over key and value
+ * ([num_tokens, num_heads * head_size] at key_stride / value_stride elements),
+ * then psk_reshape_and_cache into an fp8_e4m3fn cache with k_scale =
+ * scales_out[0], v_scale = scales_out[1].  Results (cache bytes, scales_out,
+ * amax_out) equal those two calls'.  Decode-sized batches take two launches
+ * instead of three: the append's waves reduce the partial maxima themselves
+ * and the waves of token 0 write the scales.  Other shapes run the three.
+ * `workspace` as psk_kv_amax_scale's.
+ */
+int psk_reshape_and_cache_amax(const void* key, const void* value, void* key_cache,
+                               void* value_cache, const int64_t* slot_mapping,
+                               int64_t num_tokens, int64_t num_heads, int64_t head_size,
+                               int64_t block_size, int64_t num_blocks, int64_t key_stride,
+                               int64_t value_stride, const int64_t* kc, const int64_t* vc,
+                               int in_dtype, float qmax, float* scales_out, float* amax_out,
+                               uint32_t* workspace, int64_t workspace_len, void* stream);
 
 /*
  * Host-side step metadata (replaces the per-token Python loop of

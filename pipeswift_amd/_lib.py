@@ -66,6 +66,11 @@ _SIGNATURES = {
         [_vp, _vp, _i64, _i64, _i64, _i64, _int, ctypes.c_float, _vp, _vp, _vp, _i64, _vp],
     ),
     "psk_kv_amax_workspace_len": (_i64, []),
+    "psk_reshape_and_cache_amax": (
+        _int,
+        [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _c_int64_p, _c_int64_p, _int,
+         ctypes.c_float, _vp, _vp, _vp, _i64, _vp],
+    ),
     "psk_kv_amax_scale_noalloc": (
         _int,
         [_vp, _vp, _i64, _i64, _i64, _i64, _int, ctypes.c_float, _vp, _vp, _vp],

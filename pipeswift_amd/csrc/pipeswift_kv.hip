@@ -246,8 +246,25 @@ struct SmallAppend {
   int32_t slice_shift;      // log2(slices per row); slices * 64 >= vecs
 };
 
-template <class C, int WPB>
-__global__ void __launch_bounds__(64 * WPB) paged_append_small_kernel(SmallAppend a, uint32_t num_waves) {
+// The amax finish an append can take over from amax_finalize_kernel: the
+// partial maxima of K (ws[0, nparts)) and V (ws[stride, stride + nparts)),
+// reduced by every wave for its own part, scale = amax / qmax (1.0 for an
+// all-zero part) written by the waves of token 0.
+struct AmaxFinish {
+  const uint32_t* ws;
+  int64_t stride;
+  int32_t nparts;
+  float qmax;
+  float* scale_out;  // [2]
+  float* amax_out;   // [2] or nullptr
+};
+
+// launch_scatter's answer when the fused finish does not apply to the shape:
+// nothing was launched, and the caller finalizes the scales and appends.
+constexpr int kNeedScales = 1 << 20;
+
+template <class C, int WPB, bool FIN>
+__device__ __forceinline__ void small_append(const SmallAppend& a, const AmaxFinish& f, uint32_t num_waves) {
   const int lane = threadIdx.x & (kWave - 1);
   const uint32_t wave = blockIdx.x * WPB + __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
   if (WPB > 1 && wave >= num_waves) return;  // the last workgroup's spare waves
@@ -268,12 +285,49 @@ __global__ void __launch_bounds__(64 * WPB) paged_append_small_kernel(SmallAppen
   const int il = act ? i : vecs - 1;
   const typename C::In v = vload_nt<C::IN_B>(src + t * src_stride + int64_t(il) * C::IN_B);
   const int64_t slot = a.slots[t];
-  const QScale qs = make_qscale_uniform(sp ? *sp : 1.0f);
+  float s;
+  if constexpr (FIN) {
+    // the part's amax from its partial maxima (abs bit patterns, NaN as 0),
+    // as amax_finalize_kernel takes it, while the row is in flight
+    const uint32_t* pm = f.ws + (part ? f.stride : 0);
+    uint32_t m = 0;
+    for (int k = lane; k < f.nparts; k += kWave) {
+      const uint32_t q = pm[k];
+      m = q > m ? q : m;
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+      const uint32_t o = uint32_t(__shfl_xor(int(m), off, kWave));
+      m = o > m ? o : m;
+    }
+    const float amax = __uint_as_float(uint32_t(__builtin_amdgcn_readfirstlane(int(m))));
+    s = amax > 0.0f ? amax / f.qmax : 1.0f;
+    if (t == 0 && slice == 0 && lane == 0) {
+      f.scale_out[part] = s;
+      if (f.amax_out) f.amax_out[part] = amax;
+    }
+  } else {
+    s = sp ? *sp : 1.0f;
+  }
+  const QScale qs = make_qscale_uniform(s);
   if (act && uint64_t(slot) < a.num_slots) {
     char* drow = dst + (slot >> a.bs_shift) * a.blk_stride +
                  (slot & ((int64_t(1) << a.bs_shift) - 1)) * a.page_stride;
     vstore_nt<C::OUT_B>(drow + int64_t(i) * C::OUT_B, C::apply(v, qs));
   }
+}
+
+template <class C, int WPB>
+__global__ void __launch_bounds__(64 * WPB) paged_append_small_kernel(SmallAppend a, uint32_t num_waves) {
+  small_append<C, WPB, false>(a, AmaxFinish{}, num_waves);
+}
+
+// The same append with the scales finished in-kernel from the amax partials:
+// one launch fewer than amax_finalize_kernel followed by the append.
+template <class C, int WPB>
+__global__ void __launch_bounds__(64 * WPB) paged_append_small_amax_kernel(SmallAppend a, AmaxFinish f,
+                                                                           uint32_t num_waves) {
+  small_append<C, WPB, true>(a, f, num_waves);
 }
 
 // Prefill-sized two-part rows whose second part is short (the MLA latent row:
@@ -395,14 +449,19 @@ bool launch_packed_rows(const ScatterGeom& g, const ScatterPart& p0, const Scatt
 
 bool part_flat(const ScatterPart& p, int out_b) { return p.nseg == 1 && p.inner_stride == out_b; }
 
+// fin: finish the amax scales in the append's own waves (the small kernel
+// only; other shapes return kNeedScales having launched nothing).
 template <class C>
-int launch_scatter(const ScatterGeom& g, const ScatterPart& p0, const ScatterPart& p1, hipStream_t st) {
+int launch_scatter(const ScatterGeom& g, const ScatterPart& p0, const ScatterPart& p1, hipStream_t st,
+                   const AmaxFinish* fin = nullptr) {
   const int total = p0.nseg * p0.seg_vecs > p1.nseg * p1.seg_vecs ? p0.nseg * p0.seg_vecs : p1.nseg * p1.seg_vecs;
   const ScatterShape sh = scatter_shape(g.num_tokens, total);
   const bool fast = g.bs_shift >= 0 && part_flat(p0, C::OUT_B) && (g.nparts == 1 || part_flat(p1, C::OUT_B));
+  const bool small = fast && sh.ch == 1 && g.nparts == 2 && total <= 8 * kWave && p0.blk_stride == p1.blk_stride &&
+                     p0.page_stride == p1.page_stride && g.num_tokens <= INT32_MAX / 16;
+  if (fin && !(small && C::OUT_B < C::IN_B)) return kNeedScales;
   if (!fast) return launch_scatter_shape<C, 1, 2, false, 4>(g, p0, p1, sh.ch == 1 ? sh.slice_shift : 0, st);
-  if (sh.ch == 1 && g.nparts == 2 && total <= 8 * kWave && p0.blk_stride == p1.blk_stride &&
-      p0.page_stride == p1.page_stride && g.num_tokens <= INT32_MAX / 16) {
+  if (small) {
     SmallAppend a;
     a.slots = g.slots;
     a.num_slots = uint64_t(g.num_slots);
@@ -422,6 +481,15 @@ int launch_scatter(const ScatterGeom& g, const ScatterPart& p0, const ScatterPar
     // 2048 waves 2.48 us at four against 2.61 at one; config 2's 1024 waves 2.21
     // at one against 2.25 at four).
     const int64_t waves = (g.num_tokens * 2) << sh.slice_shift;
+    if (fin) {
+      if (waves >= 2048)
+        hipLaunchKernelGGL((paged_append_small_amax_kernel<C, 4>), dim3(ceil_div(waves, 4)), dim3(4 * kWave), 0, st,
+                           a, *fin, uint32_t(waves));
+      else
+        hipLaunchKernelGGL((paged_append_small_amax_kernel<C, 1>), dim3(waves), dim3(kWave), 0, st, a, *fin,
+                           uint32_t(waves));
+      return check_launch("paged_append_small_amax_kernel launch");
+    }
     if (waves >= 2048)
       hipLaunchKernelGGL((paged_append_small_kernel<C, 4>), dim3(ceil_div(waves, 4)), dim3(4 * kWave), 0, st, a,
                          uint32_t(waves));
@@ -443,8 +511,9 @@ int launch_scatter(const ScatterGeom& g, const ScatterPart& p0, const ScatterPar
 
 // Dispatch on (in_dtype, cache_dtype, vector elements).
 int dispatch_scatter(int in_dt, int cache_dt, int elems, const ScatterGeom& g, const ScatterPart& p0,
-                     const ScatterPart& p1, hipStream_t st) {
+                     const ScatterPart& p1, hipStream_t st, const AmaxFinish* fin = nullptr) {
   if (in_dt == cache_dt) {
+    if (fin) return kNeedScales;
     switch (elems * dtype_size(in_dt)) {
       case 16: return launch_scatter<CopyConv<16>>(g, p0, p1, st);
       case 8: return launch_scatter<CopyConv<8>>(g, p0, p1, st);
@@ -457,10 +526,10 @@ int dispatch_scatter(int in_dt, int cache_dt, int elems, const ScatterGeom& g, c
   if (cache_dt != PSK_DTYPE_FP8_E4M3FN) return fail(PSK_E_DTYPE, "cache dtype must equal the input dtype or be fp8_e4m3fn");
 #define PSK_QUANT_CASES(DT)                                                   \
   switch (elems) {                                                            \
-    case 8: return launch_scatter<QuantConv<DT, 8>>(g, p0, p1, st);           \
-    case 4: return launch_scatter<QuantConv<DT, 4>>(g, p0, p1, st);           \
-    case 2: return launch_scatter<QuantConv<DT, 2>>(g, p0, p1, st);           \
-    case 1: return launch_scatter<QuantConv<DT, 1>>(g, p0, p1, st);           \
+    case 8: return launch_scatter<QuantConv<DT, 8>>(g, p0, p1, st, fin);      \
+    case 4: return launch_scatter<QuantConv<DT, 4>>(g, p0, p1, st, fin);      \
+    case 2: return launch_scatter<QuantConv<DT, 2>>(g, p0, p1, st, fin);      \
+    case 1: return launch_scatter<QuantConv<DT, 1>>(g, p0, p1, st, fin);      \
   }                                                                           \
   return fail(PSK_E_ARG, "internal: bad quant vector width");
   switch (in_dt) {
@@ -468,9 +537,9 @@ int dispatch_scatter(int in_dt, int cache_dt, int elems, const ScatterGeom& g, c
     case PSK_DTYPE_F16: { PSK_QUANT_CASES(PSK_DTYPE_F16) }
     case PSK_DTYPE_F32: {
       switch (elems) {
-        case 4: return launch_scatter<QuantConv<PSK_DTYPE_F32, 4>>(g, p0, p1, st);
-        case 2: return launch_scatter<QuantConv<PSK_DTYPE_F32, 2>>(g, p0, p1, st);
-        case 1: return launch_scatter<QuantConv<PSK_DTYPE_F32, 1>>(g, p0, p1, st);
+        case 4: return launch_scatter<QuantConv<PSK_DTYPE_F32, 4>>(g, p0, p1, st, fin);
+        case 2: return launch_scatter<QuantConv<PSK_DTYPE_F32, 2>>(g, p0, p1, st, fin);
+        case 1: return launch_scatter<QuantConv<PSK_DTYPE_F32, 1>>(g, p0, p1, st, fin);
       }
       return fail(PSK_E_ARG, "internal: bad quant vector width");
     }
@@ -1151,12 +1220,17 @@ const char* psk_last_error(void) { return g_err; }
 
 int psk_abi_version(void) { return 1; }
 
-int psk_reshape_and_cache(const void* key, const void* value, void* key_cache, void* value_cache,
-                          const int64_t* slot_mapping, int64_t num_tokens, int64_t num_heads,
-                          int64_t head_size, int64_t block_size, int64_t num_blocks, int64_t key_stride,
-                          int64_t value_stride, const int64_t* kc, const int64_t* vc, int in_dtype,
-                          int cache_dtype, const float* k_scale, const float* v_scale, void* stream) {
-  begin_device_call();
+}  // extern "C"
+
+namespace {
+
+// psk_reshape_and_cache's body; fin (FP8 only): finish the amax scales in the
+// append (kNeedScales when the shape does not take it: nothing launched).
+int append_kv(const void* key, const void* value, void* key_cache, void* value_cache, const int64_t* slot_mapping,
+              int64_t num_tokens, int64_t num_heads, int64_t head_size, int64_t block_size, int64_t num_blocks,
+              int64_t key_stride, int64_t value_stride, const int64_t* kc, const int64_t* vc, int in_dtype,
+              int cache_dtype, const float* k_scale, const float* v_scale, hipStream_t stream,
+              const AmaxFinish* fin) {
   if (num_tokens < 0 || num_heads <= 0 || head_size <= 0 || block_size <= 0 || num_blocks < 0)
     return fail(PSK_E_ARG, "bad sizes: num_tokens=%lld num_heads=%lld head_size=%lld block_size=%lld num_blocks=%lld",
                 (long long)num_tokens, (long long)num_heads, (long long)head_size, (long long)block_size,
@@ -1236,7 +1310,22 @@ int psk_reshape_and_cache(const void* key, const void* value, void* key_cache, v
   };
   const ScatterPart pk = make_part(key, key_cache, key_stride, kc, k_scale, k_flat);
   const ScatterPart pv = make_part(value, value_cache, value_stride, vc, v_scale, v_flat);
-  return dispatch_scatter(in_dtype, cache_dtype, elems, g, pk, pv, static_cast<hipStream_t>(stream));
+  return dispatch_scatter(in_dtype, cache_dtype, elems, g, pk, pv, stream, fin);
+}
+
+}  // namespace
+
+extern "C" {
+
+int psk_reshape_and_cache(const void* key, const void* value, void* key_cache, void* value_cache,
+                          const int64_t* slot_mapping, int64_t num_tokens, int64_t num_heads,
+                          int64_t head_size, int64_t block_size, int64_t num_blocks, int64_t key_stride,
+                          int64_t value_stride, const int64_t* kc, const int64_t* vc, int in_dtype,
+                          int cache_dtype, const float* k_scale, const float* v_scale, void* stream) {
+  begin_device_call();
+  return append_kv(key, value, key_cache, value_cache, slot_mapping, num_tokens, num_heads, head_size, block_size,
+                   num_blocks, key_stride, value_stride, kc, vc, in_dtype, cache_dtype, k_scale, v_scale,
+                   static_cast<hipStream_t>(stream), nullptr);
 }
 
 int psk_concat_and_cache_mla(const void* kv_c, const void* k_pe, void* kv_cache, const int64_t* slot_mapping,
@@ -1669,19 +1758,17 @@ int64_t psk_build_next_decode_metadata(int64_t num_seqs, const uint64_t* page_ta
 
 int64_t psk_kv_amax_workspace_len(void) { return kAmaxWsLen; }
 
-int psk_kv_amax_scale(const void* x0, const void* x1, int64_t rows, int64_t row_len, int64_t row_stride0,
-                      int64_t row_stride1, int dtype, float qmax, float* scale_out, float* amax_out,
-                      uint32_t* workspace, int64_t workspace_len, void* stream) {
-  begin_device_call();
-  if (rows < 0 || row_len < 0) return fail(PSK_E_ARG, "negative size");
+}  // extern "C"
+
+namespace {
+
+// psk_kv_amax_scale's first launch (its arguments checked by the caller): the
+// partial maxima into `workspace`; *args and *blocks_out describe them for the
+// finish (amax_finalize_kernel, or an append that finishes them itself).
+int amax_partials(const void* x0, const void* x1, int64_t rows, int64_t row_len, int64_t row_stride0,
+                  int64_t row_stride1, int dtype, float qmax, float* scale_out, float* amax_out, uint32_t* workspace,
+                  hipStream_t st, AmaxArgs* args, int64_t* blocks_out) {
   const int sz = dtype_size(dtype);
-  if (!sz || dtype == PSK_DTYPE_FP8_E4M3FN) return fail(PSK_E_DTYPE, "amax input must be bf16, fp16 or fp32");
-  if (!(qmax > 0.0f)) return fail(PSK_E_ARG, "qmax must be positive");
-  // an empty tensor (NULL data) reads nothing: its amax is 0 and its scale 1.0
-  if ((!x0 && rows * row_len > 0) || !scale_out || !workspace) return fail(PSK_E_ARG, "NULL pointer");
-  if (workspace_len < kAmaxWsLen)
-    return fail(PSK_E_WORKSPACE, "amax workspace needs %lld uint32 words, got %lld", (long long)kAmaxWsLen,
-                (long long)workspace_len);
   int64_t rws = rows, rl = row_len;
   // A contiguous tensor is one long row.
   const bool contig0 = row_stride0 == row_len, contig1 = !x1 || row_stride1 == row_len;
@@ -1714,7 +1801,6 @@ int psk_kv_amax_scale(const void* x0, const void* x1, int64_t rows, int64_t row_
   a.amax_out = amax_out;
   a.ws = workspace;
   const dim3 grid(unsigned(blocks), x1 ? 2u : 1u);
-  hipStream_t st = static_cast<hipStream_t>(stream);
 #define PSK_AMAX_LAUNCH(DT)                                                                                     \
   switch (vb) {                                                                                                 \
     case 16: hipLaunchKernelGGL((amax_partial_kernel<DT, 16>), grid, dim3(256), 0, st, a); break;               \
@@ -1728,7 +1814,33 @@ int psk_kv_amax_scale(const void* x0, const void* x1, int64_t rows, int64_t row_
     case PSK_DTYPE_F32: PSK_AMAX_LAUNCH(PSK_DTYPE_F32) break;
   }
 #undef PSK_AMAX_LAUNCH
-  const int st1 = check_launch("amax_partial_kernel launch");
+  *args = a;
+  *blocks_out = blocks;
+  return check_launch("amax_partial_kernel launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+int psk_kv_amax_scale(const void* x0, const void* x1, int64_t rows, int64_t row_len, int64_t row_stride0,
+                      int64_t row_stride1, int dtype, float qmax, float* scale_out, float* amax_out,
+                      uint32_t* workspace, int64_t workspace_len, void* stream) {
+  begin_device_call();
+  if (rows < 0 || row_len < 0) return fail(PSK_E_ARG, "negative size");
+  const int sz = dtype_size(dtype);
+  if (!sz || dtype == PSK_DTYPE_FP8_E4M3FN) return fail(PSK_E_DTYPE, "amax input must be bf16, fp16 or fp32");
+  if (!(qmax > 0.0f)) return fail(PSK_E_ARG, "qmax must be positive");
+  // an empty tensor (NULL data) reads nothing: its amax is 0 and its scale 1.0
+  if ((!x0 && rows * row_len > 0) || !scale_out || !workspace) return fail(PSK_E_ARG, "NULL pointer");
+  if (workspace_len < kAmaxWsLen)
+    return fail(PSK_E_WORKSPACE, "amax workspace needs %lld uint32 words, got %lld", (long long)kAmaxWsLen,
+                (long long)workspace_len);
+  AmaxArgs a;
+  int64_t blocks = 0;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int st1 = amax_partials(x0, x1, rows, row_len, row_stride0, row_stride1, dtype, qmax, scale_out, amax_out,
+                                workspace, st, &a, &blocks);
   if (st1 != PSK_OK) return st1;
   hipLaunchKernelGGL(amax_finalize_kernel, dim3(1), dim3(256), 0, st, a, int(blocks), x1 ? 2 : 1);
   return check_launch("amax_finalize_kernel launch");
@@ -1747,6 +1859,52 @@ int psk_kv_amax_scale_noalloc(const void* x0, const void* x1, int64_t rows, int6
   // psk_kv_amax_scale rejects any change that would break that.
   return psk_kv_amax_scale(x0, x1, rows, row_len, row_stride0, row_stride1, dtype, qmax, scale_out, amax_out, ws,
                            kAmaxWsLen, stream);
+}
+
+int psk_reshape_and_cache_amax(const void* key, const void* value, void* key_cache, void* value_cache,
+                               const int64_t* slot_mapping, int64_t num_tokens, int64_t num_heads,
+                               int64_t head_size, int64_t block_size, int64_t num_blocks, int64_t key_stride,
+                               int64_t value_stride, const int64_t* kc, const int64_t* vc, int in_dtype, float qmax,
+                               float* scales_out, float* amax_out, uint32_t* workspace, int64_t workspace_len,
+                               void* stream) {
+  begin_device_call();
+  if (num_tokens < 0 || num_heads <= 0 || head_size <= 0 || block_size <= 0 || num_blocks < 0)
+    return fail(PSK_E_ARG, "bad sizes: num_tokens=%lld num_heads=%lld head_size=%lld block_size=%lld num_blocks=%lld",
+                (long long)num_tokens, (long long)num_heads, (long long)head_size, (long long)block_size,
+                (long long)num_blocks);
+  if (in_dtype != PSK_DTYPE_BF16 && in_dtype != PSK_DTYPE_F16 && in_dtype != PSK_DTYPE_F32)
+    return fail(PSK_E_DTYPE, "amax-scaled append input must be bf16, fp16 or fp32 (got %d)", in_dtype);
+  if (!(qmax > 0.0f)) return fail(PSK_E_ARG, "qmax must be positive");
+  if (!scales_out || !workspace || !kc || !vc) return fail(PSK_E_ARG, "NULL pointer");
+  if (workspace_len < kAmaxWsLen)
+    return fail(PSK_E_WORKSPACE, "amax workspace needs %lld uint32 words, got %lld", (long long)kAmaxWsLen,
+                (long long)workspace_len);
+  const int64_t row = num_heads * head_size;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (num_tokens == 0) {  // empty K and V: scale 1.0 each, nothing to append
+    int r = psk_kv_amax_scale(key, nullptr, 0, row, row, row, in_dtype, qmax, scales_out, amax_out, workspace,
+                              workspace_len, stream);
+    if (r != PSK_OK) return r;
+    return psk_kv_amax_scale(value, nullptr, 0, row, row, row, in_dtype, qmax, scales_out + 1,
+                             amax_out ? amax_out + 1 : nullptr, workspace, workspace_len, stream);
+  }
+  if (!key || !value || !key_cache || !value_cache || !slot_mapping) return fail(PSK_E_ARG, "NULL tensor pointer");
+  AmaxArgs a;
+  int64_t blocks = 0;
+  int r = amax_partials(key, value, num_tokens, row, key_stride, value_stride, in_dtype, qmax, scales_out, amax_out,
+                        workspace, st, &a, &blocks);
+  if (r != PSK_OK) return r;
+  const AmaxFinish f{workspace, kAmaxMaxBlocks, int32_t(blocks), qmax, scales_out, amax_out};
+  r = append_kv(key, value, key_cache, value_cache, slot_mapping, num_tokens, num_heads, head_size, block_size,
+                num_blocks, key_stride, value_stride, kc, vc, in_dtype, PSK_DTYPE_FP8_E4M3FN, nullptr, nullptr, st, &f);
+  if (r != kNeedScales) return r;
+  // a shape the fused finish does not take: finalize, then the plain append
+  hipLaunchKernelGGL(amax_finalize_kernel, dim3(1), dim3(256), 0, st, a, int(blocks), 2);
+  r = check_launch("amax_finalize_kernel launch");
+  if (r != PSK_OK) return r;
+  return append_kv(key, value, key_cache, value_cache, slot_mapping, num_tokens, num_heads, head_size, block_size,
+                   num_blocks, key_stride, value_stride, kc, vc, in_dtype, PSK_DTYPE_FP8_E4M3FN, scales_out,
+                   scales_out + 1, st, nullptr);
 }
 
 int psk_host_alloc(int64_t bytes, void** ptr) {

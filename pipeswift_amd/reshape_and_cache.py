@@ -110,6 +110,60 @@ def reshape_and_cache_flash(
     check(status, "reshape_and_cache_flash")
 
 
+def reshape_and_cache_flash_amax(
+    key: torch.Tensor,
+    value: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    scales_out: torch.Tensor | None = None,
+    amax_out: torch.Tensor | None = None,
+    qmax: float = 448.0,
+) -> torch.Tensor:
+    """The FP8 append with per-tensor scales taken from this step's own K and
+    V: the cache bytes and scales of ``cache_ops.compute_kv_scales(key,
+    value)`` followed by ``reshape_and_cache_flash(..., k_scale=scales[0:1],
+    v_scale=scales[1:2])``, in two launches for decode-sized batches (the
+    append's waves finish the amax themselves) and three otherwise.  The
+    reference appends with scale 1.0 (fp8_kv.py:1-3, 75-77).  Returns float32
+    [2] (``scales_out`` when given), [k_scale, v_scale]."""
+    from . import cache_ops
+
+    assert key.ndim == 3 and value.ndim == 3 and key_cache.ndim == 4 and value_cache.ndim == 4
+    assert key.is_cuda and value.is_cuda and slot_mapping.is_cuda
+    num_heads, head_size = key.shape[1], key.shape[2]
+    assert value.shape[1:] == key.shape[1:] and key_cache.shape[2:] == (num_heads, head_size)
+    assert value_cache.shape[2:] == (num_heads, head_size)
+    assert key_cache.dtype == torch.float8_e4m3fn and value_cache.dtype == key_cache.dtype, "the cache must be fp8"
+    assert key.dtype in (torch.bfloat16, torch.float16, torch.float32) and value.dtype == key.dtype
+    assert key.shape[0] == value.shape[0] == slot_mapping.shape[0], "one slot per K/V row"
+    for t in (key, value):  # a token's [H, D] is one flat row
+        assert t.stride(2) == 1 and (t.stride(1) == head_size or num_heads == 1)
+    assert value_cache.stride()[:3] == key_cache.stride()[:3], "value_cache must share key_cache's strides"
+    device = key_cache.device
+    assert key.device == device and value.device == device and value_cache.device == device
+    _check_slots(slot_mapping, key.shape[0], device)
+    if scales_out is None:
+        assert not torch.cuda.is_current_stream_capturing(), "pass `scales_out` when capturing"
+        scales_out = torch.empty(2, dtype=torch.float32, device=device)
+    assert scales_out.dtype == torch.float32 and scales_out.numel() >= 2 and scales_out.is_contiguous()
+    assert scales_out.device == device
+    if amax_out is not None:
+        assert amax_out.dtype == torch.float32 and amax_out.numel() >= 2 and amax_out.device == device
+    ws = cache_ops.amax_workspace(device)
+    kc = key_cache.stride()
+    vc = (kc[0], kc[1], kc[2], value_cache.stride(3))
+    status = lib().psk_reshape_and_cache_amax(
+        ptr(key), ptr(value), ptr(key_cache), ptr(value_cache), ptr(slot_mapping),
+        key.shape[0], num_heads, head_size, key_cache.shape[1], key_cache.shape[0],
+        key.stride(0), value.stride(0), _lib.i64_array(kc), _lib.i64_array(vc),
+        dtype_code(key.dtype), float(qmax), ptr(scales_out), ptr(amax_out), ptr(ws), ws.numel(),
+        stream_handle(device),
+    )
+    check(status, "reshape_and_cache_flash_amax")
+    return scales_out
+
+
 def reshape_and_cache_flash_diffkv(
     key: torch.Tensor,
     value: torch.Tensor,
