@@ -260,7 +260,9 @@ struct AmaxFinish {
 };
 
 // launch_scatter's answer when the fused finish does not apply to the shape:
-// nothing was launched, and the caller finalizes the scales and appends.
+// nothing was launched, and the caller finalizes the scales and appends.  It
+// is no status a call returns: PSK_E_* codes are negative and HIP errors
+// (hipError_t values, returned as they are) lie far below 2^20.
 constexpr int kNeedScales = 1 << 20;
 
 template <class C, int WPB, bool FIN>
